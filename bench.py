@@ -1,0 +1,239 @@
+#!/usr/bin/env python3
+"""Benchmark of QStream's quantized matvec hot path on one MI355X.
+
+Metric: quant matvec HBM GB/s (% of ~8 TB/s peak) + us/call
+at 7B decode shapes.  The default workload is BASELINE config 1: the
+2-bit+outlier FFN gate and up projections (11008x4096 each, block 64), batch-1
+decode.  A step is one pass over one activation vector: x-prep + one grouped
+GEMV launch over gate and up.  Weights rotate over >= 512 MiB of distinct
+copies in HBM so the 256 MB Infinity Cache cannot serve them; inputs are
+resident in HBM before the timed region.
+
+    python bench.py [--steps K] [--warmup W] [--config 1|0|2|3|all]
+
+Prints one JSON line.  `value` is algorithmic bytes per step (on-disk QSF
+payload + x read once + y written, per matrix) / wall time per step, over K
+steps between two synchronisations.  `roofline.achieved` is the same bytes of
+the GEMV launch / its average duration from HIP events recorded around it on
+the launch stream.  `cpu_baseline` times QStream's own AVX2 kernel
+(oracle/_ref, reference release flags, 1 thread) on a bounded sample.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+ROTATE_BYTES = 512 << 20
+METRIC = "quant matvec HBM GB/s (% of ~8 TB/s peak) + µs/call at 7B decode shapes"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+# ---------------------------------------------------------------------------
+def cfg1_data(seed=1):
+    from qstream_amd import qsf_format as F
+    rng = np.random.default_rng(seed)
+    rows, cols, bs = 11008, 4096, 64
+    mats = []
+    for name in ("gate", "up"):
+        w = F.heavy_tail_weights(rng, rows, cols)
+        mats.append((name, np.frombuffer(F.quantize_matrix(w, F.Q2_OUTLIER, bs), np.uint8), rows, cols))
+        del w
+    x = F.gaussian(rng, cols)
+    return F.Q2_OUTLIER, bs, mats, x
+
+
+def cfg0_data(seed=0):
+    from qstream_amd import qsf_format as F
+    rng = np.random.default_rng(seed)
+    rows, cols, bs = 4096, 4096, 64
+    w = F.gaussian(rng, (rows, cols), 0.02)
+    mats = [("w", np.frombuffer(F.quantize_matrix(w, F.Q4, bs), np.uint8), rows, cols)]
+    return F.Q4, bs, mats, F.gaussian(rng, cols)
+
+
+def algo_bytes(mats) -> int:
+    return sum(len(p) + 4 * c + 4 * r for _, p, r, c in mats)
+
+
+class Events:
+    def __init__(self, torch, n):
+        self.ev = [torch.cuda.Event(enable_timing=True) for _ in range(n)]
+
+
+def run_dense(torch, hip, qt, bs, mats, x, steps, warmup, group=True):
+    """Rotating copies of `mats`; each step: xprep + grouped GEMV."""
+    per_copy = sum(len(p) for _, p, _, _ in mats)
+    n_copies = max(2, math.ceil(ROTATE_BYTES / per_copy))
+    copies = [[hip.Tensor(p, qt, r, c, bs) for _, p, r, c in mats] for _ in range(n_copies)]
+    cols = mats[0][3]
+    stream = torch.cuda.current_stream()
+    dx = torch.from_numpy(x).to("cuda:0")
+    xq = torch.empty(hip.xprep_bytes(qt, bs, cols) + 256, dtype=torch.uint8, device="cuda:0")
+    xq_addr = (xq.data_ptr() + 255) & ~255
+    ys = [torch.empty(r, device="cuda:0") for _, _, r, _ in mats]
+
+    def step(i, ev=None):
+        ts = copies[i % n_copies]
+        if ev is not None:
+            ev[0].record(stream)
+        hip.xprep(qt, bs, cols, dx, xq_addr, stream=stream)
+        if ev is not None:
+            ev[1].record(stream)
+        if group:
+            hip.matvec_group_prepared(ts, dx, xq_addr, ys, stream=stream)
+        else:
+            for t, y in zip(ts, ys):
+                hip.matvec_group_prepared([t], dx, xq_addr, [y], stream=stream)
+        if ev is not None:
+            ev[2].record(stream)
+
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    # whole-job throughput: K steps between two synchronisations
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    for i in range(steps):
+        step(i)
+    t1.record(stream)
+    torch.cuda.synchronize()
+    ms_total = t0.elapsed_time(t1)
+    # per-kernel durations (events around each launch) over a second timed pass
+    evs = [Events(torch, 3).ev for _ in range(steps)]
+    for i in range(steps):
+        step(i, evs[i])
+    torch.cuda.synchronize()
+    gemv_ms = [e[1].elapsed_time(e[2]) for e in evs]
+    xprep_ms = [e[0].elapsed_time(e[1]) for e in evs]
+    for ts in copies:
+        for t in ts:
+            t.free()
+    return {
+        "ms_per_step": ms_total / steps,
+        "gemv_ms_mean": float(np.mean(gemv_ms)),
+        "gemv_ms_median": float(np.median(gemv_ms)),
+        "xprep_ms_mean": float(np.mean(xprep_ms)),
+        "n_copies": n_copies,
+        "rotation_mib": n_copies * per_copy / (1 << 20),
+    }
+
+
+def cpu_baseline_dense(qt, bs, mats, x, budget_s=10.0):
+    """QStream's own AVX2 kernel (oracle/_ref) on host cores, 1 thread; falls
+    back to this build's scalar restatement (oracle) if _ref is absent."""
+    from oracle.oracle import Oracle, ref_avx2
+    ref = ref_avx2()
+    kind, fn = ("reference", None)
+    if ref is not None:
+        def fn(p, r, c):
+            return ref.matvec(qt, p, x, r, c, bs, isa="avx2")
+        name = "qsf_matvec_outlier_2bit_avx2" if qt == 9 else "qsf_matvec_4bit_avx2"
+    else:
+        kind = "port"
+        o = Oracle()
+
+        def fn(p, r, c):
+            return o.matvec(qt, p, x, r, c, bs)
+        name = "oracle scalar"
+    # 4 distinct host copies per matrix so the rotation exceeds the LLC
+    hcopies = [[(np.array(p, copy=True), r, c) for _, p, r, c in mats] for _ in range(4)]
+    per_step = algo_bytes(mats)
+    times = []
+    t_start = time.perf_counter()
+    i = 0
+    while time.perf_counter() - t_start < budget_s or len(times) < 3:
+        t = time.perf_counter()
+        for p, r, c in hcopies[i % 4]:
+            fn(p, r, c)
+        times.append(time.perf_counter() - t)
+        i += 1
+        if len(times) >= 200:
+            break
+    med = float(np.median(times))
+    return {"value": per_step / med / 1e9, "unit": "GB/s", "cores": 1, "kind": kind,
+            "sample": f"{name}, {len(times)} steps (gate+up per step) over 4 host copies, "
+                      f"median {med * 1e3:.1f} ms/step, {time.perf_counter() - t_start:.1f} s"}
+
+
+def bench_dense(torch, hip, cfg, steps, warmup, with_cpu=True):
+    qt, bs, mats, x = cfg1_data() if cfg == 1 else cfg0_data()
+    log(f"config {cfg}: data ready ({len(mats)} matrices)")
+    res = run_dense(torch, hip, qt, bs, mats, x, steps, warmup)
+    bytes_step = algo_bytes(mats)
+    value = bytes_step / (res["ms_per_step"] * 1e-3) / 1e9
+    achieved = bytes_step / (res["gemv_ms_mean"] * 1e-3) / 1e9
+    out = {
+        "value": value,
+        "ms_per_step": res["ms_per_step"],
+        "us_per_call": res["ms_per_step"] * 1e3 / len(mats),
+        "gemv_us": res["gemv_ms_mean"] * 1e3,
+        "xprep_us": res["xprep_ms_mean"] * 1e3,
+        "bytes_per_step": bytes_step,
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": None},
+        "rotation_mib": res["rotation_mib"],
+    }
+    if with_cpu:
+        out["cpu_baseline"] = cpu_baseline_dense(qt, bs, mats, x)
+    return out
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--config", default="1")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path "
+              "(single-GPU hot path; see DESIGN.md for how it would shard)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    from qstream_amd import qsf_hip
+    qsf_hip.init(0)
+    cfg = int(args.config) if args.config != "all" else 1
+    r = bench_dense(torch, qsf_hip, cfg, args.steps, args.warmup, with_cpu=not args.no_cpu)
+    workload = {1: "cfg1: 2-bit+outlier FFN gate+up, 2x 11008x4096, block 64, batch-1 decode",
+                0: "cfg0: 4-bit asym 4096x4096, block 64, batch-1 decode"}[cfg]
+    line = {
+        "metric": METRIC,
+        "value": round(r["value"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(r["ms_per_step"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "i4xi4->i32 dot, f32 accumulate",
+        "data": "synthetic (seeded N(0,0.02) + Student-t outliers, converter-semantics quantisation)",
+        "config": {"workload": workload, "us_per_call": round(r["us_per_call"], 3),
+                   "gemv_us": round(r["gemv_us"], 3), "xprep_us": round(r["xprep_us"], 3),
+                   "bytes_per_step": r["bytes_per_step"], "hbm_frac_of_8TBs": round(r["value"] / HBM_PEAK_GBS, 4),
+                   "rotation_mib": round(r["rotation_mib"], 1)},
+        "roofline": r["roofline"],
+    }
+    if "cpu_baseline" in r:
+        line["cpu_baseline"] = r["cpu_baseline"]
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,153 @@
+/*
+ * qsf_hip.h - C ABI of libqsf_hip, the MI355X (gfx950) backend for
+ * QStream's quantized matrix-vector hot path.
+ *
+ * Plain C: pointers, sizes and ints only.  Reference citations are relative
+ * to the QStream source tree (include/, src/, tools/).
+ *
+ * Two layers:
+ *  1. Drop-in table slots with exactly the qsf_matvec_fn signature
+ *     (include/qsf/kernels.h:53-58).  They take host pointers like the CPU
+ *     kernels, are synchronous on return, and upload a weight payload to HBM
+ *     the first time its host pointer is seen (device weight arena).
+ *  2. Device-pointer entry points for callers whose activations already live
+ *     in HBM (the device-resident engine path and the benchmarks).
+ *
+ * Status codes are QSFError values (include/qsf/error.h:14-32): 0 = QSF_OK,
+ * 4 = QSF_ERR_OUT_OF_MEMORY, 11 = QSF_ERR_INVALID_INPUT, 15 = QSF_ERR_INTERNAL.
+ * The void table slots report through qsf_set_error() when the host engine
+ * links one (src/error.c:43-53) and through qsf_hip_last_error(); on failure
+ * they fill the output with quiet NaN (there is no CPU fallback).
+ */
+#ifndef QSF_HIP_H
+#define QSF_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define QSF_HIP_QUANT_MXFP4 11   /* quant type added in an unused enum slot */
+
+/* ---- lifecycle ----------------------------------------------------------- */
+/* Select the GPU and create the library's stream.  Called implicitly by the
+ * first table-slot call (device 0).  Replaces nothing in the reference: the
+ * CPU backend needs no device (src/engine.c:435-439 is where it is called). */
+int         qsf_hip_init(int device);
+/* Free every tensor, workspace and stream. */
+void        qsf_hip_shutdown(void);
+int         qsf_hip_last_error(void);
+const char* qsf_hip_last_error_detail(void);
+
+/* ---- 1. drop-in table slots (qsf_matvec_fn) ------------------------------ */
+/* src/kernels_scalar.c:16-37 (2-bit; also QSF_QUANT_2BIT_SYM, src/engine.c:143) */
+void qsf_matvec_2bit_hip(const void* weights_q, const float* input, float* output,
+                         int rows, int cols, int block_size);
+/* src/kernels_scalar.c:40-61 */
+void qsf_matvec_3bit_hip(const void* weights_q, const float* input, float* output,
+                         int rows, int cols, int block_size);
+/* src/kernels_scalar.c:64-85 (also every type the engine maps to the 4-bit slot) */
+void qsf_matvec_4bit_hip(const void* weights_q, const float* input, float* output,
+                         int rows, int cols, int block_size);
+/* src/kernels_scalar.c:88-109; decodes nibbles as two's complement like the
+ * scalar reference (src/quant.c:166-174) */
+void qsf_matvec_4bit_sym_hip(const void* weights_q, const float* input, float* output,
+                             int rows, int cols, int block_size);
+/* src/quant.c:387-445 / src/kernels_avx2.c:420-488; weights_q points at the
+ * payload's [u32 n] outlier header */
+void qsf_matvec_outlier_2bit_hip(const void* weights_q, const float* input, float* output,
+                                 int rows, int cols, int block_size);
+/* src/quant.c:447-495 / src/kernels_avx2.c:491-549 */
+void qsf_matvec_outlier_4bit_hip(const void* weights_q, const float* input, float* output,
+                                 int rows, int cols, int block_size);
+/* New slot (no reference kernel): MXFP4 E2M1 codes + E8M0 scales per 32
+ * elements, element order of tools/convert_hf.py:1456-1495, payload
+ * [rows][cols/32][16 B codes] then [rows][cols/32] scales.  block_size is
+ * ignored (always 32). */
+void qsf_matvec_mxfp4_hip(const void* weights_q, const float* input, float* output,
+                          int rows, int cols, int block_size);
+
+/* src/kernels.c:7-65 (qsf_kernels_init).  Writes the six matvec slots at the
+ * head of a QSFKernelTable (include/qsf/kernels.h:91-98) -- call it after
+ * qsf_kernels_init() so the remaining CPU slots stay as they are.  When
+ * mxfp4_slot is non-NULL it receives qsf_matvec_mxfp4_hip (the slot the
+ * engine appends to the table for quant type 11). */
+void qsf_kernels_init_hip(void* kernel_table, const void* platform, void** mxfp4_slot);
+
+/* ---- device weight arena (replaces mmap streaming, src/file_access.c:80-88) */
+typedef struct qsf_hip_tensor qsf_hip_tensor;   /* opaque */
+
+/* Upload one tensor payload (as find_tensor returns it, src/engine.c:183-202)
+ * and register its host pointer; later table-slot calls with that pointer
+ * run from HBM.  Returns NULL on error. */
+qsf_hip_tensor* qsf_hip_tensor_upload(const void* host_payload, int quant_type,
+                                      int rows, int cols, int block_size);
+/* Tensor registered for this host pointer, or NULL. */
+qsf_hip_tensor* qsf_hip_tensor_lookup(const void* host_payload);
+void            qsf_hip_tensor_free(qsf_hip_tensor* t);
+/* Forget a host pointer (call when the caller reuses the buffer). */
+int             qsf_hip_arena_forget(const void* host_payload);
+/* Bytes of HBM held by the arena. */
+size_t          qsf_hip_arena_bytes(void);
+/* On-disk payload bytes of a registered tensor. */
+size_t          qsf_hip_tensor_payload_bytes(const qsf_hip_tensor* t);
+
+/* ---- 2. device-pointer entry points --------------------------------------- */
+/* y[rows] = W x[cols] on `stream` (hipStream_t, NULL = library stream);
+ * asynchronous.  d_x, d_y are device pointers. */
+int qsf_hip_matvec_dev(const qsf_hip_tensor* t, const float* d_x, float* d_y, void* stream);
+/* n (<= 8) tensors with the same type/cols/block size sharing one x in one
+ * launch (q/k/v, gate/up). */
+int qsf_hip_matvec_group_dev(const qsf_hip_tensor* const* t, int n, const float* d_x,
+                             float* const* d_y, void* stream);
+
+/* Split form of the two calls above, for callers that share one x between
+ * several launches or fuse the activation preparation upstream: prepare x
+ * once (block-fixed-point digits, qsf_hip_xprep_bytes bytes of device
+ * memory, 256-B aligned), then run any number of GEMVs on it.  d_x must
+ * still be passed: the outlier pass reads it. */
+size_t qsf_hip_xprep_bytes(int quant_type, int block_size, int cols);
+int qsf_hip_xprep_dev(int quant_type, int block_size, int cols, const float* d_x,
+                      void* d_xq, void* stream);
+int qsf_hip_matvec_group_prepared_dev(const qsf_hip_tensor* const* t, int n,
+                                      const float* d_x, const void* d_xq,
+                                      float* const* d_y, void* stream);
+
+/* ---- MoE FFN with MXFP4 experts (src/engine.c:951-1107) ------------------ */
+typedef struct qsf_hip_moe qsf_hip_moe;         /* opaque device expert table */
+/* gate/up: [expert_dim][hidden], down: [hidden][expert_dim], all MXFP4
+ * tensors from qsf_hip_tensor_upload.  Bias arrays are host fp16 vectors per
+ * expert (the MOE_*_BIAS tensors, src/engine.c:1039-1046); the outer array or
+ * any entry may be NULL. */
+qsf_hip_moe* qsf_hip_moe_create(int n_experts, int hidden, int expert_dim,
+                                const qsf_hip_tensor* const* gate,
+                                const qsf_hip_tensor* const* up,
+                                const qsf_hip_tensor* const* down,
+                                const uint16_t* const* gate_bias,
+                                const uint16_t* const* up_bias,
+                                const uint16_t* const* down_bias);
+void qsf_hip_moe_free(qsf_hip_moe* m);
+/* For each of ntok (<= 8) tokens: softmax(router logits), top_k by strict
+ * '>' insertion, optional renormalisation, then per selected expert
+ * gate/up + bias, activation (QSFActivation: 2 SiLU, 0/1 GELU, else ReLU)
+ * times up, down + bias, weighted sum in rank order.  d_x [ntok][hidden],
+ * d_logits [ntok][n_experts], d_out [ntok][hidden]; asynchronous. */
+int qsf_hip_moe_forward_dev(qsf_hip_moe* m, int top_k, int norm_topk, int activation,
+                            int ntok, const float* d_x, const float* d_logits,
+                            float* d_out, void* stream);
+
+/* Bit-exact unpack of `nblocks` QSF blocks already in device memory (the
+ * same device code paths the GEMV uses): codes int8[nblocks*bs] (2/3/4-bit
+ * field values; 4-bit sym as two's complement), meta u32[nblocks] (first
+ * block dword: fp16 scale | fp16 zero << 16), dequantised fp32[nblocks*bs]
+ * (scale*q + zero with separate roundings, src/quant.c:95-177).
+ * Any output pointer may be NULL. */
+int qsf_hip_unpack_dev(int quant_type, const void* d_blocks, int nblocks, int block_size,
+                       int8_t* d_codes, uint32_t* d_meta, float* d_dequant, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* QSF_HIP_H */

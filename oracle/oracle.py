@@ -1,0 +1,223 @@
+"""ctypes bindings of the CPU parity checker (test infrastructure only).
+
+``Oracle`` wraps this build's C restatement (liboracle.so); ``RefLib`` wraps
+QStream's own quant.c/kernels_scalar.c/kernels_avx2.c compiled from the
+reference tree into oracle/_ref (present only where it was built).
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import
+this module; the product path never does.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ORACLE_SO = os.path.join(HERE, "liboracle.so")
+REF_STRICT_SO = os.path.join(HERE, "_ref", "libqsf_ref_strict.so")
+REF_AVX2_SO = os.path.join(HERE, "_ref", "libqsf_ref_avx2.so")
+
+_vp, _fp, _i = C.c_void_p, C.POINTER(C.c_float), C.c_int
+
+
+def _ptr(a: np.ndarray):
+    return a.ctypes.data_as(C.c_void_p)
+
+
+def _buf(b):
+    """bytes / uint8 array -> (keepalive array, void*)."""
+    a = np.frombuffer(b, dtype=np.uint8) if isinstance(b, (bytes, bytearray)) else np.ascontiguousarray(b)
+    return a, _ptr(a)
+
+
+class Oracle:
+    def __init__(self, path: str = ORACLE_SO):
+        if not os.path.exists(path):
+            raise FileNotFoundError(f"{path} missing: run `make -C oracle`")
+        L = self.lib = C.CDLL(path)
+        L.orc_fp16_to_fp32.restype = C.c_float
+        L.orc_fp16_to_fp32.argtypes = [C.c_uint16]
+        L.orc_fp16_to_fp32_array.argtypes = [_vp, _vp, _i]
+        L.orc_block_bytes.restype = C.c_size_t
+        L.orc_block_bytes.argtypes = [_i, _i]
+        L.orc_unpack_codes.argtypes = [_i, _vp, _i, _vp]
+        L.orc_dequant_block.argtypes = [_i, _vp, _vp, _i]
+        L.orc_unpack_codes_many.argtypes = [_i, _vp, _i, _i, _vp]
+        L.orc_matvec.argtypes = [_i, _vp, _vp, _vp, _i, _i, _i]
+        L.orc_payload_bytes.restype = C.c_size_t
+        L.orc_payload_bytes.argtypes = [_i, _vp, _i, _i, _i]
+        L.orc_e2m1_to_fp32.restype = C.c_float
+        L.orc_e2m1_to_fp32.argtypes = [C.c_uint8]
+        L.orc_e8m0_to_fp32.restype = C.c_float
+        L.orc_e8m0_to_fp32.argtypes = [C.c_uint8]
+        L.orc_softmax.argtypes = [_vp, _vp, _i]
+        L.orc_act.argtypes = [_i, _vp, _i]
+        L.orc_topk.argtypes = [_vp, _i, _i, _i, _vp, _vp]
+        L.orc_moe_token.argtypes = [_vp, _i, _i, _i, _i, _i, _i, _vp, _vp, _vp]
+        L.orc_prefill_4bit.argtypes = [_vp, _vp, _vp, _i, _i, _i, _i]
+
+    def fp16_to_fp32_bits(self, h: np.ndarray) -> np.ndarray:
+        # bulk C call: a ctypes float return would quiet signalling NaNs
+        h = np.ascontiguousarray(h, np.uint16)
+        out = np.empty(len(h), np.float32)
+        self.lib.orc_fp16_to_fp32_array(_ptr(h), _ptr(out), len(h))
+        return out.view(np.uint32)
+
+    def block_bytes(self, qt: int, bs: int) -> int:
+        return self.lib.orc_block_bytes(qt, bs)
+
+    def unpack_codes(self, qt: int, block, count: int) -> np.ndarray:
+        keep, p = _buf(block)
+        out = np.zeros(count, np.int8)
+        self.lib.orc_unpack_codes(qt, p, count, _ptr(out))
+        return out
+
+    def dequant_block(self, qt: int, block, count: int) -> np.ndarray:
+        keep, p = _buf(block)
+        out = np.zeros(count, np.float32)
+        self.lib.orc_dequant_block(qt, p, _ptr(out), count)
+        return out
+
+    def unpack_codes_many(self, qt: int, blocks, nblocks: int, bs: int) -> np.ndarray:
+        keep, p = _buf(blocks)
+        out = np.zeros(nblocks * bs, np.int8)
+        self.lib.orc_unpack_codes_many(qt, p, nblocks, bs, _ptr(out))
+        return out.reshape(nblocks, bs)
+
+    def matvec(self, qt: int, payload, x: np.ndarray, rows: int, cols: int, bs: int) -> np.ndarray:
+        keep, p = _buf(payload)
+        x = np.ascontiguousarray(x, np.float32)
+        y = np.zeros(max(rows, 0), np.float32)
+        self.lib.orc_matvec(qt, p, _ptr(x), _ptr(y), rows, cols, bs)
+        return y
+
+    def payload_bytes(self, qt, payload, rows, cols, bs) -> int:
+        keep, p = _buf(payload)
+        return self.lib.orc_payload_bytes(qt, p, rows, cols, bs)
+
+    def softmax(self, x):
+        x = np.ascontiguousarray(x, np.float32)
+        out = np.zeros_like(x)
+        self.lib.orc_softmax(_ptr(x), _ptr(out), len(x))
+        return out
+
+    def act(self, act: int, x):
+        x = np.array(x, np.float32, copy=True)
+        self.lib.orc_act(act, _ptr(x), len(x))
+        return x
+
+    def topk(self, probs, k: int, norm: int):
+        probs = np.ascontiguousarray(probs, np.float32)
+        idx = np.zeros(k, np.int32)
+        w = np.zeros(k, np.float32)
+        self.lib.orc_topk(_ptr(probs), len(probs), k, norm, _ptr(idx), _ptr(w))
+        return idx, w
+
+    def moe_token(self, experts, k, norm, act, hidden, eid, x, logits):
+        """experts: list of dicts with gate/up/down payload bytes and optional
+        fp16 bias arrays (gate_bias, up_bias, down_bias)."""
+        class Ex(C.Structure):
+            _fields_ = [(n, C.c_void_p) for n in
+                        ("gate", "gate_bias", "up", "up_bias", "down", "down_bias")]
+        keep = []
+        arr = (Ex * len(experts))()
+        for i, e in enumerate(experts):
+            for n in ("gate", "gate_bias", "up", "up_bias", "down", "down_bias"):
+                v = e.get(n)
+                if v is None:
+                    setattr(arr[i], n, None)
+                    continue
+                a, p = _buf(v if not isinstance(v, np.ndarray) else np.ascontiguousarray(v))
+                keep.append(a)
+                setattr(arr[i], n, p.value)
+        x = np.ascontiguousarray(x, np.float32)
+        logits = np.ascontiguousarray(logits, np.float32)
+        out = np.zeros(hidden, np.float32)
+        self.lib.orc_moe_token(C.cast(arr, C.c_void_p), len(experts), k, norm, act,
+                               hidden, eid, _ptr(x), _ptr(logits), _ptr(out))
+        return out
+
+    def prefill_4bit(self, payload, x_bf16: np.ndarray, m, n, k, bs) -> np.ndarray:
+        keep, p = _buf(payload)
+        xb = np.ascontiguousarray(x_bf16, np.uint16)
+        y = np.zeros((m, n), np.float32)
+        self.lib.orc_prefill_4bit(p, _ptr(xb), _ptr(y), m, n, k, bs)
+        return y
+
+
+_MATVEC_SYMS = ("qsf_matvec_2bit_scalar", "qsf_matvec_3bit_scalar",
+                "qsf_matvec_4bit_scalar", "qsf_matvec_4bit_sym_scalar")
+_AVX2_SYMS = ("qsf_matvec_2bit_avx2", "qsf_matvec_4bit_avx2",
+              "qsf_matvec_4bit_sym_avx2", "qsf_matvec_outlier_2bit_avx2",
+              "qsf_matvec_outlier_4bit_avx2")
+
+
+class RefLib:
+    """QStream's own hot-path translation units (compiled into oracle/_ref)."""
+
+    def __init__(self, path: str):
+        if not os.path.exists(path):
+            raise FileNotFoundError(path)
+        L = self.lib = C.CDLL(path)
+        self.path = path
+        L.qsf_fp16_to_fp32.restype = C.c_float
+        L.qsf_fp16_to_fp32.argtypes = [C.c_uint16]
+        L.qsf_fp16_to_fp32_array.argtypes = [_vp, _vp, _i]
+        L.qsf_quant_block_size.restype = C.c_size_t
+        L.qsf_quant_block_size.argtypes = [_i, _i]
+        for n in ("qsf_dequant_block_2bit", "qsf_dequant_block_3bit",
+                  "qsf_dequant_block_4bit", "qsf_dequant_block_4bit_sym"):
+            getattr(L, n).argtypes = [_vp, _vp, _i]
+        for n in _MATVEC_SYMS:
+            getattr(L, n).argtypes = [_vp, _vp, _vp, _i, _i, _i]
+        for n in ("qsf_matvec_outlier_2bit", "qsf_matvec_outlier_4bit"):
+            getattr(L, n).argtypes = [_vp, C.c_size_t, _vp, _vp, _i, _i, _i]
+        self.has_avx2 = hasattr(L, "qsf_matvec_4bit_avx2")
+        if self.has_avx2:
+            for n in _AVX2_SYMS:
+                getattr(L, n).argtypes = [_vp, _vp, _vp, _i, _i, _i]
+        L.qsf_quant_block_2bit.argtypes = [_vp, _vp, _i]
+        L.qsf_quant_block_3bit.argtypes = [_vp, _vp, _i]
+        L.qsf_quant_block_4bit.argtypes = [_vp, _vp, _i]
+
+    def fp16_table(self) -> np.ndarray:
+        # qsf_fp16_to_fp32_array (src/quant.c:61-65) writes the bits directly
+        h = np.arange(65536, dtype=np.uint16)
+        out = np.empty(65536, np.float32)
+        self.lib.qsf_fp16_to_fp32_array(_ptr(h), _ptr(out), 65536)
+        return out.view(np.uint32)
+
+    def dequant_block(self, qt: int, block, count: int) -> np.ndarray:
+        name = {0: "2bit", 1: "2bit", 2: "3bit", 3: "4bit", 4: "4bit_sym"}[qt]
+        keep, p = _buf(block)
+        out = np.zeros(count, np.float32)
+        getattr(self.lib, f"qsf_dequant_block_{name}")(p, _ptr(out), count)
+        return out
+
+    def matvec(self, qt: int, payload, x, rows, cols, bs, isa: str = "scalar") -> np.ndarray:
+        keep, p = _buf(payload)
+        x = np.ascontiguousarray(x, np.float32)
+        y = np.zeros(max(rows, 0), np.float32)
+        if qt in (9, 10):
+            base = "2bit" if qt == 9 else "4bit"
+            if isa == "avx2":
+                getattr(self.lib, f"qsf_matvec_outlier_{base}_avx2")(p, _ptr(x), _ptr(y), rows, cols, bs)
+            else:
+                getattr(self.lib, f"qsf_matvec_outlier_{base}")(p, 0, _ptr(x), _ptr(y), rows, cols, bs)
+            return y
+        name = {0: "2bit", 1: "2bit", 2: "3bit", 4: "4bit_sym"}.get(qt, "4bit")
+        if isa == "avx2" and name != "3bit":
+            fn = getattr(self.lib, f"qsf_matvec_{name}_avx2")
+        else:
+            fn = getattr(self.lib, f"qsf_matvec_{name}_scalar")
+        fn(p, _ptr(x), _ptr(y), rows, cols, bs)
+        return y
+
+
+def ref_strict() -> RefLib | None:
+    return RefLib(REF_STRICT_SO) if os.path.exists(REF_STRICT_SO) else None
+
+
+def ref_avx2() -> RefLib | None:
+    return RefLib(REF_AVX2_SO) if os.path.exists(REF_AVX2_SO) else None

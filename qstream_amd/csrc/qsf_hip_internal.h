@@ -1,0 +1,90 @@
+/*
+ * qsf_hip_internal.h - contract between the C11 host layer (host/qsf_hip.c)
+ * and the gfx950 kernels (the csrc .hip files).  Plain C: no C++ types cross it.
+ */
+#ifndef QSF_HIP_INTERNAL_H
+#define QSF_HIP_INTERNAL_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Quant type ids (include/qsf/types.h:43-56) plus MXFP4 in unused slot 11. */
+enum {
+    QK_Q2 = 0, QK_Q2SYM = 1, QK_Q3 = 2, QK_Q4 = 3, QK_Q4SYM = 4,
+    QK_Q2_OUTLIER = 9, QK_Q4_OUTLIER = 10, QK_MXFP4 = 11
+};
+
+/* Kernel formats of the decode GEMV (what the device unpacks). */
+enum { QK_FMT_2 = 0, QK_FMT_3 = 1, QK_FMT_4 = 2, QK_FMT_4SYM = 3 };
+
+/* A weight tensor resident in HBM.  Block bytes are the QSF on-disk blocks,
+ * unchanged, relocated to a 256-byte aligned region; an outlier table is
+ * re-encoded as per-row CSR (file order kept inside a row, out-of-range
+ * entries dropped, duplicates kept). */
+typedef struct qsf_hip_tensor {
+    int      qt, rows, cols, bs;
+    int      fmt;               /* QK_FMT_* or -1 for MXFP4 */
+    int      nb;                /* blocks per row */
+    int      block_bytes;
+    const void* host_key;       /* registry key (host payload pointer) */
+    size_t   payload_bytes;     /* on-disk payload size (algorithmic bytes) */
+    uint8_t* d_blocks;          /* rows*nb*block_bytes (MXFP4: codes plane) */
+    uint8_t* d_scales;          /* MXFP4: E8M0 plane rows*nb, else NULL */
+    uint32_t n_outliers;        /* entries in the file table */
+    uint32_t n_csr;             /* entries kept (in range) */
+    uint32_t* d_row_ptr;        /* rows+1, or NULL */
+    uint32_t* d_ocol;           /* n_csr column indices */
+    uint16_t* d_oval;           /* n_csr fp16 values */
+    void*    d_alloc;           /* base of the single device allocation */
+    int      registry_owned;    /* uploaded implicitly by a table-slot call */
+    struct qsf_hip_tensor* prev; /* list of live tensors (freed at shutdown) */
+    struct qsf_hip_tensor* next;
+} qsf_hip_tensor;
+
+#define QK_MAX_GROUP 8
+
+/* Per-call prepared activation: block-fixed-point digits of x. */
+size_t qk_xprep_bytes(int fmt, int bs, int cols);
+
+/* x preparation into ws (qk_xprep_bytes(fmt, bs, cols) bytes, 256-B aligned) */
+int qk_xprep(int fmt, int bs, int cols, const float* d_x, void* d_ws, hipStream_t s);
+/* GEMV over n tensors sharing x; mode selects the x-prep and/or GEMV launch. */
+enum { QK_RUN_XPREP = 1, QK_RUN_GEMV = 2, QK_RUN_BOTH = 3 };
+int qk_gemv_group(const qsf_hip_tensor* const* t, int n, const float* d_x,
+                  float* const* d_y, void* d_ws, int mode, hipStream_t s);
+
+/* Bit-exact unpack checks: codes as int8 [nblocks][bs], meta bits u32 per
+ * block (scale | zero << 16); dequantised fp32 [nblocks][bs]. */
+int qk_unpack(int qt, const void* d_blocks, int nblocks, int bs,
+              int8_t* d_codes, uint32_t* d_meta, float* d_deq, hipStream_t s);
+
+/* MXFP4 GEMV for T tokens: y[t][rows] = W x[t]. */
+int qk_mxfp4_gemv(const qsf_hip_tensor* t, const float* d_x, int ntok,
+                  float* d_y, hipStream_t s);
+
+/* MoE FFN (src/engine.c:951-1107) for ntok <= 8 tokens, experts in MXFP4.
+ * Device-side expert table entry: codes/scales of gate, up ([eid][hidden])
+ * and down ([hidden][eid]) plus optional fp16 biases (NULL = none). */
+typedef struct {
+    const uint8_t* gc; const uint8_t* gs; const uint16_t* gb;
+    const uint8_t* uc; const uint8_t* us; const uint16_t* ub;
+    const uint8_t* dc; const uint8_t* ds; const uint16_t* db;
+} qk_mx_expert;
+size_t qk_moe_ws_bytes(int n_exp, int k, int ntok, int hidden, int eid);
+int qk_moe_launch(const qk_mx_expert* d_experts, int n_exp, int k, int norm, int act,
+                  int hidden, int eid, int ntok, const float* d_x, const float* d_logits,
+                  float* d_out, void* d_ws, hipStream_t s);
+
+/* 4-bit prefill on MFMA: y[m][n] = W[n] . float(x_bf16[m]) */
+int qk_prefill_4bit(const qsf_hip_tensor* t, const uint16_t* d_x_bf16, int m,
+                    float* d_y, hipStream_t s);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

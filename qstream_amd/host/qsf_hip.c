@@ -1,0 +1,721 @@
+/*
+ * qsf_hip.c - C11 host layer of libqsf_hip.
+ *
+ * Fills QStream's matvec table slots (src/kernels.c:7-65) with functions of
+ * the qsf_matvec_fn type (include/qsf/kernels.h:53-58) that run on the GPU,
+ * and keeps weight payloads resident in HBM (device weight arena) instead of
+ * streaming them from the mmap'd file (src/file_access.c:80-88).
+ *
+ * Behaviour the engine relies on (src/engine.c:141-152, call sites in
+ * engine.c) is kept: synchronous on return, output fully overwritten,
+ * rows <= 0 a no-op, cols == 0 writes zeros, outlier entries applied
+ * additively with out-of-range rows skipped (src/quant.c:423-444).
+ */
+#include "qsf_hip.h"
+#include "../csrc/qsf_hip_internal.h"
+
+#include <math.h>
+#include <pthread.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ---- errors --------------------------------------------------------------- */
+enum { E_OK = 0, E_OOM = 4, E_INVALID = 11, E_INTERNAL = 15 };
+
+/* The engine's error sink (src/error.c:43-53), used when the host links it. */
+extern void qsf_set_error(int err, const char* detail) __attribute__((weak));
+
+static _Thread_local int g_err;
+static _Thread_local char g_err_detail[256];
+
+static int fail(int code, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err_detail, sizeof g_err_detail, fmt, ap);
+    va_end(ap);
+    g_err = code;
+    if (qsf_set_error) qsf_set_error(code, g_err_detail);
+    return code;
+}
+
+int qsf_hip_last_error(void) { return g_err; }
+const char* qsf_hip_last_error_detail(void) { return g_err_detail; }
+
+/* ---- device state ----------------------------------------------------------- */
+typedef struct {
+    int ready, device;
+    hipStream_t stream;
+    void* ws;          size_t ws_bytes;       /* x-prep / MoE workspace */
+    float* d_x;        size_t d_x_n;          /* staging for host-pointer calls */
+    float* d_y;        size_t d_y_n;
+    float* h_x;        size_t h_x_n;          /* pinned host staging */
+    float* h_y;        size_t h_y_n;
+    size_t arena_bytes;
+} dev_state;
+
+static dev_state g_dev;
+static pthread_mutex_t g_lock = PTHREAD_MUTEX_INITIALIZER;
+
+#define HIPCHK(call, code)                                                        \
+    do {                                                                          \
+        hipError_t e_ = (call);                                                   \
+        if (e_ != hipSuccess)                                                     \
+            return fail(code, "%s: %s", #call, hipGetErrorString(e_));           \
+    } while (0)
+
+static int init_locked(int device) {
+    if (g_dev.ready) return E_OK;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0)
+        return fail(E_INTERNAL, "qsf_hip: no GPU visible");
+    if (device < 0 || device >= n) return fail(E_INVALID, "qsf_hip: device %d of %d", device, n);
+    HIPCHK(hipSetDevice(device), E_INTERNAL);
+    HIPCHK(hipStreamCreateWithFlags(&g_dev.stream, hipStreamNonBlocking), E_INTERNAL);
+    g_dev.device = device;
+    g_dev.ready = 1;
+    return E_OK;
+}
+
+int qsf_hip_init(int device) {
+    pthread_mutex_lock(&g_lock);
+    int rc = init_locked(device);
+    pthread_mutex_unlock(&g_lock);
+    return rc;
+}
+
+/* grow-only device buffer */
+static int ensure_dev(void** p, size_t* have, size_t need) {
+    if (*have >= need) return E_OK;
+    if (*p) hipFree(*p);
+    *p = NULL;
+    *have = 0;
+    size_t sz = need < 4096 ? 4096 : need + need / 2;
+    HIPCHK(hipMalloc(p, sz), E_OOM);
+    *have = sz;
+    return E_OK;
+}
+
+static int ensure_host(void** p, size_t* have, size_t need) {
+    if (*have >= need) return E_OK;
+    if (*p) hipHostFree(*p);
+    *p = NULL;
+    *have = 0;
+    size_t sz = need < 4096 ? 4096 : need + need / 2;
+    HIPCHK(hipHostMalloc(p, sz, hipHostMallocDefault), E_OOM);
+    *have = sz;
+    return E_OK;
+}
+
+/* ---- tensor payload geometry (src/quant.c:69-85) ------------------------- */
+static int kernel_fmt(int qt) {
+    switch (qt) {
+    case QK_Q2: case QK_Q2SYM: case QK_Q2_OUTLIER: return QK_FMT_2;
+    case QK_Q3: return QK_FMT_3;
+    case QK_Q4SYM: return QK_FMT_4SYM;
+    case QK_MXFP4: return -1;
+    default: return QK_FMT_4;   /* the engine maps every other type to 4-bit */
+    }
+}
+
+static int fmt_bits(int fmt) { return fmt == QK_FMT_2 ? 2 : fmt == QK_FMT_3 ? 3 : 4; }
+
+static int is_outlier(int qt) { return qt == QK_Q2_OUTLIER || qt == QK_Q4_OUTLIER; }
+
+static uint32_t rd_u32(const uint8_t* p) {
+    uint32_t v;
+    memcpy(&v, p, 4);
+    return v;
+}
+
+/* ---- registry: host payload pointer -> device tensor --------------------- */
+typedef struct {
+    const void* key;
+    qsf_hip_tensor* t;
+    uint64_t fp;       /* fingerprint of sampled payload words */
+} reg_slot;
+
+static reg_slot* g_reg;
+static size_t g_reg_cap, g_reg_n;
+
+static size_t hash_ptr(const void* p) {
+    uint64_t v = (uint64_t)(uintptr_t)p;
+    v ^= v >> 33; v *= 0xff51afd7ed558ccdULL; v ^= v >> 33;
+    return (size_t)v;
+}
+
+static uint64_t fingerprint(const uint8_t* p, size_t n) {
+    uint64_t h = 1469598103934665603ULL ^ n;
+    if (n == 0) return h;
+    size_t pos[9] = {0, n / 8, n / 4, 3 * n / 8, n / 2, 5 * n / 8, 3 * n / 4, 7 * n / 8, n - 1};
+    for (int i = 0; i < 9; i++) {
+        size_t a = pos[i] > n - 8 && n >= 8 ? n - 8 : pos[i];
+        uint64_t w = 0;
+        memcpy(&w, p + a, n >= 8 ? 8 : 1);
+        h = (h ^ w) * 1099511628211ULL;
+    }
+    return h;
+}
+
+static reg_slot* reg_find(const void* key) {
+    if (!g_reg_cap) return NULL;
+    for (size_t i = hash_ptr(key) & (g_reg_cap - 1);; i = (i + 1) & (g_reg_cap - 1)) {
+        if (g_reg[i].key == key) return &g_reg[i];
+        if (!g_reg[i].key) return NULL;
+    }
+}
+
+static int reg_put(const void* key, qsf_hip_tensor* t, uint64_t fp) {
+    if ((g_reg_n + 1) * 2 > g_reg_cap) {
+        size_t cap = g_reg_cap ? g_reg_cap * 2 : 256;
+        reg_slot* nr = calloc(cap, sizeof *nr);
+        if (!nr) return fail(E_OOM, "qsf_hip: registry");
+        for (size_t i = 0; i < g_reg_cap; i++) {
+            if (!g_reg[i].key) continue;
+            size_t j = hash_ptr(g_reg[i].key) & (cap - 1);
+            while (nr[j].key) j = (j + 1) & (cap - 1);
+            nr[j] = g_reg[i];
+        }
+        free(g_reg);
+        g_reg = nr;
+        g_reg_cap = cap;
+    }
+    size_t i = hash_ptr(key) & (g_reg_cap - 1);
+    while (g_reg[i].key && g_reg[i].key != key) i = (i + 1) & (g_reg_cap - 1);
+    if (!g_reg[i].key) g_reg_n++;
+    g_reg[i].key = key;
+    g_reg[i].t = t;
+    g_reg[i].fp = fp;
+    return E_OK;
+}
+
+static void reg_del(const void* key) {
+    reg_slot* s = reg_find(key);
+    if (!s) return;
+    size_t i = (size_t)(s - g_reg);
+    g_reg[i].key = NULL;
+    g_reg[i].t = NULL;
+    g_reg_n--;
+    /* re-insert the rest of the probe run */
+    for (size_t j = (i + 1) & (g_reg_cap - 1); g_reg[j].key; j = (j + 1) & (g_reg_cap - 1)) {
+        reg_slot tmp = g_reg[j];
+        g_reg[j].key = NULL;
+        g_reg_n--;
+        reg_put(tmp.key, tmp.t, tmp.fp);
+    }
+}
+
+/* ---- upload --------------------------------------------------------------- */
+/* Ownership: tensors returned by qsf_hip_tensor_upload belong to the caller
+ * (freed by qsf_hip_tensor_free); tensors a table-slot call uploads belong to
+ * the registry.  Registering a new tensor for a host pointer drops the old
+ * entry and frees it only if the registry owned it.  Every live tensor is on
+ * g_live so qsf_hip_shutdown can free them all. */
+static qsf_hip_tensor* g_live;
+
+static void tensor_destroy(qsf_hip_tensor* t) {
+    if (!t) return;
+    if (t->prev) t->prev->next = t->next;
+    else if (g_live == t) g_live = t->next;
+    if (t->next) t->next->prev = t->prev;
+    if (t->d_alloc) {
+        hipFree(t->d_alloc);
+        g_dev.arena_bytes -= t->payload_bytes;
+    }
+    free(t);
+}
+
+static void tensor_link(qsf_hip_tensor* t) {
+    t->prev = NULL;
+    t->next = g_live;
+    if (g_live) g_live->prev = t;
+    g_live = t;
+}
+
+/* unregister a host pointer; free its tensor if the registry owned it */
+static void reg_drop(const void* key) {
+    reg_slot* s = reg_find(key);
+    if (!s) return;
+    qsf_hip_tensor* t = s->t;
+    reg_del(key);
+    if (t && t->registry_owned) tensor_destroy(t);
+}
+
+static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+static qsf_hip_tensor* upload_locked(const void* host, int qt, int rows, int cols, int bs) {
+    if (init_locked(g_dev.ready ? g_dev.device : 0) != E_OK) return NULL;
+    if (!host || rows < 0 || cols < 0) {
+        fail(E_INVALID, "qsf_hip_tensor_upload: bad arguments");
+        return NULL;
+    }
+    const int fmt = kernel_fmt(qt);
+    if (fmt >= 0 && !(bs == 32 || bs == 64 || bs == 128 || bs == 256)) {
+        fail(E_INVALID, "qsf_hip: block size %d not in {32,64,128,256}", bs);
+        return NULL;
+    }
+    qsf_hip_tensor* t = calloc(1, sizeof *t);
+    if (!t) { fail(E_OOM, "qsf_hip: tensor"); return NULL; }
+    t->qt = qt; t->rows = rows; t->cols = cols; t->bs = fmt >= 0 ? bs : 32; t->fmt = fmt;
+    t->host_key = host;
+    const uint8_t* p = (const uint8_t*)host;
+    size_t blocks_bytes, scales_bytes = 0;
+    uint32_t n_out = 0;
+    if (fmt < 0) {
+        t->nb = (cols + 31) / 32;
+        t->block_bytes = 16;
+        blocks_bytes = (size_t)rows * t->nb * 16;
+        scales_bytes = (size_t)rows * t->nb;
+        t->payload_bytes = blocks_bytes + scales_bytes;
+    } else {
+        t->nb = (cols + bs - 1) / bs;
+        t->block_bytes = 4 + (bs * fmt_bits(fmt) + 7) / 8;
+        blocks_bytes = (size_t)rows * t->nb * t->block_bytes;
+        t->payload_bytes = blocks_bytes;
+        if (is_outlier(qt)) {
+            n_out = rd_u32(p);
+            t->payload_bytes += 4 + 6 * (size_t)n_out;
+        }
+    }
+    t->n_outliers = n_out;
+
+    /* CSR of the outlier table: stable counting sort by row keeps file order
+     * within a row; entries with row >= rows are dropped (src/quant.c:432-434). */
+    uint32_t* row_ptr = NULL;
+    uint32_t* ocol = NULL;
+    uint16_t* oval = NULL;
+    uint32_t kept = 0;
+    if (is_outlier(qt) && rows > 0 && cols > 0) {
+        const uint8_t* ent = p + 4;
+        row_ptr = calloc((size_t)rows + 1, sizeof *row_ptr);
+        ocol = malloc(sizeof *ocol * (n_out ? n_out : 1));
+        oval = malloc(sizeof *oval * (n_out ? n_out : 1));
+        if (!row_ptr || !ocol || !oval) {
+            free(row_ptr); free(ocol); free(oval); free(t);
+            fail(E_OOM, "qsf_hip: outlier CSR");
+            return NULL;
+        }
+        for (uint32_t i = 0; i < n_out; i++) {
+            uint32_t flat = rd_u32(ent + 6 * (size_t)i);
+            uint32_t r = flat / (uint32_t)cols;
+            if (r < (uint32_t)rows) row_ptr[r + 1]++;
+        }
+        for (int r = 0; r < rows; r++) row_ptr[r + 1] += row_ptr[r];
+        kept = row_ptr[rows];
+        uint32_t* fill = malloc(sizeof *fill * ((size_t)rows + 1));
+        if (!fill) {
+            free(row_ptr); free(ocol); free(oval); free(t);
+            fail(E_OOM, "qsf_hip: outlier CSR");
+            return NULL;
+        }
+        memcpy(fill, row_ptr, sizeof *fill * ((size_t)rows + 1));
+        for (uint32_t i = 0; i < n_out; i++) {
+            const uint8_t* e = ent + 6 * (size_t)i;
+            uint32_t flat = rd_u32(e);
+            uint32_t r = flat / (uint32_t)cols;
+            if (r >= (uint32_t)rows) continue;
+            uint32_t at = fill[r]++;
+            ocol[at] = flat % (uint32_t)cols;
+            memcpy(&oval[at], e + 4, 2);
+        }
+        free(fill);
+    }
+    t->n_csr = kept;
+
+    /* one allocation: [blocks][scales][row_ptr][ocol][oval], 256-B aligned parts */
+    size_t off_blocks = 0;
+    size_t off_scales = align256(blocks_bytes);
+    size_t off_rp = off_scales + align256(scales_bytes);
+    size_t rp_bytes = row_ptr ? ((size_t)rows + 1) * 4 : 0;
+    size_t off_oc = off_rp + align256(rp_bytes);
+    size_t off_ov = off_oc + align256((size_t)kept * 4);
+    size_t total = off_ov + align256((size_t)kept * 2);
+    if (total == 0) total = 256;
+    /* blocks are read with 16-byte vector loads that may reach 12 bytes past
+     * the last block: keep a tail pad */
+    total += 256;
+    hipError_t he = hipMalloc(&t->d_alloc, total);
+    if (he != hipSuccess) {
+        free(row_ptr); free(ocol); free(oval); free(t);
+        fail(E_OOM, "qsf_hip: hipMalloc(%zu): %s", total, hipGetErrorString(he));
+        return NULL;
+    }
+    uint8_t* base = (uint8_t*)t->d_alloc;
+    t->d_blocks = base + off_blocks;
+    const uint8_t* host_blocks = is_outlier(qt) ? p + 4 + 6 * (size_t)n_out : p;
+    he = hipMemcpy(t->d_blocks, host_blocks, blocks_bytes, hipMemcpyHostToDevice);
+    if (he == hipSuccess && scales_bytes) {
+        t->d_scales = base + off_scales;
+        he = hipMemcpy(t->d_scales, p + blocks_bytes, scales_bytes, hipMemcpyHostToDevice);
+    }
+    if (he == hipSuccess && row_ptr) {
+        t->d_row_ptr = (uint32_t*)(base + off_rp);
+        t->d_ocol = (uint32_t*)(base + off_oc);
+        t->d_oval = (uint16_t*)(base + off_ov);
+        he = hipMemcpy(t->d_row_ptr, row_ptr, rp_bytes, hipMemcpyHostToDevice);
+        if (he == hipSuccess && kept) he = hipMemcpy(t->d_ocol, ocol, (size_t)kept * 4, hipMemcpyHostToDevice);
+        if (he == hipSuccess && kept) he = hipMemcpy(t->d_oval, oval, (size_t)kept * 2, hipMemcpyHostToDevice);
+    }
+    free(row_ptr); free(ocol); free(oval);
+    if (he != hipSuccess) {
+        hipFree(t->d_alloc);
+        free(t);
+        fail(E_INTERNAL, "qsf_hip: upload: %s", hipGetErrorString(he));
+        return NULL;
+    }
+    g_dev.arena_bytes += t->payload_bytes;
+    tensor_link(t);
+    return t;
+}
+
+qsf_hip_tensor* qsf_hip_tensor_upload(const void* host, int qt, int rows, int cols, int bs) {
+    pthread_mutex_lock(&g_lock);
+    qsf_hip_tensor* t = upload_locked(host, qt, rows, cols, bs);
+    if (t) {
+        reg_drop(host);
+        if (reg_put(host, t, fingerprint(host, t->payload_bytes)) != E_OK) {
+            tensor_destroy(t);
+            t = NULL;
+        }
+    }
+    pthread_mutex_unlock(&g_lock);
+    return t;
+}
+
+qsf_hip_tensor* qsf_hip_tensor_lookup(const void* host) {
+    pthread_mutex_lock(&g_lock);
+    reg_slot* s = reg_find(host);
+    qsf_hip_tensor* t = s ? s->t : NULL;
+    pthread_mutex_unlock(&g_lock);
+    return t;
+}
+
+void qsf_hip_tensor_free(qsf_hip_tensor* t) {
+    if (!t) return;
+    pthread_mutex_lock(&g_lock);
+    reg_slot* s = reg_find(t->host_key);
+    if (s && s->t == t) reg_del(t->host_key);
+    tensor_destroy(t);
+    pthread_mutex_unlock(&g_lock);
+}
+
+int qsf_hip_arena_forget(const void* host) {
+    pthread_mutex_lock(&g_lock);
+    int found = reg_find(host) != NULL;
+    reg_drop(host);
+    pthread_mutex_unlock(&g_lock);
+    return found ? E_OK : E_INVALID;
+}
+
+size_t qsf_hip_arena_bytes(void) { return g_dev.arena_bytes; }
+size_t qsf_hip_tensor_payload_bytes(const qsf_hip_tensor* t) { return t ? t->payload_bytes : 0; }
+
+void qsf_hip_shutdown(void) {
+    pthread_mutex_lock(&g_lock);
+    while (g_live) tensor_destroy(g_live);
+    free(g_reg);
+    g_reg = NULL;
+    g_reg_cap = g_reg_n = 0;
+    if (g_dev.ready) {
+        hipStreamSynchronize(g_dev.stream);
+        if (g_dev.ws) hipFree(g_dev.ws);
+        if (g_dev.d_x) hipFree(g_dev.d_x);
+        if (g_dev.d_y) hipFree(g_dev.d_y);
+        if (g_dev.h_x) hipHostFree(g_dev.h_x);
+        if (g_dev.h_y) hipHostFree(g_dev.h_y);
+        hipStreamDestroy(g_dev.stream);
+    }
+    memset(&g_dev, 0, sizeof g_dev);
+    pthread_mutex_unlock(&g_lock);
+}
+
+/* ---- device-pointer entry points ----------------------------------------- */
+static hipStream_t pick_stream(void* s) { return s ? (hipStream_t)s : g_dev.stream; }
+
+static int group_locked(const qsf_hip_tensor* const* t, int n, const float* d_x,
+                        float* const* d_y, void* stream) {
+    if (n <= 0 || n > QK_MAX_GROUP || !t) return fail(E_INVALID, "qsf_hip: group of %d", n);
+    for (int i = 0; i < n; i++) {
+        if (!t[i] || !d_y || !d_y[i]) return fail(E_INVALID, "qsf_hip: null tensor/output");
+        if (t[i]->fmt < 0) return fail(E_INVALID, "qsf_hip: MXFP4 tensor in the dense path");
+        if (t[i]->fmt != t[0]->fmt || t[i]->bs != t[0]->bs || t[i]->cols != t[0]->cols)
+            return fail(E_INVALID, "qsf_hip: grouped tensors differ in type/cols/block");
+    }
+    if (t[0]->cols > 0 && !d_x) return fail(E_INVALID, "qsf_hip: null input");
+    size_t ws = qk_xprep_bytes(t[0]->fmt, t[0]->bs, t[0]->cols);
+    int rc = ensure_dev(&g_dev.ws, &g_dev.ws_bytes, ws);
+    if (rc) return rc;
+    rc = qk_gemv_group(t, n, d_x, d_y, g_dev.ws, QK_RUN_BOTH, pick_stream(stream));
+    if (rc) return fail(E_INTERNAL, "qsf_hip: GEMV launch failed (%d)", rc);
+    return E_OK;
+}
+
+size_t qsf_hip_xprep_bytes(int qt, int bs, int cols) {
+    int fmt = kernel_fmt(qt);
+    return fmt < 0 || cols <= 0 ? 0 : qk_xprep_bytes(fmt, bs, cols);
+}
+
+int qsf_hip_xprep_dev(int qt, int bs, int cols, const float* d_x, void* d_xq, void* stream) {
+    int fmt = kernel_fmt(qt);
+    if (fmt < 0 || !(bs == 32 || bs == 64 || bs == 128 || bs == 256) || cols < 0 ||
+        (cols > 0 && (!d_x || !d_xq)) || ((uintptr_t)d_xq & 255))
+        return fail(E_INVALID, "qsf_hip_xprep_dev: bad arguments");
+    if (!g_dev.ready) return fail(E_INVALID, "qsf_hip: not initialised");
+    if (qk_xprep(fmt, bs, cols, d_x, d_xq, pick_stream(stream)))
+        return fail(E_INTERNAL, "qsf_hip_xprep_dev: launch failed");
+    return E_OK;
+}
+
+int qsf_hip_matvec_group_prepared_dev(const qsf_hip_tensor* const* t, int n, const float* d_x,
+                                      const void* d_xq, float* const* d_y, void* stream) {
+    if (n <= 0 || n > QK_MAX_GROUP || !t || !d_y)
+        return fail(E_INVALID, "qsf_hip: group of %d", n);
+    for (int i = 0; i < n; i++) {
+        if (!t[i] || !d_y[i] || t[i]->fmt < 0 || t[i]->fmt != t[0]->fmt ||
+            t[i]->bs != t[0]->bs || t[i]->cols != t[0]->cols)
+            return fail(E_INVALID, "qsf_hip: grouped tensors differ in type/cols/block");
+    }
+    if (t[0]->cols > 0 && (!d_x || !d_xq || ((uintptr_t)d_xq & 255)))
+        return fail(E_INVALID, "qsf_hip: prepared input missing or misaligned");
+    if (!g_dev.ready) return fail(E_INVALID, "qsf_hip: not initialised");
+    if (qk_gemv_group(t, n, d_x, d_y, (void*)d_xq, QK_RUN_GEMV, pick_stream(stream)))
+        return fail(E_INTERNAL, "qsf_hip: GEMV launch failed");
+    return E_OK;
+}
+
+int qsf_hip_matvec_group_dev(const qsf_hip_tensor* const* t, int n, const float* d_x,
+                             float* const* d_y, void* stream) {
+    pthread_mutex_lock(&g_lock);
+    int rc = g_dev.ready ? group_locked(t, n, d_x, d_y, stream)
+                         : fail(E_INVALID, "qsf_hip: not initialised");
+    pthread_mutex_unlock(&g_lock);
+    return rc;
+}
+
+static int mxfp4_locked(const qsf_hip_tensor* t, const float* d_x, float* d_y, void* stream) {
+    int rc = qk_mxfp4_gemv(t, d_x, 1, d_y, pick_stream(stream));
+    return rc ? fail(E_INTERNAL, "qsf_hip: MXFP4 launch failed (%d)", rc) : E_OK;
+}
+
+int qsf_hip_matvec_dev(const qsf_hip_tensor* t, const float* d_x, float* d_y, void* stream) {
+    if (!t) return fail(E_INVALID, "qsf_hip: null tensor");
+    pthread_mutex_lock(&g_lock);
+    int rc;
+    if (!g_dev.ready) rc = fail(E_INVALID, "qsf_hip: not initialised");
+    else if (t->rows <= 0) rc = E_OK;
+    else if (t->fmt < 0) rc = mxfp4_locked(t, d_x, d_y, stream);
+    else rc = group_locked(&t, 1, d_x, &d_y, stream);
+    pthread_mutex_unlock(&g_lock);
+    return rc;
+}
+
+int qsf_hip_unpack_dev(int qt, const void* d_blocks, int nblocks, int bs, int8_t* d_codes,
+                       uint32_t* d_meta, float* d_deq, void* stream) {
+    if (kernel_fmt(qt) < 0 || !(bs == 32 || bs == 64 || bs == 128 || bs == 256))
+        return fail(E_INVALID, "qsf_hip_unpack_dev: type %d block %d", qt, bs);
+    pthread_mutex_lock(&g_lock);
+    int rc = init_locked(0);
+    if (!rc && qk_unpack(qt, d_blocks, nblocks, bs, d_codes, d_meta, d_deq, pick_stream(stream)))
+        rc = fail(E_INTERNAL, "qsf_hip_unpack_dev: launch failed");
+    pthread_mutex_unlock(&g_lock);
+    return rc;
+}
+
+/* ---- MoE ------------------------------------------------------------------- */
+struct qsf_hip_moe {
+    int n_exp, hidden, eid;
+    qk_mx_expert* d_table;   /* device expert table */
+    void* d_alloc;           /* table + biases */
+    void* d_ws;
+    size_t ws_bytes;
+};
+
+qsf_hip_moe* qsf_hip_moe_create(int n_exp, int hidden, int eid,
+                                const qsf_hip_tensor* const* gate, const qsf_hip_tensor* const* up,
+                                const qsf_hip_tensor* const* down, const uint16_t* const* gb,
+                                const uint16_t* const* ub, const uint16_t* const* db) {
+    if (n_exp < 1 || n_exp > 256 || hidden < 4 || eid < 4 || (hidden % 4) || (eid % 4) ||
+        !gate || !up || !down) {
+        fail(E_INVALID, "qsf_hip_moe_create: bad arguments");
+        return NULL;
+    }
+    for (int e = 0; e < n_exp; e++) {
+        const qsf_hip_tensor* t[3] = {gate[e], up[e], down[e]};
+        for (int i = 0; i < 3; i++) {
+            int r = i < 2 ? eid : hidden, c = i < 2 ? hidden : eid;
+            if (!t[i] || t[i]->fmt >= 0 || t[i]->rows != r || t[i]->cols != c) {
+                fail(E_INVALID, "qsf_hip_moe_create: expert %d tensor %d is not MXFP4 [%d][%d]",
+                     e, i, r, c);
+                return NULL;
+            }
+        }
+    }
+    pthread_mutex_lock(&g_lock);
+    qsf_hip_moe* m = calloc(1, sizeof *m);
+    qk_mx_expert* host = calloc((size_t)n_exp, sizeof *host);
+    size_t table = align256(sizeof(qk_mx_expert) * (size_t)n_exp);
+    size_t hb = align256((size_t)hidden * 2), eb = align256((size_t)eid * 2);
+    size_t total = table + (size_t)n_exp * (2 * eb + hb);
+    if (!m || !host || hipMalloc(&m->d_alloc, total) != hipSuccess) {
+        free(m); free(host);
+        fail(E_OOM, "qsf_hip_moe_create: allocation");
+        pthread_mutex_unlock(&g_lock);
+        return NULL;
+    }
+    uint8_t* base = (uint8_t*)m->d_alloc;
+    m->d_table = (qk_mx_expert*)base;
+    uint8_t* bias = base + table;
+    int rc = 0;
+    for (int e = 0; e < n_exp && !rc; e++, bias += 2 * eb + hb) {
+        host[e].gc = gate[e]->d_blocks; host[e].gs = gate[e]->d_scales;
+        host[e].uc = up[e]->d_blocks;   host[e].us = up[e]->d_scales;
+        host[e].dc = down[e]->d_blocks; host[e].ds = down[e]->d_scales;
+        const uint16_t* src[3] = {gb ? gb[e] : NULL, ub ? ub[e] : NULL, db ? db[e] : NULL};
+        uint8_t* dst[3] = {bias, bias + eb, bias + 2 * eb};
+        size_t n[3] = {(size_t)eid * 2, (size_t)eid * 2, (size_t)hidden * 2};
+        const uint16_t** slot[3] = {&host[e].gb, &host[e].ub, &host[e].db};
+        for (int i = 0; i < 3; i++) {
+            *slot[i] = NULL;
+            if (!src[i]) continue;
+            if (hipMemcpy(dst[i], src[i], n[i], hipMemcpyHostToDevice) != hipSuccess) rc = 1;
+            *slot[i] = (const uint16_t*)dst[i];
+        }
+    }
+    if (!rc && hipMemcpy(m->d_table, host, sizeof(qk_mx_expert) * (size_t)n_exp,
+                         hipMemcpyHostToDevice) != hipSuccess)
+        rc = 1;
+    free(host);
+    m->n_exp = n_exp; m->hidden = hidden; m->eid = eid;
+    m->ws_bytes = qk_moe_ws_bytes(n_exp, 8, 8, hidden, eid);
+    if (!rc && hipMalloc(&m->d_ws, m->ws_bytes) != hipSuccess) rc = 1;
+    if (rc) {
+        if (m->d_ws) hipFree(m->d_ws);
+        hipFree(m->d_alloc);
+        free(m);
+        fail(E_INTERNAL, "qsf_hip_moe_create: upload failed");
+        m = NULL;
+    }
+    pthread_mutex_unlock(&g_lock);
+    return m;
+}
+
+void qsf_hip_moe_free(qsf_hip_moe* m) {
+    if (!m) return;
+    hipFree(m->d_ws);
+    hipFree(m->d_alloc);
+    free(m);
+}
+
+int qsf_hip_moe_forward_dev(qsf_hip_moe* m, int k, int norm, int act, int ntok,
+                            const float* d_x, const float* d_logits, float* d_out, void* stream) {
+    if (!m || ntok < 1 || ntok > 8 || k < 1 || k > 8 || !d_x || !d_logits || !d_out)
+        return fail(E_INVALID, "qsf_hip_moe_forward_dev: bad arguments (ntok %d, k %d)", ntok, k);
+    if (qk_moe_launch(m->d_table, m->n_exp, k, norm, act, m->hidden, m->eid, ntok, d_x, d_logits,
+                      d_out, m->d_ws, pick_stream(stream)))
+        return fail(E_INTERNAL, "qsf_hip_moe_forward_dev: launch failed");
+    return E_OK;
+}
+
+/* ---- drop-in table slots ---------------------------------------------------- */
+static void nan_fill(float* out, int rows) {
+    for (int i = 0; i < rows; i++) out[i] = NAN;
+}
+
+/* Synchronous host-pointer matvec: look up (or upload) the payload, stage x
+ * through pinned memory, run, copy y back. */
+static void host_matvec(int qt, const void* w, const float* in, float* out,
+                        int rows, int cols, int bs) {
+    if (rows <= 0) return;
+    pthread_mutex_lock(&g_lock);
+    int rc = init_locked(g_dev.ready ? g_dev.device : 0);
+    qsf_hip_tensor* t = NULL;
+    if (!rc) {
+        reg_slot* s = reg_find(w);
+        t = s ? s->t : NULL;
+        /* a reused host buffer must not be served stale: compare geometry,
+         * then the payload size this call implies, then sampled words */
+        if (t && (t->qt != qt || t->rows != rows || t->cols != cols ||
+                  (t->fmt >= 0 && t->bs != bs) ||
+                  (is_outlier(qt) && rd_u32((const uint8_t*)w) != t->n_outliers) ||
+                  s->fp != fingerprint(w, t->payload_bytes))) {
+            reg_drop(w);
+            t = NULL;
+        }
+        if (!t) {
+            t = upload_locked(w, qt, rows, cols, bs);
+            if (t) t->registry_owned = 1;
+            if (!t || reg_put(w, t, fingerprint(w, t->payload_bytes)) != E_OK) {
+                if (t) tensor_destroy(t);
+                t = NULL;
+                rc = g_err ? g_err : E_INTERNAL;
+            }
+        }
+    }
+    if (!rc) rc = ensure_dev((void**)&g_dev.d_x, &g_dev.d_x_n, sizeof(float) * (size_t)(cols > 0 ? cols : 1));
+    if (!rc) rc = ensure_dev((void**)&g_dev.d_y, &g_dev.d_y_n, sizeof(float) * (size_t)rows);
+    if (!rc) rc = ensure_host((void**)&g_dev.h_x, &g_dev.h_x_n, sizeof(float) * (size_t)(cols > 0 ? cols : 1));
+    if (!rc) rc = ensure_host((void**)&g_dev.h_y, &g_dev.h_y_n, sizeof(float) * (size_t)rows);
+    hipStream_t s = g_dev.stream;
+    if (!rc && cols > 0) {
+        memcpy(g_dev.h_x, in, sizeof(float) * (size_t)cols);
+        if (hipMemcpyAsync(g_dev.d_x, g_dev.h_x, sizeof(float) * (size_t)cols,
+                           hipMemcpyHostToDevice, s) != hipSuccess)
+            rc = fail(E_INTERNAL, "qsf_hip: H2D copy");
+    }
+    if (!rc) {
+        if (t->fmt < 0) rc = mxfp4_locked(t, g_dev.d_x, g_dev.d_y, s);
+        else rc = group_locked((const qsf_hip_tensor* const*)&t, 1, g_dev.d_x, &g_dev.d_y, s);
+    }
+    if (!rc && hipMemcpyAsync(g_dev.h_y, g_dev.d_y, sizeof(float) * (size_t)rows,
+                              hipMemcpyDeviceToHost, s) != hipSuccess)
+        rc = fail(E_INTERNAL, "qsf_hip: D2H copy");
+    if (!rc) {
+        hipError_t e = hipStreamSynchronize(s);
+        if (e != hipSuccess) rc = fail(E_INTERNAL, "qsf_hip: %s", hipGetErrorString(e));
+    }
+    if (!rc) memcpy(out, g_dev.h_y, sizeof(float) * (size_t)rows);
+    else nan_fill(out, rows);
+    pthread_mutex_unlock(&g_lock);
+}
+
+void qsf_matvec_2bit_hip(const void* w, const float* in, float* out, int rows, int cols, int bs) {
+    host_matvec(QK_Q2, w, in, out, rows, cols, bs);
+}
+void qsf_matvec_3bit_hip(const void* w, const float* in, float* out, int rows, int cols, int bs) {
+    host_matvec(QK_Q3, w, in, out, rows, cols, bs);
+}
+void qsf_matvec_4bit_hip(const void* w, const float* in, float* out, int rows, int cols, int bs) {
+    host_matvec(QK_Q4, w, in, out, rows, cols, bs);
+}
+void qsf_matvec_4bit_sym_hip(const void* w, const float* in, float* out, int rows, int cols, int bs) {
+    host_matvec(QK_Q4SYM, w, in, out, rows, cols, bs);
+}
+void qsf_matvec_outlier_2bit_hip(const void* w, const float* in, float* out, int rows, int cols, int bs) {
+    host_matvec(QK_Q2_OUTLIER, w, in, out, rows, cols, bs);
+}
+void qsf_matvec_outlier_4bit_hip(const void* w, const float* in, float* out, int rows, int cols, int bs) {
+    host_matvec(QK_Q4_OUTLIER, w, in, out, rows, cols, bs);
+}
+void qsf_matvec_mxfp4_hip(const void* w, const float* in, float* out, int rows, int cols, int bs) {
+    (void)bs;
+    host_matvec(QK_MXFP4, w, in, out, rows, cols, 32);
+}
+
+/* The six matvec slots lead QSFKernelTable in this order
+ * (include/qsf/kernels.h:91-98). */
+typedef void (*matvec_fn)(const void*, const float*, float*, int, int, int);
+
+void qsf_kernels_init_hip(void* kernel_table, const void* platform, void** mxfp4_slot) {
+    (void)platform;
+    matvec_fn* slot = (matvec_fn*)kernel_table;
+    if (slot) {
+        slot[0] = qsf_matvec_2bit_hip;
+        slot[1] = qsf_matvec_3bit_hip;
+        slot[2] = qsf_matvec_4bit_hip;
+        slot[3] = qsf_matvec_4bit_sym_hip;
+        slot[4] = qsf_matvec_outlier_2bit_hip;
+        slot[5] = qsf_matvec_outlier_4bit_hip;
+    }
+    if (mxfp4_slot) *mxfp4_slot = (void*)qsf_matvec_mxfp4_hip;
+}

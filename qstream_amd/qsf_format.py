@@ -1,0 +1,227 @@
+"""QSF weight-payload writer: the byte formats the quantized matvec reads.
+
+Restates the block quantizers of QStream's converter so that synthetic
+weights have the exact on-disk layout engine.c hands to ``qsf_matvec_fn``:
+
+* 2/4-bit asymmetric blocks ``[fp16 scale][fp16 min][packed codes]``
+  (tools/convert_hf.py:215-262): scale = (max-min)/(2^b-1), codes =
+  clip(round((w-min)/scale)) with numpy's half-to-even ``round``.
+* 4-bit symmetric blocks ``[fp16 scale][2 B pad][nibbles]`` stored offset-8
+  (tools/convert_hf.py:264-290).
+* 3-bit blocks, LSB-first bitstream (tools/convert_hf.py:292-322).
+* Outlier payloads ``[u32 n][n x (u32 flat_idx, u16 fp16)][blocks]``: the top
+  ``frac`` of |w| are stored in fp16 and zeroed before block quantisation
+  (tools/convert_hf.py:324-364).
+* MXFP4 (quant type 11, added by this build): codes plane ``[rows][nblk][16]``
+  with element 2j in the low nibble of byte j (tools/convert_hf.py:1456-1495),
+  then an E8M0 scales plane ``[rows][nblk]``; quantised per OCP MX v1.0.
+
+Blocks are laid out per row (``ceil(cols/bs)`` blocks each, last one partial),
+which is what the kernels index (src/kernels_scalar.c:19-34).  For
+``cols % bs == 0`` this equals the converter's flat blocking.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+Q2, Q2SYM, Q3, Q4, Q4SYM = 0, 1, 2, 3, 4
+Q2_OUTLIER, Q4_OUTLIER, MXFP4 = 9, 10, 11
+QUANT_NAMES = {Q2: "2bit", Q3: "3bit", Q4: "4bit", Q4SYM: "4bit_sym",
+               Q2_OUTLIER: "2bit_outlier", Q4_OUTLIER: "4bit_outlier", MXFP4: "mxfp4"}
+
+
+def block_bytes(qt: int, bs: int) -> int:
+    """src/quant.c:69-85 (the outlier types use their base type's block)."""
+    if qt in (Q2, Q2SYM, Q2_OUTLIER):
+        return 4 + (bs * 2 + 7) // 8
+    if qt == Q3:
+        return 4 + (bs * 3 + 7) // 8
+    if qt in (Q4, Q4SYM, Q4_OUTLIER):
+        return 4 + (bs * 4 + 7) // 8
+    if qt == MXFP4:
+        return 17
+    raise ValueError(f"no fixed block for quant type {qt}")
+
+
+def payload_bytes(qt: int, rows: int, cols: int, bs: int, n_outliers: int = 0) -> int:
+    if qt == MXFP4:
+        return rows * ((cols + 31) // 32) * 17
+    nb = (cols + bs - 1) // bs
+    dense = rows * nb * block_bytes(qt, bs)
+    if qt in (Q2_OUTLIER, Q4_OUTLIER):
+        return 4 + 6 * n_outliers + dense
+    return dense
+
+
+def _row_blocks(w: np.ndarray, bs: int) -> np.ndarray:
+    """[rows, cols] -> [rows*nb, bs], zero-padding each row's last block."""
+    rows, cols = w.shape
+    nb = (cols + bs - 1) // bs
+    pad = nb * bs - cols
+    if pad:
+        w = np.concatenate([w, np.zeros((rows, pad), np.float32)], axis=1)
+    return np.ascontiguousarray(w, dtype=np.float32).reshape(rows * nb, bs)
+
+
+def _fp16_bytes(v: np.ndarray) -> np.ndarray:
+    return v.astype(np.float16).view(np.uint8).reshape(-1, 2)
+
+
+def _asym_codes(blocks: np.ndarray, maxv: int):
+    bmin = blocks.min(axis=1)
+    bmax = blocks.max(axis=1)
+    rng = bmax - bmin
+    with np.errstate(divide="ignore", invalid="ignore"):
+        scale = np.where(rng > 1e-30, rng / float(maxv), 0.0).astype(np.float32)
+        inv = np.where(scale > 1e-30, 1.0 / scale, 0.0).astype(np.float32)
+    vals = (blocks - bmin[:, None]) * inv[:, None]
+    codes = np.clip(np.round(vals), 0, maxv).astype(np.uint8)
+    return codes, scale, bmin
+
+
+def pack_codes(codes: np.ndarray, bits: int) -> np.ndarray:
+    """Pack [nblk, bs] integer codes LSB-first (2/3/4-bit)."""
+    nblk, bs = codes.shape
+    c = codes.astype(np.uint32) & ((1 << bits) - 1)
+    if bits == 4:
+        return (c[:, 0::2] | (c[:, 1::2] << 4)).astype(np.uint8)
+    if bits == 2:
+        return (c[:, 0::4] | (c[:, 1::4] << 2) | (c[:, 2::4] << 4) | (c[:, 3::4] << 6)).astype(np.uint8)
+    if bits == 3:
+        # 8 codes -> 24 bits -> 3 bytes
+        g = c.reshape(nblk, bs // 8, 8)
+        word = np.zeros((nblk, bs // 8), np.uint32)
+        for i in range(8):
+            word |= g[:, :, i] << (3 * i)
+        out = np.stack([(word >> (8 * j)) & 0xFF for j in range(3)], axis=-1)
+        return out.reshape(nblk, bs * 3 // 8).astype(np.uint8)
+    raise ValueError(bits)
+
+
+def quantize_blocks(blocks: np.ndarray, qt: int) -> np.ndarray:
+    """Quantise [nblk, bs] fp32 blocks to [nblk, block_bytes] uint8."""
+    nblk, bs = blocks.shape
+    if qt in (Q2, Q2SYM, Q4, Q3):
+        bits = {Q2: 2, Q2SYM: 2, Q4: 4, Q3: 3}[qt]
+        codes, scale, bmin = _asym_codes(blocks, (1 << bits) - 1)
+        return np.concatenate([_fp16_bytes(scale), _fp16_bytes(bmin), pack_codes(codes, bits)], axis=1)
+    if qt == Q4SYM:
+        absmax = np.abs(blocks).max(axis=1)
+        with np.errstate(divide="ignore", invalid="ignore"):
+            scale = np.where(absmax > 1e-30, absmax / 7.0, 0.0).astype(np.float32)
+            inv = np.where(scale > 1e-30, 1.0 / scale, 0.0).astype(np.float32)
+        vals = np.clip(np.round(blocks * inv[:, None]), -7, 7).astype(np.int8)
+        codes = (vals + 8).astype(np.uint8)  # offset-8 storage (convert_hf.py:276)
+        pad = np.zeros((nblk, 2), np.uint8)
+        return np.concatenate([_fp16_bytes(scale), pad, pack_codes(codes, 4)], axis=1)
+    raise ValueError(f"quantize_blocks: unsupported quant type {qt}")
+
+
+def quantize_matrix(w: np.ndarray, qt: int, bs: int, outlier_frac: float = 0.005) -> bytes:
+    """Full tensor payload for ``qt`` as engine.c passes it to the matvec."""
+    w = np.asarray(w, dtype=np.float32)
+    if w.ndim == 1:
+        w = w.reshape(1, -1)
+    if qt == MXFP4:
+        return quantize_mxfp4(w)
+    if qt in (Q2_OUTLIER, Q4_OUTLIER):
+        return quantize_outlier(w, qt, bs, outlier_frac)
+    return quantize_blocks(_row_blocks(w, bs), qt).tobytes()
+
+
+def quantize_outlier(w: np.ndarray, qt: int, bs: int, frac: float = 0.005,
+                     indices: np.ndarray | None = None) -> bytes:
+    """tools/convert_hf.py:324-364: n = max(1, int(N*frac)) largest |w| kept in
+    fp16 (argpartition order), zeroed, remainder quantised at the base width."""
+    rows, cols = w.shape
+    flat = w.reshape(-1)
+    n = max(1, int(flat.size * frac))
+    if indices is None:
+        indices = np.argpartition(np.abs(flat), -n)[-n:]
+    indices = np.asarray(indices, dtype=np.int64)
+    vals16 = flat[indices].astype(np.float16)
+    clean = flat.copy()
+    clean[indices] = 0.0
+    table = np.zeros(len(indices), dtype=[("idx", "<u4"), ("val", "<u2")])
+    table["idx"] = indices.astype(np.uint32)
+    table["val"] = vals16.view(np.uint16)
+    base = Q2 if qt == Q2_OUTLIER else Q4
+    blocks = quantize_blocks(_row_blocks(clean.reshape(rows, cols), bs), base)
+    return np.uint32(len(indices)).tobytes() + table.tobytes() + blocks.tobytes()
+
+
+def outlier_payload(n_idx: np.ndarray, vals_f16_bits: np.ndarray, blocks: bytes) -> bytes:
+    """Assemble an outlier payload from explicit entries (edge-case tests)."""
+    table = np.zeros(len(n_idx), dtype=[("idx", "<u4"), ("val", "<u2")])
+    table["idx"] = np.asarray(n_idx, dtype=np.uint32)
+    table["val"] = np.asarray(vals_f16_bits, dtype=np.uint16)
+    return np.uint32(len(n_idx)).tobytes() + table.tobytes() + bytes(blocks)
+
+
+# ---- MXFP4 (OCP Microscaling Formats v1.0) --------------------------------
+E2M1_MAG = np.array([0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0], np.float32)
+
+
+def _e2m1_encode(v: np.ndarray) -> np.ndarray:
+    """Round fp32 to the nearest E2M1 value, ties to even code, saturating."""
+    mag = np.minimum(np.abs(v), 6.0)
+    # candidate codes below/above; nearest with ties to the even mantissa
+    idx = np.searchsorted(E2M1_MAG, mag, side="left")
+    idx = np.clip(idx, 0, 7)
+    lo = np.clip(idx - 1, 0, 7)
+    d_hi = np.abs(E2M1_MAG[idx] - mag)
+    d_lo = np.abs(mag - E2M1_MAG[lo])
+    pick_lo = (d_lo < d_hi) | ((d_lo == d_hi) & (lo % 2 == 0))
+    code = np.where(pick_lo, lo, idx).astype(np.uint8)
+    sign = (np.signbit(v) & (code != 0)).astype(np.uint8) << 3
+    return code | sign
+
+
+def quantize_mxfp4(w: np.ndarray) -> bytes:
+    """OCP MX: shared scale 2^(floor(log2(amax)) - 2) per 32 elements."""
+    rows, cols = w.shape
+    blocks = _row_blocks(w, 32)
+    amax = np.abs(blocks).max(axis=1)
+    with np.errstate(divide="ignore"):
+        e = np.where(amax > 0, np.floor(np.log2(np.maximum(amax, 1e-38))) - 2, -127)
+    e = np.clip(e, -127, 127).astype(np.int32)
+    scaled = blocks / np.ldexp(np.float32(1.0), e)[:, None].astype(np.float32)
+    codes = _e2m1_encode(scaled.astype(np.float32))
+    packed = (codes[:, 0::2] | (codes[:, 1::2] << 4)).astype(np.uint8)
+    scales = (e + 127).astype(np.uint8)
+    return packed.tobytes() + scales.tobytes()
+
+
+def random_mxfp4(rng: np.random.Generator, rows: int, cols: int,
+                 e_lo: int = 118, e_hi: int = 122) -> bytes:
+    """Valid MXFP4 payload with uniform random codes and scales 2^(E-127),
+    E in [e_lo, e_hi] (|w| ~ 0.02): same bytes per element as quantised
+    N(0, 0.02) weights, generated without the fp32 intermediate."""
+    nb = (cols + 31) // 32
+    codes = rng.integers(0, 256, size=rows * nb * 16, dtype=np.uint8)
+    scales = rng.integers(e_lo, e_hi + 1, size=rows * nb, dtype=np.uint8)
+    return codes.tobytes() + scales.tobytes()
+
+
+# ---- seeded synthetic inputs of the BASELINE configs -----------------------
+def gaussian(rng: np.random.Generator, shape, std: float = 1.0) -> np.ndarray:
+    return (rng.standard_normal(shape, dtype=np.float32) * np.float32(std)).astype(np.float32)
+
+
+def heavy_tail_weights(rng: np.random.Generator, rows: int, cols: int,
+                       frac: float = 0.005, std: float = 0.02, scale: float = 10.0) -> np.ndarray:
+    """N(0, std) with a seeded ``frac`` of entries replaced by Student-t(3)
+    samples scaled by ``scale*std`` (config 1's outlier injection)."""
+    w = gaussian(rng, (rows, cols), std)
+    n = int(rows * cols * frac)
+    pos = rng.choice(rows * cols, size=n, replace=False)
+    w.reshape(-1)[pos] = (rng.standard_t(3, size=n) * (scale * std)).astype(np.float32)
+    return w
+
+
+def bf16_bits(x: np.ndarray) -> np.ndarray:
+    """fp32 -> bf16 bit patterns, round to nearest even (NaN kept quiet)."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32)
+    rounded = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    nan = np.isnan(x)
+    return np.where(nan, ((u >> 16) | 0x40).astype(np.uint16), rounded).astype(np.uint16)

@@ -1,0 +1,235 @@
+"""ctypes binding of libqsf_hip (include/qsf_hip.h).
+
+Mirrors QStream's kernel-table interface (include/qsf/kernels.h:91-126):
+``KernelTable().matvec_4bit(w, x, out, rows, cols, bs)`` has the argument
+meaning of ``qsf_matvec_fn`` and, like it, returns nothing and overwrites
+``out``.  The device entry points take torch CUDA tensors (or raw device
+addresses) and a stream.
+
+Loading fails loudly when the built library is missing: there is no CPU
+fallback on this path.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(PKG, "libqsf_hip.so")
+
+_vp, _i, _fp = C.c_void_p, C.c_int, C.POINTER(C.c_float)
+
+MATVEC_SLOTS = ("matvec_2bit", "matvec_3bit", "matvec_4bit", "matvec_4bit_sym",
+                "matvec_outlier_2bit", "matvec_outlier_4bit")
+EXPORTS = (
+    "qsf_hip_init", "qsf_hip_shutdown", "qsf_hip_last_error", "qsf_hip_last_error_detail",
+    "qsf_matvec_2bit_hip", "qsf_matvec_3bit_hip", "qsf_matvec_4bit_hip",
+    "qsf_matvec_4bit_sym_hip", "qsf_matvec_outlier_2bit_hip", "qsf_matvec_outlier_4bit_hip",
+    "qsf_matvec_mxfp4_hip", "qsf_kernels_init_hip",
+    "qsf_hip_tensor_upload", "qsf_hip_tensor_lookup", "qsf_hip_tensor_free",
+    "qsf_hip_arena_forget", "qsf_hip_arena_bytes", "qsf_hip_tensor_payload_bytes",
+    "qsf_hip_matvec_dev", "qsf_hip_matvec_group_dev", "qsf_hip_xprep_bytes",
+    "qsf_hip_xprep_dev", "qsf_hip_matvec_group_prepared_dev",
+    "qsf_hip_moe_create", "qsf_hip_moe_free", "qsf_hip_moe_forward_dev",
+    "qsf_hip_unpack_dev",
+)
+
+_lib = None
+
+
+class QsfHipError(RuntimeError):
+    pass
+
+
+def load(path: str = LIB_PATH) -> C.CDLL:
+    """Load libqsf_hip.so (built by qstream_amd.build); raise if absent."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise QsfHipError(f"{path} is not built: run `python -m qstream_amd.build`")
+    L = C.CDLL(path)
+    L.qsf_hip_init.argtypes = [_i]
+    L.qsf_hip_init.restype = _i
+    L.qsf_hip_last_error.restype = _i
+    L.qsf_hip_last_error_detail.restype = C.c_char_p
+    for s in MATVEC_SLOTS + ("matvec_mxfp4",):
+        f = getattr(L, f"qsf_{s}_hip")
+        f.argtypes = [_vp, _vp, _vp, _i, _i, _i]
+        f.restype = None
+    L.qsf_kernels_init_hip.argtypes = [_vp, _vp, C.POINTER(_vp)]
+    L.qsf_hip_tensor_upload.argtypes = [_vp, _i, _i, _i, _i]
+    L.qsf_hip_tensor_upload.restype = _vp
+    L.qsf_hip_tensor_lookup.argtypes = [_vp]
+    L.qsf_hip_tensor_lookup.restype = _vp
+    L.qsf_hip_tensor_free.argtypes = [_vp]
+    L.qsf_hip_arena_forget.argtypes = [_vp]
+    L.qsf_hip_arena_bytes.restype = C.c_size_t
+    L.qsf_hip_tensor_payload_bytes.argtypes = [_vp]
+    L.qsf_hip_tensor_payload_bytes.restype = C.c_size_t
+    L.qsf_hip_matvec_dev.argtypes = [_vp, _vp, _vp, _vp]
+    L.qsf_hip_matvec_dev.restype = _i
+    L.qsf_hip_matvec_group_dev.argtypes = [C.POINTER(_vp), _i, _vp, C.POINTER(_vp), _vp]
+    L.qsf_hip_matvec_group_dev.restype = _i
+    L.qsf_hip_xprep_bytes.argtypes = [_i, _i, _i]
+    L.qsf_hip_xprep_bytes.restype = C.c_size_t
+    L.qsf_hip_xprep_dev.argtypes = [_i, _i, _i, _vp, _vp, _vp]
+    L.qsf_hip_xprep_dev.restype = _i
+    L.qsf_hip_matvec_group_prepared_dev.argtypes = [C.POINTER(_vp), _i, _vp, _vp, C.POINTER(_vp), _vp]
+    L.qsf_hip_matvec_group_prepared_dev.restype = _i
+    L.qsf_hip_moe_create.argtypes = [_i, _i, _i] + [C.POINTER(_vp)] * 6
+    L.qsf_hip_moe_create.restype = _vp
+    L.qsf_hip_moe_free.argtypes = [_vp]
+    L.qsf_hip_moe_forward_dev.argtypes = [_vp, _i, _i, _i, _i, _vp, _vp, _vp, _vp]
+    L.qsf_hip_moe_forward_dev.restype = _i
+    L.qsf_hip_unpack_dev.argtypes = [_i, _vp, _i, _i, _vp, _vp, _vp, _vp]
+    L.qsf_hip_unpack_dev.restype = _i
+    _lib = L
+    return L
+
+
+def last_error() -> tuple[int, str]:
+    L = load()
+    d = L.qsf_hip_last_error_detail()
+    return L.qsf_hip_last_error(), (d.decode() if d else "")
+
+
+def _check(rc: int, what: str) -> None:
+    if rc != 0:
+        code, detail = last_error()
+        raise QsfHipError(f"{what} failed ({rc}): {detail}")
+
+
+def _addr(t) -> int:
+    """Device address of a torch tensor, or an int address."""
+    if t is None:
+        return None
+    if isinstance(t, int):
+        return t
+    return t.data_ptr()
+
+
+def _stream(s) -> int | None:
+    if s is None:
+        return None
+    if isinstance(s, int):
+        return s
+    return s.cuda_stream
+
+
+def init(device: int = 0) -> None:
+    _check(load().qsf_hip_init(device), "qsf_hip_init")
+
+
+class KernelTable:
+    """The six matvec slots of QSFKernelTable backed by libqsf_hip.
+
+    Each slot takes (weights_q: bytes|np.ndarray, input: float32[cols],
+    output: float32[rows], rows, cols, block_size) like qsf_matvec_fn.
+    """
+
+    def __init__(self):
+        self._L = load()
+        for s in MATVEC_SLOTS + ("matvec_mxfp4",):
+            setattr(self, s, self._slot(getattr(self._L, f"qsf_{s}_hip")))
+        self._keep = []
+
+    def _slot(self, fn):
+        def call(w, x, out, rows, cols, bs):
+            wa = np.frombuffer(w, np.uint8) if isinstance(w, (bytes, bytearray)) else w
+            self._keep.append(wa)   # the library keys uploaded payloads by address
+            if not (out.dtype == np.float32 and out.flags.c_contiguous):
+                raise TypeError("output must be a contiguous float32 array")
+            xa = np.ascontiguousarray(x, np.float32)
+            fn(wa.ctypes.data, xa.ctypes.data, out.ctypes.data, rows, cols, bs)
+        return call
+
+
+class Tensor:
+    """A weight payload resident in HBM (device weight arena)."""
+
+    def __init__(self, payload, qt: int, rows: int, cols: int, bs: int):
+        self._host = np.frombuffer(payload, np.uint8) if isinstance(payload, (bytes, bytearray)) \
+            else np.ascontiguousarray(payload)
+        self.qt, self.rows, self.cols, self.bs = qt, rows, cols, bs
+        L = load()
+        self.handle = L.qsf_hip_tensor_upload(self._host.ctypes.data, qt, rows, cols, bs)
+        if not self.handle:
+            _check(-1, "qsf_hip_tensor_upload")
+        self.payload_bytes = L.qsf_hip_tensor_payload_bytes(self.handle)
+
+    def matvec(self, x, y, stream=None) -> None:
+        _check(load().qsf_hip_matvec_dev(self.handle, _addr(x), _addr(y), _stream(stream)),
+               "qsf_hip_matvec_dev")
+
+    def free(self) -> None:
+        if self.handle:
+            load().qsf_hip_tensor_free(self.handle)
+            self.handle = None
+
+
+def matvec_group(tensors, x, ys, stream=None) -> None:
+    n = len(tensors)
+    th = (_vp * n)(*[t.handle for t in tensors])
+    yh = (_vp * n)(*[_addr(y) for y in ys])
+    _check(load().qsf_hip_matvec_group_dev(th, n, _addr(x), yh, _stream(stream)),
+           "qsf_hip_matvec_group_dev")
+
+
+def xprep_bytes(qt: int, bs: int, cols: int) -> int:
+    return load().qsf_hip_xprep_bytes(qt, bs, cols)
+
+
+def xprep(qt: int, bs: int, cols: int, x, xq, stream=None) -> None:
+    _check(load().qsf_hip_xprep_dev(qt, bs, cols, _addr(x), _addr(xq), _stream(stream)),
+           "qsf_hip_xprep_dev")
+
+
+def matvec_group_prepared(tensors, x, xq, ys, stream=None) -> None:
+    n = len(tensors)
+    th = (_vp * n)(*[t.handle for t in tensors])
+    yh = (_vp * n)(*[_addr(y) for y in ys])
+    _check(load().qsf_hip_matvec_group_prepared_dev(th, n, _addr(x), _addr(xq), yh, _stream(stream)),
+           "qsf_hip_matvec_group_prepared_dev")
+
+
+def unpack(qt: int, d_blocks, nblocks: int, bs: int, codes=None, meta=None, deq=None,
+           stream=None) -> None:
+    _check(load().qsf_hip_unpack_dev(qt, _addr(d_blocks), nblocks, bs, _addr(codes),
+                                     _addr(meta), _addr(deq), _stream(stream)),
+           "qsf_hip_unpack_dev")
+
+
+class Moe:
+    """Device expert table for the MXFP4 MoE FFN (src/engine.c:951-1107)."""
+
+    def __init__(self, gate, up, down, hidden: int, eid: int,
+                 gate_bias=None, up_bias=None, down_bias=None):
+        n = len(gate)
+        self.n_exp, self.hidden, self.eid = n, hidden, eid
+        self._keep = [gate, up, down]
+        arr = lambda ts: (_vp * n)(*[t.handle for t in ts])
+
+        def biases(bs):
+            if bs is None:
+                return None
+            hs = [None if b is None else np.ascontiguousarray(b, np.uint16) for b in bs]
+            self._keep.append(hs)
+            return (_vp * n)(*[None if b is None else b.ctypes.data for b in hs])
+        L = load()
+        self.handle = L.qsf_hip_moe_create(n, hidden, eid, arr(gate), arr(up), arr(down),
+                                           biases(gate_bias), biases(up_bias), biases(down_bias))
+        if not self.handle:
+            _check(-1, "qsf_hip_moe_create")
+
+    def forward(self, k, norm_topk, act, ntok, x, logits, out, stream=None) -> None:
+        _check(load().qsf_hip_moe_forward_dev(self.handle, k, norm_topk, act, ntok, _addr(x),
+                                              _addr(logits), _addr(out), _stream(stream)),
+               "qsf_hip_moe_forward_dev")
+
+    def free(self) -> None:
+        if self.handle:
+            load().qsf_hip_moe_free(self.handle)
+            self.handle = None

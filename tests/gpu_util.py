@@ -1,0 +1,33 @@
+"""Shared helpers of the GPU parity tests (imported by tests only)."""
+from __future__ import annotations
+
+import numpy as np
+
+REL_L2 = 1e-5   # north_star bar: max relative L2 error vs the scalar reference
+
+
+def rel_l2(y: np.ndarray, ref: np.ndarray) -> float:
+    y = np.asarray(y, np.float64)
+    ref = np.asarray(ref, np.float64)
+    den = np.linalg.norm(ref)
+    num = np.linalg.norm(y - ref)
+    if den == 0.0:
+        return 0.0 if num == 0.0 else float("inf")
+    return float(num / den)
+
+
+def torch_cuda():
+    import torch
+    assert torch.cuda.is_available(), "GPU tests need cuda:0"
+    return torch
+
+
+def dev(a: np.ndarray):
+    torch = torch_cuda()
+    return torch.from_numpy(np.ascontiguousarray(a)).to("cuda:0")
+
+
+def host(t) -> np.ndarray:
+    torch = torch_cuda()
+    torch.cuda.synchronize()
+    return t.cpu().numpy()

@@ -1,0 +1,201 @@
+"""GPU parity of the decode GEMV family against the CPU oracle.
+
+Every case calls libqsf_hip through its C ABI (ctypes) on cuda:0 and compares
+with oracle/ (a strict restatement of src/kernels_scalar.c and src/quant.c,
+itself pinned bit-exactly to the compiled reference in test_oracle.py):
+  * unpack: codes, block meta and dequantised values bit-exact;
+  * matvec: relative L2 error <= 1e-5, fp32 accumulate.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from qstream_amd import qsf_format as F
+from tests.gpu_util import REL_L2, dev, host, rel_l2, torch_cuda
+
+pytestmark = pytest.mark.gpu
+
+DENSE = [F.Q2, F.Q3, F.Q4, F.Q4SYM]
+ALL = DENSE + [F.Q2_OUTLIER, F.Q4_OUTLIER]
+
+
+@pytest.fixture(scope="module")
+def hip():
+    from qstream_amd import qsf_hip
+    qsf_hip.init(0)
+    return qsf_hip
+
+
+def _stream():
+    return torch_cuda().cuda.current_stream()
+
+
+def _random_blocks(rng, qt, bs, nblocks, special=False):
+    bb = F.block_bytes(qt, bs)
+    raw = rng.integers(0, 256, size=(nblocks, bb), dtype=np.uint8)
+    # finite fp16 scale/zero, including subnormals, negatives and large values
+    s = rng.standard_normal(nblocks).astype(np.float32) * np.float32(0.05)
+    z = rng.standard_normal(nblocks).astype(np.float32)
+    if special:
+        s[::7] = np.float32(3e-6)      # fp16 subnormal
+        z[1::5] = np.float32(-6e4)
+    raw[:, 0:2] = s.astype(np.float16).view(np.uint8).reshape(-1, 2)
+    raw[:, 2:4] = z.astype(np.float16).view(np.uint8).reshape(-1, 2)
+    return raw
+
+
+@pytest.mark.parametrize("qt", DENSE)
+@pytest.mark.parametrize("bs", [32, 64, 128, 256])
+def test_unpack_bit_exact(hip, oracle, qt, bs):
+    """Codes, meta words and dequantised values match src/quant.c:95-177."""
+    torch = torch_cuda()
+    rng = np.random.default_rng(1000 + 10 * qt + bs)
+    n = 97
+    raw = _random_blocks(rng, qt, bs, n, special=True)
+    d_raw = dev(raw.reshape(-1))
+    codes = torch.empty(n * bs, dtype=torch.int8, device="cuda:0")
+    meta = torch.empty(n, dtype=torch.int32, device="cuda:0")
+    deq = torch.empty(n * bs, dtype=torch.float32, device="cuda:0")
+    hip.unpack(qt, d_raw, n, bs, codes, meta, deq, stream=_stream())
+    c, m, d = host(codes).reshape(n, bs), host(meta).view(np.uint32), host(deq).reshape(n, bs)
+    for b in range(n):
+        ref_codes = oracle.unpack_codes(qt, raw[b], bs)
+        assert np.array_equal(c[b], ref_codes), f"codes differ in block {b}"
+        ref_deq = oracle.dequant_block(qt, raw[b], bs)
+        assert np.array_equal(d[b].view(np.uint32), ref_deq.view(np.uint32)), f"dequant differs in block {b}"
+    assert np.array_equal(m, raw[:, :4].copy().view(np.uint32).reshape(-1))
+
+
+def _case(oracle, qt, rows, cols, bs, seed, outlier_frac=0.005):
+    rng = np.random.default_rng(seed)
+    w = F.gaussian(rng, (rows, cols), 0.02)
+    x = F.gaussian(rng, cols)
+    payload = F.quantize_matrix(w, qt, bs, outlier_frac)
+    ref = oracle.matvec(qt, payload, x, rows, cols, bs)
+    return payload, x, ref
+
+
+SHAPES = [(64, 64), (37, 300), (5, 33), (130, 1000), (300, 4096), (1, 17), (96, 2880)]
+
+
+@pytest.mark.parametrize("qt", ALL)
+@pytest.mark.parametrize("bs", [32, 64, 128, 256])
+def test_matvec_slot_parity(hip, oracle, qt, bs):
+    """Drop-in table slot (host pointers, synchronous) vs scalar oracle."""
+    kt = hip.KernelTable()
+    slot = {F.Q2: kt.matvec_2bit, F.Q3: kt.matvec_3bit, F.Q4: kt.matvec_4bit,
+            F.Q4SYM: kt.matvec_4bit_sym, F.Q2_OUTLIER: kt.matvec_outlier_2bit,
+            F.Q4_OUTLIER: kt.matvec_outlier_4bit}[qt]
+    for i, (rows, cols) in enumerate(SHAPES):
+        payload, x, ref = _case(oracle, qt, rows, cols, bs, seed=7 * i + qt * 131 + bs)
+        out = np.full(rows, np.nan, np.float32)
+        slot(payload, x, out, rows, cols, bs)
+        err = rel_l2(out, ref)
+        print(f"qt={qt} bs={bs} {rows}x{cols} rel_l2={err:.3e}")
+        assert err <= REL_L2, (qt, bs, rows, cols, err)
+
+
+def test_reference_ramp_cases(hip, oracle):
+    """tests/test_core.c:597-677: 4x64 ramp, 4-bit and 2-bit, through the slots."""
+    rows, cols, bs = 4, 64, 64
+    w = (np.arange(rows * cols, dtype=np.float32) / 256.0 - 0.5).reshape(rows, cols)
+    x = np.arange(cols, dtype=np.float32) / 64.0 - 0.5
+    kt = hip.KernelTable()
+    for qt, slot in ((F.Q4, kt.matvec_4bit), (F.Q2, kt.matvec_2bit)):
+        payload = F.quantize_matrix(w, qt, bs)
+        ref = oracle.matvec(qt, payload, x, rows, cols, bs)
+        out = np.zeros(rows, np.float32)
+        slot(payload, x, out, rows, cols, bs)
+        assert np.max(np.abs(out - ref)) <= 1e-3
+        assert rel_l2(out, ref) <= REL_L2
+
+
+@pytest.mark.parametrize("qt,rows,cols,bs", [
+    (F.Q4, 4096, 4096, 64),              # config 0
+    (F.Q2_OUTLIER, 11008, 4096, 64),     # config 1 (one of gate/up)
+    (F.Q3, 4096, 11008, 128),            # config 2 down_proj
+    (F.Q3, 11008, 4096, 128),            # config 2 gate/up
+])
+def test_matvec_full_shapes(hip, oracle, qt, rows, cols, bs):
+    torch = torch_cuda()
+    rng = np.random.default_rng(rows + cols + qt)
+    if qt == F.Q2_OUTLIER:
+        w = F.heavy_tail_weights(rng, rows, cols)
+    else:
+        w = F.gaussian(rng, (rows, cols), 0.02)
+    x = F.gaussian(rng, cols)
+    payload = F.quantize_matrix(w, qt, bs)
+    ref = oracle.matvec(qt, payload, x, rows, cols, bs)
+    t = hip.Tensor(payload, qt, rows, cols, bs)
+    y = torch.full((rows,), float("nan"), device="cuda:0")
+    t.matvec(dev(x), y, stream=_stream())
+    err = rel_l2(host(y), ref)
+    print(f"full qt={qt} {rows}x{cols} bs{bs}: rel_l2={err:.3e}")
+    assert err <= REL_L2
+    t.free()
+
+
+def test_group_launch_matches_single(hip, oracle):
+    """gate+up in one launch equals two single launches (and the oracle)."""
+    torch = torch_cuda()
+    rng = np.random.default_rng(5)
+    rows, cols, bs = 1100, 4096, 64
+    ts, refs = [], []
+    x = F.gaussian(rng, cols)
+    for r in (rows, rows + 7):
+        w = F.heavy_tail_weights(rng, r, cols)
+        p = F.quantize_matrix(w, F.Q2_OUTLIER, bs)
+        ts.append(hip.Tensor(p, F.Q2_OUTLIER, r, cols, bs))
+        refs.append(oracle.matvec(F.Q2_OUTLIER, p, x, r, cols, bs))
+    dx = dev(x)
+    ys = [torch.empty(t.rows, device="cuda:0") for t in ts]
+    hip.matvec_group(ts, dx, ys, stream=_stream())
+    singles = [torch.empty(t.rows, device="cuda:0") for t in ts]
+    for t, y in zip(ts, singles):
+        t.matvec(dx, y, stream=_stream())
+    for y, s, ref in zip(ys, singles, refs):
+        assert np.array_equal(host(y), host(s))
+        assert rel_l2(host(y), ref) <= REL_L2
+
+
+def test_outlier_edge_cases(hip, oracle):
+    """Out-of-range entries are skipped, duplicates add twice, n=0 is plain
+    (src/quant.c:423-444)."""
+    rows, cols, bs = 9, 128, 64
+    rng = np.random.default_rng(11)
+    w = F.gaussian(rng, (rows, cols), 0.02)
+    x = F.gaussian(rng, cols)
+    blocks = F.quantize_blocks(F._row_blocks(w, bs), F.Q2).tobytes()
+    vals = np.array([1.5, -2.0, 0.75, 3.0, 1.0, -1.0], np.float16).view(np.uint16)
+    idx = np.array([5, rows * cols + 3, 5, 0, rows * cols - 1, 2 * rows * cols], np.uint32)
+    kt = hip.KernelTable()
+    for n in (0, len(idx)):
+        payload = F.outlier_payload(idx[:n], vals[:n], blocks)
+        ref = oracle.matvec(F.Q2_OUTLIER, payload, x, rows, cols, bs)
+        out = np.zeros(rows, np.float32)
+        kt.matvec_outlier_2bit(payload, x, out, rows, cols, bs)
+        assert rel_l2(out, ref) <= REL_L2, n
+
+
+def test_degenerate_shapes(hip, oracle):
+    kt = hip.KernelTable()
+    # rows = 0: no-op
+    out = np.full(3, 7.0, np.float32)
+    kt.matvec_4bit(b"\x00" * 64, np.zeros(4, np.float32), out, 0, 4, 64)
+    assert np.all(out == 7.0)
+    # cols = 0: the scalar reference writes zeros
+    out = np.full(5, 7.0, np.float32)
+    kt.matvec_4bit(b"\x00" * 64, np.zeros(1, np.float32), out, 5, 0, 64)
+    assert np.all(out == 0.0)
+
+
+def test_nonfinite_input_gives_nan(hip):
+    rows, cols, bs = 8, 256, 64
+    rng = np.random.default_rng(3)
+    p = F.quantize_matrix(F.gaussian(rng, (rows, cols), 0.02), F.Q4, bs)
+    x = F.gaussian(rng, cols)
+    x[70] = np.inf
+    out = np.zeros(rows, np.float32)
+    hip.KernelTable().matvec_4bit(p, x, out, rows, cols, bs)
+    assert np.all(~np.isfinite(out))

@@ -1,0 +1,130 @@
+"""GPU parity of the MXFP4 matvec and the MoE FFN against the CPU oracle.
+
+The oracle restates src/engine.c:951-1107 (softmax, strict '>' top-K,
+renormalisation, gate/up/act/mul/down, rank-order weighted sum) with the
+MXFP4 element order of tools/convert_hf.py:1456-1495 and the OCP MX scale.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from qstream_amd import qsf_format as F
+from tests.gpu_util import REL_L2, dev, host, rel_l2, torch_cuda
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def hip():
+    from qstream_amd import qsf_hip
+    qsf_hip.init(0)
+    return qsf_hip
+
+
+def _stream():
+    return torch_cuda().cuda.current_stream()
+
+
+def test_mxfp4_unpack_every_code_and_scale(hip, oracle):
+    """All 16 E2M1 codes in both nibble positions x a sweep of E8M0 scales,
+    through the table slot with one-hot activations: output row r, input
+    col c gives exactly e2m1(code) * 2^(E-127)."""
+    rows, cols = 16, 32
+    codes = np.zeros((rows, 1, 16), np.uint8)
+    for r in range(rows):
+        for j in range(16):
+            lo, hi = (r + 2 * j) % 16, (r + 2 * j + 1) % 16
+            codes[r, 0, j] = lo | (hi << 4)
+    kt = hip.KernelTable()
+    for e in (1, 100, 127, 130, 200, 254):
+        scales = np.full((rows, 1), e, np.uint8)
+        payload = codes.tobytes() + scales.tobytes()
+        got = np.zeros((cols, rows), np.float32)
+        for c in range(cols):
+            x = np.zeros(cols, np.float32)
+            x[c] = 1.0
+            kt.matvec_mxfp4(payload, x, got[c], rows, cols, 32)
+        for r in range(rows):
+            for c in range(cols):
+                nib = (codes[r, 0, c // 2] >> (4 * (c % 2))) & 15
+                want = np.float32(oracle.lib.orc_e2m1_to_fp32(int(nib))) * np.float32(2.0 ** (e - 127))
+                assert got[c, r] == want, (e, r, c, got[c, r], want)
+
+
+@pytest.mark.parametrize("rows,cols", [(64, 64), (2880, 2880), (100, 320), (7, 96)])
+def test_mxfp4_matvec(hip, oracle, rows, cols):
+    rng = np.random.default_rng(rows * 7 + cols)
+    w = F.gaussian(rng, (rows, cols), 0.02)
+    x = F.gaussian(rng, cols)
+    p = F.quantize_mxfp4(w)
+    ref = oracle.matvec(F.MXFP4, p, x, rows, cols, 32)
+    out = np.zeros(rows, np.float32)
+    hip.KernelTable().matvec_mxfp4(p, x, out, rows, cols, 32)
+    assert rel_l2(out, ref) <= REL_L2
+
+
+def _experts(rng, n_exp, hidden, eid, bias):
+    ex = []
+    big = hidden * eid > 1 << 20
+    mk = (lambda r, c: F.random_mxfp4(rng, r, c)) if big else \
+        (lambda r, c: F.quantize_mxfp4(F.gaussian(rng, (r, c), 0.02)))
+    for _ in range(n_exp):
+        e = {"gate": mk(eid, hidden), "up": mk(eid, hidden), "down": mk(hidden, eid)}
+        if bias:
+            e["gate_bias"] = F.gaussian(rng, eid, 0.1).astype(np.float16).view(np.uint16)
+            e["up_bias"] = F.gaussian(rng, eid, 0.1).astype(np.float16).view(np.uint16)
+            e["down_bias"] = F.gaussian(rng, hidden, 0.1).astype(np.float16).view(np.uint16)
+        ex.append(e)
+    return ex
+
+
+@pytest.mark.parametrize("n_exp,k,hidden,eid,ntok,norm,act,bias", [
+    (32, 4, 2880, 2880, 1, 1, 2, False),     # config 3, batch 1
+    (32, 4, 2880, 2880, 8, 1, 2, False),     # config 3, batch 8
+    (8, 2, 256, 512, 3, 0, 0, True),         # GELU, biases, no renorm
+    (4, 4, 128, 64, 8, 1, 3, True),          # every expert picked, ReLU
+])
+def test_moe_forward(hip, oracle, n_exp, k, hidden, eid, ntok, norm, act, bias):
+    torch = torch_cuda()
+    rng = np.random.default_rng(n_exp * 1000 + ntok * 10 + k)
+    ex = _experts(rng, n_exp, hidden, eid, bias)
+    x = F.gaussian(rng, (ntok, hidden))
+    logits = F.gaussian(rng, (ntok, n_exp))
+    ref = np.stack([oracle.moe_token(ex, k, norm, act, hidden, eid, x[t], logits[t])
+                    for t in range(ntok)])
+    tens = {n: [hip.Tensor(e[n], F.MXFP4, *( (eid, hidden) if n != "down" else (hidden, eid)), 32)
+                for e in ex] for n in ("gate", "up", "down")}
+    biases = {n: ([e[n] for e in ex] if bias else None) for n in ("gate_bias", "up_bias", "down_bias")}
+    moe = hip.Moe(tens["gate"], tens["up"], tens["down"], hidden, eid, **biases)
+    out = torch.full((ntok, hidden), float("nan"), device="cuda:0")
+    moe.forward(k, norm, act, ntok, dev(x), dev(logits), out, stream=_stream())
+    got = host(out)
+    for t in range(ntok):
+        err = rel_l2(got[t], ref[t])
+        print(f"moe E={n_exp} k={k} tok {t}: rel_l2={err:.3e}")
+        assert err <= REL_L2
+    moe.free()
+    for ts in tens.values():
+        for t in ts:
+            t.free()
+
+
+def test_moe_tie_keeps_lower_expert(hip, oracle):
+    """Equal router logits: strict '>' keeps the lower expert ids
+    (src/engine.c:994; tests/test_core.c:712-748)."""
+    torch = torch_cuda()
+    rng = np.random.default_rng(42)
+    n_exp, k, hidden, eid = 6, 2, 64, 64
+    ex = _experts(rng, n_exp, hidden, eid, False)
+    x = F.gaussian(rng, (1, hidden))
+    logits = np.zeros((1, n_exp), np.float32)
+    ref = oracle.moe_token(ex, k, 1, 2, hidden, eid, x[0], logits[0])
+    idx, _ = oracle.topk(oracle.softmax(logits[0]), k, 1)
+    assert list(idx) == [0, 1]
+    tens = {n: [hip.Tensor(e[n], F.MXFP4, *((eid, hidden) if n != "down" else (hidden, eid)), 32)
+                for e in ex] for n in ("gate", "up", "down")}
+    moe = hip.Moe(tens["gate"], tens["up"], tens["down"], hidden, eid)
+    out = torch.zeros((1, hidden), device="cuda:0")
+    moe.forward(k, 1, 2, 1, dev(x), dev(logits), out, stream=_stream())
+    assert rel_l2(host(out)[0], ref) <= REL_L2
