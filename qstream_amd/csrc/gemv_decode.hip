@@ -9,13 +9,15 @@
 //   sum_k (s*q_k + z) x_k = s * sum_k q_k x_k + z * sum_k x_k
 // and the code/activation products are done exactly in integers: the x-prep
 // kernel turns each block of x into block-fixed-point integers X_k = x_k*2^sh
-// (|X| < 2^XB, XB = 19..22 bits) and splits every X into six signed base-16
-// digits.  The GEMV multiplies raw code nibbles by digit nibbles with
+// (|X| <= 2^XB, XB = 24..26 bits) and splits every X into seven signed
+// base-16 digits.  The GEMV multiplies raw code nibbles by digit nibbles with
 // v_dot8_i32_i4 (8 products per instruction, exact int32), recombines the
-// digits per block (Horner, exact), converts once and applies the fp16
-// scale/zero in fp32.  The only rounding beyond fp32 accumulation is x -> X
-// (relative 2^-XB of the block's max |x|), about 3e-7 relative L2 on the
-// output -- inside the 1e-5 bar against the strict scalar reference.
+// digits per block in two exact int32 groups (digits 0-3 and 4-6), joins them
+// with one fp32 FMA and applies the fp16 scale/zero in fp32.  The rounding
+// beyond fp32 accumulation is x -> X, at most 2^-(XB+1) of the block's max
+// |x| -- finer than fp32 itself for the block's largest elements, so even a
+// row whose result cancels 100x stays inside the 1e-5 bar against the strict
+// scalar reference.
 //
 // Code unpacking is pure masking, chosen so each nibble holds one signed
 // 4-bit value that the digit tables pair with the right x:
@@ -40,10 +42,10 @@
 
 namespace {
 
-constexpr int ND = 6;                  // balanced base-16 digits per multiplier
-constexpr uint32_t DIGIT_BIAS = 0x888888u;  // 8 * (16^6 - 1) / 15
+constexpr int ND = 7;                  // balanced base-16 digits per multiplier
+constexpr int ND_LO = 4;               // digits 0-3 and 4-6 are recombined separately
+constexpr uint32_t DIGIT_BIAS = 0x8888888u;  // 8 * (16^7 - 1) / 15
 
-constexpr int ilog2(int v) { return v <= 1 ? 0 : 1 + ilog2(v >> 1); }
 
 template <int FMT, int BS>
 struct Fmt {
@@ -53,12 +55,12 @@ struct Fmt {
     static constexpr int NA = FMT == QK_FMT_3 ? 2 : 1;              // accumulator sets
     static constexpr int BB = 4 + 4 * CW;                           // block bytes
     static constexpr int DW = CW * NC * ND;                         // digit dwords / block
-    // |X| bound so that every per-block int32 sum stays exact:
-    //   4-bit: 8*BS*2^XB <= 2^30;  2-bit: 3*BS*2^XB < 2^31;  3-bit: S_B <= 2^30.5
-    static constexpr int XB =
-        FMT == QK_FMT_2 ? (BS <= 128 ? 22 : 21)
-      : FMT == QK_FMT_3 ? (BS <= 128 ? 20 : 19)
-      : (27 - ilog2(BS) < 22 ? 27 - ilog2(BS) : 22);
+    static constexpr int DWS = (DW + 3) & ~3;                       // 16-B aligned stride
+    // |X| <= 2^XB.  Digit multipliers M = X * 2^shift (shift <= 2 for 3-bit)
+    // must lie in the 7-digit balanced range [-0x8888888, 0x7777777]; the
+    // low-group sum is <= 8 * 34952 * BS and the high-group sum
+    // <= 8 * (2^(XB+2)/65536 + 1) * BS, both far inside int32.
+    static constexpr int XB = FMT == QK_FMT_3 ? 24 : 26;
 };
 
 // 3-bit masks for code dword w with w % 3 == k.  Nibble g = 8w + i has
@@ -156,7 +158,7 @@ __global__ __launch_bounds__(256) void xprep_kernel(const float* __restrict__ x,
         uint32_t out = 0;
 #pragma unroll
         for (int m = 0; m < 8; m++) out |= ((us[wave][wc * 8 + m] >> (4 * d)) & 15u) << (4 * m);
-        xq[(size_t)b * F::DW + o] = out ^ 0x88888888u;  // nibble n-8 in two's complement
+        xq[(size_t)b * F::DWS + o] = out ^ 0x88888888u;  // nibble n-8 in two's complement
     }
     if (lane == 0) {
         float f = ldexpf(1.0f, -sh);
@@ -203,15 +205,15 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
         // stage this chunk's digits and block meta in LDS
         __syncthreads();
         {
-            const uint4* src = reinterpret_cast<const uint4*>(a.xq + (size_t)c0 * F::DW);
+            const uint4* src = reinterpret_cast<const uint4*>(a.xq + (size_t)c0 * F::DWS);
             uint4* dst = reinterpret_cast<uint4*>(lds);
-            const int n4 = (c1 - c0) * F::DW / 4;
+            const int n4 = (c1 - c0) * F::DWS / 4;
             for (int i = threadIdx.x; i < n4; i += WAVES * 64) dst[i] = src[i];
-            float2* mdst = reinterpret_cast<float2*>(lds + a.chunk * F::DW);
+            float2* mdst = reinterpret_cast<float2*>(lds + a.chunk * F::DWS);
             for (int i = threadIdx.x; i < c1 - c0; i += WAVES * 64) mdst[i] = a.xmeta[c0 + i];
         }
         __syncthreads();
-        const float2* meta = reinterpret_cast<const float2*>(lds + a.chunk * F::DW);
+        const float2* meta = reinterpret_cast<const float2*>(lds + a.chunk * F::DWS);
 
         for (int b = c0 + lig; b < c1; b += lpg) {
             uint32_t wv[R][1 + F::CW];
@@ -228,7 +230,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
                     for (int i = 0; i < 1 + F::CW; i++) wv[r][i] = 0u;
                 }
             }
-            const uint32_t* dg = lds + (size_t)(b - c0) * F::DW;
+            const uint32_t* dg = lds + (size_t)(b - c0) * F::DWS;
             int acc[R][F::NA][ND];
 #pragma unroll
             for (int r = 0; r < R; r++)
@@ -265,10 +267,14 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
                 float sf = 0.0f;
 #pragma unroll
                 for (int s = 0; s < F::NA; s++) {
-                    uint32_t h = (uint32_t)acc[r][s][ND - 1];
+                    uint32_t lo = (uint32_t)acc[r][s][ND_LO - 1];
 #pragma unroll
-                    for (int d = ND - 2; d >= 0; d--) h = (h << 4) + (uint32_t)acc[r][s][d];
-                    sf = s == 0 ? (float)(int)h : fmaf(0.25f, (float)(int)h, sf);
+                    for (int d = ND_LO - 2; d >= 0; d--) lo = (lo << 4) + (uint32_t)acc[r][s][d];
+                    uint32_t hi = (uint32_t)acc[r][s][ND - 1];
+#pragma unroll
+                    for (int d = ND - 2; d >= ND_LO; d--) hi = (hi << 4) + (uint32_t)acc[r][s][d];
+                    const float v = fmaf((float)(int)hi, 65536.0f, (float)(int)lo);
+                    sf = s == 0 ? v : fmaf(0.25f, v, sf);
                 }
                 const float sc = qsf::f16_lo(wv[r][0]);
                 const float coef = sc * xm.x;
@@ -322,7 +328,7 @@ template <int FMT, int BS>
 size_t xprep_bytes_t(int cols) {
     using F = Fmt<FMT, BS>;
     size_t nb = (size_t)((cols + BS - 1) / BS);
-    size_t dig = nb * F::DW * 4;
+    size_t dig = nb * F::DWS * 4;
     return ((dig + 255) & ~(size_t)255) + nb * sizeof(float2);
 }
 
@@ -332,7 +338,7 @@ int launch_t(const qsf_hip_tensor* const* t, int n, int cols, const float* d_x,
     using F = Fmt<FMT, BS>;
     const int nb = (cols + BS - 1) / BS;
     uint32_t* xq = (uint32_t*)d_ws;
-    size_t dig = (size_t)nb * F::DW * 4;
+    size_t dig = (size_t)nb * F::DWS * 4;
     float2* xmeta = (float2*)((uint8_t*)d_ws + ((dig + 255) & ~(size_t)255));
     if (mode & QK_RUN_XPREP)
         hipLaunchKernelGGL((xprep_kernel<FMT, BS>), dim3((nb + 3) / 4), dim3(256), 0, s,
@@ -346,7 +352,7 @@ int launch_t(const qsf_hip_tensor* const* t, int n, int cols, const float* d_x,
     int lpg = 1;
     while (lpg < nb && lpg < 64) lpg <<= 1;
     a.lpg = lpg;
-    const int per_block = F::DW * 4 + (int)sizeof(float2);
+    const int per_block = F::DWS * 4 + (int)sizeof(float2);
     a.chunk = nb < kLdsBudget / per_block ? nb : kLdsBudget / per_block;
     const int rows_per_wg = kWaves * (64 / lpg) * kR;
     a.tile0[0] = 0;

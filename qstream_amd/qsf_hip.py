@@ -50,6 +50,13 @@ def load(path: str = LIB_PATH) -> C.CDLL:
         return _lib
     if not os.path.exists(path):
         raise QsfHipError(f"{path} is not built: run `python -m qstream_amd.build`")
+    # One HIP runtime per process: when torch is present its bundled
+    # libamdhip64 (soname libamdhip64.so.7) must be loaded first so this
+    # library's DT_NEEDED binds to it instead of pulling in a second runtime.
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     L = C.CDLL(path)
     L.qsf_hip_init.argtypes = [_i]
     L.qsf_hip_init.restype = _i
