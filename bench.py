@@ -73,8 +73,10 @@ class Events:
         self.ev = [torch.cuda.Event(enable_timing=True) for _ in range(n)]
 
 
-def run_dense(torch, hip, qt, bs, mats, x, steps, warmup, group=True):
-    """Rotating copies of `mats`; each step: xprep + grouped GEMV."""
+def run_dense(torch, hip, qt, bs, mats, x, steps, warmup, split=False):
+    """Rotating copies of `mats`.  Each step is one grouped GEMV launch that
+    prepares x inside its workgroups; with split=True, a stand-alone x-prep
+    launch followed by the GEMV on the prepared digits."""
     per_copy = sum(len(p) for _, p, _, _ in mats)
     n_copies = max(2, math.ceil(ROTATE_BYTES / per_copy))
     copies = [[hip.Tensor(p, qt, r, c, bs) for _, p, r, c in mats] for _ in range(n_copies)]
@@ -89,44 +91,64 @@ def run_dense(torch, hip, qt, bs, mats, x, steps, warmup, group=True):
         ts = copies[i % n_copies]
         if ev is not None:
             ev[0].record(stream)
-        hip.xprep(qt, bs, cols, dx, xq_addr, stream=stream)
+        if split:
+            hip.xprep(qt, bs, cols, dx, xq_addr, stream=stream)
         if ev is not None:
             ev[1].record(stream)
-        if group:
+        if split:
             hip.matvec_group_prepared(ts, dx, xq_addr, ys, stream=stream)
         else:
-            for t, y in zip(ts, ys):
-                hip.matvec_group_prepared([t], dx, xq_addr, [y], stream=stream)
+            hip.matvec_group(ts, dx, ys, stream=stream)
         if ev is not None:
             ev[2].record(stream)
 
     for i in range(warmup):
         step(i)
     torch.cuda.synchronize()
-    # whole-job throughput: K steps between two synchronisations
-    t0 = torch.cuda.Event(enable_timing=True)
-    t1 = torch.cuda.Event(enable_timing=True)
-    t0.record(stream)
-    for i in range(steps):
-        step(i)
-    t1.record(stream)
-    torch.cuda.synchronize()
-    ms_total = t0.elapsed_time(t1)
-    # per-kernel durations (events around each launch) over a second timed pass
+
+    def timed(fn):
+        t0 = torch.cuda.Event(enable_timing=True)
+        t1 = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        t0.record(stream)
+        fn()
+        t1.record(stream)
+        torch.cuda.synchronize()
+        return t0.elapsed_time(t1)
+
+    # Eager: K steps launched one by one from Python (host launch rate bound
+    # for these few-microsecond kernels).
+    ms_eager = timed(lambda: [step(i) for i in range(steps)])
+    # Graph: the same K launches captured once and replayed (the way a decode
+    # loop submits them); K steps between two synchronisations.
+    graph = torch.cuda.CUDAGraph()
+    cap = torch.cuda.Stream()
+    cap.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(cap):
+        stream = cap
+        with torch.cuda.graph(graph, stream=cap):
+            for i in range(steps):
+                step(i)
+    stream = torch.cuda.current_stream()
+    for _ in range(2):
+        graph.replay()
+    ms_graph = timed(graph.replay)
+    # per-launch event timing (eager, events around each launch)
     evs = [Events(torch, 3).ev for _ in range(steps)]
     for i in range(steps):
         step(i, evs[i])
     torch.cuda.synchronize()
     gemv_ms = [e[1].elapsed_time(e[2]) for e in evs]
     xprep_ms = [e[0].elapsed_time(e[1]) for e in evs]
+    del graph
     for ts in copies:
         for t in ts:
             t.free()
     return {
-        "ms_per_step": ms_total / steps,
-        "gemv_ms_mean": float(np.mean(gemv_ms)),
-        "gemv_ms_median": float(np.median(gemv_ms)),
-        "xprep_ms_mean": float(np.mean(xprep_ms)),
+        "ms_per_step": ms_graph / steps,
+        "ms_per_step_eager": ms_eager / steps,
+        "gemv_ms_event_mean": float(np.mean(gemv_ms)),
+        "xprep_ms_event_mean": float(np.mean(xprep_ms)),
         "n_copies": n_copies,
         "rotation_mib": n_copies * per_copy / (1 << 20),
     }
@@ -169,19 +191,21 @@ def cpu_baseline_dense(qt, bs, mats, x, budget_s=10.0):
                       f"median {med * 1e3:.1f} ms/step, {time.perf_counter() - t_start:.1f} s"}
 
 
-def bench_dense(torch, hip, cfg, steps, warmup, with_cpu=True):
+def bench_dense(torch, hip, cfg, steps, warmup, with_cpu=True, split=False):
     qt, bs, mats, x = cfg1_data() if cfg == 1 else cfg0_data()
     log(f"config {cfg}: data ready ({len(mats)} matrices)")
-    res = run_dense(torch, hip, qt, bs, mats, x, steps, warmup)
+    res = run_dense(torch, hip, qt, bs, mats, x, steps, warmup, split)
     bytes_step = algo_bytes(mats)
     value = bytes_step / (res["ms_per_step"] * 1e-3) / 1e9
-    achieved = bytes_step / (res["gemv_ms_mean"] * 1e-3) / 1e9
+    # one launch per step: its average duration on the launch stream is the
+    # replayed step time (an upper bound: it includes the inter-launch gap)
+    achieved = value
     out = {
         "value": value,
         "ms_per_step": res["ms_per_step"],
         "us_per_call": res["ms_per_step"] * 1e3 / len(mats),
-        "gemv_us": res["gemv_ms_mean"] * 1e3,
-        "xprep_us": res["xprep_ms_mean"] * 1e3,
+        "us_per_step_eager": res["ms_per_step_eager"] * 1e3,
+        "us_event_per_launch_eager": res["gemv_ms_event_mean"] * 1e3,
         "bytes_per_step": bytes_step,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": None},
@@ -192,6 +216,28 @@ def bench_dense(torch, hip, cfg, steps, warmup, with_cpu=True):
     return out
 
 
+def copy_calibration(torch, steps, warmup, mib=512):
+    """Plain device-to-device copy of a known size: the reference point for
+    HBM counters (FETCH_SIZE / WRITE_SIZE per byte moved) and for what the
+    memory system sustains on this box."""
+    n = (mib << 20) // 4
+    a = torch.randn(n, device="cuda:0")
+    b = torch.empty_like(a)
+    stream = torch.cuda.current_stream()
+    for _ in range(warmup):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    for _ in range(steps):
+        b.copy_(a)
+    t1.record(stream)
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / steps
+    moved = 2 * n * 4
+    return {"copy_mib": mib, "ms_per_copy": ms, "read_plus_write_GBs": moved / (ms * 1e-3) / 1e9}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -199,6 +245,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="1")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--split", action="store_true",
+                    help="stand-alone x-prep launch + GEMV on prepared digits")
+    ap.add_argument("--copy-mib", type=int, default=512, help="size of --config copy")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
@@ -207,8 +256,12 @@ def main():
     import torch
     from qstream_amd import qsf_hip
     qsf_hip.init(0)
+    if args.config == "copy":
+        print(json.dumps(copy_calibration(torch, args.steps, args.warmup, args.copy_mib)), flush=True)
+        return
     cfg = int(args.config) if args.config != "all" else 1
-    r = bench_dense(torch, qsf_hip, cfg, args.steps, args.warmup, with_cpu=not args.no_cpu)
+    r = bench_dense(torch, qsf_hip, cfg, args.steps, args.warmup, with_cpu=not args.no_cpu,
+                    split=args.split)
     workload = {1: "cfg1: 2-bit+outlier FFN gate+up, 2x 11008x4096, block 64, batch-1 decode",
                 0: "cfg0: 4-bit asym 4096x4096, block 64, batch-1 decode"}[cfg]
     line = {
@@ -225,8 +278,12 @@ def main():
         "dtype": "i4xi4->i32 dot, f32 accumulate",
         "data": "synthetic (seeded N(0,0.02) + Student-t outliers, converter-semantics quantisation)",
         "config": {"workload": workload, "us_per_call": round(r["us_per_call"], 3),
-                   "gemv_us": round(r["gemv_us"], 3), "xprep_us": round(r["xprep_us"], 3),
-                   "bytes_per_step": r["bytes_per_step"], "hbm_frac_of_8TBs": round(r["value"] / HBM_PEAK_GBS, 4),
+                   "us_per_step_graph": round(r["ms_per_step"] * 1e3, 3),
+                   "us_per_step_eager": round(r["us_per_step_eager"], 3),
+                   "us_event_per_launch_eager": round(r["us_event_per_launch_eager"], 3),
+                   "launch": "split x-prep + GEMV" if args.split else "one fused launch per step",
+                   "bytes_per_step": r["bytes_per_step"],
+                   "hbm_frac_of_8TBs": round(r["value"] / HBM_PEAK_GBS, 4),
                    "rotation_mib": round(r["rotation_mib"], 1)},
         "roofline": r["roofline"],
     }

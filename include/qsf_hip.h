@@ -95,8 +95,10 @@ size_t          qsf_hip_arena_bytes(void);
 size_t          qsf_hip_tensor_payload_bytes(const qsf_hip_tensor* t);
 
 /* ---- 2. device-pointer entry points --------------------------------------- */
-/* y[rows] = W x[cols] on `stream` (hipStream_t, NULL = library stream);
- * asynchronous.  d_x, d_y are device pointers. */
+/* y[rows] = W x[cols] on `stream` (hipStream_t; NULL = the default stream);
+ * asynchronous.  d_x, d_y are device pointers.  Calls that use the library
+ * workspace (all but the prepared form) must not overlap on different
+ * streams. */
 int qsf_hip_matvec_dev(const qsf_hip_tensor* t, const float* d_x, float* d_y, void* stream);
 /* n (<= 8) tensors with the same type/cols/block size sharing one x in one
  * launch (q/k/v, gate/up). */

@@ -7,17 +7,16 @@
 //
 // Arithmetic.  Per block the reference computes sum_k (s*q_k + z) * x_k.  Here
 //   sum_k (s*q_k + z) x_k = s * sum_k q_k x_k + z * sum_k x_k
-// and the code/activation products are done exactly in integers: the x-prep
-// kernel turns each block of x into block-fixed-point integers X_k = x_k*2^sh
-// (|X| <= 2^XB, XB = 24..26 bits) and splits every X into seven signed
-// base-16 digits.  The GEMV multiplies raw code nibbles by digit nibbles with
-// v_dot8_i32_i4 (8 products per instruction, exact int32), recombines the
-// digits per block in two exact int32 groups (digits 0-3 and 4-6), joins them
-// with one fp32 FMA and applies the fp16 scale/zero in fp32.  The rounding
-// beyond fp32 accumulation is x -> X, at most 2^-(XB+1) of the block's max
-// |x| -- finer than fp32 itself for the block's largest elements, so even a
-// row whose result cancels 100x stays inside the 1e-5 bar against the strict
-// scalar reference.
+// and the code/activation products are done exactly in integers: each block
+// of x becomes block-fixed-point integers X_k = x_k*2^sh (|X| <= 2^XB,
+// XB = 24..26 bits) split into seven signed base-16 digits.  The GEMV
+// multiplies raw code nibbles by digit nibbles with v_dot8_i32_i4 (8 exact
+// products per instruction), recombines the digits per block in two exact
+// int32 groups (digits 0-3 and 4-6), joins them with one fp32 FMA and applies
+// the fp16 scale/zero in fp32.  The rounding beyond fp32 accumulation is
+// x -> X, at most 2^-(XB+1) of the block's max |x| -- finer than fp32 itself
+// for the block's largest elements, so even a row whose result cancels 100x
+// stays inside the 1e-5 bar against the strict scalar reference.
 //
 // Code unpacking is pure masking, chosen so each nibble holds one signed
 // 4-bit value that the digit tables pair with the right x:
@@ -30,11 +29,14 @@
 //                shifted right by one) carry them, with digit tables scaled by
 //                powers of two so that sum = S_A + S_B/4 exactly.
 //
-// Layout.  A wave owns R rows (x LG row groups when a row has < 64 blocks);
-// lane l of a group handles blocks l, l+LPG, ...  of those rows, so each lane
-// reads whole blocks (dword loads from 4-byte aligned blocks) and reuses its
-// block's digits from LDS for R rows.  Partial sums are reduced with lane
-// shuffles; a fused CSR pass adds the fp16 outliers of the wave's rows.
+// Launch.  Persistent 1024-thread workgroups, one per CU by default.  Each
+// workgroup first turns x into digits in LDS itself (no separate launch;
+// a v_perm nibble transpose builds the digit words), then its 16 waves walk
+// their share of R-row tiles.  Within a tile, lane l of a row group handles
+// blocks l, l+LPG, ... so each lane reads whole blocks (dword loads from
+// 4-byte aligned blocks, 32-bit offsets) and reuses its block's digits
+// (odd LDS stride: conflict-free) for R rows.  A fused CSR pass adds the fp16
+// outliers of each tile's rows; partial sums are reduced with DPP.
 #include "qsf_device.h"
 #include "qsf_hip_internal.h"
 
@@ -45,7 +47,12 @@ namespace {
 constexpr int ND = 7;                  // balanced base-16 digits per multiplier
 constexpr int ND_LO = 4;               // digits 0-3 and 4-6 are recombined separately
 constexpr uint32_t DIGIT_BIAS = 0x8888888u;  // 8 * (16^7 - 1) / 15
+constexpr int WAVES = 16;              // waves per GEMV workgroup
+constexpr int MAXT = 4;                // tiles per wave (compile-time bound)
+constexpr int kLdsBudget = 64 * 1024;  // block digits + meta held at once
+constexpr size_t kLdsLimit = 64 * 1024;  // whole dynamic LDS of a GEMV workgroup
 
+constexpr int pow2ceil(int v) { return v <= 1 ? 1 : 2 * pow2ceil((v + 1) / 2); }
 
 template <int FMT, int BS>
 struct Fmt {
@@ -55,7 +62,8 @@ struct Fmt {
     static constexpr int NA = FMT == QK_FMT_3 ? 2 : 1;              // accumulator sets
     static constexpr int BB = 4 + 4 * CW;                           // block bytes
     static constexpr int DW = CW * NC * ND;                         // digit dwords / block
-    static constexpr int DWS = (DW + 3) & ~3;                       // 16-B aligned stride
+    static constexpr int DWS = DW | 1;                              // odd LDS stride
+    static constexpr int LPB = pow2ceil(CW);                        // x-prep lanes / block
     // |X| <= 2^XB.  Digit multipliers M = X * 2^shift (shift <= 2 for 3-bit)
     // must lie in the 7-digit balanced range [-0x8888888, 0x7777777]; the
     // low-group sum is <= 8 * 34952 * BS and the high-group sum
@@ -92,227 +100,628 @@ __device__ __forceinline__ void slot_code(int w, int c, int m, int& code, int& s
     if constexpr (FMT == QK_FMT_2) { code = 16 * w + 2 * m + c; shift = 0; }
     else if constexpr (FMT == QK_FMT_3) {
         int g = 8 * w + m;
-        int delta = g % 3;
         code = (4 * g) / 3 + c;
-        shift = delta;
+        shift = g % 3;
     } else { code = 8 * w + m; shift = 0; }
 }
 
-// ---------------------------------------------------------------------------
-// x preparation: one wave per block of x.
-// Output per block b: Fmt::DW digit dwords (layout [w][c][digit]) and
-// meta {f_b = 2^-sh, sum_k X_k * f_b}.
-template <int FMT, int BS>
-__global__ __launch_bounds__(256) void xprep_kernel(const float* __restrict__ x, int cols, int nb,
-                                                    uint32_t* __restrict__ xq,
-                                                    float2* __restrict__ xmeta) {
-    using F = Fmt<FMT, BS>;
-    constexpr int NSLOT = F::CW * F::NC * 8;
-    __shared__ int xs[4][BS];
-    __shared__ uint32_t us[4][NSLOT];
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int b = blockIdx.x * 4 + wave;
-    const bool live = b < nb;
+// Eight 28-bit biased multipliers U[m] -> seven digit words: nibble m of
+// word d = nibble d of U[m], re-biased to two's complement (n - 8).
+__device__ __forceinline__ void digit_words(const uint32_t (&U)[8], uint32_t (&out)[ND]) {
+    uint32_t P[4], Q[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        // byte k of P[j]: digit 2k of U[2j] | digit 2k of U[2j+1] << 4; Q: digit 2k+1
+        P[j] = (U[2 * j] & 0x0F0F0F0Fu) | ((U[2 * j + 1] & 0x0F0F0F0Fu) << 4);
+        Q[j] = ((U[2 * j] >> 4) & 0x0F0F0F0Fu) | (U[2 * j + 1] & 0xF0F0F0F0u);
+    }
+    // 4x4 byte transposes (v_perm_b32: selector byte 0-3 = src1 byte, 4-7 = src0 byte)
+    const uint32_t pa0 = __builtin_amdgcn_perm(P[1], P[0], 0x05010400u);
+    const uint32_t pa1 = __builtin_amdgcn_perm(P[1], P[0], 0x07030602u);
+    const uint32_t pb0 = __builtin_amdgcn_perm(P[3], P[2], 0x05010400u);
+    const uint32_t pb1 = __builtin_amdgcn_perm(P[3], P[2], 0x07030602u);
+    const uint32_t qa0 = __builtin_amdgcn_perm(Q[1], Q[0], 0x05010400u);
+    const uint32_t qa1 = __builtin_amdgcn_perm(Q[1], Q[0], 0x07030602u);
+    const uint32_t qb0 = __builtin_amdgcn_perm(Q[3], Q[2], 0x05010400u);
+    const uint32_t qb1 = __builtin_amdgcn_perm(Q[3], Q[2], 0x07030602u);
+    out[0] = __builtin_amdgcn_perm(pb0, pa0, 0x05040100u) ^ 0x88888888u;
+    out[2] = __builtin_amdgcn_perm(pb0, pa0, 0x07060302u) ^ 0x88888888u;
+    out[4] = __builtin_amdgcn_perm(pb1, pa1, 0x05040100u) ^ 0x88888888u;
+    out[6] = __builtin_amdgcn_perm(pb1, pa1, 0x07060302u) ^ 0x88888888u;
+    out[1] = __builtin_amdgcn_perm(qb0, qa0, 0x05040100u) ^ 0x88888888u;
+    out[3] = __builtin_amdgcn_perm(qb0, qa0, 0x07060302u) ^ 0x88888888u;
+    out[5] = __builtin_amdgcn_perm(qb1, qa1, 0x05040100u) ^ 0x88888888u;
+}
 
-    float v[(BS + 63) / 64];
+// x preparation for one block b by a group of LPB lanes (lane w owns code
+// dword w): block max, shift, X, digit words into dst[(w*NC + c)*ND + d], and
+// from lane 0 the block meta {f = 2^-sh, sum_k X_k * f}.  All lanes of the
+// group must call it together (group shuffles).
+// Split in a load half and a compute half so callers can issue the x loads
+// before other vector-memory traffic (loads return in issue order).
+template <int FMT, int BS>
+__device__ __forceinline__ void prep_load(const float* __restrict__ x, int cols, int b, bool live,
+                                          int w, float (&xv)[Fmt<FMT, BS>::NC * 8]) {
+    using F = Fmt<FMT, BS>;
+    constexpr int NS = F::NC * 8;
+    const bool lane_live = live && w < F::CW;
+    if constexpr (FMT != QK_FMT_3) {
+        // 2/4-bit: the lane's slots are NS consecutive x values (16-B vector
+        // loads when in range and aligned), re-ordered to slot order
+        constexpr int CPD = NS;                        // codes per code dword
+        float xr[CPD];
+        const int col0 = b * BS + w * CPD;
+        const bool full = lane_live && col0 + CPD <= cols &&
+                          ((reinterpret_cast<uintptr_t>(x) & 15) == 0);
+        if (full) {
+            const float4* x4 = reinterpret_cast<const float4*>(x + col0);
+#pragma unroll
+            for (int k = 0; k < CPD / 4; k++) {
+                const float4 v = x4[k];
+                xr[4 * k] = v.x; xr[4 * k + 1] = v.y; xr[4 * k + 2] = v.z; xr[4 * k + 3] = v.w;
+            }
+        } else {
+#pragma unroll
+            for (int k = 0; k < CPD; k++) {
+                const int col = col0 + k;
+                const float v = x[min(max(col, 0), cols - 1)];
+                xr[k] = (lane_live && col < cols) ? v : 0.0f;
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < NS; s++) {
+            int code, shift;
+            slot_code<FMT>(0, s / 8, s % 8, code, shift);
+            xv[s] = xr[code];
+        }
+    } else {
+#pragma unroll
+        for (int s = 0; s < NS; s++) {
+            int code, shift;
+            slot_code<FMT>(w, s / 8, s % 8, code, shift);
+            const int col = b * BS + code;
+            const float v = x[min(max(col, 0), cols - 1)];
+            xv[s] = (lane_live && col < cols) ? v : 0.0f;
+        }
+    }
+}
+
+// Block meta: f = 2^-sh and sx = f * sum_k X_k, both exact in fp64.
+// xs (optional): fp32 x copied to LDS for the outlier pass.
+template <int FMT, int BS>
+__device__ __forceinline__ void prep_finish(const float (&xv)[Fmt<FMT, BS>::NC * 8], int b,
+                                            bool live, int w, uint32_t* dst, double2* meta,
+                                            float* xs, int cols) {
+    using F = Fmt<FMT, BS>;
+    constexpr int NS = F::NC * 8;
+    const bool lane_live = live && w < F::CW;
+    if (xs && lane_live) {
+#pragma unroll
+        for (int s = 0; s < NS; s++) {
+            int code, shift;
+            slot_code<FMT>(w, s / 8, s % 8, code, shift);
+            const int col = b * BS + code;
+            bool own = col < cols;
+            if constexpr (FMT == QK_FMT_3) own = own && (3 * code) / 4 == 8 * w + s % 8;
+            if (own) xs[col] = xv[s];
+        }
+    }
     float amax = 0.0f;
     int bad = 0;
 #pragma unroll
-    for (int j = 0; j < (BS + 63) / 64; j++) {
-        int k = lane + 64 * j;
-        int col = b * BS + k;
-        float t = (live && k < BS && col < cols) ? x[col] : 0.0f;
-        v[j] = t;
-        if (!(fabsf(t) <= 3.402823466e38f)) bad = 1;   // Inf or NaN
-        else amax = fmaxf(amax, fabsf(t));
+    for (int s = 0; s < NS; s++) {
+        if (!(fabsf(xv[s]) <= 3.402823466e38f)) bad = 1;   // Inf or NaN
+        else amax = fmaxf(amax, fabsf(xv[s]));
     }
-    amax = qsf::wave_max(amax);
-    bad = qsf::wave_or_i(bad);
+#pragma unroll
+    for (int off = F::LPB / 2; off > 0; off >>= 1) {
+        amax = fmaxf(amax, __shfl_xor(amax, off, F::LPB));
+        bad |= __shfl_xor(bad, off, F::LPB);
+    }
     int sh = 0;
     if (amax > 0.0f) {
         sh = F::XB - 1 - ilogbf(amax);                 // amax * 2^sh < 2^XB
         sh = sh > 126 ? 126 : (sh < -100 ? -100 : sh);
     }
-    int sumx = 0;
+    uint32_t U[NS];
+    int sum = 0;
 #pragma unroll
-    for (int j = 0; j < (BS + 63) / 64; j++) {
-        int k = lane + 64 * j;
-        if (k < BS) {
-            int X = bad ? 0 : (int)rintf(ldexpf(v[j], sh));
-            xs[wave][k] = X;
-            sumx += X;
+    for (int s = 0; s < NS; s++) {
+        int code, shift;
+        slot_code<FMT>(w, s / 8, s % 8, code, shift);
+        const int X = bad ? 0 : (int)rintf(ldexpf(xv[s], sh));
+        U[s] = (uint32_t)(X * (1 << shift) + (int)DIGIT_BIAS);
+        // count every code once: 3-bit codes at the nibble holding their bit 0
+        if constexpr (FMT == QK_FMT_3) {
+            if ((3 * code) / 4 == 8 * w + s % 8) sum += X;
+        } else {
+            sum += X;
         }
     }
-    sumx = qsf::wave_sum_i(sumx);
-    __syncthreads();
-    for (int s = lane; s < NSLOT; s += 64) {
-        int w = s / (F::NC * 8), c = (s / 8) % F::NC, m = s % 8, code, shift;
-        slot_code<FMT>(w, c, m, code, shift);
-        int M = xs[wave][code] * (1 << shift);
-        us[wave][s] = (uint32_t)(M + (int)DIGIT_BIAS);
-    }
-    __syncthreads();
-    if (!live) return;
-    for (int o = lane; o < F::DW; o += 64) {
-        int wc = o / ND, d = o % ND;                  // wc = w * NC + c
-        uint32_t out = 0;
+    // per-lane |sum| <= NS * 2^XB < 2^31; the block total (up to 2^34) in fp64
+    double dsum = (double)sum;
 #pragma unroll
-        for (int m = 0; m < 8; m++) out |= ((us[wave][wc * 8 + m] >> (4 * d)) & 15u) << (4 * m);
-        xq[(size_t)b * F::DWS + o] = out ^ 0x88888888u;  // nibble n-8 in two's complement
+    for (int off = F::LPB / 2; off > 0; off >>= 1) dsum += __shfl_xor(dsum, off, F::LPB);
+    if (lane_live) {
+#pragma unroll
+        for (int c = 0; c < F::NC; c++) {
+            uint32_t u8[8], dw[ND];
+#pragma unroll
+            for (int m = 0; m < 8; m++) u8[m] = U[c * 8 + m];
+            digit_words(u8, dw);
+#pragma unroll
+            for (int d = 0; d < ND; d++) dst[(w * F::NC + c) * ND + d] = dw[d];
+        }
     }
-    if (lane == 0) {
-        float f = ldexpf(1.0f, -sh);
-        if (bad) f = __builtin_nanf("");
-        xmeta[b] = make_float2(f, (float)sumx * f);
+    if (live && w == 0) {
+        double f = ldexp(1.0, -sh);
+        if (bad) f = __builtin_nan("");
+        *meta = make_double2(f, dsum * f);
     }
 }
+
+template <int FMT, int BS>
+__device__ __forceinline__ void prep_block(const float* __restrict__ x, int cols, int b, bool live,
+                                           int w, uint32_t* dst, double2* meta, float* xs) {
+    float xv[Fmt<FMT, BS>::NC * 8];
+    prep_load<FMT, BS>(x, cols, b, live, w, xv);
+    prep_finish<FMT, BS>(xv, b, live, w, dst, meta, xs, cols);
+}
+
+// Stand-alone x preparation (prepared mode): 256 threads, 256/LPB blocks each.
+template <int FMT, int BS>
+__global__ __launch_bounds__(256) void xprep_kernel(const float* __restrict__ x, int cols, int nb,
+                                                    uint32_t* __restrict__ xq,
+                                                    double2* __restrict__ xmeta) {
+    using F = Fmt<FMT, BS>;
+    const int b = blockIdx.x * (256 / F::LPB) + threadIdx.x / F::LPB;
+    const bool live = b < nb;
+    const int bb = live ? b : 0;
+    prep_block<FMT, BS>(x, cols, b, live, threadIdx.x & (F::LPB - 1), xq + (size_t)bb * F::DWS,
+                        xmeta + bb, nullptr);
+}
+
+// Group sum over `lpg` lanes (power of two) in fp64; the total is valid in
+// the group's last lane (all lanes for lpg <= 16).  Each DPP move carries one
+// half of the double; lanes a row mask leaves out read 0 (+0.0).
+#define QSF_DPP(v, ctrl, rmask)                                                              \
+    __builtin_bit_cast(double, make_int2(__builtin_amdgcn_update_dpp(                        \
+                                             0, __builtin_bit_cast(int2, (v)).x, (ctrl),      \
+                                             (rmask), 0xF, false),                            \
+                                         __builtin_amdgcn_update_dpp(                        \
+                                             0, __builtin_bit_cast(int2, (v)).y, (ctrl),      \
+                                             (rmask), 0xF, false)))
+__device__ __forceinline__ double group_reduce(double v, int lpg) {
+    if (lpg >= 2) v += QSF_DPP(v, 0xB1, 0xF);     // quad_perm [1,0,3,2]
+    if (lpg >= 4) v += QSF_DPP(v, 0x4E, 0xF);     // quad_perm [2,3,0,1]
+    if (lpg >= 8) v += QSF_DPP(v, 0x141, 0xF);    // row_half_mirror
+    if (lpg >= 16) v += QSF_DPP(v, 0x140, 0xF);   // row_mirror
+    if (lpg >= 32) v += QSF_DPP(v, 0x142, 0xA);   // row_bcast15 into rows 1, 3
+    if (lpg >= 64) v += QSF_DPP(v, 0x143, 0xC);   // row_bcast31 into rows 2, 3
+    return v;
+}
+#undef QSF_DPP
 
 struct GemvArgs {
     const uint8_t* w[QK_MAX_GROUP];
     float* y[QK_MAX_GROUP];
-    const uint32_t* rp[QK_MAX_GROUP];
-    const uint32_t* oc[QK_MAX_GROUP];
-    const uint16_t* ov[QK_MAX_GROUP];
+    const uint32_t* rp[QK_MAX_GROUP];   // outlier CSR row pointers (rows + 1), or null
+    const uint32_t* oe[QK_MAX_GROUP];   // packed entries col | fp16 << 16 (cols <= 65536)
+    const uint32_t* oc[QK_MAX_GROUP];   // else split entries: columns ...
+    const uint16_t* ov[QK_MAX_GROUP];   // ... and fp16 values
     int rows[QK_MAX_GROUP];
-    int tile0[QK_MAX_GROUP + 1];
-    int n, cols, nb, lpg, chunk;
-    const uint32_t* xq;
-    const float2* xmeta;
+    int tile0[QK_MAX_GROUP + 1];   // prefix sums of tiles (R * 64/lpg rows each)
+    int n, cols, nb, lpg, chunk, tpw;
+    int xs_off;                    // LDS dword offset of fp32 x for the outlier pass, or -1
+    int st_off, st_wave;           // LDS dword offset / doubles per wave of the result stash
+    const uint32_t* xq;            // prepared digits (stride DWS), or null: prepare here
+    const double2* xmeta;
     const float* x;
 };
 
-template <int FMT, int BS, int R, int WAVES>
-__global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
+// fp16 value and column of outlier entry e of matrix m.
+__device__ __forceinline__ void entry_at(const GemvArgs& a, int m, uint32_t e, uint32_t& col,
+                                         uint32_t& val) {
+    if (a.oe[m]) {
+        const uint32_t u = a.oe[m][e];
+        col = u & 0xFFFFu;
+        val = u >> 16;
+    } else {
+        col = a.oc[m][e];
+        val = a.ov[m][e];
+    }
+}
+
+// Weights of one block for the R rows of a tile (row offsets in roff).
+template <int FMT, int BS, int R>
+__device__ __forceinline__ void load_block(const uint8_t* __restrict__ w, const uint32_t (&roff)[R],
+                                           int b, uint32_t (&wv)[R][1 + Fmt<FMT, BS>::CW]) {
     using F = Fmt<FMT, BS>;
-    extern __shared__ uint32_t lds[];
-    const int tile = blockIdx.x;
-    int m = 0;
-    while (m + 1 < a.n && tile >= a.tile0[m + 1]) m++;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int lpg = a.lpg, grp = lane / lpg, lig = lane % lpg;
-    const int rows_per_wave = (64 / lpg) * R;
-    const int row0 = (tile - a.tile0[m]) * WAVES * rows_per_wave + wave * rows_per_wave + grp * R;
-    const int rows = a.rows[m];
-    const uint8_t* __restrict__ wbase = a.w[m];
-    const size_t row_bytes = (size_t)a.nb * F::BB;
-
-    float rsum[R];
 #pragma unroll
-    for (int r = 0; r < R; r++) rsum[r] = 0.0f;
+    for (int r = 0; r < R; r++) {
+        const uint32_t* p = reinterpret_cast<const uint32_t*>(w + (roff[r] + (uint32_t)b * F::BB));
+#pragma unroll
+        for (int i = 0; i < 1 + F::CW; i++) wv[r][i] = __builtin_nontemporal_load(p + i);
+    }
+}
 
-    for (int c0 = 0; c0 < a.nb; c0 += a.chunk) {
-        const int c1 = min(a.nb, c0 + a.chunk);
-        // stage this chunk's digits and block meta in LDS
-        __syncthreads();
-        {
-            const uint4* src = reinterpret_cast<const uint4*>(a.xq + (size_t)c0 * F::DWS);
-            uint4* dst = reinterpret_cast<uint4*>(lds);
-            const int n4 = (c1 - c0) * F::DWS / 4;
-            for (int i = threadIdx.x; i < n4; i += WAVES * 64) dst[i] = src[i];
-            float2* mdst = reinterpret_cast<float2*>(lds + a.chunk * F::DWS);
-            for (int i = threadIdx.x; i < c1 - c0; i += WAVES * 64) mdst[i] = a.xmeta[c0 + i];
-        }
-        __syncthreads();
-        const float2* meta = reinterpret_cast<const float2*>(lds + a.chunk * F::DWS);
-
-        for (int b = c0 + lig; b < c1; b += lpg) {
-            uint32_t wv[R][1 + F::CW];
+// Dequant-dot of one block for R rows: rs[r] += s*sum(q*x) + z*sum(x), the
+// integer digit sums joined exactly and the row sums accumulated in fp64.
+template <int FMT, int BS, int R>
+__device__ __forceinline__ void compute_block(const uint32_t (&wv)[R][1 + Fmt<FMT, BS>::CW],
+                                              const uint32_t* __restrict__ dg, double2 xm,
+                                              double (&rs)[R]) {
+    using F = Fmt<FMT, BS>;
+    {
+        int acc[R][F::NA][ND];
+        auto step = [&](auto wic) {
+            constexpr int wi = decltype(wic)::value;
+            uint32_t dd[F::NC][ND];
+#pragma unroll
+            for (int c = 0; c < F::NC; c++)
+#pragma unroll
+                for (int d = 0; d < ND; d++) dd[c][d] = dg[(wi * F::NC + c) * ND + d];
 #pragma unroll
             for (int r = 0; r < R; r++) {
-                const int row = row0 + r;
-                if (row < rows) {
-                    const uint32_t* p = reinterpret_cast<const uint32_t*>(
-                        wbase + (size_t)row * row_bytes + (size_t)b * F::BB);
 #pragma unroll
-                    for (int i = 0; i < 1 + F::CW; i++) wv[r][i] = __builtin_nontemporal_load(p + i);
-                } else {
+                for (int c = 0; c < F::NC; c++) {
+                    const uint32_t nib = extract<FMT, wi>(wv[r][1 + wi], c);
+                    const int s = F::NA == 2 ? c : 0;
+                    const bool first = wi == 0 && (F::NA == 2 || c == 0);
 #pragma unroll
-                    for (int i = 0; i < 1 + F::CW; i++) wv[r][i] = 0u;
+                    for (int d = 0; d < ND; d++)
+                        acc[r][s][d] = qsf::sdot8(nib, dd[c][d], first ? 0 : acc[r][s][d]);
                 }
             }
-            const uint32_t* dg = lds + (size_t)(b - c0) * F::DWS;
-            int acc[R][F::NA][ND];
-#pragma unroll
-            for (int r = 0; r < R; r++)
-#pragma unroll
-                for (int s = 0; s < F::NA; s++)
-#pragma unroll
-                    for (int d = 0; d < ND; d++) acc[r][s][d] = 0;
+        };
+        [&]<int... I>(std::integer_sequence<int, I...>) {
+            (step(std::integral_constant<int, I>{}), ...);
+        }(std::make_integer_sequence<int, F::CW>{});
 
-            auto step = [&](auto wic) {
-                constexpr int wi = decltype(wic)::value;
-                uint32_t dig[F::NC][ND];
 #pragma unroll
-                for (int c = 0; c < F::NC; c++)
+        for (int r = 0; r < R; r++) {
+            double sf = 0.0;
 #pragma unroll
-                    for (int d = 0; d < ND; d++) dig[c][d] = dg[(wi * F::NC + c) * ND + d];
+            for (int s = 0; s < F::NA; s++) {
+                uint32_t lo = (uint32_t)acc[r][s][ND_LO - 1];
 #pragma unroll
-                for (int r = 0; r < R; r++) {
+                for (int d = ND_LO - 2; d >= 0; d--) lo = (lo << 4) + (uint32_t)acc[r][s][d];
+                uint32_t hi = (uint32_t)acc[r][s][ND - 1];
 #pragma unroll
-                    for (int c = 0; c < F::NC; c++) {
-                        const uint32_t nib = extract<FMT, wi>(wv[r][1 + wi], c);
-                        const int s = F::NA == 2 ? c : 0;
-#pragma unroll
-                        for (int d = 0; d < ND; d++) acc[r][s][d] = qsf::sdot8(nib, dig[c][d], acc[r][s][d]);
-                    }
-                }
-            };
-            [&]<int... I>(std::integer_sequence<int, I...>) {
-                (step(std::integral_constant<int, I>{}), ...);
-            }(std::make_integer_sequence<int, F::CW>{});
-
-            const float2 xm = meta[b - c0];
-#pragma unroll
-            for (int r = 0; r < R; r++) {
-                float sf = 0.0f;
-#pragma unroll
-                for (int s = 0; s < F::NA; s++) {
-                    uint32_t lo = (uint32_t)acc[r][s][ND_LO - 1];
-#pragma unroll
-                    for (int d = ND_LO - 2; d >= 0; d--) lo = (lo << 4) + (uint32_t)acc[r][s][d];
-                    uint32_t hi = (uint32_t)acc[r][s][ND - 1];
-#pragma unroll
-                    for (int d = ND - 2; d >= ND_LO; d--) hi = (hi << 4) + (uint32_t)acc[r][s][d];
-                    const float v = fmaf((float)(int)hi, 65536.0f, (float)(int)lo);
-                    sf = s == 0 ? v : fmaf(0.25f, v, sf);
-                }
-                const float sc = qsf::f16_lo(wv[r][0]);
-                const float coef = sc * xm.x;
-                if constexpr (FMT == QK_FMT_4SYM) {
-                    rsum[r] = fmaf(coef, sf, rsum[r]);
-                } else {
-                    float z = qsf::f16_hi(wv[r][0]);
-                    if constexpr (FMT == QK_FMT_4) z = fmaf(8.0f, sc, z);
-                    rsum[r] = fmaf(coef, sf, rsum[r]);
-                    rsum[r] = fmaf(z, xm.y, rsum[r]);
-                }
+                for (int d = ND - 2; d >= ND_LO; d--) hi = (hi << 4) + (uint32_t)acc[r][s][d];
+                const double v = fma((double)(int)hi, 65536.0, (double)(int)lo);   // exact
+                sf = s == 0 ? v : fma(0.25, v, sf);                                 // exact
+            }
+            const double sc = (double)qsf::f16_lo(wv[r][0]);
+            rs[r] = fma(sc * xm.x, sf, rs[r]);             // sc * 2^-sh is exact
+            if constexpr (FMT != QK_FMT_4SYM) {
+                double z = (double)qsf::f16_hi(wv[r][0]);
+                if constexpr (FMT == QK_FMT_4) z = fma(8.0, sc, z);   // exact
+                rs[r] = fma(z, xm.y, rs[r]);
             }
         }
     }
+}
 
-    // fused sparse pass: fp16 outliers of this group's rows (src/quant.c:481-494)
+// Stage block digits + meta for blocks [c0, c1) in LDS: prepare them from x
+// here, or copy the ones a stand-alone x-prep launch left in global memory.
+// xs (whole-row staging only, c0 == 0) also receives fp32 x.
+template <int FMT, int BS>
+__device__ __forceinline__ void stage_x(const GemvArgs& a, int c0, int c1, uint32_t* dig,
+                                        double2* meta, float* xs) {
+    using F = Fmt<FMT, BS>;
+    if (a.xq) {
+        for (int i = threadIdx.x; i < (c1 - c0) * F::DWS; i += WAVES * 64)
+            dig[i] = a.xq[(size_t)c0 * F::DWS + i];
+        for (int i = threadIdx.x; i < c1 - c0; i += WAVES * 64) meta[i] = a.xmeta[c0 + i];
+        if (xs)
+            for (int i = threadIdx.x; i < a.cols; i += WAVES * 64) xs[i] = a.x[i];
+    } else {
+        const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+        for (int base = c0; base < c1; base += WAVES * 64 / F::LPB) {
+            if (base + wave * (64 / F::LPB) >= c1) break;      // whole wave past the end
+            const int b = base + threadIdx.x / F::LPB;
+            const bool live = b < c1;
+            const int bb = live ? b : c0;
+            prep_block<FMT, BS>(a.x, a.cols, b, live, threadIdx.x & (F::LPB - 1),
+                                dig + (bb - c0) * F::DWS, meta + (bb - c0), xs);
+        }
+    }
+}
+
+// Tile t -> matrix m and first row of this lane's row group.
+__device__ __forceinline__ void tile_of(const GemvArgs& a, int t, int rows_per_tile, int grp, int R,
+                                        int& m, int& row0) {
+    m = 0;
+    while (m + 1 < a.n && t >= a.tile0[m + 1]) m++;
+    row0 = (t - a.tile0[m]) * rows_per_tile + grp * R;
+}
+
+// Fused sparse pass (fp16 outliers of the tile's rows, src/quant.c:481-494),
+// group reduction and store of one finished tile (chunked path).
+template <int R>
+__device__ __forceinline__ void flush_tile(const GemvArgs& a, int m, int row0, int lig, int lpg,
+                                           double (&rs)[R]) {
+    const int rows = a.rows[m];
     const uint32_t* rp = a.rp[m];
     if (rp) {
-        const uint32_t* __restrict__ oc = a.oc[m];
-        const uint16_t* __restrict__ ov = a.ov[m];
 #pragma unroll
         for (int r = 0; r < R; r++) {
             const int row = row0 + r;
             if (row < rows) {
                 const uint32_t e1 = rp[row + 1];
-                for (uint32_t j = rp[row] + lig; j < e1; j += lpg)
-                    rsum[r] = fmaf(qsf::f16_bits(ov[j]), a.x[oc[j]], rsum[r]);
+                for (uint32_t e = rp[row] + lig; e < e1; e += lpg) {
+                    uint32_t col, val;
+                    entry_at(a, m, e, col, val);
+                    rs[r] = fma((double)qsf::f16_bits(val), (double)a.x[col], rs[r]);
+                }
+            }
+        }
+    }
+    float* __restrict__ y = a.y[m];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        const double v = group_reduce(rs[r], lpg);
+        if (lig == lpg - 1 && row0 + r < rows) y[row0 + r] = (float)v;
+        rs[r] = 0.0;
+    }
+}
+
+// Main path (all block digits fit in LDS at once).  A wave's work is the
+// list of (tile, block) items, the same count for every lane; weights are
+// loaded D items ahead into a ring of register sets.  Vector-memory loads
+// return in issue order, so the order is: x loads of the prep, the outlier
+// row pointers of the wave's rows, the first D weight items, the first
+// outlier entry per lane and row, the prep arithmetic, the item loop, and
+// last the remaining outlier entries.  Finished tiles of a matrix with
+// outliers park their fp64 row sums in LDS until the sparse terms are in.
+template <int FMT, int BS, int R, int D, bool OUT>
+__global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
+    using F = Fmt<FMT, BS>;
+    extern __shared__ __align__(16) uint32_t lds[];
+    double2* meta = reinterpret_cast<double2*>(lds);
+    uint32_t* dig = lds + 4 * a.chunk;
+    float* xs = a.xs_off >= 0 ? reinterpret_cast<float*>(lds + a.xs_off) : nullptr;
+    // wave index made provably uniform: tile -> matrix lookups then stay in
+    // scalar registers (kernel arguments via s_load, no vector-memory waits)
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lpg = a.lpg, grp = lane / lpg, lig = lane & (lpg - 1);
+    const int rows_per_tile = R * (64 / lpg);
+    const int tw = blockIdx.x * a.tpw + wave;                 // this wave's first tile
+    const int t_end = min(a.tile0[a.n], blockIdx.x * a.tpw + a.tpw);
+    const int nt = tw < t_end ? min(MAXT, (t_end - tw + WAVES - 1) / WAVES) : 0;
+    const int ipt = (a.nb + lpg - 1) / lpg;                   // items per tile
+    const int ni = nt * ipt;
+    const uint32_t row_bytes = (uint32_t)a.nb * F::BB;
+
+    auto issue = [&](int ii, uint32_t (&wv)[R][1 + F::CW]) {
+        int m, row0;
+        tile_of(a, tw + WAVES * (ii / ipt), rows_per_tile, grp, R, m, row0);
+        const int b = min(lig + (ii % ipt) * lpg, a.nb - 1);
+        uint32_t roff[R];
+#pragma unroll
+        for (int r = 0; r < R; r++) roff[r] = (uint32_t)min(row0 + r, a.rows[m] - 1) * row_bytes;
+        load_block<FMT, BS, R>(a.w[m], roff, b, wv);
+    };
+
+    // x values of this thread's first prep block group, requested first;
+    // waves past the last block skip the prep
+    constexpr int PASS = WAVES * 64 / F::LPB;                 // blocks per prep pass
+    const int pw = threadIdx.x & (F::LPB - 1);
+    const int pb = threadIdx.x / F::LPB;
+    const bool prep_wave = !a.xq && wave * (64 / F::LPB) < a.nb;
+    float xv0[F::NC * 8];
+    if (prep_wave) prep_load<FMT, BS>(a.x, a.cols, pb, pb < a.nb, pw, xv0);
+
+    // CSR bounds of this lane's rows: row r of tile j owns [rpv[j][r], rpv[j][r+1])
+    uint32_t rpv[MAXT][R + 1];
+#pragma unroll
+    for (int j = 0; j < MAXT; j++) {
+#pragma unroll
+        for (int r = 0; r <= R; r++) rpv[j][r] = 0;
+        if (OUT && j < nt) {
+            int m, row0;
+            tile_of(a, tw + WAVES * j, rows_per_tile, grp, R, m, row0);
+            if (a.rp[m]) {
+#pragma unroll
+                for (int r = 0; r <= R; r++) rpv[j][r] = a.rp[m][min(row0 + r, a.rows[m])];
             }
         }
     }
 
+    uint32_t wv[D][R][1 + F::CW];
 #pragma unroll
-    for (int r = 0; r < R; r++) rsum[r] = qsf::group_sum(rsum[r], lpg);
-    // every lane of the group holds all R sums; lane (r mod LPG) stores row r
-    float* __restrict__ y = a.y[m];
+    for (int k = 0; k < D; k++)
+        if (k < ni) issue(k, wv[k]);
+
+    // first entry of every row for this lane (packed tables)
+    uint32_t e0[MAXT][R];
 #pragma unroll
-    for (int r = 0; r < R; r++)
-        if (lig == (r & (lpg - 1)) && row0 + r < rows) y[row0 + r] = rsum[r];
+    for (int j = 0; j < MAXT; j++) {
+#pragma unroll
+        for (int r = 0; r < R; r++) e0[j][r] = 0;
+        if (OUT && j < nt) {
+            int m, row0;
+            tile_of(a, tw + WAVES * j, rows_per_tile, grp, R, m, row0);
+            if (a.oe[m]) {
+#pragma unroll
+                for (int r = 0; r < R; r++)
+                    if (rpv[j][r] + lig < rpv[j][r + 1]) e0[j][r] = a.oe[m][rpv[j][r] + lig];
+            }
+        }
+    }
+
+    if (a.xq) {
+        stage_x<FMT, BS>(a, 0, a.nb, dig, meta, xs);
+    } else {
+        if (prep_wave) {
+            const int b0 = pb < a.nb ? pb : 0;
+            prep_finish<FMT, BS>(xv0, pb, pb < a.nb, pw, dig + b0 * F::DWS, meta + b0, xs, a.cols);
+        }
+        for (int base = PASS; base < a.nb; base += PASS) {
+            if (base + wave * (64 / F::LPB) >= a.nb) break;
+            const int b = base + pb;
+            const bool live = b < a.nb;
+            const int bb = live ? b : 0;
+            prep_block<FMT, BS>(a.x, a.cols, b, live, pw, dig + bb * F::DWS, meta + bb, xs);
+        }
+    }
+    __syncthreads();
+
+    double* stash = reinterpret_cast<double*>(lds + a.st_off) + wave * a.st_wave;
+    double rs[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) rs[r] = 0.0;
+    for (int i0 = 0; i0 < ni; i0 += D) {
+#pragma unroll
+        for (int k = 0; k < D; k++) {
+            const int ii = i0 + k;
+            if (ii < ni) {
+                const int b = lig + (ii % ipt) * lpg;
+                if (b < a.nb) compute_block<FMT, BS, R>(wv[k], dig + b * F::DWS, meta[b], rs);
+                if (ii + D < ni) issue(ii + D, wv[k]);
+                if (ii % ipt == ipt - 1) {
+                    const int j = ii / ipt;
+                    int m, row0;
+                    tile_of(a, tw + WAVES * j, rows_per_tile, grp, R, m, row0);
+#pragma unroll
+                    for (int r = 0; r < R; r++) {
+                        const double v = group_reduce(rs[r], lpg);
+                        rs[r] = 0.0;
+                        if (lig == lpg - 1) {
+                            if (OUT && a.rp[m]) stash[j * rows_per_tile + grp * R + r] = v;
+                            else if (row0 + r < a.rows[m]) a.y[m][row0 + r] = (float)v;
+                        }
+                    }
+                }
+            }
+        }
+    }
+
+    if constexpr (!OUT) return;
+    // sparse pass (src/quant.c:481-494): fp64 sums of fp16 value * x[col]
+    bool any_out = false;
+    double os[MAXT][R];
+#pragma unroll
+    for (int j = 0; j < MAXT; j++) {
+#pragma unroll
+        for (int r = 0; r < R; r++) os[j][r] = 0.0;
+        if (j < nt) {
+            int m, row0;
+            tile_of(a, tw + WAVES * j, rows_per_tile, grp, R, m, row0);
+            any_out |= a.rp[m] != nullptr;
+            if (a.oe[m]) {
+#pragma unroll
+                for (int r = 0; r < R; r++) {
+                    if (rpv[j][r] + lig < rpv[j][r + 1]) {
+                        const uint32_t col = e0[j][r] & 0xFFFFu;
+                        const float xc = xs ? xs[col] : a.x[col];
+                        os[j][r] = (double)qsf::f16_bits(e0[j][r] >> 16) * (double)xc;
+                    }
+                }
+            }
+        }
+    }
+    if (!any_out) return;
+    // remaining entries: one per lane and row each step, loads batched over rows
+    for (int k = 0;; k++) {
+        bool ok[MAXT][R];
+        bool more = false;
+        uint32_t ec[MAXT][R], ev[MAXT][R];
+#pragma unroll
+        for (int j = 0; j < MAXT; j++) {
+            int m = 0, row0 = 0;
+            if (j < nt) tile_of(a, tw + WAVES * j, rows_per_tile, grp, R, m, row0);
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                const uint32_t e = rpv[j][r] + lig + (uint32_t)(k + (a.oe[m] ? 1 : 0)) * lpg;
+                ok[j][r] = j < nt && a.rp[m] && e < rpv[j][r + 1];
+                more |= ok[j][r];
+                if (ok[j][r]) entry_at(a, m, e, ec[j][r], ev[j][r]);
+            }
+        }
+        if (!__any(more)) break;
+#pragma unroll
+        for (int j = 0; j < MAXT; j++)
+#pragma unroll
+            for (int r = 0; r < R; r++)
+                if (ok[j][r]) {
+                    const float xc = xs ? xs[ec[j][r]] : a.x[ec[j][r]];
+                    os[j][r] = fma((double)qsf::f16_bits(ev[j][r]), (double)xc, os[j][r]);
+                }
+    }
+#pragma unroll
+    for (int j = 0; j < MAXT; j++) {
+        if (j < nt) {
+            int m, row0;
+            tile_of(a, tw + WAVES * j, rows_per_tile, grp, R, m, row0);
+            if (a.rp[m]) {
+#pragma unroll
+                for (int r = 0; r < R; r++) {
+                    const double v = group_reduce(os[j][r], lpg);
+                    if (lig == lpg - 1 && row0 + r < a.rows[m])
+                        a.y[m][row0 + r] = (float)(stash[j * rows_per_tile + grp * R + r] + v);
+                }
+            }
+        }
+    }
+}
+
+// Fallback when the digits of a row do not fit in LDS: K in chunks, at most
+// MAXT tiles a wave kept in registers across chunks, no prefetch.
+template <int FMT, int BS, int R>
+__global__ __launch_bounds__(WAVES * 64) void gemv_chunked_kernel(GemvArgs a) {
+    using F = Fmt<FMT, BS>;
+    extern __shared__ __align__(16) uint32_t lds[];
+    double2* meta = reinterpret_cast<double2*>(lds);
+    uint32_t* dig = lds + 4 * a.chunk;
+    // wave index made provably uniform: tile -> matrix lookups then stay in
+    // scalar registers (kernel arguments via s_load, no vector-memory waits)
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lpg = a.lpg, grp = lane / lpg, lig = lane & (lpg - 1);
+    const int rows_per_tile = R * (64 / lpg);
+    const int t_begin = blockIdx.x * a.tpw;
+    const int t_end = min(a.tile0[a.n], t_begin + a.tpw);
+    const uint32_t row_bytes = (uint32_t)a.nb * F::BB;
+
+    double rs[MAXT][R];
+#pragma unroll
+    for (int j = 0; j < MAXT; j++)
+#pragma unroll
+        for (int r = 0; r < R; r++) rs[j][r] = 0.0;
+
+    for (int c0 = 0; c0 < a.nb; c0 += a.chunk) {
+        const int c1 = min(a.nb, c0 + a.chunk);
+        __syncthreads();
+        stage_x<FMT, BS>(a, c0, c1, dig, meta, nullptr);
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < MAXT; j++) {
+            const int t = t_begin + wave + WAVES * j;
+            if (t >= t_end) break;
+            int m, row0;
+            tile_of(a, t, rows_per_tile, grp, R, m, row0);
+            if (row0 >= a.rows[m]) continue;
+            uint32_t roff[R];
+#pragma unroll
+            for (int r = 0; r < R; r++) roff[r] = (uint32_t)min(row0 + r, a.rows[m] - 1) * row_bytes;
+            for (int b = c0 + lig; b < c1; b += lpg) {
+                uint32_t wv[R][1 + F::CW];
+                load_block<FMT, BS, R>(a.w[m], roff, b, wv);
+                compute_block<FMT, BS, R>(wv, dig + (b - c0) * F::DWS, meta[b - c0], rs[j]);
+            }
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < MAXT; j++) {
+        const int t = t_begin + wave + WAVES * j;
+        if (t >= t_end) break;
+        int m, row0;
+        tile_of(a, t, rows_per_tile, grp, R, m, row0);
+        flush_tile<R>(a, m, row0, lig, lpg, rs[j]);
+    }
 }
 
 __global__ void fill_kernel(float* y, int n, float v) {
@@ -320,29 +729,55 @@ __global__ void fill_kernel(float* y, int n, float v) {
     if (i < n) y[i] = v;
 }
 
-constexpr int kLdsBudget = 64 * 1024;
-constexpr int kR = 4;
-constexpr int kWaves = 4;
+int num_cus() {
+    static int n = 0;
+    if (!n) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+            n = 256;
+    }
+    return n;
+}
 
 template <int FMT, int BS>
 size_t xprep_bytes_t(int cols) {
     using F = Fmt<FMT, BS>;
     size_t nb = (size_t)((cols + BS - 1) / BS);
     size_t dig = nb * F::DWS * 4;
-    return ((dig + 255) & ~(size_t)255) + nb * sizeof(float2);
+    return ((dig + 255) & ~(size_t)255) + nb * sizeof(double2);
+}
+
+// Dynamic LDS a GEMV workgroup may use in total (digits, meta, staged x, stash).
+size_t lds_limit() {
+    return kLdsLimit;
+}
+
+// rows per tile: 2 for 64-code-or-smaller blocks, else 1 (register budget);
+// prefetch depth: about 48 registers of weights in flight per lane
+template <int FMT, int BS>
+constexpr int tile_rows() { return Fmt<FMT, BS>::CW <= 8 ? 2 : 1; }
+// (one item for 3-bit 256-code blocks: 25 dwords a row plus two accumulator
+// sets leave no room for a second set within 128 VGPRs)
+template <int FMT, int BS>
+constexpr int prefetch_depth() {
+    constexpr int per = tile_rows<FMT, BS>() * (1 + Fmt<FMT, BS>::CW);
+    if (FMT == QK_FMT_3 && Fmt<FMT, BS>::CW >= 24) return 1;
+    return 48 / per < 2 ? 2 : (48 / per > 4 ? 4 : 48 / per);
 }
 
 template <int FMT, int BS>
 int launch_t(const qsf_hip_tensor* const* t, int n, int cols, const float* d_x,
              float* const* d_y, void* d_ws, int mode, hipStream_t s) {
     using F = Fmt<FMT, BS>;
+    constexpr int R = tile_rows<FMT, BS>();
     const int nb = (cols + BS - 1) / BS;
     uint32_t* xq = (uint32_t*)d_ws;
     size_t dig = (size_t)nb * F::DWS * 4;
-    float2* xmeta = (float2*)((uint8_t*)d_ws + ((dig + 255) & ~(size_t)255));
-    if (mode & QK_RUN_XPREP)
-        hipLaunchKernelGGL((xprep_kernel<FMT, BS>), dim3((nb + 3) / 4), dim3(256), 0, s,
-                           d_x, cols, nb, xq, xmeta);
+    double2* xmeta = (double2*)((uint8_t*)d_ws + ((dig + 255) & ~(size_t)255));
+    if ((mode & QK_RUN_XPREP) && (!(mode & QK_RUN_GEMV) || (mode & QK_RUN_STANDALONE_PREP)))
+        hipLaunchKernelGGL((xprep_kernel<FMT, BS>), dim3((nb + 256 / F::LPB - 1) / (256 / F::LPB)),
+                           dim3(256), 0, s, d_x, cols, nb, xq, xmeta);
     if (!(mode & QK_RUN_GEMV)) return hipGetLastError() == hipSuccess ? 0 : -1;
 
     GemvArgs a = {};
@@ -352,26 +787,74 @@ int launch_t(const qsf_hip_tensor* const* t, int n, int cols, const float* d_x,
     int lpg = 1;
     while (lpg < nb && lpg < 64) lpg <<= 1;
     a.lpg = lpg;
-    const int per_block = F::DWS * 4 + (int)sizeof(float2);
+    const int per_block = F::DWS * 4 + (int)sizeof(double2);
     a.chunk = nb < kLdsBudget / per_block ? nb : kLdsBudget / per_block;
-    const int rows_per_wg = kWaves * (64 / lpg) * kR;
+    const int rows_per_tile = R * (64 / lpg);
+    bool any_out = false;
     a.tile0[0] = 0;
     for (int i = 0; i < n; i++) {
+        if ((size_t)t[i]->rows * nb * F::BB > 0xFFFFFFF0ull) return -2;   // 32-bit offsets
         a.w[i] = t[i]->d_blocks;
         a.y[i] = d_y[i];
         a.rp[i] = t[i]->d_row_ptr;
+        a.oe[i] = t[i]->d_oent;
         a.oc[i] = t[i]->d_ocol;
         a.ov[i] = t[i]->d_oval;
         a.rows[i] = t[i]->rows;
-        a.tile0[i + 1] = a.tile0[i] + (t[i]->rows + rows_per_wg - 1) / rows_per_wg;
+        a.tile0[i + 1] = a.tile0[i] + (t[i]->rows + rows_per_tile - 1) / rows_per_tile;
+        any_out |= t[i]->d_row_ptr != nullptr;
     }
-    a.xq = xq;
+    const int tiles = a.tile0[n];
+    if (tiles == 0) return 0;
+    // one workgroup per CU (fewer for small problems); at most MAXT tiles a wave
+    int grid = (tiles + WAVES - 1) / WAVES;
+    grid = grid < num_cus() ? grid : num_cus();
+    if ((tiles + grid - 1) / grid > WAVES * MAXT) grid = (tiles + WAVES * MAXT - 1) / (WAVES * MAXT);
+    a.tpw = (tiles + grid - 1) / grid;
+    const bool prepared = !(mode & QK_RUN_XPREP) || (mode & QK_RUN_STANDALONE_PREP);
+    a.xq = prepared ? xq : nullptr;
     a.xmeta = xmeta;
     a.x = d_x;
-    const size_t lds = (size_t)a.chunk * per_block;
-    if (a.tile0[n] > 0)
-        hipLaunchKernelGGL((gemv_kernel<FMT, BS, kR, kWaves>), dim3(a.tile0[n]), dim3(kWaves * 64),
-                           lds, s, a);
+
+    // LDS: [meta: chunk x 16 B][digits: chunk x DWS dwords][stash][x]
+    size_t lds = (size_t)a.chunk * per_block;
+    bool whole = a.chunk >= nb;
+    a.xs_off = -1;
+    a.st_off = 0;
+    a.st_wave = 0;
+    if (whole && any_out) {
+        // fp64 stash of the rows of each wave's finished tiles; fewer tiles a
+        // workgroup when it would not fit
+        const size_t per_tile = (size_t)WAVES * rows_per_tile * sizeof(double);
+        const size_t st_at = (lds + 7) & ~(size_t)7;
+        const size_t room = lds_limit() > st_at ? (lds_limit() - st_at) / per_tile : 0;
+        if (room == 0) {
+            whole = false;                     // the chunked kernel needs no stash
+        } else {
+            if ((size_t)a.tpw > WAVES * room) a.tpw = (int)(WAVES * room);
+            const int ntc = (a.tpw + WAVES - 1) / WAVES;
+            a.st_off = (int)(st_at / 4);
+            a.st_wave = ntc * rows_per_tile;
+            lds = st_at + (size_t)ntc * per_tile;
+            if (lds + (size_t)cols * 4 <= lds_limit()) {
+                a.xs_off = (int)(lds / 4);
+                lds += (size_t)cols * 4;
+            }
+        }
+    }
+    grid = (tiles + a.tpw - 1) / a.tpw;
+    constexpr int D = prefetch_depth<FMT, BS>();
+    // only the 2-bit and 4-bit asymmetric formats have outlier variants
+    constexpr bool kHasOut = FMT == QK_FMT_2 || FMT == QK_FMT_4;
+    if (any_out && !kHasOut) return -2;
+    if (whole && kHasOut && any_out)
+        hipLaunchKernelGGL((gemv_kernel<FMT, BS, R, D, kHasOut>), dim3(grid), dim3(WAVES * 64), lds,
+                           s, a);
+    else if (whole)
+        hipLaunchKernelGGL((gemv_kernel<FMT, BS, R, D, false>), dim3(grid), dim3(WAVES * 64), lds,
+                           s, a);
+    else
+        hipLaunchKernelGGL((gemv_chunked_kernel<FMT, BS, R>), dim3(grid), dim3(WAVES * 64), lds, s, a);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

@@ -38,8 +38,9 @@ typedef struct qsf_hip_tensor {
     uint32_t n_outliers;        /* entries in the file table */
     uint32_t n_csr;             /* entries kept (in range) */
     uint32_t* d_row_ptr;        /* rows+1, or NULL */
-    uint32_t* d_ocol;           /* n_csr column indices */
-    uint16_t* d_oval;           /* n_csr fp16 values */
+    uint32_t* d_oent;           /* n_csr packed entries col | fp16 << 16 (cols <= 65536), or NULL */
+    uint32_t* d_ocol;           /* else n_csr column indices ... */
+    uint16_t* d_oval;           /* ... and n_csr fp16 values */
     void*    d_alloc;           /* base of the single device allocation */
     int      registry_owned;    /* uploaded implicitly by a table-slot call */
     struct qsf_hip_tensor* prev; /* list of live tensors (freed at shutdown) */
@@ -53,8 +54,10 @@ size_t qk_xprep_bytes(int fmt, int bs, int cols);
 
 /* x preparation into ws (qk_xprep_bytes(fmt, bs, cols) bytes, 256-B aligned) */
 int qk_xprep(int fmt, int bs, int cols, const float* d_x, void* d_ws, hipStream_t s);
-/* GEMV over n tensors sharing x; mode selects the x-prep and/or GEMV launch. */
-enum { QK_RUN_XPREP = 1, QK_RUN_GEMV = 2, QK_RUN_BOTH = 3 };
+/* GEMV over n tensors sharing x.  mode: QK_RUN_BOTH prepares x inside the
+ * GEMV workgroups (one launch); QK_RUN_GEMV reads digits prepared into ws by
+ * qk_xprep; QK_RUN_BOTH | QK_RUN_STANDALONE_PREP launches both kernels. */
+enum { QK_RUN_XPREP = 1, QK_RUN_GEMV = 2, QK_RUN_BOTH = 3, QK_RUN_STANDALONE_PREP = 4 };
 int qk_gemv_group(const qsf_hip_tensor* const* t, int n, const float* d_x,
                   float* const* d_y, void* d_ws, int mode, hipStream_t s);
 

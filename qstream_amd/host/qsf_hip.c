@@ -323,6 +323,12 @@ static qsf_hip_tensor* upload_locked(const void* host, int qt, int rows, int col
     }
     t->n_csr = kept;
 
+    /* Entries are packed into one dword (col | fp16 << 16) when every column
+     * fits 16 bits: one 4-byte load per entry instead of two loads. */
+    const int packed = cols <= 65536;
+    if (row_ptr && packed)
+        for (uint32_t i = 0; i < kept; i++) ocol[i] |= (uint32_t)oval[i] << 16;
+
     /* one allocation: [blocks][scales][row_ptr][ocol][oval], 256-B aligned parts */
     size_t off_blocks = 0;
     size_t off_scales = align256(blocks_bytes);
@@ -330,7 +336,7 @@ static qsf_hip_tensor* upload_locked(const void* host, int qt, int rows, int col
     size_t rp_bytes = row_ptr ? ((size_t)rows + 1) * 4 : 0;
     size_t off_oc = off_rp + align256(rp_bytes);
     size_t off_ov = off_oc + align256((size_t)kept * 4);
-    size_t total = off_ov + align256((size_t)kept * 2);
+    size_t total = off_ov + (packed ? 0 : align256((size_t)kept * 2));
     if (total == 0) total = 256;
     /* blocks are read with 16-byte vector loads that may reach 12 bytes past
      * the last block: keep a tail pad */
@@ -351,11 +357,19 @@ static qsf_hip_tensor* upload_locked(const void* host, int qt, int rows, int col
     }
     if (he == hipSuccess && row_ptr) {
         t->d_row_ptr = (uint32_t*)(base + off_rp);
-        t->d_ocol = (uint32_t*)(base + off_oc);
-        t->d_oval = (uint16_t*)(base + off_ov);
         he = hipMemcpy(t->d_row_ptr, row_ptr, rp_bytes, hipMemcpyHostToDevice);
-        if (he == hipSuccess && kept) he = hipMemcpy(t->d_ocol, ocol, (size_t)kept * 4, hipMemcpyHostToDevice);
-        if (he == hipSuccess && kept) he = hipMemcpy(t->d_oval, oval, (size_t)kept * 2, hipMemcpyHostToDevice);
+        if (packed) {
+            t->d_oent = (uint32_t*)(base + off_oc);
+            if (he == hipSuccess && kept)
+                he = hipMemcpy(t->d_oent, ocol, (size_t)kept * 4, hipMemcpyHostToDevice);
+        } else {
+            t->d_ocol = (uint32_t*)(base + off_oc);
+            t->d_oval = (uint16_t*)(base + off_ov);
+            if (he == hipSuccess && kept)
+                he = hipMemcpy(t->d_ocol, ocol, (size_t)kept * 4, hipMemcpyHostToDevice);
+            if (he == hipSuccess && kept)
+                he = hipMemcpy(t->d_oval, oval, (size_t)kept * 2, hipMemcpyHostToDevice);
+        }
     }
     free(row_ptr); free(ocol); free(oval);
     if (he != hipSuccess) {
@@ -431,7 +445,10 @@ void qsf_hip_shutdown(void) {
 }
 
 /* ---- device-pointer entry points ----------------------------------------- */
-static hipStream_t pick_stream(void* s) { return s ? (hipStream_t)s : g_dev.stream; }
+/* Device-pointer entry points run on the caller's stream; NULL is the HIP
+ * default (null) stream, as everywhere in HIP.  Only the synchronous table
+ * slots use the library's own stream. */
+static hipStream_t pick_stream(void* s) { return (hipStream_t)s; }
 
 static int group_locked(const qsf_hip_tensor* const* t, int n, const float* d_x,
                         float* const* d_y, void* stream) {

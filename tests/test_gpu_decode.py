@@ -67,6 +67,69 @@ def test_unpack_bit_exact(hip, oracle, qt, bs):
     assert np.array_equal(m, raw[:, :4].copy().view(np.uint32).reshape(-1))
 
 
+def _slots(qt, bs):
+    """(w, c, m) -> (code, shift) of the digit tables: which x element (and
+    power of two) nibble m of copy c of code dword w is paired with."""
+    bits = {F.Q2: 2, F.Q3: 3}.get(qt, 4)
+    cw, nc = bs * bits // 32, (2 if bits in (2, 3) else 1)
+    out = {}
+    for w in range(cw):
+        for c in range(nc):
+            for m in range(8):
+                if bits == 2:
+                    out[w, c, m] = (16 * w + 2 * m + c, 0)
+                elif bits == 3:
+                    g = 8 * w + m
+                    out[w, c, m] = ((4 * g) // 3 + c, g % 3)
+                else:
+                    out[w, c, m] = (8 * w + m, 0)
+    return cw, nc, out
+
+
+@pytest.mark.parametrize("qt,bs", [(F.Q4, 64), (F.Q2, 64), (F.Q3, 128), (F.Q4SYM, 32),
+                                   (F.Q3, 32), (F.Q2, 256), (F.Q4, 256)])
+def test_xprep_digits_exact(hip, qt, bs):
+    """x -> block-fixed-point X = rint(x * 2^sh) with amax * 2^sh < 2^XB, and
+    the seven balanced base-16 digit words of every multiplier X * 2^shift,
+    reconstructed exactly; block meta f = 2^-sh and sum(X) * f."""
+    torch = torch_cuda()
+    rng = np.random.default_rng(bs + qt)
+    cols = 5 * bs + bs // 2 + 3                  # partial last block
+    x = F.gaussian(rng, cols)
+    x[bs:2 * bs] = 0.0                           # an all-zero block
+    x[2 * bs:3 * bs] *= np.float32(1e-30)        # tiny scale
+    nb = (cols + bs - 1) // bs
+    cw, nc, slots = _slots(qt, bs)
+    dws = (cw * nc * 7) | 1
+    xb = 24 if qt == F.Q3 else 26
+    nbytes = hip.xprep_bytes(qt, bs, cols)
+    buf = torch.zeros(nbytes + 256, dtype=torch.uint8, device="cuda:0")
+    addr = (buf.data_ptr() + 255) & ~255
+    hip.xprep(qt, bs, cols, dev(x), addr, stream=_stream())
+    raw = host(buf)[addr - buf.data_ptr():][:nbytes]
+    dig = raw[:nb * dws * 4].view(np.uint32).reshape(nb, dws)
+    moff = (nb * dws * 4 + 255) & ~255
+    meta = raw[moff:moff + nb * 16].view(np.float64).reshape(nb, 2)
+    xp = np.zeros(nb * bs, np.float64)
+    xp[:cols] = x
+    for b in range(nb):
+        blk = xp[b * bs:(b + 1) * bs]
+        amax = np.abs(blk).max()
+        sh = 0 if amax == 0 else xb - 1 - int(np.floor(np.log2(amax)))
+        sh = min(max(sh, -100), 126)
+        X = np.rint(blk * 2.0 ** sh).astype(np.int64)
+        assert np.abs(X).max() <= 2 ** xb
+        # meta = {2^-sh, 2^-sh * sum X} in fp64, both exact
+        assert meta[b, 0] == 2.0 ** -sh, (b, meta[b, 0], sh)
+        assert meta[b, 1] == float(X.sum()) * 2.0 ** -sh, (b, meta[b, 1])
+        for (w, c, m), (code, shift) in slots.items():
+            words = dig[b, (w * nc + c) * 7:(w * nc + c) * 7 + 7]
+            nib = (words >> np.uint32(4 * m)) & np.uint32(15)
+            sd = np.where(nib >= 8, nib.astype(np.int64) - 16, nib.astype(np.int64))
+            rec = int(sum(int(sd[d]) * 16 ** d for d in range(7)))
+            assert rec == int(X[code]) * 2 ** shift, (b, w, c, m, rec, X[code])
+
+
 def _case(oracle, qt, rows, cols, bs, seed, outlier_frac=0.005):
     rng = np.random.default_rng(seed)
     w = F.gaussian(rng, (rows, cols), 0.02)
@@ -116,6 +179,8 @@ def test_reference_ramp_cases(hip, oracle):
     (F.Q2_OUTLIER, 11008, 4096, 64),     # config 1 (one of gate/up)
     (F.Q3, 4096, 11008, 128),            # config 2 down_proj
     (F.Q3, 11008, 4096, 128),            # config 2 gate/up
+    (F.Q3, 70, 16384, 128),              # digits exceed LDS: K in chunks
+    (F.Q4, 37, 20000, 64),               # K in chunks, partial last block
 ])
 def test_matvec_full_shapes(hip, oracle, qt, rows, cols, bs):
     torch = torch_cuda()
@@ -176,6 +241,66 @@ def test_outlier_edge_cases(hip, oracle):
         out = np.zeros(rows, np.float32)
         kt.matvec_outlier_2bit(payload, x, out, rows, cols, bs)
         assert rel_l2(out, ref) <= REL_L2, n
+
+
+@pytest.mark.parametrize("qt", ALL)
+def test_constant_x_large_blocks(hip, oracle, qt):
+    """Same-sign x fills a 256-code block with |X| near 2^XB: the block sum of
+    X reaches 2^34 and must not wrap."""
+    rows, cols, bs = 33, 1000, 256
+    rng = np.random.default_rng(qt + 40)
+    w = F.gaussian(rng, (rows, cols), 0.02)
+    payload = F.quantize_matrix(w, qt, bs)
+    for x in (np.ones(cols, np.float32), np.full(cols, -3.0e-3, np.float32)):
+        ref = oracle.matvec(qt, payload, x, rows, cols, bs)
+        out = np.full(rows, np.nan, np.float32)
+        _slot(hip, qt)(payload, x, out, rows, cols, bs)
+        assert rel_l2(out, ref) <= REL_L2, (qt, x[0])
+
+
+@pytest.mark.parametrize("qt", [F.Q2_OUTLIER, F.Q4_OUTLIER])
+@pytest.mark.parametrize("rows,cols,bs,frac", [
+    (40, 4096, 64, 0.2),       # ~800 entries a row: many steps of the sparse pass
+    (70, 300, 32, 0.3),        # 16-lane row groups, ~90 entries a row
+    (3, 70000, 64, 0.01),      # columns beyond 16 bits: split entry tables
+])
+def test_outlier_dense_and_wide(hip, oracle, qt, rows, cols, bs, frac):
+    rng = np.random.default_rng(rows * 7 + qt)
+    x = F.gaussian(rng, cols)
+    w = F.gaussian(rng, (rows, cols), 0.02)
+    payload = F.quantize_matrix(w, qt, bs, frac)
+    ref = oracle.matvec(qt, payload, x, rows, cols, bs)
+    out = np.full(rows, np.nan, np.float32)
+    _slot(hip, qt)(payload, x, out, rows, cols, bs)
+    err = rel_l2(out, ref)
+    print(f"outlier qt={qt} {rows}x{cols} frac={frac}: rel_l2={err:.3e}")
+    assert err <= REL_L2
+
+
+def test_outlier_many_short_rows(hip, oracle):
+    """1.6M rows of one block: 128-row tiles, the per-wave result stash caps
+    the tiles a workgroup takes."""
+    rows, cols, bs = 1_600_000, 17, 32
+    rng = np.random.default_rng(99)
+    w = F.gaussian(rng, (rows, cols), 0.02)
+    x = F.gaussian(rng, cols)
+    payload = F.quantize_matrix(w, F.Q2_OUTLIER, bs)
+    del w
+    ref = oracle.matvec(F.Q2_OUTLIER, payload, x, rows, cols, bs)
+    torch = torch_cuda()
+    t = hip.Tensor(payload, F.Q2_OUTLIER, rows, cols, bs)
+    y = torch.full((rows,), float("nan"), device="cuda:0")
+    t.matvec(dev(x), y, stream=_stream())
+    err = rel_l2(host(y), ref)
+    t.free()
+    assert err <= REL_L2, err
+
+
+def _slot(hip, qt):
+    kt = hip.KernelTable()
+    return {F.Q2: kt.matvec_2bit, F.Q3: kt.matvec_3bit, F.Q4: kt.matvec_4bit,
+            F.Q4SYM: kt.matvec_4bit_sym, F.Q2_OUTLIER: kt.matvec_outlier_2bit,
+            F.Q4_OUTLIER: kt.matvec_outlier_4bit}[qt]
 
 
 def test_degenerate_shapes(hip, oracle):
