@@ -50,9 +50,14 @@ constexpr uint32_t DIGIT_BIAS = 0x8888888u;  // 8 * (16^7 - 1) / 15
 constexpr int WAVES = 16;              // waves per GEMV workgroup
 constexpr int MAXT = 4;                // tiles per wave (compile-time bound)
 constexpr int kLdsBudget = 64 * 1024;  // block digits + meta held at once
-constexpr size_t kLdsLimit = 64 * 1024;  // whole dynamic LDS of a GEMV workgroup
+constexpr size_t kLdsLimit = 160 * 1024; // cap on a GEMV workgroup's dynamic LDS (gfx950 LDS)
 
 constexpr int pow2ceil(int v) { return v <= 1 ? 1 : 2 * pow2ceil((v + 1) / 2); }
+
+// 4-byte alignment is all global dwordx4 loads need; x may be any float*
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef f32x4 f32x4_a4 __attribute__((aligned(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 template <int FMT, int BS>
 struct Fmt {
@@ -139,15 +144,15 @@ __device__ __forceinline__ void digit_words(const uint32_t (&U)[8], uint32_t (&o
 // group must call it together (group shuffles).
 // Split in a load half and a compute half so callers can issue the x loads
 // before other vector-memory traffic (loads return in issue order).
-template <int FMT, int BS>
+template <int FMT, int BS, bool V4 = false>
 __device__ __forceinline__ void prep_load(const float* __restrict__ x, int cols, int b, bool live,
                                           int w, float (&xv)[Fmt<FMT, BS>::NC * 8]) {
     using F = Fmt<FMT, BS>;
     constexpr int NS = F::NC * 8;
     const bool lane_live = live && w < F::CW;
-    if constexpr (FMT != QK_FMT_3) {
-        // 2/4-bit: the lane's slots are NS consecutive x values (16-B vector
-        // loads when in range and aligned), re-ordered to slot order
+    if constexpr (FMT != QK_FMT_3 && !V4) {
+        // 2/4-bit, any cols: the lane's slots are NS consecutive x values
+        // (16-B vector loads when in range and aligned), re-ordered to slot order
         constexpr int CPD = NS;                        // codes per code dword
         float xr[CPD];
         const int col0 = b * BS + w * CPD;
@@ -174,6 +179,17 @@ __device__ __forceinline__ void prep_load(const float* __restrict__ x, int cols,
             slot_code<FMT>(0, s / 8, s % 8, code, shift);
             xv[s] = xr[code];
         }
+    } else if constexpr (FMT != QK_FMT_3) {
+        // 2/4-bit, cols >= 4 (V4): only the loads -- the lane's NS
+        // consecutive x values as dwordx4 (4-byte alignment suffices) at
+        // clamped addresses, raw into xv; prep_settle() fixes them up once
+        // they are needed, so nothing here waits for them
+        const int col0 = b * BS + w * NS;
+#pragma unroll
+        for (int k = 0; k < NS / 4; k++) {
+            const f32x4 v = *reinterpret_cast<const f32x4_a4*>(x + min(col0 + 4 * k, cols - 4));
+            xv[4 * k] = v.x; xv[4 * k + 1] = v.y; xv[4 * k + 2] = v.z; xv[4 * k + 3] = v.w;
+        }
     } else {
 #pragma unroll
         for (int s = 0; s < NS; s++) {
@@ -181,17 +197,62 @@ __device__ __forceinline__ void prep_load(const float* __restrict__ x, int cols,
             slot_code<FMT>(w, s / 8, s % 8, code, shift);
             const int col = b * BS + code;
             const float v = x[min(max(col, 0), cols - 1)];
-            xv[s] = (lane_live && col < cols) ? v : 0.0f;
+            if constexpr (V4) xv[s] = v;                      // masked in prep_settle()
+            else xv[s] = (lane_live && col < cols) ? v : 0.0f;
+        }
+    }
+}
+
+// Second half of a V4 prep_load: zero what lies past the last column or
+// belongs to no block, re-index a clamped 2/4-bit chunk (chunk k was read at
+// base = min(col0 + 4k, cols - 4); column c sits at c - base when c < cols)
+// and put 2/4-bit values in slot order.
+template <int FMT, int BS>
+__device__ __forceinline__ void prep_settle(int b, bool live, int w, int cols,
+                                            float (&xv)[Fmt<FMT, BS>::NC * 8]) {
+    using F = Fmt<FMT, BS>;
+    constexpr int NS = F::NC * 8;
+    const bool lane_live = live && w < F::CW;
+    if constexpr (FMT != QK_FMT_3) {
+        const int col0 = b * BS + w * NS;
+        if (!lane_live || col0 + NS > cols) {
+#pragma unroll
+            for (int k = 0; k < NS / 4; k++) {
+                const int base = min(col0 + 4 * k, cols - 4);
+                const float v0 = xv[4 * k], v1 = xv[4 * k + 1], v2 = xv[4 * k + 2], v3 = xv[4 * k + 3];
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int c = col0 + 4 * k + i, at = c - base;
+                    const float v = at == 0 ? v0 : (at == 1 ? v1 : (at == 2 ? v2 : v3));
+                    xv[4 * k + i] = (lane_live && c < cols) ? v : 0.0f;
+                }
+            }
+        }
+        float xr[NS];
+#pragma unroll
+        for (int s = 0; s < NS; s++) xr[s] = xv[s];
+#pragma unroll
+        for (int s = 0; s < NS; s++) {
+            int code, shift;
+            slot_code<FMT>(0, s / 8, s % 8, code, shift);
+            xv[s] = xr[code];
+        }
+    } else {
+#pragma unroll
+        for (int s = 0; s < NS; s++) {
+            int code, shift;
+            slot_code<FMT>(w, s / 8, s % 8, code, shift);
+            xv[s] = (lane_live && b * BS + code < cols) ? xv[s] : 0.0f;
         }
     }
 }
 
 // Block meta: f = 2^-sh and sx = f * sum_k X_k, both exact in fp64.
-// xs (optional): fp32 x copied to LDS for the outlier pass.
+// xs (optional): the lane's x values copied to LDS (columns < cols).
 template <int FMT, int BS>
 __device__ __forceinline__ void prep_finish(const float (&xv)[Fmt<FMT, BS>::NC * 8], int b,
                                             bool live, int w, uint32_t* dst, double2* meta,
-                                            float* xs, int cols) {
+                                            float* xs = nullptr, int cols = 0) {
     using F = Fmt<FMT, BS>;
     constexpr int NS = F::NC * 8;
     const bool lane_live = live && w < F::CW;
@@ -262,7 +323,8 @@ __device__ __forceinline__ void prep_finish(const float (&xv)[Fmt<FMT, BS>::NC *
 
 template <int FMT, int BS>
 __device__ __forceinline__ void prep_block(const float* __restrict__ x, int cols, int b, bool live,
-                                           int w, uint32_t* dst, double2* meta, float* xs) {
+                                           int w, uint32_t* dst, double2* meta,
+                                           float* xs = nullptr) {
     float xv[Fmt<FMT, BS>::NC * 8];
     prep_load<FMT, BS>(x, cols, b, live, w, xv);
     prep_finish<FMT, BS>(xv, b, live, w, dst, meta, xs, cols);
@@ -278,7 +340,7 @@ __global__ __launch_bounds__(256) void xprep_kernel(const float* __restrict__ x,
     const bool live = b < nb;
     const int bb = live ? b : 0;
     prep_block<FMT, BS>(x, cols, b, live, threadIdx.x & (F::LPB - 1), xq + (size_t)bb * F::DWS,
-                        xmeta + bb, nullptr);
+                        xmeta + bb);
 }
 
 // Group sum over `lpg` lanes (power of two) in fp64; the total is valid in
@@ -311,18 +373,35 @@ struct GemvArgs {
     const uint16_t* ov[QK_MAX_GROUP];   // ... and fp16 values
     int rows[QK_MAX_GROUP];
     int tile0[QK_MAX_GROUP + 1];   // prefix sums of tiles (R * 64/lpg rows each)
-    int n, cols, nb, lpg, chunk, tpw;
-    int xs_off;                    // LDS dword offset of fp32 x for the outlier pass, or -1
+    int nent[QK_MAX_GROUP];             // outlier entries kept per matrix
+    // main kernel: matrix blockIdx.y, all its fields in one record (read at
+    // an address known when the wave starts, in one batch of scalar loads)
+    struct Mat {
+        const uint8_t* w;
+        float* y;
+        const uint32_t* rp;                 // null: no outliers
+        const uint32_t* oe;                 // packed entries
+        int rows, nent, tiles, pad;
+    } mat[QK_MAX_GROUP];
+    int n, cols, nb, lpg, lpg_log2, chunk, tpw;
+    int xs_off;                    // LDS dword offset of fp32 x (main kernel)
     int st_off, st_wave;           // LDS dword offset / doubles per wave of the result stash
     const uint32_t* xq;            // prepared digits (stride DWS), or null: prepare here
     const double2* xmeta;
     const float* x;
 };
 
-// fp16 value and column of outlier entry e of matrix m.
+
+// Main-kernel limits: x as XV (1 or kXvMax) float4 a thread, prepared digits
+// as at most DV dwordx4 a thread, one block meta a thread.
+constexpr int kXvMax = 4;              // cols <= 4 * kXvMax * 1024
+constexpr int DV = 4;                  // nb * DWS <= 4 * DV * 1024 dwords
+constexpr int kMainMaxNb = WAVES * 64;
+
+// fp16 value and column of outlier entry e of matrix m (packed or split table).
 __device__ __forceinline__ void entry_at(const GemvArgs& a, int m, uint32_t e, uint32_t& col,
                                          uint32_t& val) {
-    if (a.oe[m]) {
+    if (a.oe[m] != nullptr) {
         const uint32_t u = a.oe[m][e];
         col = u & 0xFFFFu;
         val = u >> 16;
@@ -405,17 +484,14 @@ __device__ __forceinline__ void compute_block(const uint32_t (&wv)[R][1 + Fmt<FM
 
 // Stage block digits + meta for blocks [c0, c1) in LDS: prepare them from x
 // here, or copy the ones a stand-alone x-prep launch left in global memory.
-// xs (whole-row staging only, c0 == 0) also receives fp32 x.
 template <int FMT, int BS>
 __device__ __forceinline__ void stage_x(const GemvArgs& a, int c0, int c1, uint32_t* dig,
-                                        double2* meta, float* xs) {
+                                        double2* meta) {
     using F = Fmt<FMT, BS>;
     if (a.xq) {
         for (int i = threadIdx.x; i < (c1 - c0) * F::DWS; i += WAVES * 64)
             dig[i] = a.xq[(size_t)c0 * F::DWS + i];
         for (int i = threadIdx.x; i < c1 - c0; i += WAVES * 64) meta[i] = a.xmeta[c0 + i];
-        if (xs)
-            for (int i = threadIdx.x; i < a.cols; i += WAVES * 64) xs[i] = a.x[i];
     } else {
         const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
         for (int base = c0; base < c1; base += WAVES * 64 / F::LPB) {
@@ -424,7 +500,7 @@ __device__ __forceinline__ void stage_x(const GemvArgs& a, int c0, int c1, uint3
             const bool live = b < c1;
             const int bb = live ? b : c0;
             prep_block<FMT, BS>(a.x, a.cols, b, live, threadIdx.x & (F::LPB - 1),
-                                dig + (bb - c0) * F::DWS, meta + (bb - c0), xs);
+                                dig + (bb - c0) * F::DWS, meta + (bb - c0));
         }
     }
 }
@@ -467,202 +543,324 @@ __device__ __forceinline__ void flush_tile(const GemvArgs& a, int m, int row0, i
     }
 }
 
-// Main path (all block digits fit in LDS at once).  A wave's work is the
-// list of (tile, block) items, the same count for every lane; weights are
-// loaded D items ahead into a ring of register sets.  Vector-memory loads
-// return in issue order, so the order is: x loads of the prep, the outlier
-// row pointers of the wave's rows, the first D weight items, the first
-// outlier entry per lane and row, the prep arithmetic, the item loop, and
-// last the remaining outlier entries.  Finished tiles of a matrix with
-// outliers park their fp64 row sums in LDS until the sparse terms are in.
-template <int FMT, int BS, int R, int D, bool OUT>
+// Main path: block digits, block meta and fp32 x of a whole row fit in LDS.
+// A wave's work is the list of (tile, block) items, the same count for every
+// lane; weights are loaded D items ahead into a ring of register sets.
+//
+// Vector-memory loads return in issue order and s_waitcnt counts them, and
+// the compiler can only place tight waits across a straight-line load
+// sequence: a load or store issued on some paths but not on others, between a
+// load and its use, makes the wait for that load conservative (in practice,
+// wait for everything in flight).  So every load up to the end of the item
+// loop is issued unconditionally -- past a wave's last item at its last
+// tile's row starts, for absent outlier tables at the group's own row -- and
+// no global store happens before the end: finished rows park fp64 sums in
+// LDS.  The setup avoids chains of dependent scalar loads (kernel-argument
+// arrays are read with static indices) and integer divisions, since every
+// such step waits behind the weight stream once it is in flight.
+// Issue order: x (coalesced), prepared digits, outlier row pointers, the first
+// D weight items, the first outlier entry per lane and row; then the prep
+// arithmetic, the item loop (the first entries join the row sums before the
+// one reduction a row), the remaining outlier entries and the stores.
+template <int FMT, int BS, int R, int D, bool OUT, bool PREP>
 __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
+    constexpr int XV = kXvMax;
     using F = Fmt<FMT, BS>;
+    using WV = uint32_t[R][1 + F::CW];
+    constexpr int NT = WAVES * 64;
     extern __shared__ __align__(16) uint32_t lds[];
-    double2* meta = reinterpret_cast<double2*>(lds);
-    uint32_t* dig = lds + 4 * a.chunk;
-    float* xs = a.xs_off >= 0 ? reinterpret_cast<float*>(lds + a.xs_off) : nullptr;
+    double2* meta = reinterpret_cast<double2*>(lds);          // nb x 16 B
+    uint32_t* dig = lds + 4 * a.nb;                           // nb x DWS dwords (+ pad to 4)
+    float* xs = reinterpret_cast<float*>(lds + a.xs_off);     // nb*BS floats, zero past cols
     // wave index made provably uniform: tile -> matrix lookups then stay in
     // scalar registers (kernel arguments via s_load, no vector-memory waits)
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int lpg = a.lpg, grp = lane / lpg, lig = lane & (lpg - 1);
-    const int rows_per_tile = R * (64 / lpg);
-    const int tw = blockIdx.x * a.tpw + wave;                 // this wave's first tile
-    const int t_end = min(a.tile0[a.n], blockIdx.x * a.tpw + a.tpw);
+    const int lgl = a.lpg_log2, lpg = 1 << lgl;
+    const int grp = lane >> lgl, lig = lane & (lpg - 1);
+    const int rpt = R << (6 - lgl);                           // rows per tile
+    // the workgroup's matrix: blockIdx.y (a workgroup never spans two)
+    const GemvArgs::Mat& M = a.mat[blockIdx.y];
+    const uint8_t* const W = M.w;
+    float* const Y = M.y;
+    const uint32_t* const RP = M.rp;                          // null: no outliers
+    const uint32_t* const OE = M.oe;
+    const int rows = M.rows;
+    const uint32_t last = (uint32_t)max(M.nent - 1, 0);
+    const int wgm = (int)blockIdx.x;                          // workgroup within the matrix
+    const int mtiles = M.tiles;
+    const int tw = wgm * a.tpw + wave;                        // this wave's first tile
+    const int t_end = min(mtiles, wgm * a.tpw + a.tpw);
     const int nt = tw < t_end ? min(MAXT, (t_end - tw + WAVES - 1) / WAVES) : 0;
-    const int ipt = (a.nb + lpg - 1) / lpg;                   // items per tile
+    const int ipt = (a.nb + lpg - 1) >> lgl;                  // items per tile
     const int ni = nt * ipt;
+    const int tl = nt > 0 ? tw : 0;                           // tile the loads are anchored on
+    const int ntl = nt > 0 ? nt : 1;
     const uint32_t row_bytes = (uint32_t)a.nb * F::BB;
 
-    auto issue = [&](int ii, uint32_t (&wv)[R][1 + F::CW]) {
-        int m, row0;
-        tile_of(a, tw + WAVES * (ii / ipt), rows_per_tile, grp, R, m, row0);
-        const int b = min(lig + (ii % ipt) * lpg, a.nb - 1);
-        uint32_t roff[R];
-#pragma unroll
-        for (int r = 0; r < R; r++) roff[r] = (uint32_t)min(row0 + r, a.rows[m] - 1) * row_bytes;
-        load_block<FMT, BS, R>(a.w[m], roff, b, wv);
+    // first row of the lane's group in tile j (clamped to the wave's last)
+    auto row_of = [&](int j) __attribute__((always_inline)) {
+        return (tl + WAVES * min(j, ntl - 1)) * rpt + grp * R;
+    };
+    // first dwords of the group's first row in tile j: what a load reads
+    // where an outlier table is absent
+    auto own_of = [&](int j) __attribute__((always_inline)) {
+        return reinterpret_cast<const uint32_t*>(W + (size_t)min(row_of(j), rows - 1) * row_bytes);
     };
 
-    // x values of this thread's first prep block group, requested first;
-    // waves past the last block skip the prep
-    constexpr int PASS = WAVES * 64 / F::LPB;                 // blocks per prep pass
-    const int pw = threadIdx.x & (F::LPB - 1);
-    const int pb = threadIdx.x / F::LPB;
-    const bool prep_wave = !a.xq && wave * (64 / F::LPB) < a.nb;
-    float xv0[F::NC * 8];
-    if (prep_wave) prep_load<FMT, BS>(a.x, a.cols, pb, pb < a.nb, pw, xv0);
+    // issue cursor: tile ij, step iq; row offsets of that tile
+    int ij = 0, iq = 0;
+    uint32_t ioff[R];
+    auto at_tile = [&](int j) __attribute__((always_inline)) {
+        const int r0 = row_of(j);
+#pragma unroll
+        for (int r = 0; r < R; r++) ioff[r] = (uint32_t)min(r0 + r, rows - 1) * row_bytes;
+    };
+    at_tile(0);
+    // The matrix record is materialised here, with the other arguments, in
+    // one scalar round trip; left to the scheduler its loads sink behind the
+    // x loads and cost a second round trip before the first weight load.
+    asm volatile("" ::"s"(W), "s"(RP), "s"(OE), "s"(last), "s"(a.x), "s"(a.cols), "s"(a.xq));
+    __builtin_amdgcn_sched_barrier(0);
+    // next item's weights; past the last item, the last tile's row starts
+    auto issue = [&](WV& wv) __attribute__((always_inline)) {
+        const int b = ij < nt ? min(lig + (iq << lgl), a.nb - 1) : 0;
+        load_block<FMT, BS, R>(W, ioff, b, wv);
+        if (++iq == ipt) {
+            iq = 0;
+            ++ij;
+            at_tile(min(ij, ntl - 1));
+        }
+    };
 
-    // CSR bounds of this lane's rows: row r of tile j owns [rpv[j][r], rpv[j][r+1])
+    // 1. Preparing here: the prep waves load the x of their first pass of
+    //    blocks (before any weights, so it returns first); the other waves
+    //    start with their weights.  Prepared digits: digits and meta, and for
+    //    the outliers x, as whole float4s (the host guarantees cols >= 4) plus
+    //    the cols % 4 tail (threads 0-2).  Loads past the end re-read the
+    //    thread's own first element (never one address for the whole chip:
+    //    that serialises on one L2 channel).
+    constexpr int PASS = NT / F::LPB;                         // blocks per prep pass
+    const int t_id = (int)threadIdx.x;
+    const int pw = t_id & (F::LPB - 1), pb = t_id / F::LPB;
+    const bool prep_wave = !PREP && wave * (64 / F::LPB) < a.nb;
+    float xv0[F::NC * 8];
+    if (prep_wave) prep_load<FMT, BS, true>(a.x, a.cols, pb, pb < a.nb, pw, xv0);
+    constexpr bool XS = PREP && OUT;
+    const int nf = a.cols >> 2;
+    f32x4 xr[XV];
+    float xt = 0.0f;
+    if constexpr (XS) {
+#pragma unroll
+        for (int i = 0; i < XV; i++) {
+            const int f = t_id + i * NT;
+            xr[i] = *reinterpret_cast<const f32x4_a4*>(a.x + 4 * (f < nf ? f : min(t_id, nf - 1)));
+        }
+        xt = a.x[t_id < 3 ? min(4 * nf + t_id, a.cols - 1) : min(t_id, a.cols - 1)];
+    }
+    const int nq = (a.nb * F::DWS + 3) >> 2;                  // dwordx4 of prepared digits
+    u32x4 qr[DV];
+    double2 mr;
+    if constexpr (PREP) {
+#pragma unroll
+        for (int i = 0; i < DV; i++) {
+            const int q = t_id + i * NT;
+            qr[i] = reinterpret_cast<const u32x4*>(a.xq)[q < nq ? q : min(t_id, nq - 1)];
+        }
+        mr = a.xmeta[t_id < a.nb ? t_id : min(t_id & 63, a.nb - 1)];
+    }
+
+    // 2. CSR bounds of this lane's rows: row r of tile j owns
+    //    [rpv[j][r], rpv[j][r+1]) (matrices without outliers read their own row)
     uint32_t rpv[MAXT][R + 1];
+    if constexpr (OUT) {
+        const bool has = RP != nullptr;
 #pragma unroll
-    for (int j = 0; j < MAXT; j++) {
+        for (int j = 0; j < MAXT; j++) {
+            const int row0 = row_of(j);
+            const uint32_t* rp = has ? RP : own_of(j);
 #pragma unroll
-        for (int r = 0; r <= R; r++) rpv[j][r] = 0;
-        if (OUT && j < nt) {
-            int m, row0;
-            tile_of(a, tw + WAVES * j, rows_per_tile, grp, R, m, row0);
-            if (a.rp[m]) {
-#pragma unroll
-                for (int r = 0; r <= R; r++) rpv[j][r] = a.rp[m][min(row0 + r, a.rows[m])];
-            }
+            for (int r = 0; r <= R; r++)
+                rpv[j][r] = rp[has ? min(row0 + r, rows) : min(r, (int)F::BB / 4 - 1)];
         }
     }
 
+    // 3. the first D weight items
     uint32_t wv[D][R][1 + F::CW];
 #pragma unroll
-    for (int k = 0; k < D; k++)
-        if (k < ni) issue(k, wv[k]);
+    for (int k = 0; k < D; k++) issue(wv[k]);
 
-    // first entry of every row for this lane (packed tables)
+    // 4. first outlier entry of every row for this lane (packed tables)
     uint32_t e0[MAXT][R];
+    if constexpr (OUT) {
+        const bool pk = OE != nullptr;
 #pragma unroll
-    for (int j = 0; j < MAXT; j++) {
+        for (int j = 0; j < MAXT; j++) {
+            const uint32_t* oe = pk ? OE : own_of(j);
 #pragma unroll
-        for (int r = 0; r < R; r++) e0[j][r] = 0;
-        if (OUT && j < nt) {
-            int m, row0;
-            tile_of(a, tw + WAVES * j, rows_per_tile, grp, R, m, row0);
-            if (a.oe[m]) {
-#pragma unroll
-                for (int r = 0; r < R; r++)
-                    if (rpv[j][r] + lig < rpv[j][r + 1]) e0[j][r] = a.oe[m][rpv[j][r] + lig];
-            }
+            for (int r = 0; r < R; r++) e0[j][r] = oe[pk ? min(rpv[j][r] + lig, last) : 0u];
         }
     }
 
-    if (a.xq) {
-        stage_x<FMT, BS>(a, 0, a.nb, dig, meta, xs);
+    // 5. LDS: prepared digits, meta and x as loaded; or the digits and meta
+    //    of every block prepared here, with x copied alongside for the
+    //    outliers.  Passes after the first load their x now, behind the
+    //    weights (only rows wider than one pass get there).
+    if constexpr (PREP) {
+        if constexpr (XS) {
+#pragma unroll
+            for (int i = 0; i < XV; i++) {
+                const int f = t_id + i * NT;
+                if (f < nf) *reinterpret_cast<f32x4*>(xs + 4 * f) = xr[i];
+            }
+            if (t_id < a.cols - 4 * nf) xs[4 * nf + t_id] = xt;   // cols % 4 tail
+        }
+#pragma unroll
+        for (int i = 0; i < DV; i++) {
+            const int q = t_id + i * NT;
+            if (q < nq) reinterpret_cast<u32x4*>(dig)[q] = qr[i];
+        }
+        if (t_id < a.nb) meta[t_id] = mr;
     } else {
+        float* xcopy = OUT ? xs : nullptr;
         if (prep_wave) {
             const int b0 = pb < a.nb ? pb : 0;
-            prep_finish<FMT, BS>(xv0, pb, pb < a.nb, pw, dig + b0 * F::DWS, meta + b0, xs, a.cols);
+            prep_settle<FMT, BS>(pb, pb < a.nb, pw, a.cols, xv0);
+            prep_finish<FMT, BS>(xv0, pb, pb < a.nb, pw, dig + b0 * F::DWS, meta + b0, xcopy, a.cols);
         }
         for (int base = PASS; base < a.nb; base += PASS) {
-            if (base + wave * (64 / F::LPB) >= a.nb) break;
+            if (base + wave * (64 / F::LPB) >= a.nb) break;     // whole wave past the end
             const int b = base + pb;
             const bool live = b < a.nb;
             const int bb = live ? b : 0;
-            prep_block<FMT, BS>(a.x, a.cols, b, live, pw, dig + bb * F::DWS, meta + bb, xs);
+            prep_block<FMT, BS>(a.x, a.cols, b, live, pw, dig + bb * F::DWS, meta + bb, xcopy);
         }
     }
     __syncthreads();
 
+    // 7. item loop.  At a tile's end the first outlier entry of each row joins
+    //    the lane sums (src/quant.c:481-494, fp64 value * x[col]), the row is
+    //    reduced once and its sum parked in the stash.
     double* stash = reinterpret_cast<double*>(lds + a.st_off) + wave * a.st_wave;
     double rs[R];
 #pragma unroll
     for (int r = 0; r < R; r++) rs[r] = 0.0;
-    for (int i0 = 0; i0 < ni; i0 += D) {
+    int cj = 0, cq = 0;                                       // compute cursor
+    // first outlier entry of each row of tile J (static J: no indexed arrays)
+    auto first_entries = [&](auto jc) __attribute__((always_inline)) {
+        constexpr int J = decltype(jc)::value;
+        const bool pk = OE != nullptr;
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const uint32_t e = e0[J][r];
+            const bool ok = pk && rpv[J][r] + lig < rpv[J][r + 1];
+            const double p = (double)qsf::f16_bits(e >> 16) * (double)xs[ok ? e & 0xFFFFu : 0u];
+            rs[r] += ok ? p : 0.0;
+        }
+    };
+    auto tile_end = [&]() __attribute__((always_inline)) {
+        if constexpr (OUT) {
+            [&]<int... I>(std::integer_sequence<int, I...>) {
+                ((cj == I ? first_entries(std::integral_constant<int, I>{}) : void()), ...);
+            }(std::make_integer_sequence<int, MAXT>{});
+        }
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const double v = group_reduce(rs[r], lpg);
+            rs[r] = 0.0;
+            if (lig == lpg - 1) stash[cj * rpt + grp * R + r] = v;
+        }
+    };
+    auto compute = [&](const WV& w) __attribute__((always_inline)) {
+        const int b = lig + (cq << lgl);
+        if (b < a.nb) compute_block<FMT, BS, R>(w, dig + b * F::DWS, meta[b], rs);
+        if (++cq == ipt) {
+            tile_end();
+            cq = 0;
+            ++cj;
+        }
+    };
+    // Blocks of D items.  Every block but the last refills each slot as it
+    // frees it (items past the end: issue()'s broadcast loads, back long
+    // before the end); the last block issues nothing, since a wave cannot
+    // retire before its loads return.
+    const int nblk = (ni + D - 1) / D;
+    for (int q = 0; q + 1 < nblk; q++) {
 #pragma unroll
         for (int k = 0; k < D; k++) {
-            const int ii = i0 + k;
-            if (ii < ni) {
-                const int b = lig + (ii % ipt) * lpg;
-                if (b < a.nb) compute_block<FMT, BS, R>(wv[k], dig + b * F::DWS, meta[b], rs);
-                if (ii + D < ni) issue(ii + D, wv[k]);
-                if (ii % ipt == ipt - 1) {
-                    const int j = ii / ipt;
-                    int m, row0;
-                    tile_of(a, tw + WAVES * j, rows_per_tile, grp, R, m, row0);
-#pragma unroll
-                    for (int r = 0; r < R; r++) {
-                        const double v = group_reduce(rs[r], lpg);
-                        rs[r] = 0.0;
-                        if (lig == lpg - 1) {
-                            if (OUT && a.rp[m]) stash[j * rows_per_tile + grp * R + r] = v;
-                            else if (row0 + r < a.rows[m]) a.y[m][row0 + r] = (float)v;
-                        }
-                    }
-                }
-            }
+            compute(wv[k]);
+            issue(wv[k]);
         }
+    }
+    if (nblk > 0) {
+#pragma unroll
+        for (int k = 0; k < D; k++)
+            if ((nblk - 1) * D + k < ni) compute(wv[k]);
     }
 
-    if constexpr (!OUT) return;
-    // sparse pass (src/quant.c:481-494): fp64 sums of fp16 value * x[col]
-    bool any_out = false;
-    double os[MAXT][R];
-#pragma unroll
-    for (int j = 0; j < MAXT; j++) {
-#pragma unroll
-        for (int r = 0; r < R; r++) os[j][r] = 0.0;
-        if (j < nt) {
-            int m, row0;
-            tile_of(a, tw + WAVES * j, rows_per_tile, grp, R, m, row0);
-            any_out |= a.rp[m] != nullptr;
-            if (a.oe[m]) {
-#pragma unroll
-                for (int r = 0; r < R; r++) {
-                    if (rpv[j][r] + lig < rpv[j][r + 1]) {
-                        const uint32_t col = e0[j][r] & 0xFFFFu;
-                        const float xc = xs ? xs[col] : a.x[col];
-                        os[j][r] = (double)qsf::f16_bits(e0[j][r] >> 16) * (double)xc;
-                    }
-                }
-            }
-        }
-    }
-    if (!any_out) return;
-    // remaining entries: one per lane and row each step, loads batched over rows
-    for (int k = 0;; k++) {
-        bool ok[MAXT][R];
-        bool more = false;
-        uint32_t ec[MAXT][R], ev[MAXT][R];
-#pragma unroll
-        for (int j = 0; j < MAXT; j++) {
-            int m = 0, row0 = 0;
-            if (j < nt) tile_of(a, tw + WAVES * j, rows_per_tile, grp, R, m, row0);
-#pragma unroll
-            for (int r = 0; r < R; r++) {
-                const uint32_t e = rpv[j][r] + lig + (uint32_t)(k + (a.oe[m] ? 1 : 0)) * lpg;
-                ok[j][r] = j < nt && a.rp[m] && e < rpv[j][r + 1];
-                more |= ok[j][r];
-                if (ok[j][r]) entry_at(a, m, e, ec[j][r], ev[j][r]);
-            }
-        }
-        if (!__any(more)) break;
+    // 8. remaining outlier entries, one per lane and row each step; every
+    //    slot loads (clamped index, own row where absent)
+    if constexpr (OUT) {
+        double orem[MAXT][R];
 #pragma unroll
         for (int j = 0; j < MAXT; j++)
 #pragma unroll
-            for (int r = 0; r < R; r++)
-                if (ok[j][r]) {
-                    const float xc = xs ? xs[ec[j][r]] : a.x[ec[j][r]];
-                    os[j][r] = fma((double)qsf::f16_bits(ev[j][r]), (double)xc, os[j][r]);
+            for (int r = 0; r < R; r++) orem[j][r] = 0.0;
+        bool any_rem = false;
+        for (uint32_t k = 1;; k++) {
+            bool ok[MAXT][R];
+            bool more = false;
+#pragma unroll
+            for (int j = 0; j < MAXT; j++) {
+                const bool live = j < nt && OE != nullptr;
+#pragma unroll
+                for (int r = 0; r < R; r++) {
+                    ok[j][r] = live && rpv[j][r] + lig + (k << lgl) < rpv[j][r + 1];
+                    more |= ok[j][r];
                 }
+            }
+            if (!__any(more)) break;
+            any_rem = true;
+            uint32_t eu[MAXT][R];
+            const bool pk = OE != nullptr;
+#pragma unroll
+            for (int j = 0; j < MAXT; j++) {
+                const uint32_t* oe = pk ? OE : own_of(j);
+#pragma unroll
+                for (int r = 0; r < R; r++)
+                    eu[j][r] = oe[pk ? min(rpv[j][r] + lig + (k << lgl), last) : 0u];
+            }
+#pragma unroll
+            for (int j = 0; j < MAXT; j++)
+#pragma unroll
+                for (int r = 0; r < R; r++) {
+                    const uint32_t col = ok[j][r] ? eu[j][r] & 0xFFFFu : 0u;
+                    const double p = (double)qsf::f16_bits(eu[j][r] >> 16) * (double)xs[col];
+                    orem[j][r] += ok[j][r] ? p : 0.0;
+                }
+        }
+        if (any_rem) {
+#pragma unroll
+            for (int j = 0; j < MAXT; j++)
+                if (j < nt) {
+#pragma unroll
+                    for (int r = 0; r < R; r++) {
+                        const double v = group_reduce(orem[j][r], lpg);
+                        if (lig == lpg - 1) stash[j * rpt + grp * R + r] += v;
+                    }
+                }
+        }
     }
+
+    // 9. stores
 #pragma unroll
     for (int j = 0; j < MAXT; j++) {
         if (j < nt) {
-            int m, row0;
-            tile_of(a, tw + WAVES * j, rows_per_tile, grp, R, m, row0);
-            if (a.rp[m]) {
+            const int row0 = row_of(j);
 #pragma unroll
-                for (int r = 0; r < R; r++) {
-                    const double v = group_reduce(os[j][r], lpg);
-                    if (lig == lpg - 1 && row0 + r < a.rows[m])
-                        a.y[m][row0 + r] = (float)(stash[j * rows_per_tile + grp * R + r] + v);
-                }
+            for (int r = 0; r < R; r++) {
+                const int row = row0 + r;
+                if (lig == lpg - 1 && row < rows) Y[row] = (float)stash[j * rpt + grp * R + r];
             }
         }
     }
@@ -695,7 +893,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_chunked_kernel(GemvArgs a) {
     for (int c0 = 0; c0 < a.nb; c0 += a.chunk) {
         const int c1 = min(a.nb, c0 + a.chunk);
         __syncthreads();
-        stage_x<FMT, BS>(a, c0, c1, dig, meta, nullptr);
+        stage_x<FMT, BS>(a, c0, c1, dig, meta);
         __syncthreads();
 #pragma unroll
         for (int j = 0; j < MAXT; j++) {
@@ -750,7 +948,30 @@ size_t xprep_bytes_t(int cols) {
 
 // Dynamic LDS a GEMV workgroup may use in total (digits, meta, staged x, stash).
 size_t lds_limit() {
-    return kLdsLimit;
+    static size_t v = 0;
+    if (!v) {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) == hipSuccess &&
+            n > 0)
+            v = (size_t)n;
+        else
+            v = 64 * 1024;
+        v = v < kLdsLimit ? v : kLdsLimit;
+    }
+    return v;
+}
+
+// Launch a main-path instantiation, allowing it the device's full LDS once.
+template <auto K>
+void launch_main(dim3 g, dim3 b, size_t lds, hipStream_t s, const GemvArgs& a) {
+    static bool allowed = false;
+    if (!allowed) {
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(K),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_limit());
+        allowed = true;
+    }
+    hipLaunchKernelGGL(K, g, b, lds, s, a);
 }
 
 // rows per tile: 2 for 64-code-or-smaller blocks, else 1 (register budget);
@@ -759,11 +980,14 @@ template <int FMT, int BS>
 constexpr int tile_rows() { return Fmt<FMT, BS>::CW <= 8 ? 2 : 1; }
 // (one item for 3-bit 256-code blocks: 25 dwords a row plus two accumulator
 // sets leave no room for a second set within 128 VGPRs)
-template <int FMT, int BS>
+// (outlier kernels keep ~20 more registers of CSR state: 36)
+template <int FMT, int BS, bool OUT>
 constexpr int prefetch_depth() {
     constexpr int per = tile_rows<FMT, BS>() * (1 + Fmt<FMT, BS>::CW);
+    constexpr int budget = OUT ? 36 : 48;
     if (FMT == QK_FMT_3 && Fmt<FMT, BS>::CW >= 24) return 1;
-    return 48 / per < 2 ? 2 : (48 / per > 4 ? 4 : 48 / per);
+    if (OUT && per > 24) return 1;
+    return budget / per < 2 ? 2 : (budget / per > 4 ? 4 : budget / per);
 }
 
 template <int FMT, int BS>
@@ -784,13 +1008,17 @@ int launch_t(const qsf_hip_tensor* const* t, int n, int cols, const float* d_x,
     a.n = n;
     a.cols = cols;
     a.nb = nb;
-    int lpg = 1;
-    while (lpg < nb && lpg < 64) lpg <<= 1;
+    int lpg = 1, lgl = 0;
+    while (lpg < nb && lpg < 64) {
+        lpg <<= 1;
+        lgl++;
+    }
     a.lpg = lpg;
+    a.lpg_log2 = lgl;
     const int per_block = F::DWS * 4 + (int)sizeof(double2);
     a.chunk = nb < kLdsBudget / per_block ? nb : kLdsBudget / per_block;
     const int rows_per_tile = R * (64 / lpg);
-    bool any_out = false;
+    bool any_out = false, split = false;
     a.tile0[0] = 0;
     for (int i = 0; i < n; i++) {
         if ((size_t)t[i]->rows * nb * F::BB > 0xFFFFFFF0ull) return -2;   // 32-bit offsets
@@ -800,9 +1028,13 @@ int launch_t(const qsf_hip_tensor* const* t, int n, int cols, const float* d_x,
         a.oe[i] = t[i]->d_oent;
         a.oc[i] = t[i]->d_ocol;
         a.ov[i] = t[i]->d_oval;
+        a.nent[i] = (int)t[i]->n_csr;
         a.rows[i] = t[i]->rows;
-        a.tile0[i + 1] = a.tile0[i] + (t[i]->rows + rows_per_tile - 1) / rows_per_tile;
+        a.mat[i] = {t[i]->d_blocks, d_y[i], t[i]->d_row_ptr, t[i]->d_oent, t[i]->rows,
+                    (int)t[i]->n_csr, (t[i]->rows + rows_per_tile - 1) / rows_per_tile, 0};
+        a.tile0[i + 1] = a.tile0[i] + a.mat[i].tiles;
         any_out |= t[i]->d_row_ptr != nullptr;
+        split |= t[i]->d_row_ptr != nullptr && t[i]->d_oent == nullptr;
     }
     const int tiles = a.tile0[n];
     if (tiles == 0) return 0;
@@ -816,45 +1048,54 @@ int launch_t(const qsf_hip_tensor* const* t, int n, int cols, const float* d_x,
     a.xmeta = xmeta;
     a.x = d_x;
 
-    // LDS: [meta: chunk x 16 B][digits: chunk x DWS dwords][stash][x]
-    size_t lds = (size_t)a.chunk * per_block;
-    bool whole = a.chunk >= nb;
-    a.xs_off = -1;
+    // Main kernel LDS: [meta: nb x 16 B][digits: nb x DWS dwords, padded to
+    // 4][x: nb*BS floats][fp64 stash: a wave's tiles x rows_per_tile].  When
+    // the stash would not fit, fewer tiles a workgroup.
+    const size_t dig_dw = ((size_t)nb * F::DWS + 3) & ~(size_t)3;
+    const size_t main_fixed = (size_t)nb * 16 + dig_dw * 4 + (size_t)nb * BS * 4;
+    const size_t per_tile = (size_t)WAVES * rows_per_tile * sizeof(double);
+    // (the main kernel reads packed outlier tables only)
+    const bool whole = !split && cols >= 4 && cols <= 4 * kXvMax * WAVES * 64 && nb <= kMainMaxNb &&
+                       (!prepared || dig_dw <= (size_t)4 * DV * WAVES * 64) &&
+                       main_fixed + per_tile <= lds_limit();
+    size_t lds = (size_t)a.chunk * per_block;                 // chunked kernel
+    a.xs_off = 0;
     a.st_off = 0;
     a.st_wave = 0;
-    if (whole && any_out) {
-        // fp64 stash of the rows of each wave's finished tiles; fewer tiles a
-        // workgroup when it would not fit
-        const size_t per_tile = (size_t)WAVES * rows_per_tile * sizeof(double);
-        const size_t st_at = (lds + 7) & ~(size_t)7;
-        const size_t room = lds_limit() > st_at ? (lds_limit() - st_at) / per_tile : 0;
-        if (room == 0) {
-            whole = false;                     // the chunked kernel needs no stash
-        } else {
-            if ((size_t)a.tpw > WAVES * room) a.tpw = (int)(WAVES * room);
-            const int ntc = (a.tpw + WAVES - 1) / WAVES;
-            a.st_off = (int)(st_at / 4);
-            a.st_wave = ntc * rows_per_tile;
-            lds = st_at + (size_t)ntc * per_tile;
-            if (lds + (size_t)cols * 4 <= lds_limit()) {
-                a.xs_off = (int)(lds / 4);
-                lds += (size_t)cols * 4;
-            }
+    if (whole) {
+        const size_t room = (lds_limit() - main_fixed) / per_tile;
+        if ((size_t)a.tpw > WAVES * room) a.tpw = (int)(WAVES * room);
+        const int ntc = (a.tpw + WAVES - 1) / WAVES;
+        a.xs_off = (int)((size_t)nb * 4 + dig_dw);
+        a.st_off = a.xs_off + nb * BS;
+        a.st_wave = ntc * rows_per_tile;
+        lds = main_fixed + (size_t)ntc * per_tile;
+        // main kernel: workgroups (x, matrix y); a matrix with fewer tiles
+        // than the largest leaves its last workgroups without tiles
+        grid = 0;
+        for (int i = 0; i < n; i++) {
+            const int g = (a.mat[i].tiles + a.tpw - 1) / a.tpw;
+            grid = g > grid ? g : grid;
         }
+    } else {
+        grid = (tiles + a.tpw - 1) / a.tpw;
     }
-    grid = (tiles + a.tpw - 1) / a.tpw;
-    constexpr int D = prefetch_depth<FMT, BS>();
     // only the 2-bit and 4-bit asymmetric formats have outlier variants
     constexpr bool kHasOut = FMT == QK_FMT_2 || FMT == QK_FMT_4;
+    constexpr int D = prefetch_depth<FMT, BS, false>();
+    constexpr int DO = prefetch_depth<FMT, BS, kHasOut>();
     if (any_out && !kHasOut) return -2;
-    if (whole && kHasOut && any_out)
-        hipLaunchKernelGGL((gemv_kernel<FMT, BS, R, D, kHasOut>), dim3(grid), dim3(WAVES * 64), lds,
-                           s, a);
-    else if (whole)
-        hipLaunchKernelGGL((gemv_kernel<FMT, BS, R, D, false>), dim3(grid), dim3(WAVES * 64), lds,
-                           s, a);
+    const dim3 g(grid, whole ? n : 1), b(WAVES * 64);
+    if (!whole)
+        hipLaunchKernelGGL((gemv_chunked_kernel<FMT, BS, R>), g, b, lds, s, a);
+    else if (prepared && any_out)
+        launch_main<gemv_kernel<FMT, BS, R, DO, kHasOut, true>>(g, b, lds, s, a);
+    else if (prepared)
+        launch_main<gemv_kernel<FMT, BS, R, D, false, true>>(g, b, lds, s, a);
+    else if (any_out)
+        launch_main<gemv_kernel<FMT, BS, R, DO, kHasOut, false>>(g, b, lds, s, a);
     else
-        hipLaunchKernelGGL((gemv_chunked_kernel<FMT, BS, R>), dim3(grid), dim3(WAVES * 64), lds, s, a);
+        launch_main<gemv_kernel<FMT, BS, R, D, false, false>>(g, b, lds, s, a);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
