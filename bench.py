@@ -13,10 +13,14 @@ resident in HBM before the timed region.
 
 Prints one JSON line.  `value` is algorithmic bytes per step (on-disk QSF
 payload + x read once + y written, per matrix) / wall time per step, over K
-steps between two synchronisations.  `roofline.achieved` is the same bytes of
-the GEMV launch / its average duration from HIP events recorded around it on
-the launch stream.  `cpu_baseline` times QStream's own AVX2 kernel
-(oracle/_ref, reference release flags, 1 thread) on a bounded sample.
+steps replayed from one HIP graph between two synchronisations.
+`roofline.achieved` is the same bytes / the GEMV kernel's mean duration, from
+HIP event pairs recorded at the kernel's own start and end on its launch
+stream (hipExtLaunchKernel, via qsf_hip_kernel_timing).  `roofline.traffic`
+is the HBM bytes per launch measured with rocprofv3 counters
+(profiles/traffic.json), or null.  `cpu_baseline` times QStream's own AVX2
+kernel (oracle/_ref, reference release flags, 1 thread) on a bounded sample.
+`--profile` runs eager launches only, for rocprofv3 counter passes.
 """
 from __future__ import annotations
 
@@ -140,6 +144,14 @@ def run_dense(torch, hip, qt, bs, mats, x, steps, warmup, split=False):
     torch.cuda.synchronize()
     gemv_ms = [e[1].elapsed_time(e[2]) for e in evs]
     xprep_ms = [e[0].elapsed_time(e[1]) for e in evs]
+    # kernel durations: HIP event pairs recorded at each GEMV kernel's own
+    # start and end on the launch stream (no launch gaps)
+    hip.kernel_timing(True)
+    for i in range(steps):
+        step(i)
+    torch.cuda.synchronize()
+    kern_us = hip.kernel_timing_read(steps)
+    hip.kernel_timing(False)
     del graph
     for ts in copies:
         for t in ts:
@@ -149,6 +161,8 @@ def run_dense(torch, hip, qt, bs, mats, x, steps, warmup, split=False):
         "ms_per_step_eager": ms_eager / steps,
         "gemv_ms_event_mean": float(np.mean(gemv_ms)),
         "xprep_ms_event_mean": float(np.mean(xprep_ms)),
+        "kernel_us_mean": float(np.mean(kern_us)) if len(kern_us) else float("nan"),
+        "kernel_us_n": int(len(kern_us)),
         "n_copies": n_copies,
         "rotation_mib": n_copies * per_copy / (1 << 20),
     }
@@ -191,24 +205,55 @@ def cpu_baseline_dense(qt, bs, mats, x, budget_s=10.0):
                       f"median {med * 1e3:.1f} ms/step, {time.perf_counter() - t_start:.1f} s"}
 
 
+def measured_traffic(key: str):
+    """HBM bytes per launch measured with rocprofv3 FETCH_SIZE / WRITE_SIZE
+    (scaled by the copy-kernel calibration), as recorded in
+    profiles/traffic.json; None when not measured."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f)[key]["traffic_bytes"]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
+def run_profile(torch, hip, cfg, steps, warmup):
+    """Eager launches only (no graph, no events): the command the rocprofv3
+    counter passes run."""
+    qt, bs, mats, x = cfg1_data() if cfg == 1 else cfg0_data()
+    per_copy = sum(len(p) for _, p, _, _ in mats)
+    n_copies = max(2, math.ceil(ROTATE_BYTES / per_copy))
+    copies = [[hip.Tensor(p, qt, r, c, bs) for _, p, r, c in mats] for _ in range(n_copies)]
+    dx = torch.from_numpy(x).to("cuda:0")
+    ys = [torch.empty(r, device="cuda:0") for _, _, r, _ in mats]
+    stream = torch.cuda.current_stream()
+    for i in range(warmup + steps):
+        hip.matvec_group(copies[i % n_copies], dx, ys, stream=stream)
+    torch.cuda.synchronize()
+    log(f"profile run: config {cfg}, {warmup} + {steps} launches done")
+
+
 def bench_dense(torch, hip, cfg, steps, warmup, with_cpu=True, split=False):
     qt, bs, mats, x = cfg1_data() if cfg == 1 else cfg0_data()
     log(f"config {cfg}: data ready ({len(mats)} matrices)")
     res = run_dense(torch, hip, qt, bs, mats, x, steps, warmup, split)
     bytes_step = algo_bytes(mats)
     value = bytes_step / (res["ms_per_step"] * 1e-3) / 1e9
-    # one launch per step: its average duration on the launch stream is the
-    # replayed step time (an upper bound: it includes the inter-launch gap)
-    achieved = value
+    # one GEMV launch per step: algorithmic bytes / its mean kernel duration
+    achieved = bytes_step / (res["kernel_us_mean"] * 1e-6) / 1e9
     out = {
         "value": value,
         "ms_per_step": res["ms_per_step"],
         "us_per_call": res["ms_per_step"] * 1e3 / len(mats),
         "us_per_step_eager": res["ms_per_step_eager"] * 1e3,
         "us_event_per_launch_eager": res["gemv_ms_event_mean"] * 1e3,
+        "us_kernel": res["kernel_us_mean"],
         "bytes_per_step": bytes_step,
-        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": None},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic(f"cfg{cfg}"),
+                     "kernel_us": round(res["kernel_us_mean"], 3),
+                     "launches_timed": res["kernel_us_n"]},
         "rotation_mib": res["rotation_mib"],
     }
     if with_cpu:
@@ -248,6 +293,8 @@ def main():
     ap.add_argument("--split", action="store_true",
                     help="stand-alone x-prep launch + GEMV on prepared digits")
     ap.add_argument("--copy-mib", type=int, default=512, help="size of --config copy")
+    ap.add_argument("--profile", action="store_true",
+                    help="eager launches only, no timing (for rocprofv3 counter passes)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
@@ -260,6 +307,9 @@ def main():
         print(json.dumps(copy_calibration(torch, args.steps, args.warmup, args.copy_mib)), flush=True)
         return
     cfg = int(args.config) if args.config != "all" else 1
+    if args.profile:
+        run_profile(torch, qsf_hip, cfg, args.steps, args.warmup)
+        return
     r = bench_dense(torch, qsf_hip, cfg, args.steps, args.warmup, with_cpu=not args.no_cpu,
                     split=args.split)
     workload = {1: "cfg1: 2-bit+outlier FFN gate+up, 2x 11008x4096, block 64, batch-1 decode",
@@ -275,7 +325,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "i4xi4->i32 dot, f32 accumulate",
+        "dtype": "i4xi4->i32 digit dot, f64 accumulate",
         "data": "synthetic (seeded N(0,0.02) + Student-t outliers, converter-semantics quantisation)",
         "config": {"workload": workload, "us_per_call": round(r["us_per_call"], 3),
                    "us_per_step_graph": round(r["ms_per_step"] * 1e3, 3),

@@ -117,6 +117,15 @@ int qsf_hip_matvec_group_prepared_dev(const qsf_hip_tensor* const* t, int n,
                                       const float* d_x, const void* d_xq,
                                       float* const* d_y, void* stream);
 
+/* Kernel timing (diagnostics; no counterpart in the reference).  While
+ * enabled, each decode GEMV launch records a HIP event pair at the kernel's
+ * own start and end on its stream (up to 4096 launches; enabling resets the
+ * record).  _read waits for the recorded launches and writes their
+ * durations in microseconds; it returns how many it wrote, or a negative
+ * status.  Do not enable it while a graph is being captured. */
+int qsf_hip_kernel_timing(int enable);
+int qsf_hip_kernel_timing_read(float* us, int max);
+
 /* ---- MoE FFN with MXFP4 experts (src/engine.c:951-1107) ------------------ */
 typedef struct qsf_hip_moe qsf_hip_moe;         /* opaque device expert table */
 /* gate/up: [expert_dim][hidden], down: [hidden][expert_dim], all MXFP4

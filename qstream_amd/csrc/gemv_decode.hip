@@ -40,6 +40,8 @@
 #include "qsf_device.h"
 #include "qsf_hip_internal.h"
 
+#include <hip/hip_ext.h>
+
 #include <utility>
 
 namespace {
@@ -963,6 +965,17 @@ size_t lds_limit() {
 }
 
 // Launch a main-path instantiation, allowing it the device's full LDS once.
+// Kernel timing (diagnostics): while on, main-path GEMV launches record an
+// event pair at the kernel's own start and end (hipExtLaunchKernel), so the
+// durations exclude launch gaps.  Not for use under graph capture.
+struct KernelTiming {
+    static constexpr int N = 4096;
+    bool on = false;
+    int used = 0;
+    hipEvent_t ev[N][2] = {};
+};
+KernelTiming g_timing;
+
 template <auto K>
 void launch_main(dim3 g, dim3 b, size_t lds, hipStream_t s, const GemvArgs& a) {
     static bool allowed = false;
@@ -970,6 +983,16 @@ void launch_main(dim3 g, dim3 b, size_t lds, hipStream_t s, const GemvArgs& a) {
         (void)hipFuncSetAttribute(reinterpret_cast<const void*>(K),
                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_limit());
         allowed = true;
+    }
+    if (g_timing.on && g_timing.used < KernelTiming::N) {
+        hipEvent_t* p = g_timing.ev[g_timing.used];
+        if (!p[0] && (hipEventCreate(&p[0]) != hipSuccess || hipEventCreate(&p[1]) != hipSuccess)) {
+            hipLaunchKernelGGL(K, g, b, lds, s, a);
+            return;
+        }
+        g_timing.used++;
+        hipExtLaunchKernelGGL(K, g, b, (uint32_t)lds, s, p[0], p[1], 0, a);
+        return;
     }
     hipLaunchKernelGGL(K, g, b, lds, s, a);
 }
@@ -1242,4 +1265,22 @@ extern "C" int qk_unpack(int qt, const void* d_blocks, int nblocks, int bs, int8
     case QK_Q4SYM: return unpack_bs<QK_FMT_4SYM>(bs, b, nblocks, d_codes, d_meta, d_deq, s);
     default: return unpack_bs<QK_FMT_4>(bs, b, nblocks, d_codes, d_meta, d_deq, s);
     }
+}
+
+extern "C" int qk_timing(int enable) {
+    g_timing.on = enable != 0;
+    if (enable) g_timing.used = 0;
+    return 0;
+}
+
+extern "C" int qk_timing_read(float* us, int max) {
+    const int n = g_timing.used < max ? g_timing.used : max;
+    for (int i = 0; i < n; i++) {
+        float ms = 0.0f;
+        if (hipEventSynchronize(g_timing.ev[i][1]) != hipSuccess ||
+            hipEventElapsedTime(&ms, g_timing.ev[i][0], g_timing.ev[i][1]) != hipSuccess)
+            return -1;
+        us[i] = ms * 1000.0f;
+    }
+    return n;
 }

@@ -61,6 +61,11 @@ enum { QK_RUN_XPREP = 1, QK_RUN_GEMV = 2, QK_RUN_BOTH = 3, QK_RUN_STANDALONE_PRE
 int qk_gemv_group(const qsf_hip_tensor* const* t, int n, const float* d_x,
                   float* const* d_y, void* d_ws, int mode, hipStream_t s);
 
+/* Kernel timing of main-path GEMV launches (event pair at the kernel's own
+ * start and end): on/off (on resets the record), then read durations in us. */
+int qk_timing(int enable);
+int qk_timing_read(float* us, int max);
+
 /* Bit-exact unpack checks: codes as int8 [nblocks][bs], meta bits u32 per
  * block (scale | zero << 16); dequantised fp32 [nblocks][bs]. */
 int qk_unpack(int qt, const void* d_blocks, int nblocks, int bs,

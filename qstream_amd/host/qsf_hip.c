@@ -539,6 +539,21 @@ int qsf_hip_unpack_dev(int qt, const void* d_blocks, int nblocks, int bs, int8_t
     return rc;
 }
 
+int qsf_hip_kernel_timing(int enable) {
+    pthread_mutex_lock(&g_lock);
+    int rc = qk_timing(enable);
+    pthread_mutex_unlock(&g_lock);
+    return rc ? fail(E_INTERNAL, "qsf_hip_kernel_timing") : E_OK;
+}
+
+int qsf_hip_kernel_timing_read(float* us, int max) {
+    if (!us || max < 0) return -fail(E_INVALID, "qsf_hip_kernel_timing_read: bad buffer");
+    pthread_mutex_lock(&g_lock);
+    int n = qk_timing_read(us, max);
+    pthread_mutex_unlock(&g_lock);
+    return n < 0 ? -fail(E_INTERNAL, "qsf_hip_kernel_timing_read: event query failed") : n;
+}
+
 /* ---- MoE ------------------------------------------------------------------- */
 struct qsf_hip_moe {
     int n_exp, hidden, eid;

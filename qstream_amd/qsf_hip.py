@@ -33,7 +33,7 @@ EXPORTS = (
     "qsf_hip_matvec_dev", "qsf_hip_matvec_group_dev", "qsf_hip_xprep_bytes",
     "qsf_hip_xprep_dev", "qsf_hip_matvec_group_prepared_dev",
     "qsf_hip_moe_create", "qsf_hip_moe_free", "qsf_hip_moe_forward_dev",
-    "qsf_hip_unpack_dev",
+    "qsf_hip_unpack_dev", "qsf_hip_kernel_timing", "qsf_hip_kernel_timing_read",
 )
 
 _lib = None
@@ -93,8 +93,27 @@ def load(path: str = LIB_PATH) -> C.CDLL:
     L.qsf_hip_moe_forward_dev.restype = _i
     L.qsf_hip_unpack_dev.argtypes = [_i, _vp, _i, _i, _vp, _vp, _vp, _vp]
     L.qsf_hip_unpack_dev.restype = _i
+    L.qsf_hip_kernel_timing.argtypes = [_i]
+    L.qsf_hip_kernel_timing.restype = _i
+    L.qsf_hip_kernel_timing_read.argtypes = [C.POINTER(C.c_float), _i]
+    L.qsf_hip_kernel_timing_read.restype = _i
     _lib = L
     return L
+
+
+def kernel_timing(enable: bool) -> None:
+    """Record an event pair at each decode GEMV kernel's own start and end."""
+    _check(load().qsf_hip_kernel_timing(1 if enable else 0), "qsf_hip_kernel_timing")
+
+
+def kernel_timing_read(max_n: int = 4096):
+    """Durations (us) of the launches recorded since timing was enabled."""
+    import numpy as np
+    buf = (C.c_float * max_n)()
+    n = load().qsf_hip_kernel_timing_read(buf, max_n)
+    if n < 0:
+        _check(n, "qsf_hip_kernel_timing_read")
+    return np.frombuffer(buf, dtype=np.float32, count=n).copy()
 
 
 def last_error() -> tuple[int, str]:
