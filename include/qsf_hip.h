@@ -149,6 +149,16 @@ int qsf_hip_moe_forward_dev(qsf_hip_moe* m, int top_k, int norm_topk, int activa
                             int ntok, const float* d_x, const float* d_logits,
                             float* d_out, void* stream);
 
+/* Batched prefill through the 4-bit format (no reference kernel: the engine
+ * runs one qsf_matvec_4bit call per token, src/engine.c:1289-1295):
+ * d_y[m][rows] = W . float(d_x[m][cols]) for m tokens.  W is a 4-bit
+ * asymmetric tensor (block 64, 128 or 256, no outliers); its weights are
+ * dequantised in registers, s*q + z exactly in fp32, rounded to bf16
+ * (round-to-nearest-even) and contracted on MFMA in fp32.  d_x is bf16
+ * [m][cols] (16-byte aligned, cols % 8 == 0); asynchronous on `stream`. */
+int qsf_hip_prefill_4bit_dev(const qsf_hip_tensor* t, const uint16_t* d_x_bf16, int m,
+                             float* d_y, void* stream);
+
 /* Bit-exact unpack of `nblocks` QSF blocks already in device memory (the
  * same device code paths the GEMV uses): codes int8[nblocks*bs] (2/3/4-bit
  * field values; 4-bit sym as two's complement), meta u32[nblocks] (first

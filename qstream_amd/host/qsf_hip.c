@@ -527,6 +527,25 @@ int qsf_hip_matvec_dev(const qsf_hip_tensor* t, const float* d_x, float* d_y, vo
     return rc;
 }
 
+int qsf_hip_prefill_4bit_dev(const qsf_hip_tensor* t, const uint16_t* d_x_bf16, int m,
+                             float* d_y, void* stream) {
+    if (!t) return fail(E_INVALID, "qsf_hip_prefill_4bit_dev: null tensor");
+    if (t->fmt != QK_FMT_4 || t->n_outliers || !(t->bs == 64 || t->bs == 128 || t->bs == 256))
+        return fail(E_INVALID, "qsf_hip_prefill_4bit_dev: needs a 4-bit asymmetric tensor with "
+                               "block 64, 128 or 256 and no outliers");
+    if (m < 0 || t->cols % 8 != 0 || ((uintptr_t)d_x_bf16 & 15u) != 0)
+        return fail(E_INVALID, "qsf_hip_prefill_4bit_dev: m >= 0, cols %% 8 == 0 and a 16-byte "
+                               "aligned x are required");
+    pthread_mutex_lock(&g_lock);
+    int rc;
+    if (!g_dev.ready) rc = fail(E_INVALID, "qsf_hip: not initialised");
+    else if (qk_prefill_4bit(t, d_x_bf16, m, d_y, pick_stream(stream)))
+        rc = fail(E_INTERNAL, "qsf_hip_prefill_4bit_dev: launch failed");
+    else rc = E_OK;
+    pthread_mutex_unlock(&g_lock);
+    return rc;
+}
+
 int qsf_hip_unpack_dev(int qt, const void* d_blocks, int nblocks, int bs, int8_t* d_codes,
                        uint32_t* d_meta, float* d_deq, void* stream) {
     if (kernel_fmt(qt) < 0 || !(bs == 32 || bs == 64 || bs == 128 || bs == 256))

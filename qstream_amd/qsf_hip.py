@@ -34,6 +34,7 @@ EXPORTS = (
     "qsf_hip_xprep_dev", "qsf_hip_matvec_group_prepared_dev",
     "qsf_hip_moe_create", "qsf_hip_moe_free", "qsf_hip_moe_forward_dev",
     "qsf_hip_unpack_dev", "qsf_hip_kernel_timing", "qsf_hip_kernel_timing_read",
+    "qsf_hip_prefill_4bit_dev",
 )
 
 _lib = None
@@ -93,6 +94,8 @@ def load(path: str = LIB_PATH) -> C.CDLL:
     L.qsf_hip_moe_forward_dev.restype = _i
     L.qsf_hip_unpack_dev.argtypes = [_i, _vp, _i, _i, _vp, _vp, _vp, _vp]
     L.qsf_hip_unpack_dev.restype = _i
+    L.qsf_hip_prefill_4bit_dev.argtypes = [_vp, _vp, _i, _vp, _vp]
+    L.qsf_hip_prefill_4bit_dev.restype = _i
     L.qsf_hip_kernel_timing.argtypes = [_i]
     L.qsf_hip_kernel_timing.restype = _i
     L.qsf_hip_kernel_timing_read.argtypes = [C.POINTER(C.c_float), _i]
@@ -185,6 +188,11 @@ class Tensor:
         if not self.handle:
             _check(-1, "qsf_hip_tensor_upload")
         self.payload_bytes = L.qsf_hip_tensor_payload_bytes(self.handle)
+
+    def prefill(self, x_bf16, m: int, y, stream=None) -> None:
+        """y[m][rows] = W . float(x_bf16[m][cols]) on MFMA (4-bit tensors)."""
+        _check(load().qsf_hip_prefill_4bit_dev(self.handle, _addr(x_bf16), m, _addr(y),
+                                               _stream(stream)), "qsf_hip_prefill_4bit_dev")
 
     def matvec(self, x, y, stream=None) -> None:
         _check(load().qsf_hip_matvec_dev(self.handle, _addr(x), _addr(y), _stream(stream)),
