@@ -37,6 +37,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+BF16_MFMA_PEAK_TFS = 2500.0     # dense bf16 MFMA, MI355X
 ROTATE_BYTES = 512 << 20
 METRIC = "quant matvec HBM GB/s (% of ~8 TB/s peak) + µs/call at 7B decode shapes"
 
@@ -66,6 +67,17 @@ def cfg0_data(seed=0):
     w = F.gaussian(rng, (rows, cols), 0.02)
     mats = [("w", np.frombuffer(F.quantize_matrix(w, F.Q4, bs), np.uint8), rows, cols)]
     return F.Q4, bs, mats, F.gaussian(rng, cols)
+
+
+def cfg4_data(seed=4):
+    from qstream_amd import qsf_format as F
+    rng = np.random.default_rng(seed)
+    m, n, k, bs = 512, 14336, 4096, 64
+    w = F.gaussian(rng, (n, k), 0.02)
+    payload = np.frombuffer(F.quantize_matrix(w, F.Q4, bs), np.uint8)
+    del w
+    xb = F.bf16_bits(rng.standard_normal((m, k)).astype(np.float32))
+    return payload, xb, m, n, k, bs
 
 
 def algo_bytes(mats) -> int:
@@ -261,6 +273,104 @@ def bench_dense(torch, hip, cfg, steps, warmup, with_cpu=True, split=False):
     return out
 
 
+def cpu_baseline_prefill(payload, xb, m, n, k, bs, budget_s=10.0):
+    """The reference's prefill: one qsf_matvec_4bit call per token
+    (src/engine.c:1289-1295), QStream's AVX2 kernel (oracle/_ref), 1 thread,
+    on as many of the M tokens as fit in the time budget."""
+    from oracle.oracle import Oracle, ref_avx2
+    from qstream_amd import qsf_format as F
+    ref = ref_avx2()
+    xf = (xb.astype(np.uint32) << 16).view(np.float32)
+    if ref is not None:
+        kind, name = "reference", "qsf_matvec_4bit_avx2"
+
+        def fn(x):
+            return ref.matvec(F.Q4, payload, x, n, k, bs, isa="avx2")
+    else:
+        kind, name, o = "port", "oracle scalar", Oracle()
+
+        def fn(x):
+            return o.matvec(F.Q4, payload, x, n, k, bs)
+    t0 = time.perf_counter()
+    done = 0
+    while done < m and (time.perf_counter() - t0 < budget_s or done < 2):
+        fn(xf[done])
+        done += 1
+    el = time.perf_counter() - t0
+    return {"value": 2.0 * n * k * done / el / 1e12, "unit": "TFLOP/s", "cores": 1, "kind": kind,
+            "sample": f"{name}, {done} of {m} tokens (one {n}x{k} matvec each), {el:.1f} s"}
+
+
+def profile_prefill(torch, hip, steps, warmup):
+    """Eager config-4 launches only (for rocprofv3 passes)."""
+    from qstream_amd import qsf_format as F
+    payload, xb, m, n, k, bs = cfg4_data()
+    n_copies = max(2, math.ceil(ROTATE_BYTES / len(payload)))
+    copies = [hip.Tensor(payload, F.Q4, n, k, bs) for _ in range(n_copies)]
+    dx = torch.from_numpy(xb.view(np.int16).copy()).to("cuda:0")
+    y = torch.empty((m, n), device="cuda:0")
+    for i in range(warmup + steps):
+        copies[i % n_copies].prefill(dx, m, y, stream=torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    log(f"profile run: config 4, {warmup} + {steps} launches done")
+
+
+def bench_prefill(torch, hip, steps, warmup, with_cpu=True):
+    """Config 4: one MFMA prefill launch per step over a rotating weight copy."""
+    from qstream_amd import qsf_format as F
+    payload, xb, m, n, k, bs = cfg4_data()
+    log(f"config 4: data ready ({m}x{n}x{k}, block {bs})")
+    n_copies = max(2, math.ceil(ROTATE_BYTES / len(payload)))
+    copies = [hip.Tensor(payload, F.Q4, n, k, bs) for _ in range(n_copies)]
+    dx = torch.from_numpy(xb.view(np.int16).copy()).to("cuda:0")
+    y = torch.empty((m, n), device="cuda:0")
+    stream = torch.cuda.current_stream()
+
+    def step(i):
+        copies[i % n_copies].prefill(dx, m, y, stream=stream)
+
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    cap = torch.cuda.Stream()
+    cap.wait_stream(stream)
+    with torch.cuda.stream(cap):
+        with torch.cuda.graph(graph, stream=cap):
+            for i in range(steps):
+                copies[i % n_copies].prefill(dx, m, y, stream=cap)
+    graph.replay()
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    graph.replay()
+    t1.record(stream)
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / steps
+    hip.kernel_timing(True)
+    for i in range(steps):
+        step(i)
+    torch.cuda.synchronize()
+    kern_us = hip.kernel_timing_read(steps)
+    hip.kernel_timing(False)
+    del graph
+    for t in copies:
+        t.free()
+    flops = 2.0 * m * n * k
+    kus = float(np.mean(kern_us))
+    out = {"value": flops / (ms * 1e-3) / 1e12, "ms_per_step": ms, "us_kernel": kus,
+           "flops_per_step": flops, "weight_bytes": len(payload),
+           "roofline": {"bound": "mfma", "achieved": round(flops / (kus * 1e-6) / 1e12, 2),
+                        "peak": BF16_MFMA_PEAK_TFS, "unit": "TFLOP/s",
+                        "frac": round(flops / (kus * 1e-6) / 1e12 / BF16_MFMA_PEAK_TFS, 4),
+                        "traffic": measured_traffic("cfg4"), "kernel_us": round(kus, 3),
+                        "launches_timed": len(kern_us)},
+           "rotation_mib": n_copies * len(payload) / (1 << 20), "m": m, "n": n, "k": k}
+    if with_cpu:
+        out["cpu_baseline"] = cpu_baseline_prefill(payload, xb, m, n, k, bs)
+    return out
+
+
 def copy_calibration(torch, steps, warmup, mib=512):
     """Plain device-to-device copy of a known size: the reference point for
     HBM counters (FETCH_SIZE / WRITE_SIZE per byte moved) and for what the
@@ -307,6 +417,37 @@ def main():
         print(json.dumps(copy_calibration(torch, args.steps, args.warmup, args.copy_mib)), flush=True)
         return
     cfg = int(args.config) if args.config != "all" else 1
+    if cfg == 4 and args.profile:
+        profile_prefill(torch, qsf_hip, args.steps, args.warmup)
+        return
+    if cfg == 4:
+        r = bench_prefill(torch, qsf_hip, args.steps, args.warmup, with_cpu=not args.no_cpu)
+        line = {
+            "metric": "batched 4-bit prefill TFLOP/s (bf16 MFMA, % of 2.5 PFLOP/s dense peak)",
+            "value": round(r["value"], 2),
+            "unit": "TFLOP/s",
+            "n_gpus": 1,
+            "steps": args.steps,
+            "warmup": args.warmup,
+            "ms_per_step": round(r["ms_per_step"], 5),
+            "higher_is_better": True,
+            "scaling": "weak",
+            "vs_baseline": None,
+            "dtype": "bf16 x bf16 -> f32 MFMA (weights dequantised from 4-bit in registers)",
+            "data": "synthetic (seeded N(0,0.02) weights, converter-semantics quantisation; "
+                    "bf16 N(0,1) activations)",
+            "config": {"workload": f"cfg4: 4-bit asym prefill M={r['m']} x K={r['k']} x "
+                                   f"N={r['n']}, block 64", "us_kernel": round(r["us_kernel"], 3),
+                       "us_per_step_graph": round(r["ms_per_step"] * 1e3, 3),
+                       "mfma_util_of_peak": round(r["value"] / BF16_MFMA_PEAK_TFS, 4),
+                       "flops_per_step": r["flops_per_step"],
+                       "rotation_mib": round(r["rotation_mib"], 1)},
+            "roofline": r["roofline"],
+        }
+        if "cpu_baseline" in r:
+            line["cpu_baseline"] = r["cpu_baseline"]
+        print(json.dumps(line), flush=True)
+        return
     if args.profile:
         run_profile(torch, qsf_hip, cfg, args.steps, args.warmup)
         return

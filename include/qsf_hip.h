@@ -155,7 +155,9 @@ int qsf_hip_moe_forward_dev(qsf_hip_moe* m, int top_k, int norm_topk, int activa
  * asymmetric tensor (block 64, 128 or 256, no outliers); its weights are
  * dequantised in registers, s*q + z exactly in fp32, rounded to bf16
  * (round-to-nearest-even) and contracted on MFMA in fp32.  d_x is bf16
- * [m][cols] (16-byte aligned, cols % 8 == 0); asynchronous on `stream`. */
+ * [m][cols] (16-byte aligned, cols >= 32, cols % 8 == 0); asynchronous on
+ * `stream`.  Uses the library workspace (x repacked, about 2*m*cols bytes):
+ * calls must not overlap with other workspace users on other streams. */
 int qsf_hip_prefill_4bit_dev(const qsf_hip_tensor* t, const uint16_t* d_x_bf16, int m,
                              float* d_y, void* stream);
 

@@ -965,9 +965,10 @@ size_t lds_limit() {
 }
 
 // Launch a main-path instantiation, allowing it the device's full LDS once.
-// Kernel timing (diagnostics): while on, main-path GEMV launches record an
-// event pair at the kernel's own start and end (hipExtLaunchKernel), so the
-// durations exclude launch gaps.  Not for use under graph capture.
+// Kernel timing (diagnostics): while on, timed launches (main-path GEMV,
+// prefill) record an event pair at the kernel's own start and end
+// (hipExtLaunchKernel), so the durations exclude launch gaps.  Not for use
+// under graph capture.
 struct KernelTiming {
     static constexpr int N = 4096;
     bool on = false;
@@ -975,6 +976,21 @@ struct KernelTiming {
     hipEvent_t ev[N][2] = {};
 };
 KernelTiming g_timing;
+
+}  // namespace
+
+extern "C" int qk_timing_pair(hipEvent_t* start, hipEvent_t* stop) {
+    if (!g_timing.on || g_timing.used >= KernelTiming::N) return 0;
+    hipEvent_t* p = g_timing.ev[g_timing.used];
+    if (!p[0] && (hipEventCreate(&p[0]) != hipSuccess || hipEventCreate(&p[1]) != hipSuccess))
+        return 0;
+    g_timing.used++;
+    *start = p[0];
+    *stop = p[1];
+    return 1;
+}
+
+namespace {
 
 template <auto K>
 void launch_main(dim3 g, dim3 b, size_t lds, hipStream_t s, const GemvArgs& a) {
@@ -984,17 +1000,11 @@ void launch_main(dim3 g, dim3 b, size_t lds, hipStream_t s, const GemvArgs& a) {
                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_limit());
         allowed = true;
     }
-    if (g_timing.on && g_timing.used < KernelTiming::N) {
-        hipEvent_t* p = g_timing.ev[g_timing.used];
-        if (!p[0] && (hipEventCreate(&p[0]) != hipSuccess || hipEventCreate(&p[1]) != hipSuccess)) {
-            hipLaunchKernelGGL(K, g, b, lds, s, a);
-            return;
-        }
-        g_timing.used++;
-        hipExtLaunchKernelGGL(K, g, b, (uint32_t)lds, s, p[0], p[1], 0, a);
-        return;
-    }
-    hipLaunchKernelGGL(K, g, b, lds, s, a);
+    hipEvent_t e0, e1;
+    if (qk_timing_pair(&e0, &e1))
+        hipExtLaunchKernelGGL(K, g, b, (uint32_t)lds, s, e0, e1, 0, a);
+    else
+        hipLaunchKernelGGL(K, g, b, lds, s, a);
 }
 
 // rows per tile: 2 for 64-code-or-smaller blocks, else 1 (register budget);

@@ -61,10 +61,13 @@ enum { QK_RUN_XPREP = 1, QK_RUN_GEMV = 2, QK_RUN_BOTH = 3, QK_RUN_STANDALONE_PRE
 int qk_gemv_group(const qsf_hip_tensor* const* t, int n, const float* d_x,
                   float* const* d_y, void* d_ws, int mode, hipStream_t s);
 
-/* Kernel timing of main-path GEMV launches (event pair at the kernel's own
- * start and end): on/off (on resets the record), then read durations in us. */
+/* Kernel timing of main-path GEMV and prefill launches (event pair at the
+ * kernel's own start and end): on/off (on resets the record), then read
+ * durations in us.  qk_timing_pair hands a launcher the next event pair for
+ * hipExtLaunchKernel, or returns 0 when timing is off or the record is full. */
 int qk_timing(int enable);
 int qk_timing_read(float* us, int max);
+int qk_timing_pair(hipEvent_t* start, hipEvent_t* stop);
 
 /* Bit-exact unpack checks: codes as int8 [nblocks][bs], meta bits u32 per
  * block (scale | zero << 16); dequantised fp32 [nblocks][bs]. */
@@ -88,9 +91,12 @@ int qk_moe_launch(const qk_mx_expert* d_experts, int n_exp, int k, int norm, int
                   int hidden, int eid, int ntok, const float* d_x, const float* d_logits,
                   float* d_out, void* d_ws, hipStream_t s);
 
-/* 4-bit prefill on MFMA: y[m][n] = W[n] . float(x_bf16[m]) */
+/* 4-bit prefill on MFMA: y[m][n] = W[n] . float(x_bf16[m]).  d_ws holds
+ * x repacked into MFMA fragment order: qk_prefill_ws_bytes(m, cols) bytes,
+ * 16-byte aligned. */
+size_t qk_prefill_ws_bytes(int m, int cols);
 int qk_prefill_4bit(const qsf_hip_tensor* t, const uint16_t* d_x_bf16, int m,
-                    float* d_y, hipStream_t s);
+                    float* d_y, void* d_ws, hipStream_t s);
 
 #ifdef __cplusplus
 }

@@ -533,15 +533,14 @@ int qsf_hip_prefill_4bit_dev(const qsf_hip_tensor* t, const uint16_t* d_x_bf16, 
     if (t->fmt != QK_FMT_4 || t->n_outliers || !(t->bs == 64 || t->bs == 128 || t->bs == 256))
         return fail(E_INVALID, "qsf_hip_prefill_4bit_dev: needs a 4-bit asymmetric tensor with "
                                "block 64, 128 or 256 and no outliers");
-    if (m < 0 || t->cols % 8 != 0 || ((uintptr_t)d_x_bf16 & 15u) != 0)
-        return fail(E_INVALID, "qsf_hip_prefill_4bit_dev: m >= 0, cols %% 8 == 0 and a 16-byte "
-                               "aligned x are required");
+    if (m < 0 || t->cols < 32 || t->cols % 8 != 0 || ((uintptr_t)d_x_bf16 & 15u) != 0)
+        return fail(E_INVALID, "qsf_hip_prefill_4bit_dev: m >= 0, cols >= 32, cols %% 8 == 0 "
+                               "and a 16-byte aligned x are required");
     pthread_mutex_lock(&g_lock);
-    int rc;
-    if (!g_dev.ready) rc = fail(E_INVALID, "qsf_hip: not initialised");
-    else if (qk_prefill_4bit(t, d_x_bf16, m, d_y, pick_stream(stream)))
+    int rc = g_dev.ready ? E_OK : fail(E_INVALID, "qsf_hip: not initialised");
+    if (rc == E_OK) rc = ensure_dev(&g_dev.ws, &g_dev.ws_bytes, qk_prefill_ws_bytes(m, t->cols));
+    if (rc == E_OK && qk_prefill_4bit(t, d_x_bf16, m, d_y, g_dev.ws, pick_stream(stream)))
         rc = fail(E_INTERNAL, "qsf_hip_prefill_4bit_dev: launch failed");
-    else rc = E_OK;
     pthread_mutex_unlock(&g_lock);
     return rc;
 }
