@@ -9,18 +9,22 @@
 // v_cvt_pk_bf16_f32) and contracted with v_mfma_f32_16x16x32_bf16 in fp32.
 // The one rounding beyond fp32 accumulation is that of w to bf16.
 //
-// Tiling.  One 256-thread workgroup per 256 (m) x 112 (n) tile of Y; at
-// config-4 shape (M 512, N 14336) that is exactly one workgroup per CU.  Wave
-// w owns rows 64w..64w+63 and all 112 columns: 4 x 7 MFMA tiles, 112 fp32
-// accumulators per lane.  K advances in stages of 128 codes (4 MFMA
-// k-steps):
-//  * B (weights): the workgroup dequantises the stage's 112 x 128 codes once
-//    into an LDS tile (bf16 [112][128 + 8 pad], two buffers), 7 items of 8
-//    codes per thread, interleaved with the previous stage's MFMAs;
-//  * A (activations): each wave's rows are private, so its fragments come
-//    straight from global memory into registers, loaded two stages ahead.
-// One barrier per stage.  All loads are issued unconditionally (clamped
-// addresses) so the compiler's wait counts stay exact.
+// Tiling.  One 512-thread workgroup per 256 (m) x 112 (n) tile of Y; at
+// config-4 shape (M 512, N 14336) that is exactly one workgroup per CU.  K
+// advances in stages of 128 codes (4 MFMA k-steps).  The waves split by role,
+// one of each per SIMD, so dequantisation (VALU) and MFMAs overlap in the
+// hardware rather than in one instruction stream:
+//  * 4 producer waves dequantise stage s+1's 112 x 128 codes into a bf16 LDS
+//    tile ([112][128 + 8 pad], two buffers) while stage s is contracted;
+//    codes are loaded two stages ahead;
+//  * 4 consumer waves each own 64 rows x 112 columns (4 x 7 MFMA tiles, 112
+//    fp32 accumulators per lane).  A fragments come from x repacked into
+//    fragment order (xpack_kernel: one contiguous 1 KB load per fragment),
+//    one stage ahead in registers; B fragments come from LDS one k-step
+//    ahead.
+// One barrier per stage.  Loads go through raw buffer descriptors: offsets
+// past a tensor read zeros, so prefetches past the end need no clamps and
+// all loads are issued unconditionally (exact compiler wait counts).
 //
 #include "qsf_device.h"
 #include "qsf_hip_internal.h"
@@ -39,7 +43,8 @@ constexpr int BM = 256, BN = 112;      // workgroup tile: 4 waves x 64 m, 7 x 16
 constexpr int MT = 4, NT = 7;          // 16x16 MFMA tiles per wave
 constexpr int SK = 128;                // k per stage (4 MFMA k-steps)
 constexpr int PITCH = SK + 8;          // LDS row pitch of the B tile, bf16
-constexpr int NR = BN * (SK / 8) / 256;   // dequant items (8 codes) per thread per stage
+constexpr int EP_PITCH = BN + 4;       // LDS row pitch of the output staging tile, fp32
+constexpr int EP_FLOATS = 4 * 64 * EP_PITCH;
 
 // Eight codes (one dword, low nibble = even code) -> bf16(s*q + z) x 8.
 __device__ __forceinline__ bf16x8 dequant8(uint32_t w, float s, float z) {
@@ -60,6 +65,34 @@ __device__ __forceinline__ bf16x8 dequant8(uint32_t w, float s, float z) {
     return r;
 }
 
+// The same with one shift and one and-or per pair of codes: code q becomes
+// the fp16 value 1 + q/16 (q in mantissa bits 6..9 of 1.0), and
+// fma(16 s, 1 + q/16, c) with c = z - 16 s equals fp32(s q + z) exactly
+// whenever c is exact in fp32 (the caller checks that per block).
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ bf16x8 dequant8_m16(uint32_t w, float s16, float c) {
+    const uint32_t h[4] = {((w << 6) & 0x03C003C0u) | 0x3C003C00u,   // codes 0, 4
+                           ((w << 2) & 0x03C003C0u) | 0x3C003C00u,   // codes 1, 5
+                           ((w >> 2) & 0x03C003C0u) | 0x3C003C00u,   // codes 2, 6
+                           ((w >> 6) & 0x03C003C0u) | 0x3C003C00u};  // codes 3, 7
+    float x[8];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const f16x2 p = __builtin_bit_cast(f16x2, h[j]);
+        x[j] = (float)p[0];
+        x[j + 4] = (float)p[1];
+    }
+    bf16x8 r;
+#pragma unroll
+    for (int j = 0; j < 8; j += 2) {
+        const f32x2 v = {fmaf(s16, x[j], c), fmaf(s16, x[j + 1], c)};
+        const bf16x2 b = __builtin_convertvector(v, bf16x2);
+        r[j] = b[0];
+        r[j + 1] = b[1];
+    }
+    return r;
+}
+
 struct PrefillArgs {
     const uint8_t* w;        // QSF 4-bit blocks, rows n, row stride nb*BB
     const u32x4* xp;         // x in A-fragment order (xpack_kernel)
@@ -73,15 +106,28 @@ struct PrefillArgs {
 // 32-wide k-step kk < ksp, 64 chunks of 16 bytes, chunk l holding row
 // 16 g + l%16, columns 32 kk + 8 (l/16)..+7 (zero past m or k).  The GEMM
 // then loads each fragment as one contiguous 1 KB read instead of 64
-// scattered 16-byte pieces.
+// scattered 16-byte pieces.  One workgroup per (row group, 8 k-steps): the
+// 16 x 256 tile is read row-contiguously into LDS and written back in
+// fragment order, both coalesced.
+constexpr int XP_PITCH = 256 + 8;      // LDS row pitch of the pack tile, bf16
 __global__ __launch_bounds__(256) void xpack_kernel(const uint16_t* __restrict__ x, u32x4* xp,
-                                                   int m, int k, int ksp, uint32_t chunks) {
-    for (uint32_t c = blockIdx.x * 256u + threadIdx.x; c < chunks; c += gridDim.x * 256u) {
-        const uint32_t l = c & 63u, f = c >> 6, kk = f % (uint32_t)ksp, g = f / (uint32_t)ksp;
-        const int row = (int)(g * 16 + (l & 15u)), col = (int)(kk * 32 + 8 * (l >> 4));
+                                                   int m, int k, int ksp) {
+    __shared__ __align__(16) uint16_t tile[16 * XP_PITCH];
+    const int g = blockIdx.y, kk0 = blockIdx.x * 8, t = threadIdx.x;
+    const int c = t & 31;                      // 16-byte chunk of a 256-wide row piece
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        const int r = (t >> 5) + 8 * h, row = g * 16 + r, col = kk0 * 32 + 8 * c;
         u32x4 v = {0u, 0u, 0u, 0u};
         if (row < m && col < k) v = *reinterpret_cast<const u32x4*>(x + (size_t)row * k + col);
-        xp[c] = v;
+        *reinterpret_cast<u32x4*>(&tile[r * XP_PITCH + 8 * c]) = v;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        const int j = t + 256 * h, kk = j >> 6, l = j & 63;
+        xp[((size_t)g * ksp + kk0 + kk) * 64 + l] =
+            *reinterpret_cast<const u32x4*>(&tile[(l & 15) * XP_PITCH + kk * 32 + 8 * (l >> 4)]);
     }
 }
 
@@ -107,7 +153,8 @@ template <int BS, bool RAGGED>
 __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
     constexpr int BB = 4 + BS / 2;             // block bytes
     constexpr int BUF = BN * PITCH;            // bf16 per B buffer
-    __shared__ __align__(16) __bf16 lds[2 * BUF];
+    // two B buffers during the main loop; the output staging tile after it
+    __shared__ __align__(16) __bf16 lds[2 * BUF > EP_FLOATS * 2 ? 2 * BUF : EP_FLOATS * 2];
 
     const int t = threadIdx.x, lane = t & 63;
     const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
@@ -118,38 +165,52 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
 
     if (wave >= 4) {
         // ---- producer waves: dequantise stage s+1's B tile during stage s.
-        // Thread p converts dword d = p%16 of the stage's 16 code dwords
-        // (128 codes) of columns p/16 + 16 r, r < NR.  Byte offsets in a
-        // row: the lane part is fixed, the stage part uniform; columns past
-        // n read zeros.
+        // Item p < 2 BN: column p/2, codes 64 (p%2)..+63 of the stage, read
+        // as one meta dword and two 16-byte loads; each becomes 8 LDS
+        // writes of 8 bf16.  Byte offsets in a row: the lane part is fixed,
+        // the stage part uniform; columns past n read zeros.
         const uint32_t row_bytes = (uint32_t)a.nb * BB;
         const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.w, a.w_bytes);
-        const int p = t - 256, d = p & 15, c0 = p >> 4;
-        const uint32_t lane_meta = BS <= SK ? (uint32_t)(8 * d / BS) * BB : 0u;
-        const uint32_t lane_code = lane_meta + 4 + 4 * (uint32_t)((8 * d % BS) / 8);
-        const uint32_t wv = (uint32_t)(n0 + c0) * row_bytes;
-        const int it_base = c0 * PITCH + 8 * d;
-        auto load_codes = [&](int s, uint32_t (&code)[NR], uint32_t (&meta)[NR]) {
+        const int p = t - 256, col = p >> 1, h = p & 1;
+        const bool active = p < 2 * BN;
+        // 64 codes (p%2) of the stage: block offset and the codes' offset in it
+        const uint32_t lane_meta = BS == 64 ? (uint32_t)h * BB : 0u;
+        const uint32_t lane_code = lane_meta + 4 + (BS == 64 ? 0u : (uint32_t)h * 32);
+        const uint32_t wv = (uint32_t)(n0 + col) * row_bytes;
+        const int it_base = col * PITCH + 64 * h;
+        auto load_codes = [&](int s, u32x4 (&code)[2], uint32_t& meta) __attribute__((always_inline)) {
             const uint32_t sm = BS <= SK ? (uint32_t)s * (SK / BS) * BB : (uint32_t)(s / (BS / SK)) * BB;
             const uint32_t sc = BS <= SK ? sm : sm + (uint32_t)(s % (BS / SK)) * (SK / 2);
-            const uint32_t mo = wv + lane_meta + sm, co = wv + lane_code + sc;
-#pragma unroll
-            for (int r = 0; r < NR; r++) {
-                meta[r] = __builtin_amdgcn_raw_buffer_load_b32(wr, mo + 16 * r * row_bytes, 0, 0);
-                code[r] = __builtin_amdgcn_raw_buffer_load_b32(wr, co + 16 * r * row_bytes, 0, 0);
-            }
+            meta = __builtin_amdgcn_raw_buffer_load_b32(wr, wv + lane_meta + sm, 0, 0);
+            code[0] = __builtin_amdgcn_raw_buffer_load_b128(wr, wv + lane_code + sc, 0, 0);
+            code[1] = __builtin_amdgcn_raw_buffer_load_b128(wr, wv + lane_code + sc + 16, 0, 0);
         };
-        auto dequant = [&](int s, const uint32_t (&code)[NR], const uint32_t (&meta)[NR], __bf16* buf) {
-            const bool zero = RAGGED && s * SK + 8 * d >= a.k;
+        auto dequant = [&](int s, const u32x4 (&code)[2], uint32_t meta, __bf16* buf) __attribute__((always_inline)) {
+            if (!active) return;
+            const float sc = qsf::f16_lo(meta), zp = qsf::f16_hi(meta);
+            // z - 16 s is exact in fp64 (fp16 operands); the short form
+            // applies when it is also exact (and finite) in fp32
+            const double cd = (double)zp - 16.0 * (double)sc;
+            const float c = (float)cd;
+            if (__builtin_isfinite(cd) && (double)c == cd) {
 #pragma unroll
-            for (int r = 0; r < NR; r++) {
-                bf16x8 v = dequant8(code[r], qsf::f16_lo(meta[r]), qsf::f16_hi(meta[r]));
-                if (zero) v = bf16x8{};
-                *reinterpret_cast<bf16x8*>(buf + it_base + 16 * r * PITCH) = v;
+                for (int j = 0; j < 8; j++) {
+                    bf16x8 v = dequant8_m16(code[j >> 2][j & 3], 16.0f * sc, c);
+                    if (RAGGED && s * SK + 64 * h + 8 * j >= a.k) v = bf16x8{};
+                    *reinterpret_cast<bf16x8*>(buf + it_base + 8 * j) = v;
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    bf16x8 v = dequant8(code[j >> 2][j & 3], sc, zp);
+                    if (RAGGED && s * SK + 64 * h + 8 * j >= a.k) v = bf16x8{};
+                    *reinterpret_cast<bf16x8*>(buf + it_base + 8 * j) = v;
+                }
             }
         };
         // codes double-buffered two stages ahead
-        uint32_t ca[NR], ma[NR], cb[NR], mb[NR];
+        u32x4 ca[2], cb[2];
+        uint32_t ma, mb;
         load_codes(0, ca, ma);
         load_codes(1, cb, mb);
         dequant(0, ca, ma, lds);
@@ -163,6 +224,7 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
             load_codes(s + 4, ca, ma);
             __syncthreads();
         }
+        __syncthreads();                           // the consumers' epilogue barrier
         return;
     }
 
@@ -232,17 +294,36 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
         stage(s + 1, lds + BUF, lds);
     }
 
+    // Epilogue: each wave stages its 64 x 112 fp32 tile in LDS (once every
+    // wave is past its last B read) and writes whole row pieces with 16-byte
+    // stores, instead of 4-byte stores scattered over four rows each.
+    __syncthreads();
+    float* ep = reinterpret_cast<float*>(lds) + wave * 64 * EP_PITCH;
 #pragma unroll
     for (int mt = 0; mt < MT; mt++)
 #pragma unroll
-        for (int nt = 0; nt < NT; nt++) {
-            const int n = n0 + nt * 16 + l16;
+        for (int nt = 0; nt < NT; nt++)
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int m = m0 + mt * 16 + 4 * g4 + i;
-                if (m < a.m && n < a.n) a.y[(size_t)m * a.n + n] = acc[mt][nt][i];
-            }
+            for (int i = 0; i < 4; i++) ep[(mt * 16 + 4 * g4 + i) * EP_PITCH + nt * 16 + l16] = acc[mt][nt][i];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const bool vec = (a.n & 3) == 0;               // rows 16-byte aligned
+#pragma unroll 4
+    for (int c = lane; c < 64 * (BN / 4); c += 64) {
+        const int r = c / (BN / 4), q = c - r * (BN / 4);
+        const int m = m0 + r, n = n0 + 4 * q;
+        if (m >= a.m || n >= a.n) continue;
+        const f32x4 v = *reinterpret_cast<const f32x4*>(ep + r * EP_PITCH + 4 * q);
+        float* dst = a.y + (size_t)m * a.n + n;
+        if (vec) {
+            *reinterpret_cast<f32x4*>(dst) = v;
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                if (n + e < a.n) dst[e] = v[e];
         }
+    }
 }
 
 template <auto K>
@@ -281,12 +362,8 @@ extern "C" int qk_prefill_4bit(const qsf_hip_tensor* t, const uint16_t* d_x_bf16
     const int tiles_n = (t->rows + BN - 1) / BN;
     const int pairs = (t->cols + 2 * SK - 1) / (2 * SK);
     const bool ragged = t->cols % (2 * SK) != 0;
-    {
-        const uint32_t chunks = (uint32_t)(xp_bytes / 16);
-        const int blocks = (int)((chunks + 255) / 256 < 4096 ? (chunks + 255) / 256 : 4096);
-        hipLaunchKernelGGL(xpack_kernel, dim3(blocks), dim3(256), 0, s, d_x_bf16,
-                           static_cast<u32x4*>(d_ws), m, t->cols, packed_ksp(t->cols), chunks);
-    }
+    hipLaunchKernelGGL(xpack_kernel, dim3(packed_ksp(t->cols) / 8, (m + 15) / 16), dim3(256), 0, s,
+                       d_x_bf16, static_cast<u32x4*>(d_ws), m, t->cols, packed_ksp(t->cols));
     PrefillArgs a = {t->d_blocks, static_cast<const u32x4*>(d_ws), d_y, m, t->rows, t->cols, t->nb,
                      tiles_n, pairs, (uint32_t)((uint64_t)t->rows * t->nb * bb), (uint32_t)xp_bytes};
     const dim3 grid(tiles_n * tiles_m), block(512);
