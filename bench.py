@@ -80,6 +80,30 @@ def cfg4_data(seed=4):
     return payload, xb, m, n, k, bs
 
 
+def cfg2_layer(seed=2):
+    """One 7B decoder layer at 3-bit, block 128: q/k/v/o 4096x4096, gate/up
+    11008x4096, down 4096x11008 (N(0,0.02) weights, quantised).  The 32
+    layers of config 2 are distinct device copies of these payloads."""
+    from qstream_amd import qsf_format as F
+    rng = np.random.default_rng(seed)
+    shapes = [("q", 4096, 4096), ("k", 4096, 4096), ("v", 4096, 4096), ("o", 4096, 4096),
+              ("gate", 11008, 4096), ("up", 11008, 4096), ("down", 4096, 11008)]
+    mats = []
+    for name, r, c in shapes:
+        w = F.gaussian(rng, (r, c), 0.02)
+        mats.append((name, np.frombuffer(F.quantize_matrix(w, F.Q3, 128), np.uint8), r, c))
+        del w
+    return F.Q3, 128, mats
+
+
+def cfg3_experts(seed=3, n_exp=32, dim=2880):
+    """32 MXFP4 experts (gate, up [2880][2880], down [2880][2880]) with
+    random E2M1 codes and E8M0 scales around 2^-6 (|w| ~ 0.02)."""
+    from qstream_amd import qsf_format as F
+    rng = np.random.default_rng(seed)
+    return [{n: F.random_mxfp4(rng, dim, dim) for n in ("gate", "up", "down")} for _ in range(n_exp)]
+
+
 def algo_bytes(mats) -> int:
     return sum(len(p) + 4 * c + 4 * r for _, p, r, c in mats)
 
@@ -371,6 +395,166 @@ def bench_prefill(torch, hip, steps, warmup, with_cpu=True):
     return out
 
 
+def _graph_ms(torch, fn, steps):
+    """Mean ms per step of `fn(i)` for i < steps, captured once into a HIP
+    graph and replayed between two synchronisations."""
+    graph = torch.cuda.CUDAGraph()
+    cap = torch.cuda.Stream()
+    cap.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(cap):
+        with torch.cuda.graph(graph, stream=cap):
+            for i in range(steps):
+                fn(i, cap)
+    graph.replay()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    graph.replay()
+    t1.record(stream)
+    torch.cuda.synchronize()
+    del graph
+    return t0.elapsed_time(t1) / steps
+
+
+def bench_layers(torch, hip, steps, warmup, with_cpu=True):
+    """Config 2: 32 decoder layers at 3-bit back to back.  A step is the
+    whole stack: per layer q/k/v in one grouped launch, o, gate/up grouped,
+    down -- 128 launches, each on its own fresh x."""
+    qt, bs, mats = cfg2_layer()
+    log("config 2: layer quantised")
+    layers = [[hip.Tensor(p, qt, r, c, bs) for _, p, r, c in mats] for _ in range(32)]
+    rng = np.random.default_rng(20)
+    xs = [torch.from_numpy(rng.standard_normal((4, 11008)).astype(np.float32)).to("cuda:0")
+          for _ in range(32)]
+    ys = {n: torch.empty(r, device="cuda:0") for n, _, r, _ in mats}
+
+    def step(i, stream):
+        for li, ts in enumerate(layers):
+            x = xs[li]
+            hip.matvec_group(ts[0:3], x[0, :4096], [ys["q"], ys["k"], ys["v"]], stream=stream)
+            hip.matvec_group(ts[3:4], x[1, :4096], [ys["o"]], stream=stream)
+            hip.matvec_group(ts[4:6], x[2, :4096], [ys["gate"], ys["up"]], stream=stream)
+            hip.matvec_group(ts[6:7], x[3], [ys["down"]], stream=stream)
+
+    for i in range(warmup):
+        step(i, torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    ms = _graph_ms(torch, step, steps)
+    hip.kernel_timing(True)
+    step(0, torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    kern = hip.kernel_timing_read(4096)
+    hip.kernel_timing(False)
+    for ts in layers:
+        for t in ts:
+            t.free()
+    per_layer = algo_bytes(mats)
+    total = 32 * per_layer
+    out = {"value": total / (ms * 1e-3) / 1e9, "ms_per_step": ms, "bytes_per_step": total,
+           "kernel_us_sum": float(np.sum(kern)), "launches": len(kern)}
+    out["roofline"] = {"bound": "hbm", "achieved": round(total / (out["kernel_us_sum"] * 1e-6) / 1e9, 2),
+                       "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                       "frac": round(total / (out["kernel_us_sum"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                       "traffic": measured_traffic("cfg2"), "kernel_us": round(out["kernel_us_sum"], 3),
+                       "launches_timed": len(kern)}
+    if with_cpu:
+        out["cpu_baseline"] = cpu_baseline_layer(qt, bs, mats)
+    return out
+
+
+def cpu_baseline_layer(qt, bs, mats, budget_s=10.0):
+    """The reference's 3-bit matvec is scalar on every ISA
+    (src/kernels.c:10): qsf_matvec_3bit_scalar from oracle/_ref (reference
+    release flags), 1 thread, over one layer's matrices."""
+    from oracle.oracle import Oracle, ref_avx2
+    ref = ref_avx2()
+    rng = np.random.default_rng(21)
+    kind = "reference" if ref is not None else "port"
+    o = None if ref is not None else Oracle()
+    t0 = time.perf_counter()
+    done = 0
+    nbytes = 0
+    while time.perf_counter() - t0 < budget_s or done == 0:
+        for _, p, r, c in mats:
+            x = rng.standard_normal(c).astype(np.float32)
+            if ref is not None:
+                ref.matvec(qt, p, x, r, c, bs, isa="scalar")
+            else:
+                o.matvec(qt, p, x, r, c, bs)
+            nbytes += len(p) + 4 * c + 4 * r
+        done += 1
+    el = time.perf_counter() - t0
+    return {"value": nbytes / el / 1e9, "unit": "GB/s", "cores": 1, "kind": kind,
+            "sample": f"qsf_matvec_3bit_scalar over {done} layer(s) of 7 matrices, {el:.1f} s"}
+
+
+def bench_moe(torch, hip, steps, warmup, ntok, with_cpu=True):
+    """Config 3: MXFP4 MoE FFN, 32 experts, hidden = expert dim = 2880,
+    top-4 softmax routing, ntok tokens per step.  Each step draws new router
+    logits (64 seeded sets in rotation), so the experts read change."""
+    from qstream_amd import qsf_format as F
+    n_exp, dim, k = 32, 2880, 4
+    ex = cfg3_experts()
+    log(f"config 3: experts ready (batch {ntok})")
+    tens = {n: [hip.Tensor(e[n], F.MXFP4, dim, dim, 32) for e in ex] for n in ("gate", "up", "down")}
+    moe = hip.Moe(tens["gate"], tens["up"], tens["down"], dim, dim)
+    rng = np.random.default_rng(30 + ntok)
+    nset = 64
+    logits_h = rng.standard_normal((nset, ntok, n_exp)).astype(np.float32)
+    xs = torch.from_numpy(rng.standard_normal((nset, ntok, dim)).astype(np.float32)).to("cuda:0")
+    logits = torch.from_numpy(logits_h).to("cuda:0")
+    out = torch.empty((ntok, dim), device="cuda:0")
+
+    def step(i, stream):
+        j = i % nset
+        moe.forward(k, 1, 2, ntok, xs[j], logits[j], out, stream=stream)
+
+    for i in range(warmup):
+        step(i, torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    ms = _graph_ms(torch, step, steps)
+    # algorithmic bytes per step: distinct experts x 3 matrices + activations
+    per_mat = dim * (dim // 32) * 17
+    distinct = []
+    for i in range(steps):
+        lg = logits_h[i % nset]
+        sel = set()
+        for t in range(ntok):
+            sel.update(np.argsort(-lg[t], kind="stable")[:k].tolist())
+        distinct.append(len(sel))
+    bytes_step = float(np.mean(distinct)) * 3 * per_mat + ntok * dim * 4 * 2
+    moe.free()
+    for ts in tens.values():
+        for t in ts:
+            t.free()
+    res = {"value": bytes_step / (ms * 1e-3) / 1e9, "ms_per_step": ms, "bytes_per_step": bytes_step,
+           "distinct_experts_mean": float(np.mean(distinct))}
+    if with_cpu:
+        res["cpu_baseline"] = cpu_baseline_moe(ex, ntok, k, dim, logits_h, xs.cpu().numpy())
+    return res
+
+
+def cpu_baseline_moe(ex, ntok, k, dim, logits_h, xs, budget_s=10.0):
+    """No reference CPU kernel reads MXFP4 (the reference re-quantises GPT-OSS
+    experts to its own formats).  This times this build's scalar restatement
+    of the same MoE token (oracle, strict fp32, 1 thread)."""
+    from oracle.oracle import Oracle
+    o = Oracle()
+    t0 = time.perf_counter()
+    toks = 0
+    nbytes = 0.0
+    per_mat = dim * (dim // 32) * 17
+    while time.perf_counter() - t0 < budget_s or toks == 0:
+        j = toks % len(logits_h)
+        o.moe_token(ex, k, 1, 2, dim, dim, xs[j, 0], logits_h[j, 0])
+        toks += 1
+        nbytes += k * 3 * per_mat + 2 * dim * 4
+    el = time.perf_counter() - t0
+    return {"value": nbytes / el / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"oracle MoE token (scalar MXFP4), {toks} tokens, {el:.1f} s"}
+
+
 def copy_calibration(torch, steps, warmup, mib=512):
     """Plain device-to-device copy of a known size: the reference point for
     HBM counters (FETCH_SIZE / WRITE_SIZE per byte moved) and for what the
@@ -400,6 +584,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="1")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--moe-batch", type=int, default=1, help="tokens per step for --config 3")
     ap.add_argument("--split", action="store_true",
                     help="stand-alone x-prep launch + GEMV on prepared digits")
     ap.add_argument("--copy-mib", type=int, default=512, help="size of --config copy")
@@ -417,6 +602,31 @@ def main():
         print(json.dumps(copy_calibration(torch, args.steps, args.warmup, args.copy_mib)), flush=True)
         return
     cfg = int(args.config) if args.config != "all" else 1
+    if cfg in (2, 3):
+        if cfg == 2:
+            r = bench_layers(torch, qsf_hip, args.steps, args.warmup, with_cpu=not args.no_cpu)
+            workload = "cfg2: 32 x 7B decoder layer at 3-bit block 128, batch-1 decode, back to back"
+            extra = {"launches_per_step": 128, "us_per_step_graph": round(r["ms_per_step"] * 1e3, 3)}
+        else:
+            r = bench_moe(torch, qsf_hip, args.steps, args.warmup, args.moe_batch, with_cpu=not args.no_cpu)
+            workload = (f"cfg3: MXFP4 MoE FFN, 32 experts 2880x2880, top-4, batch {args.moe_batch}")
+            extra = {"distinct_experts_mean": round(r["distinct_experts_mean"], 2),
+                     "us_per_step_graph": round(r["ms_per_step"] * 1e3, 3)}
+        line = {
+            "metric": METRIC, "value": round(r["value"], 2), "unit": "GB/s", "n_gpus": 1,
+            "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(r["ms_per_step"], 5),
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+            "dtype": "i4xi4->i32 digit dot, f64 accumulate" if cfg == 2 else "e2m1 x f32, f32 accumulate",
+            "data": "synthetic (seeded; cfg2 N(0,0.02) quantised, cfg3 random E2M1 codes / E8M0 scales)",
+            "config": dict({"workload": workload, "bytes_per_step": r["bytes_per_step"],
+                            "hbm_frac_of_8TBs": round(r["value"] / HBM_PEAK_GBS, 4)}, **extra),
+        }
+        if "roofline" in r:
+            line["roofline"] = r["roofline"]
+        if "cpu_baseline" in r:
+            line["cpu_baseline"] = r["cpu_baseline"]
+        print(json.dumps(line), flush=True)
+        return
     if cfg == 4 and args.profile:
         profile_prefill(torch, qsf_hip, args.steps, args.warmup)
         return

@@ -12,11 +12,13 @@
 // XB = 24..26 bits) split into seven signed base-16 digits.  The GEMV
 // multiplies raw code nibbles by digit nibbles with v_dot8_i32_i4 (8 exact
 // products per instruction), recombines the digits per block in two exact
-// int32 groups (digits 0-3 and 4-6), joins them with one fp32 FMA and applies
-// the fp16 scale/zero in fp32.  The rounding beyond fp32 accumulation is
-// x -> X, at most 2^-(XB+1) of the block's max |x| -- finer than fp32 itself
-// for the block's largest elements, so even a row whose result cancels 100x
-// stays inside the 1e-5 bar against the strict scalar reference.
+// int32 groups (digits 0-3 and 4-6), joins them exactly in fp64 and adds
+// s * sum q X + z' * sum X into an fp64 row sum (the block's fp64 meta holds
+// the power-of-two rescale).  The one rounding before the final fp32 store
+// is x -> X, at most 2^-(XB+1) of the block's max |x| -- finer than fp32
+// itself for the block's largest elements, so even a row whose result
+// cancels 100x stays inside the 1e-5 bar against the strict scalar
+// reference.
 //
 // Code unpacking is pure masking, chosen so each nibble holds one signed
 // 4-bit value that the digit tables pair with the right x:
@@ -29,14 +31,19 @@
 //                shifted right by one) carry them, with digit tables scaled by
 //                powers of two so that sum = S_A + S_B/4 exactly.
 //
-// Launch.  Persistent 1024-thread workgroups, one per CU by default.  Each
-// workgroup first turns x into digits in LDS itself (no separate launch;
-// a v_perm nibble transpose builds the digit words), then its 16 waves walk
-// their share of R-row tiles.  Within a tile, lane l of a row group handles
-// blocks l, l+LPG, ... so each lane reads whole blocks (dword loads from
-// 4-byte aligned blocks, 32-bit offsets) and reuses its block's digits
-// (odd LDS stride: conflict-free) for R rows.  A fused CSR pass adds the fp16
-// outliers of each tile's rows; partial sums are reduced with DPP.
+// Launch.  1024-thread workgroups on a 2-D grid: blockIdx.y picks the
+// matrix of a group (gate/up share one launch and one x), blockIdx.x a run
+// of tpw R-row tiles, about one workgroup per CU in total.  Each workgroup
+// first turns x into digits in LDS itself (no separate launch; a v_perm
+// nibble transpose builds the digit words), then its 16 waves walk their
+// tiles.  Within a tile, lane l of a row group handles blocks l, l+LPG, ...
+// so each lane reads whole blocks (dword loads from 4-byte aligned blocks,
+// 32-bit offsets) and reuses its block's digits (odd LDS stride:
+// conflict-free) for R rows.  Weight loads are issued straight-line, D
+// blocks ahead, with no loads or stores inside conditionals (the compiler's
+// wait counts stay exact); row sums go to an LDS stash and are stored at the
+// end.  A fused CSR pass adds the fp16 outliers of each tile's rows; partial
+// sums are reduced with DPP in fp64.
 #include "qsf_device.h"
 #include "qsf_hip_internal.h"
 

@@ -54,10 +54,32 @@ __device__ __forceinline__ float block_dot(uint4 c, const float* __restrict__ x,
         }
     } else {
         for (int k = 0; k < count; k++) {
-            uint32_t nib = (w[k >> 3] >> (4 * (k & 7))) & 15u;
+            // (a select chain: a runtime index into w[] would put it in scratch)
+            const uint32_t wk = k < 8 ? c.x : k < 16 ? c.y : k < 24 ? c.z : c.w;
+            uint32_t nib = (wk >> (4 * (k & 7))) & 15u;
             f2 v = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(nib, 1.0f, 0);
             acc = fmaf(v.x, x[k], acc);
         }
+    }
+    return acc;
+}
+
+// sum_{k<32} e2m1(code_k) * x[k] for a whole block (x 16-byte aligned).
+__device__ __forceinline__ float block_dot32(uint4 c, const float* __restrict__ x) {
+    float acc = 0.0f;
+    const uint32_t w[4] = {c.x, c.y, c.z, c.w};
+    const float4* x4 = reinterpret_cast<const float4*>(x);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float4 xa = x4[2 * i], xb = x4[2 * i + 1];
+        f2 v0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w[i], 1.0f, 0);
+        f2 v1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w[i], 1.0f, 1);
+        f2 v2 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w[i], 1.0f, 2);
+        f2 v3 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w[i], 1.0f, 3);
+        acc = fmaf(v0.x, xa.x, acc); acc = fmaf(v0.y, xa.y, acc);
+        acc = fmaf(v1.x, xa.z, acc); acc = fmaf(v1.y, xa.w, acc);
+        acc = fmaf(v2.x, xb.x, acc); acc = fmaf(v2.y, xb.y, acc);
+        acc = fmaf(v3.x, xb.z, acc); acc = fmaf(v3.y, xb.w, acc);
     }
     return acc;
 }
@@ -146,75 +168,23 @@ typedef qk_mx_expert MxExpert;
 constexpr int MAX_TOK = 8;
 constexpr int MAX_K = 8;
 constexpr int MAX_EXP = 256;
+constexpr int MAX_SLOTS = MAX_TOK * MAX_K;     // slot s = t*K + rank; one lane each
 
-// Routing result shared by the three MoE kernels.
+// A distinct expert and the slots that picked it, in slot order (a token
+// picks an expert at most once, so at most MAX_TOK slots).
+struct Work {
+    int expert, n;
+    int slot[MAX_TOK];
+};
 struct Route {
-    int idx[MAX_TOK][MAX_K];
-    float w[MAX_TOK][MAX_K];
-    int owner[MAX_TOK * MAX_K];            // 1 if slot (t,k) is the first to pick its expert
-    int ntl[MAX_TOK * MAX_K];              // tokens served by an owner slot
-    int tl[MAX_TOK * MAX_K][MAX_TOK];      // their slot ids (t*K + k)
+    int idx[MAX_SLOTS];        // expert of slot s (-1: none)
+    float w[MAX_SLOTS];        // its routing weight
+    int nwork;
+    Work work[MAX_SLOTS];      // distinct experts in order of first pick
 };
 
-// softmax (src/kernels_scalar.c:187-214) + top-K (src/engine.c:987-1018)
-__device__ void route_token(const float* __restrict__ logits, int n_exp, int k, int norm,
-                            float* probs, int* idx, float* w) {
-    float mx = logits[0];
-    for (int i = 1; i < n_exp; i++) mx = logits[i] > mx ? logits[i] : mx;
-    float sum = 0.0f;
-    for (int i = 0; i < n_exp; i++) { probs[i] = expf(logits[i] - mx); sum += probs[i]; }
-    if (sum < 1e-30f) {
-        for (int i = 0; i < n_exp; i++) probs[i] = 1.0f / (float)n_exp;
-    } else {
-        const float inv = 1.0f / sum;
-        for (int i = 0; i < n_exp; i++) probs[i] *= inv;
-    }
-    for (int i = 0; i < k; i++) { idx[i] = -1; w[i] = -1e30f; }
-    for (int e = 0; e < n_exp; e++) {
-        const float p = probs[e];
-        for (int i = 0; i < k; i++) {
-            if (p > w[i]) {
-                for (int q = k - 1; q > i; q--) { w[q] = w[q - 1]; idx[q] = idx[q - 1]; }
-                w[i] = p; idx[i] = e;
-                break;
-            }
-        }
-    }
-    if (norm) {
-        float s = 0.0f;
-        for (int i = 0; i < k; i++) s += w[i];
-        if (s > 0.0f) {
-            const float inv = 1.0f / s;
-            for (int i = 0; i < k; i++) w[i] *= inv;
-        }
-    }
-}
-
-// Every workgroup of the gate/up kernel computes the (tiny) routing itself;
-// workgroup 0 also publishes it for the down and combine kernels.
-__device__ void compute_route(const float* __restrict__ logits, int n_exp, int k, int norm,
-                              int ntok, Route& rt, float* probs_lds) {
-    if (threadIdx.x < ntok) {
-        const int t = threadIdx.x;
-        route_token(logits + (size_t)t * n_exp, n_exp, k, norm, probs_lds + t * n_exp,
-                    rt.idx[t], rt.w[t]);
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const int ns = ntok * k;
-        for (int s = 0; s < ns; s++) {
-            const int e = rt.idx[s / k][s % k];
-            int first = e >= 0;
-            for (int q = 0; q < s && first; q++)
-                if (rt.idx[q / k][q % k] == e) first = 0;
-            rt.owner[s] = first;
-            rt.ntl[s] = 0;
-            if (first)
-                for (int q = s; q < ns; q++)
-                    if (rt.idx[q / k][q % k] == e) rt.tl[s][rt.ntl[s]++] = q;
-        }
-    }
-    __syncthreads();
+__device__ __forceinline__ float rdlane(float v, int l) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
 }
 
 __device__ __forceinline__ float act_fn(int act, float v) {
@@ -233,93 +203,285 @@ struct MoeArgs {
     const float* logits;   // [ntok][n_exp]
     float* out;            // [ntok][hidden]
     Route* route;          // workspace
-    float* h;              // [ntok*k][eid]   act(gate)*up
-    float* d;              // [ntok*k][hidden] down outputs
-    int tiles_gu, tiles_dn;
+    float* h;              // [ntok*k][eid]   act(gate)*up per slot
+    float* d;              // [ntok*k][hidden] down outputs per slot
 };
 
-__global__ __launch_bounds__(WAVES * 64) void moe_gate_up_kernel(MoeArgs a) {
-    __shared__ Route rt;
-    __shared__ float probs[MAX_TOK * MAX_EXP];
-    compute_route(a.logits, a.n_exp, a.k, a.norm, a.ntok, rt, probs);
-    if (blockIdx.x == 0) {
-        for (int i = threadIdx.x; i < (int)(sizeof(Route) / 4); i += blockDim.x)
-            reinterpret_cast<int*>(a.route)[i] = reinterpret_cast<const int*>(&rt)[i];
+// Routing of token t by one wave, into s_idx/s_w[t*K .. t*K+K-1]:
+// softmax (src/kernels_scalar.c:187-214) with the max and the sum taken in
+// index order as the reference does (lane values read back with readlane),
+// exps one expert per lane; top-K (src/engine.c:987-1018) as ranks: expert e
+// takes place r = #{q : p_q > p_e, or p_q == p_e and q < e} among those with
+// p > -1e30 (NaN never qualifies), which is the order the strict '>'
+// insertion from a -1e30 start produces; then optional renormalisation by
+// the rank-ordered sum.
+constexpr int RJ = MAX_EXP / 64;          // experts per lane
+
+__device__ void route_token(const float* __restrict__ lg, int n, int k, int norm, int t,
+                            int* s_idx, float* s_w) {
+    const int lane = threadIdx.x & 63;
+    if (lane < k) { s_idx[t * k + lane] = -1; s_w[t * k + lane] = -1e30f; }
+    float v[RJ];
+#pragma unroll
+    for (int j = 0; j < RJ; j++) v[j] = lane + 64 * j < n ? lg[lane + 64 * j] : 0.0f;
+    float mx = rdlane(v[0], 0);
+#pragma unroll
+    for (int j = 0; j < RJ; j++)
+        for (int l = 0; l < 64 && 64 * j + l < n; l++) {
+            const float q = rdlane(v[j], l);
+            mx = q > mx ? q : mx;
+        }
+#pragma unroll
+    for (int j = 0; j < RJ; j++) v[j] = expf(v[j] - mx);
+    float sum = 0.0f;
+#pragma unroll
+    for (int j = 0; j < RJ; j++)
+        for (int l = 0; l < 64 && 64 * j + l < n; l++) sum += rdlane(v[j], l);
+    const bool flat = sum < 1e-30f;
+    const float inv = 1.0f / sum;
+#pragma unroll
+    for (int j = 0; j < RJ; j++) v[j] = flat ? 1.0f / (float)n : v[j] * inv;
+    int rank[RJ];
+#pragma unroll
+    for (int j = 0; j < RJ; j++) rank[j] = 0;
+#pragma unroll
+    for (int jq = 0; jq < RJ; jq++)
+        for (int l = 0; l < 64 && 64 * jq + l < n; l++) {
+            const float pq = rdlane(v[jq], l);
+            const int q = 64 * jq + l;
+#pragma unroll
+            for (int j = 0; j < RJ; j++) {
+                const int e = lane + 64 * j;
+                rank[j] += pq > -1e30f && (pq > v[j] || (pq == v[j] && q < e)) ? 1 : 0;
+            }
+        }
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int j = 0; j < RJ; j++) {
+        const int e = lane + 64 * j;
+        if (e < n && v[j] > -1e30f && rank[j] < k) { s_idx[t * k + rank[j]] = e; s_w[t * k + rank[j]] = v[j]; }
     }
-    const int slot = blockIdx.x / a.tiles_gu, tile = blockIdx.x % a.tiles_gu;
-    if (slot >= a.ntok * a.k || !rt.owner[slot]) return;
-    const int e = rt.idx[slot / a.k][slot % a.k];
-    const MxExpert ex = a.experts[e];
-    const int nb = (a.hidden + 31) / 32;
-    const MxMat g = {ex.gc, ex.gs, a.eid, a.hidden, nb};
-    const MxMat u = {ex.uc, ex.us, a.eid, a.hidden, nb};
-    const int ntl = rt.ntl[slot];
-    const int* tl = rt.tl[slot];
-    auto xf = [&](int t) { return a.x + (size_t)(tl[t] / a.k) * a.hidden; };
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int lpg = pick_lpg(nb), grp = lane / lpg, lig = lane % lpg;
-    const int rows_per_wave = (64 / lpg) * R;
-    const int row0 = tile * WAVES * rows_per_wave + wave * rows_per_wave + grp * R;
-    float rg[R][MAXT], ru[R][MAXT];
-    zero_rs(rg);
-    zero_rs(ru);
-    mx_rows(g, ntl, xf, row0, lig, lpg, rg);
-    mx_rows(u, ntl, xf, row0, lig, lpg, ru);
+    __builtin_amdgcn_wave_barrier();
+    if (norm) {
+        float ws = 0.0f;
+        for (int i = 0; i < k; i++) ws += s_w[t * k + i];
+        __builtin_amdgcn_wave_barrier();
+        if (ws > 0.0f && lane < k) s_w[t * k + lane] *= 1.0f / ws;
+    }
+}
+
+// The distinct experts of the routed slots, in order of first pick, each
+// with the slots that picked it (wave 0, after every token is routed).
+__device__ void build_work(const int* s_idx, int ns, Route& rt) {
+    const int lane = threadIdx.x & 63;
+    const int e = lane < ns ? s_idx[lane] : -1;
+    bool first = e >= 0;
+    for (int q = 0; q < ns; q++) {
+        const int eq = __builtin_amdgcn_readlane(e, q);
+        if (q < lane && eq == e) first = false;
+    }
+    const uint64_t owners = __ballot(first);
+    const int wi = __popcll(owners & ((1ull << lane) - 1));
+    int cnt = 0;
+    for (int q = 0; q < ns; q++) {
+        const int eq = __builtin_amdgcn_readlane(e, q);
+        if (first && q >= lane && eq == e) rt.work[wi].slot[cnt++] = q;
+    }
+    if (first) {
+        rt.work[wi].expert = e;
+        rt.work[wi].n = cnt;
+    }
+    if (lane == 0) rt.nwork = __popcll(owners);
+}
+
+// Expert GEMV tile: NM matrices with the same shape ([rows][cols] MXFP4)
+// against the inputs xs[i] (LDS, i < n) of one work item.  A 32-lane group
+// owns MR consecutive rows; lane l reads blocks l, l+32, ... of each row, so
+// a row's 16-byte code loads are contiguous across the group, and all NI
+// blocks of a lane are loaded before stage() stages the inputs.  The codes
+// stay in registers while a runtime loop walks the inputs; for each input
+// the lane partial sums acc[m][r] go to done(i, acc).
+// Rows per 32-lane group: 2 for the gate/up pair, 4 for down (the same code
+// registers); rows per workgroup WAVES * 2 * MR.
+template <int NM>
+constexpr int kMR = NM == 2 ? 2 : 4;
+
+template <int NM, int NI, int MR, typename STAGE, typename DONE>
+__device__ __forceinline__ void mx_tile(const MxMat (&mat)[NM], const float* xs, int n, int row0,
+                                        int lig, STAGE stage, DONE done) {
+    uint4 c[NI][NM][MR];
+    float sc[NI][NM][MR];
 #pragma unroll
-    for (int i = 0; i < MAXT; i++) {
-        if (i < ntl) {
-            const int s2 = tl[i];
+    for (int it = 0; it < NI; it++) {
+        const int b = min(lig + 32 * it, mat[0].nb - 1);
 #pragma unroll
-            for (int r = 0; r < R; r++) {
-                const float gv = qsf::group_sum(rg[r][i], lpg);
-                const float uv = qsf::group_sum(ru[r][i], lpg);
-                const int row = row0 + r;
-                if (lig == (r & (lpg - 1)) && row < a.eid) {
-                    float gg = gv, uu = uv;
-                    if (ex.gb) gg += qsf::f16_bits(ex.gb[row]);
-                    if (ex.ub) uu += qsf::f16_bits(ex.ub[row]);
-                    a.h[(size_t)s2 * a.eid + row] = act_fn(a.act, gg) * uu;
+        for (int m = 0; m < NM; m++)
+#pragma unroll
+            for (int r = 0; r < MR; r++) {
+                const size_t at = (size_t)min(row0 + r, mat[m].rows - 1) * mat[m].nb + b;
+                c[it][m][r] = ld_nt16(mat[m].codes + at * 16);
+                sc[it][m][r] = e8m0(mat[m].scales[at]);
+            }
+    }
+    stage();                               // inputs to LDS while the codes load
+#pragma unroll 1
+    for (int i = 0; i < n; i++) {
+        float acc[NM][MR];
+#pragma unroll
+        for (int m = 0; m < NM; m++)
+#pragma unroll
+            for (int r = 0; r < MR; r++) acc[m][r] = 0.0f;
+#pragma unroll
+        for (int it = 0; it < NI; it++) {
+            const int b = lig + 32 * it;
+            // inputs are zero-padded to whole blocks in LDS; lanes past the
+            // last block add nothing
+            const float4* x4 = reinterpret_cast<const float4*>(xs + (size_t)i * 32 * mat[0].nb +
+                                                               32 * min(b, mat[0].nb - 1));
+            const bool live = b < mat[0].nb;
+            float dot[NM][MR];
+#pragma unroll
+            for (int m = 0; m < NM; m++)
+#pragma unroll
+                for (int r = 0; r < MR; r++) dot[m][r] = 0.0f;
+            // one code word (8 elements) of every row at a time, so only
+            // that word's values are live
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const float4 xa = x4[2 * q], xc = x4[2 * q + 1];
+#pragma unroll
+                for (int m = 0; m < NM; m++)
+#pragma unroll
+                    for (int r = 0; r < MR; r++) {
+                        uint32_t w = q == 0 ? c[it][m][r].x : q == 1 ? c[it][m][r].y
+                                   : q == 2 ? c[it][m][r].z : c[it][m][r].w;
+                        // converted per input: hoisting the conversions out
+                        // of the input loop would hold every row's 32 floats
+                        asm volatile("" : "+v"(w));
+                        const f2 v0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 0);
+                        const f2 v1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 1);
+                        const f2 v2 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 2);
+                        const f2 v3 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 3);
+                        float d = dot[m][r];
+                        d = fmaf(v0.x, xa.x, d); d = fmaf(v0.y, xa.y, d);
+                        d = fmaf(v1.x, xa.z, d); d = fmaf(v1.y, xa.w, d);
+                        d = fmaf(v2.x, xc.x, d); d = fmaf(v2.y, xc.y, d);
+                        d = fmaf(v3.x, xc.z, d); d = fmaf(v3.y, xc.w, d);
+                        dot[m][r] = d;
+                    }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+#pragma unroll
+            for (int m = 0; m < NM; m++)
+#pragma unroll
+                for (int r = 0; r < MR; r++) {
+                    const float v = fmaf(dot[m][r], sc[it][m][r], acc[m][r]);
+                    acc[m][r] = live ? v : acc[m][r];
                 }
-            }
         }
+        done(i, acc);
     }
 }
 
-__global__ __launch_bounds__(WAVES * 64) void moe_down_kernel(MoeArgs a) {
-    const Route* rt = a.route;
-    const int slot = blockIdx.x / a.tiles_dn, tile = blockIdx.x % a.tiles_dn;
-    if (slot >= a.ntok * a.k || !rt->owner[slot]) return;
-    const int e = rt->idx[slot / a.k][slot % a.k];
-    const MxExpert ex = a.experts[e];
-    const int nb = (a.eid + 31) / 32;
-    const MxMat dm = {ex.dc, ex.ds, a.hidden, a.eid, nb};
-    const int ntl = rt->ntl[slot];
-    const int* tl = rt->tl[slot];
-    auto xf = [&](int t) { return (const float*)(a.h + (size_t)tl[t] * a.eid); };
+// Stage a work item's input vectors (n rows of `cols` floats, row i at
+// src(i)) into LDS, each zero-padded to `pad` (whole 32-element blocks).
+template <typename SRC>
+__device__ __forceinline__ void stage_inputs(float* xs, int n, int cols, int pad, SRC src) {
+    for (int i = 0; i < n; i++) {
+        const float4* s4 = reinterpret_cast<const float4*>(src(i));
+        float4* d4 = reinterpret_cast<float4*>(xs + (size_t)i * pad);
+#pragma unroll 4
+        for (int j = threadIdx.x; j < pad / 4; j += blockDim.x)
+            d4[j] = j < cols / 4 ? s4[j] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+}
+
+// Routing once per step: one wave per token, then the distinct-expert list
+// (one launch of MAX_TOK waves; the expert kernels read the result).
+__global__ __launch_bounds__(MAX_TOK * 64) void moe_route_kernel(MoeArgs a) {
+    __shared__ int s_idx[MAX_SLOTS];
+    __shared__ float s_w[MAX_SLOTS];
+    const int t = threadIdx.x >> 6;
+    if (t < a.ntok) route_token(a.logits + (size_t)t * a.n_exp, a.n_exp, a.k, a.norm, t, s_idx, s_w);
+    __syncthreads();
+    if (t != 0) return;
+    const int lane = threadIdx.x, ns = a.ntok * a.k;
+    Route& rt = *a.route;
+    if (lane < ns) {
+        rt.idx[lane] = s_idx[lane];
+        rt.w[lane] = s_w[lane];
+    }
+    build_work(s_idx, ns, rt);
+}
+
+// Gate/up: workgroup (x, y) computes rows of row tile x of the gate and up
+// matrices of distinct expert y for the tokens that picked it:
+// h[slot] = act(gate + b) * (up + b).
+template <int NI>
+__global__ __launch_bounds__(WAVES * 64) void moe_gate_up_kernel(MoeArgs a) {
+    extern __shared__ __align__(16) float xs[];           // [n][hidden, padded]
+    if ((int)blockIdx.y >= a.route->nwork) return;
+    const Work& wk = a.route->work[blockIdx.y];
+    const MxExpert ex = a.experts[wk.expert];
+    const int nb = (a.hidden + 31) / 32;
+    const MxMat mat[2] = {{ex.gc, ex.gs, a.eid, a.hidden, nb}, {ex.uc, ex.us, a.eid, a.hidden, nb}};
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int lpg = pick_lpg(nb), grp = lane / lpg, lig = lane % lpg;
-    const int rows_per_wave = (64 / lpg) * R;
-    const int row0 = tile * WAVES * rows_per_wave + wave * rows_per_wave + grp * R;
-    float rs[R][MAXT];
-    zero_rs(rs);
-    mx_rows(dm, ntl, xf, row0, lig, lpg, rs);
+    const int lig = lane & 31;
+    constexpr int MR = kMR<2>;
+    const int row0 = blockIdx.x * (WAVES * 2 * MR) + wave * 2 * MR + (lane >> 5) * MR;
+    auto stage = [&]() {
+        stage_inputs(xs, wk.n, a.hidden, 32 * nb, [&](int i) { return a.x + (size_t)(wk.slot[i] / a.k) * a.hidden; });
+        __syncthreads();
+    };
+    mx_tile<2, NI, MR>(mat, xs, wk.n, row0, lig, stage, [&](int i, const float (&acc)[2][MR]) {
+        const int s2 = wk.slot[i];
 #pragma unroll
-    for (int i = 0; i < MAXT; i++) {
-        if (i < ntl) {
-            float* y = a.d + (size_t)tl[i] * a.hidden;
-#pragma unroll
-            for (int r = 0; r < R; r++) {
-                const float v = qsf::group_sum(rs[r][i], lpg);
-                const int row = row0 + r;
-                if (lig == (r & (lpg - 1)) && row < a.hidden)
-                    y[row] = ex.db ? v + qsf::f16_bits(ex.db[row]) : v;
+        for (int r = 0; r < MR; r++) {
+            const float gv = qsf::group_sum_last(acc[0][r], 32);
+            const float uv = qsf::group_sum_last(acc[1][r], 32);
+            const int row = row0 + r;
+            if (lig == 31 && row < a.eid) {
+                float gg = gv, uu = uv;
+                if (ex.gb) gg += qsf::f16_bits(ex.gb[row]);
+                if (ex.ub) uu += qsf::f16_bits(ex.ub[row]);
+                a.h[(size_t)s2 * a.eid + row] = act_fn(a.act, gg) * uu;
             }
         }
-    }
+    });
 }
 
-// out[t] = sum over the token's experts, in rank order, of w * down
-// (src/engine.c:1021, 1104-1106).
+// Down: workgroup (x, y) computes rows of row tile x of expert y's down
+// matrix for its slots, d[slot] = down h[slot] + b.
+template <int NI>
+__global__ __launch_bounds__(WAVES * 64) void moe_down_kernel(MoeArgs a) {
+    extern __shared__ __align__(16) float xs[];           // [n][eid, padded]
+    if ((int)blockIdx.y >= a.route->nwork) return;
+    const Work& wk = a.route->work[blockIdx.y];
+    const int n = wk.n;
+    const MxExpert ex = a.experts[wk.expert];
+    const int nb = (a.eid + 31) / 32;
+    const MxMat mat[1] = {{ex.dc, ex.ds, a.hidden, a.eid, nb}};
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lig = lane & 31;
+    constexpr int MR = kMR<1>;
+    const int row0 = blockIdx.x * (WAVES * 2 * MR) + wave * 2 * MR + (lane >> 5) * MR;
+    auto stage = [&]() {
+        stage_inputs(xs, n, a.eid, 32 * nb, [&](int i) { return (const float*)(a.h + (size_t)wk.slot[i] * a.eid); });
+        __syncthreads();
+    };
+    mx_tile<1, NI, MR>(mat, xs, n, row0, lig, stage, [&](int i, const float (&acc)[1][MR]) {
+        float* y = a.d + (size_t)wk.slot[i] * a.hidden;
+#pragma unroll
+        for (int r = 0; r < MR; r++) {
+            const float v = qsf::group_sum_last(acc[0][r], 32);
+            const int row = row0 + r;
+            if (lig == 31 && row < a.hidden) y[row] = ex.db ? v + qsf::f16_bits(ex.db[row]) : v;
+        }
+    });
+}
+
+// out[t] = sum over the token's ranks of w * d (src/engine.c:1021,
+// 1104-1106); slots without an expert are skipped.
 __global__ void moe_combine_kernel(MoeArgs a) {
     const Route& rt = *a.route;
     const int t = blockIdx.y;
@@ -327,10 +489,23 @@ __global__ void moe_combine_kernel(MoeArgs a) {
     if (i >= a.hidden) return;
     float acc = 0.0f;
     for (int q = 0; q < a.k; q++) {
-        if (rt.idx[t][q] < 0) continue;
-        acc += rt.w[t][q] * a.d[(size_t)(t * a.k + q) * a.hidden + i];
+        if (rt.idx[t * a.k + q] < 0) continue;
+        acc += rt.w[t * a.k + q] * a.d[(size_t)(t * a.k + q) * a.hidden + i];
     }
     a.out[(size_t)t * a.hidden + i] = acc;
+}
+
+// Launch with `lds` bytes of dynamic LDS; the first launch of an
+// instantiation allows it up to 160 KB (inputs of 8 tokens exceed 64 KB).
+template <auto K>
+void launch_lds(dim3 g, dim3 b, size_t lds, hipStream_t s, const MoeArgs& a) {
+    static bool allowed = false;
+    if (!allowed) {
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(K),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024 - 8192);
+        allowed = true;
+    }
+    hipLaunchKernelGGL(K, g, b, lds, s, a);
 }
 
 }  // namespace
@@ -349,19 +524,19 @@ extern "C" int qk_mxfp4_gemv(const qsf_hip_tensor* t, const float* d_x, int ntok
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
+// Workspace: routing | h [MAX_TOK*MAX_K][eid] | d [MAX_TOK*MAX_K][hidden].
+static size_t al256(size_t v) { return (v + 255) & ~(size_t)255; }
+
 extern "C" size_t qk_moe_ws_bytes(int n_exp, int k, int ntok, int hidden, int eid) {
-    (void)n_exp;
-    size_t r = (sizeof(Route) + 255) & ~(size_t)255;
-    size_t h = ((size_t)ntok * k * eid * 4 + 255) & ~(size_t)255;
-    size_t d = ((size_t)ntok * k * hidden * 4 + 255) & ~(size_t)255;
-    return r + h + d;
+    (void)n_exp; (void)k; (void)ntok;
+    return al256(sizeof(Route)) + al256((size_t)MAX_SLOTS * eid * 4) + al256((size_t)MAX_SLOTS * hidden * 4);
 }
 
 extern "C" int qk_moe_launch(const qk_mx_expert* d_experts, int n_exp, int k, int norm, int act,
                              int hidden, int eid, int ntok, const float* d_x,
                              const float* d_logits, float* d_out, void* d_ws, hipStream_t s) {
     if (ntok < 1 || ntok > MAX_TOK || k < 1 || k > MAX_K || n_exp < 1 || n_exp > MAX_EXP ||
-        hidden < 1 || eid < 1 || (hidden % 4) || (eid % 4))
+        hidden < 1 || eid < 1 || (hidden % 4) || (eid % 4) || hidden > 4096 || eid > 4096)
         return -2;
     MoeArgs a = {};
     a.experts = d_experts;
@@ -370,21 +545,31 @@ extern "C" int qk_moe_launch(const qk_mx_expert* d_experts, int n_exp, int k, in
     a.x = d_x; a.logits = d_logits; a.out = d_out;
     uint8_t* ws = (uint8_t*)d_ws;
     a.route = (Route*)ws;
-    size_t r = (sizeof(Route) + 255) & ~(size_t)255;
-    a.h = (float*)(ws + r);
-    a.d = (float*)(ws + r + (((size_t)ntok * k * eid * 4 + 255) & ~(size_t)255));
-    auto tiles = [](int rows, int cols) {
-        int nb = (cols + 31) / 32, lpg = 1;
-        while (lpg < nb && lpg < 64) lpg <<= 1;
-        const int rpw = WAVES * (64 / lpg) * R;
-        return (rows + rpw - 1) / rpw;
-    };
-    a.tiles_gu = tiles(eid, hidden);
-    a.tiles_dn = tiles(hidden, eid);
-    const int slots = ntok * k;
-    hipLaunchKernelGGL(moe_gate_up_kernel, dim3(slots * a.tiles_gu), dim3(WAVES * 64), 0, s, a);
-    hipLaunchKernelGGL(moe_down_kernel, dim3(slots * a.tiles_dn), dim3(WAVES * 64), 0, s, a);
+    ws += al256(sizeof(Route));
+    a.h = (float*)ws;
+    ws += al256((size_t)MAX_SLOTS * eid * 4);
+    a.d = (float*)ws;
+    // work items: distinct experts, at most min(n_exp, ntok*k)
+    const int items = ntok * k < n_exp ? ntok * k : n_exp;
+    const dim3 block(WAVES * 64);
+    constexpr int rows_gu = WAVES * 2 * kMR<2>;
+    constexpr int rows_dn = WAVES * 2 * kMR<1>;
+    const dim3 g_gu((eid + rows_gu - 1) / rows_gu, items), g_dn((hidden + rows_dn - 1) / rows_dn, items);
+    hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(MAX_TOK * 64), 0, s, a);
+    const size_t lds_gu = (size_t)ntok * ((hidden + 31) / 32) * 128, lds_dn = (size_t)ntok * ((eid + 31) / 32) * 128;
+    const int ni_gu = (hidden + 1023) / 1024, ni_dn = (eid + 1023) / 1024;
+    switch (ni_gu) {
+    case 1: launch_lds<moe_gate_up_kernel<1>>(g_gu, block, lds_gu, s, a); break;
+    case 2: launch_lds<moe_gate_up_kernel<2>>(g_gu, block, lds_gu, s, a); break;
+    case 3: launch_lds<moe_gate_up_kernel<3>>(g_gu, block, lds_gu, s, a); break;
+    default: launch_lds<moe_gate_up_kernel<4>>(g_gu, block, lds_gu, s, a); break;
+    }
+    switch (ni_dn) {
+    case 1: launch_lds<moe_down_kernel<1>>(g_dn, block, lds_dn, s, a); break;
+    case 2: launch_lds<moe_down_kernel<2>>(g_dn, block, lds_dn, s, a); break;
+    case 3: launch_lds<moe_down_kernel<3>>(g_dn, block, lds_dn, s, a); break;
+    default: launch_lds<moe_down_kernel<4>>(g_dn, block, lds_dn, s, a); break;
+    }
     hipLaunchKernelGGL(moe_combine_kernel, dim3((hidden + 255) / 256, ntok), dim3(256), 0, s, a);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
-

@@ -30,6 +30,20 @@ __device__ __forceinline__ float group_sum(float v, int width) {
     for (int off = width >> 1; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
     return v;
 }
+// Sum over groups of `width` consecutive lanes (power of two, <= 64) with
+// DPP; the group's total lands in its last lane (others hold partials).
+__device__ __forceinline__ float group_sum_last(float v, int width) {
+#define QSF_DPPF(x, ctrl, rmask) \
+    __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, (x)), (ctrl), (rmask), 0xF, false))
+    if (width >= 2) v += QSF_DPPF(v, 0xB1, 0xF);     // quad_perm [1,0,3,2]
+    if (width >= 4) v += QSF_DPPF(v, 0x4E, 0xF);     // quad_perm [2,3,0,1]
+    if (width >= 8) v += QSF_DPPF(v, 0x141, 0xF);    // row_half_mirror
+    if (width >= 16) v += QSF_DPPF(v, 0x140, 0xF);   // row_mirror
+    if (width >= 32) v += QSF_DPPF(v, 0x142, 0xA);   // row_bcast15 into rows 1, 3
+    if (width >= 64) v += QSF_DPPF(v, 0x143, 0xC);   // row_bcast31 into rows 2, 3
+#undef QSF_DPPF
+    return v;
+}
 __device__ __forceinline__ float wave_max(float v) {
     for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
     return v;

@@ -639,6 +639,7 @@ qsf_hip_moe* qsf_hip_moe_create(int n_exp, int hidden, int eid,
     m->n_exp = n_exp; m->hidden = hidden; m->eid = eid;
     m->ws_bytes = qk_moe_ws_bytes(n_exp, 8, 8, hidden, eid);
     if (!rc && hipMalloc(&m->d_ws, m->ws_bytes) != hipSuccess) rc = 1;
+
     if (rc) {
         if (m->d_ws) hipFree(m->d_ws);
         hipFree(m->d_alloc);

@@ -128,3 +128,30 @@ def test_moe_tie_keeps_lower_expert(hip, oracle):
     out = torch.zeros((1, hidden), device="cuda:0")
     moe.forward(k, 1, 2, 1, dev(x), dev(logits), out, stream=_stream())
     assert rel_l2(host(out)[0], ref) <= REL_L2
+
+
+def test_moe_repeated_calls_reuse_workspace(hip, oracle):
+    """One expert table, calls with different token counts and K in a row:
+    the workspace (routing, per-tile completion counters) is reused and
+    every call must still match the oracle."""
+    torch = torch_cuda()
+    rng = np.random.default_rng(7)
+    n_exp, hidden, eid = 8, 256, 512
+    ex = _experts(rng, n_exp, hidden, eid, True)
+    tens = {n: [hip.Tensor(e[n], F.MXFP4, *((eid, hidden) if n != "down" else (hidden, eid)), 32)
+                for e in ex] for n in ("gate", "up", "down")}
+    biases = {n: [e[n] for e in ex] for n in ("gate_bias", "up_bias", "down_bias")}
+    moe = hip.Moe(tens["gate"], tens["up"], tens["down"], hidden, eid, **biases)
+    for ntok, k in ((8, 4), (1, 2), (5, 3), (8, 8), (2, 1)):
+        x = F.gaussian(rng, (ntok, hidden))
+        logits = F.gaussian(rng, (ntok, n_exp))
+        out = torch.full((ntok, hidden), float("nan"), device="cuda:0")
+        moe.forward(k, 1, 2, ntok, dev(x), dev(logits), out, stream=_stream())
+        got = host(out)
+        for t in range(ntok):
+            ref = oracle.moe_token(ex, k, 1, 2, hidden, eid, x[t], logits[t])
+            assert rel_l2(got[t], ref) <= REL_L2, (ntok, k, t)
+    moe.free()
+    for ts in tens.values():
+        for t in ts:
+            t.free()
