@@ -699,18 +699,6 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
 #pragma unroll
     for (int k = 0; k < D; k++) issue(wv[k]);
 
-    // 4. first outlier entry of every row for this lane (packed tables)
-    uint32_t e0[MAXT][R];
-    if constexpr (OUT) {
-        const bool pk = OE != nullptr;
-#pragma unroll
-        for (int j = 0; j < MAXT; j++) {
-            const uint32_t* oe = pk ? OE : own_of(j);
-#pragma unroll
-            for (int r = 0; r < R; r++) e0[j][r] = oe[pk ? min(rpv[j][r] + lig, last) : 0u];
-        }
-    }
-
     // 5. LDS: prepared digits, meta and x as loaded; or the digits and meta
     //    of every block prepared here, with x copied alongside for the
     //    outliers.  Passes after the first load their x now, behind the
@@ -746,6 +734,21 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
         }
     }
     __syncthreads();
+
+    // 4. first outlier entry of every row for this lane (packed tables).
+    //    Their addresses come from the CSR bounds loaded in step 2: issued
+    //    here, after the preparation, that round trip overlaps the digit
+    //    work instead of holding it up; they are first used at a tile's end.
+    uint32_t e0[MAXT][R];
+    if constexpr (OUT) {
+        const bool pk = OE != nullptr;
+#pragma unroll
+        for (int j = 0; j < MAXT; j++) {
+            const uint32_t* oe = pk ? OE : own_of(j);
+#pragma unroll
+            for (int r = 0; r < R; r++) e0[j][r] = oe[pk ? min(rpv[j][r] + lig, last) : 0u];
+        }
+    }
 
     // 7. item loop.  At a tile's end the first outlier entry of each row joins
     //    the lane sums (src/quant.c:481-494, fp64 value * x[col]), the row is

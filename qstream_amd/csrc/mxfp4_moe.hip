@@ -215,8 +215,8 @@ struct MoeArgs {
 // p > -1e30 (NaN never qualifies), which is the order the strict '>'
 // insertion from a -1e30 start produces; then optional renormalisation by
 // the rank-ordered sum.
-constexpr int RJ = MAX_EXP / 64;          // experts per lane
-
+// RJ experts per lane: 1 for up to 64 experts, else MAX_EXP / 64.
+template <int RJ>
 __device__ void route_token(const float* __restrict__ lg, int n, int k, int norm, int t,
                             int* s_idx, float* s_w) {
     const int lane = threadIdx.x & 63;
@@ -402,7 +402,10 @@ __global__ __launch_bounds__(MAX_TOK * 64) void moe_route_kernel(MoeArgs a) {
     __shared__ int s_idx[MAX_SLOTS];
     __shared__ float s_w[MAX_SLOTS];
     const int t = threadIdx.x >> 6;
-    if (t < a.ntok) route_token(a.logits + (size_t)t * a.n_exp, a.n_exp, a.k, a.norm, t, s_idx, s_w);
+    if (t < a.ntok) {
+        if (a.n_exp <= 64) route_token<1>(a.logits + (size_t)t * a.n_exp, a.n_exp, a.k, a.norm, t, s_idx, s_w);
+        else route_token<MAX_EXP / 64>(a.logits + (size_t)t * a.n_exp, a.n_exp, a.k, a.norm, t, s_idx, s_w);
+    }
     __syncthreads();
     if (t != 0) return;
     const int lane = threadIdx.x, ns = a.ntok * a.k;
