@@ -294,6 +294,11 @@ __device__ void build_work(const int* s_idx, int ns, Route& rt) {
     if (lane == 0) rt.nwork = __popcll(owners);
 }
 
+// LDS pitch of one staged 32-element block, in floats: 4 floats of padding
+// put the blocks that neighbouring lanes read 16 bytes apart in the banks
+// (at a 128-byte pitch eight lanes of a 16-byte read hit the same banks).
+constexpr int XBP = 36;
+
 // Expert GEMV tile: NM matrices with the same shape ([rows][cols] MXFP4)
 // against the inputs xs[i] (LDS, i < n) of one work item.  A 32-lane group
 // owns MR consecutive rows; lane l reads blocks l, l+32, ... of each row, so
@@ -336,8 +341,8 @@ __device__ __forceinline__ void mx_tile(const MxMat (&mat)[NM], const float* xs,
             const int b = lig + 32 * it;
             // inputs are zero-padded to whole blocks in LDS; lanes past the
             // last block add nothing
-            const float4* x4 = reinterpret_cast<const float4*>(xs + (size_t)i * 32 * mat[0].nb +
-                                                               32 * min(b, mat[0].nb - 1));
+            const float4* x4 = reinterpret_cast<const float4*>(xs + (size_t)i * XBP * mat[0].nb +
+                                                               XBP * min(b, mat[0].nb - 1));
             const bool live = b < mat[0].nb;
             float dot[NM][MR];
 #pragma unroll
@@ -384,15 +389,16 @@ __device__ __forceinline__ void mx_tile(const MxMat (&mat)[NM], const float* xs,
 }
 
 // Stage a work item's input vectors (n rows of `cols` floats, row i at
-// src(i)) into LDS, each zero-padded to `pad` (whole 32-element blocks).
+// src(i)) into LDS as nb blocks of XBP floats, zero past cols.
 template <typename SRC>
-__device__ __forceinline__ void stage_inputs(float* xs, int n, int cols, int pad, SRC src) {
+__device__ __forceinline__ void stage_inputs(float* xs, int n, int cols, int nb, SRC src) {
     for (int i = 0; i < n; i++) {
         const float4* s4 = reinterpret_cast<const float4*>(src(i));
-        float4* d4 = reinterpret_cast<float4*>(xs + (size_t)i * pad);
+        float* d = xs + (size_t)i * nb * XBP;
 #pragma unroll 4
-        for (int j = threadIdx.x; j < pad / 4; j += blockDim.x)
-            d4[j] = j < cols / 4 ? s4[j] : make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int j = threadIdx.x; j < nb * 8; j += blockDim.x)
+            *reinterpret_cast<float4*>(d + (j >> 3) * XBP + 4 * (j & 7)) =
+                j < cols / 4 ? s4[j] : make_float4(0.f, 0.f, 0.f, 0.f);
     }
 }
 
@@ -433,7 +439,7 @@ __global__ __launch_bounds__(WAVES * 64) void moe_gate_up_kernel(MoeArgs a) {
     constexpr int MR = kMR<2>;
     const int row0 = blockIdx.x * (WAVES * 2 * MR) + wave * 2 * MR + (lane >> 5) * MR;
     auto stage = [&]() {
-        stage_inputs(xs, wk.n, a.hidden, 32 * nb, [&](int i) { return a.x + (size_t)(wk.slot[i] / a.k) * a.hidden; });
+        stage_inputs(xs, wk.n, a.hidden, nb, [&](int i) { return a.x + (size_t)(wk.slot[i] / a.k) * a.hidden; });
         __syncthreads();
     };
     mx_tile<2, NI, MR>(mat, xs, wk.n, row0, lig, stage, [&](int i, const float (&acc)[2][MR]) {
@@ -469,7 +475,7 @@ __global__ __launch_bounds__(WAVES * 64) void moe_down_kernel(MoeArgs a) {
     constexpr int MR = kMR<1>;
     const int row0 = blockIdx.x * (WAVES * 2 * MR) + wave * 2 * MR + (lane >> 5) * MR;
     auto stage = [&]() {
-        stage_inputs(xs, n, a.eid, 32 * nb, [&](int i) { return (const float*)(a.h + (size_t)wk.slot[i] * a.eid); });
+        stage_inputs(xs, n, a.eid, nb, [&](int i) { return (const float*)(a.h + (size_t)wk.slot[i] * a.eid); });
         __syncthreads();
     };
     mx_tile<1, NI, MR>(mat, xs, n, row0, lig, stage, [&](int i, const float (&acc)[1][MR]) {
@@ -559,7 +565,8 @@ extern "C" int qk_moe_launch(const qk_mx_expert* d_experts, int n_exp, int k, in
     constexpr int rows_dn = WAVES * 2 * kMR<1>;
     const dim3 g_gu((eid + rows_gu - 1) / rows_gu, items), g_dn((hidden + rows_dn - 1) / rows_dn, items);
     hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(MAX_TOK * 64), 0, s, a);
-    const size_t lds_gu = (size_t)ntok * ((hidden + 31) / 32) * 128, lds_dn = (size_t)ntok * ((eid + 31) / 32) * 128;
+    const size_t lds_gu = (size_t)ntok * ((hidden + 31) / 32) * XBP * 4,
+                 lds_dn = (size_t)ntok * ((eid + 31) / 32) * XBP * 4;
     const int ni_gu = (hidden + 1023) / 1024, ni_dn = (eid + 1023) / 1024;
     switch (ni_gu) {
     case 1: launch_lds<moe_gate_up_kernel<1>>(g_gu, block, lds_gu, s, a); break;
