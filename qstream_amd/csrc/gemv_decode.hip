@@ -9,16 +9,16 @@
 //   sum_k (s*q_k + z) x_k = s * sum_k q_k x_k + z * sum_k x_k
 // and the code/activation products are done exactly in integers: each block
 // of x becomes block-fixed-point integers X_k = x_k*2^sh (|X| <= 2^XB,
-// XB = 24..26 bits) split into seven signed base-16 digits.  The GEMV
-// multiplies raw code nibbles by digit nibbles with v_dot8_i32_i4 (8 exact
-// products per instruction), recombines the digits per block in two exact
-// int32 groups (digits 0-3 and 4-6), joins them exactly in fp64 and adds
-// s * sum q X + z' * sum X into an fp64 row sum (the block's fp64 meta holds
-// the power-of-two rescale).  The one rounding before the final fp32 store
-// is x -> X, at most 2^-(XB+1) of the block's max |x| -- finer than fp32
-// itself for the block's largest elements, so even a row whose result
-// cancels 100x stays inside the 1e-5 bar against the strict scalar
-// reference.
+// XB = 22 bits, 20 for 3-bit) split into six signed base-16 digits.  The
+// GEMV multiplies raw code nibbles by digit nibbles with v_dot8_i32_i4 (8
+// exact products per instruction), recombines the digits per block in two
+// exact int32 groups (digits 0-2 and 3-5), converts each exactly to fp32,
+// joins them and adds s * sum q X + z' * sum X into an fp32 row sum (the
+// block's meta holds the power-of-two rescale).  The roundings are x -> X
+// (at most 2^-(XB+1) of the block's max |x|) and those of fp32 arithmetic on
+// block partial sums, the same order as the reference's own fp32
+// accumulation; for normal-distributed x the result sits within about 1e-6
+// relative L2 of the fp64 value, an order inside the 1e-5 bar.
 //
 // Code unpacking is pure masking, chosen so each nibble holds one signed
 // 4-bit value that the digit tables pair with the right x:
@@ -43,7 +43,7 @@
 // blocks ahead, with no loads or stores inside conditionals (the compiler's
 // wait counts stay exact); row sums go to an LDS stash and are stored at the
 // end.  A fused CSR pass adds the fp16 outliers of each tile's rows; partial
-// sums are reduced with DPP in fp64.
+// sums are reduced with DPP.
 #include "qsf_device.h"
 #include "qsf_hip_internal.h"
 
@@ -53,9 +53,9 @@
 
 namespace {
 
-constexpr int ND = 7;                  // balanced base-16 digits per multiplier
-constexpr int ND_LO = 4;               // digits 0-3 and 4-6 are recombined separately
-constexpr uint32_t DIGIT_BIAS = 0x8888888u;  // 8 * (16^7 - 1) / 15
+constexpr int ND = 6;                  // balanced base-16 digits per multiplier
+constexpr int ND_LO = 3;               // digits 0-2 and 3-5 are recombined separately
+constexpr uint32_t DIGIT_BIAS = 0x888888u;   // 8 * (16^6 - 1) / 15
 constexpr int WAVES = 16;              // waves per GEMV workgroup
 constexpr int MAXT = 4;                // tiles per wave (compile-time bound)
 constexpr int kLdsBudget = 64 * 1024;  // block digits + meta held at once
@@ -67,6 +67,7 @@ constexpr int pow2ceil(int v) { return v <= 1 ? 1 : 2 * pow2ceil((v + 1) / 2); }
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef f32x4 f32x4_a4 __attribute__((aligned(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef u32x4 u32x4_a4 __attribute__((aligned(4)));
 
 template <int FMT, int BS>
 struct Fmt {
@@ -79,10 +80,10 @@ struct Fmt {
     static constexpr int DWS = DW | 1;                              // odd LDS stride
     static constexpr int LPB = pow2ceil(CW);                        // x-prep lanes / block
     // |X| <= 2^XB.  Digit multipliers M = X * 2^shift (shift <= 2 for 3-bit)
-    // must lie in the 7-digit balanced range [-0x8888888, 0x7777777]; the
-    // low-group sum is <= 8 * 34952 * BS and the high-group sum
-    // <= 8 * (2^(XB+2)/65536 + 1) * BS, both far inside int32.
-    static constexpr int XB = FMT == QK_FMT_3 ? 24 : 26;
+    // must lie in the 6-digit balanced range [-0x888888, 0x777777].  A
+    // digit sum over a block is at most 8 * 8 * BS <= 2^14 in magnitude, so
+    // each 3-digit group sum stays below 273 * 2^14 < 2^23: exact in fp32.
+    static constexpr int XB = FMT == QK_FMT_3 ? 20 : 22;
 };
 
 // 3-bit masks for code dword w with w % 3 == k.  Nibble g = 8w + i has
@@ -119,7 +120,7 @@ __device__ __forceinline__ void slot_code(int w, int c, int m, int& code, int& s
     } else { code = 8 * w + m; shift = 0; }
 }
 
-// Eight 28-bit biased multipliers U[m] -> seven digit words: nibble m of
+// Eight 24-bit biased multipliers U[m] -> six digit words: nibble m of
 // word d = nibble d of U[m], re-biased to two's complement (n - 8).
 __device__ __forceinline__ void digit_words(const uint32_t (&U)[8], uint32_t (&out)[ND]) {
     uint32_t P[4], Q[4];
@@ -141,10 +142,10 @@ __device__ __forceinline__ void digit_words(const uint32_t (&U)[8], uint32_t (&o
     out[0] = __builtin_amdgcn_perm(pb0, pa0, 0x05040100u) ^ 0x88888888u;
     out[2] = __builtin_amdgcn_perm(pb0, pa0, 0x07060302u) ^ 0x88888888u;
     out[4] = __builtin_amdgcn_perm(pb1, pa1, 0x05040100u) ^ 0x88888888u;
-    out[6] = __builtin_amdgcn_perm(pb1, pa1, 0x07060302u) ^ 0x88888888u;
     out[1] = __builtin_amdgcn_perm(qb0, qa0, 0x05040100u) ^ 0x88888888u;
     out[3] = __builtin_amdgcn_perm(qb0, qa0, 0x07060302u) ^ 0x88888888u;
     out[5] = __builtin_amdgcn_perm(qb1, qa1, 0x05040100u) ^ 0x88888888u;
+    (void)pb1;
 }
 
 // x preparation for one block b by a group of LPB lanes (lane w owns code
@@ -256,11 +257,11 @@ __device__ __forceinline__ void prep_settle(int b, bool live, int w, int cols,
     }
 }
 
-// Block meta: f = 2^-sh and sx = f * sum_k X_k, both exact in fp64.
+// Block meta: f = 2^-sh (exact) and sx = f * sum_k X_k (rounded once), fp32.
 // xs (optional): the lane's x values copied to LDS (columns < cols).
 template <int FMT, int BS>
 __device__ __forceinline__ void prep_finish(const float (&xv)[Fmt<FMT, BS>::NC * 8], int b,
-                                            bool live, int w, uint32_t* dst, double2* meta,
+                                            bool live, int w, uint32_t* dst, float2* meta,
                                             float* xs = nullptr, int cols = 0) {
     using F = Fmt<FMT, BS>;
     constexpr int NS = F::NC * 8;
@@ -291,7 +292,7 @@ __device__ __forceinline__ void prep_finish(const float (&xv)[Fmt<FMT, BS>::NC *
     int sh = 0;
     if (amax > 0.0f) {
         sh = F::XB - 1 - ilogbf(amax);                 // amax * 2^sh < 2^XB
-        sh = sh > 126 ? 126 : (sh < -100 ? -100 : sh);
+        sh = sh > 126 ? 126 : sh;                      // f = 2^-sh stays a normal fp32
     }
     uint32_t U[NS];
     int sum = 0;
@@ -308,7 +309,7 @@ __device__ __forceinline__ void prep_finish(const float (&xv)[Fmt<FMT, BS>::NC *
             sum += X;
         }
     }
-    // per-lane |sum| <= NS * 2^XB < 2^31; the block total (up to 2^34) in fp64
+    // per-lane |sum| <= NS * 2^XB < 2^31; the block total (up to 2^30) in fp64
     double dsum = (double)sum;
 #pragma unroll
     for (int off = F::LPB / 2; off > 0; off >>= 1) dsum += __shfl_xor(dsum, off, F::LPB);
@@ -324,15 +325,15 @@ __device__ __forceinline__ void prep_finish(const float (&xv)[Fmt<FMT, BS>::NC *
         }
     }
     if (live && w == 0) {
-        double f = ldexp(1.0, -sh);
-        if (bad) f = __builtin_nan("");
-        *meta = make_double2(f, dsum * f);
+        // f exact; sx = f * sum X rounded once (the fp64 product is exact)
+        const float f = bad ? __builtin_nanf("") : ldexpf(1.0f, -sh);
+        *meta = make_float2(f, (float)(dsum * ldexp(1.0, -sh)));
     }
 }
 
 template <int FMT, int BS>
 __device__ __forceinline__ void prep_block(const float* __restrict__ x, int cols, int b, bool live,
-                                           int w, uint32_t* dst, double2* meta,
+                                           int w, uint32_t* dst, float2* meta,
                                            float* xs = nullptr) {
     float xv[Fmt<FMT, BS>::NC * 8];
     prep_load<FMT, BS>(x, cols, b, live, w, xv);
@@ -343,7 +344,7 @@ __device__ __forceinline__ void prep_block(const float* __restrict__ x, int cols
 template <int FMT, int BS>
 __global__ __launch_bounds__(256) void xprep_kernel(const float* __restrict__ x, int cols, int nb,
                                                     uint32_t* __restrict__ xq,
-                                                    double2* __restrict__ xmeta) {
+                                                    float2* __restrict__ xmeta) {
     using F = Fmt<FMT, BS>;
     const int b = blockIdx.x * (256 / F::LPB) + threadIdx.x / F::LPB;
     const bool live = b < nb;
@@ -352,25 +353,9 @@ __global__ __launch_bounds__(256) void xprep_kernel(const float* __restrict__ x,
                         xmeta + bb);
 }
 
-// Group sum over `lpg` lanes (power of two) in fp64; the total is valid in
-// the group's last lane (all lanes for lpg <= 16).  Each DPP move carries one
-// half of the double; lanes a row mask leaves out read 0 (+0.0).
-#define QSF_DPP(v, ctrl, rmask)                                                              \
-    __builtin_bit_cast(double, make_int2(__builtin_amdgcn_update_dpp(                        \
-                                             0, __builtin_bit_cast(int2, (v)).x, (ctrl),      \
-                                             (rmask), 0xF, false),                            \
-                                         __builtin_amdgcn_update_dpp(                        \
-                                             0, __builtin_bit_cast(int2, (v)).y, (ctrl),      \
-                                             (rmask), 0xF, false)))
-__device__ __forceinline__ double group_reduce(double v, int lpg) {
-    if (lpg >= 2) v += QSF_DPP(v, 0xB1, 0xF);     // quad_perm [1,0,3,2]
-    if (lpg >= 4) v += QSF_DPP(v, 0x4E, 0xF);     // quad_perm [2,3,0,1]
-    if (lpg >= 8) v += QSF_DPP(v, 0x141, 0xF);    // row_half_mirror
-    if (lpg >= 16) v += QSF_DPP(v, 0x140, 0xF);   // row_mirror
-    if (lpg >= 32) v += QSF_DPP(v, 0x142, 0xA);   // row_bcast15 into rows 1, 3
-    if (lpg >= 64) v += QSF_DPP(v, 0x143, 0xC);   // row_bcast31 into rows 2, 3
-    return v;
-}
+// Group sum over `lpg` lanes (power of two) with DPP; the total is valid in
+// the group's last lane (all lanes for lpg <= 16).
+__device__ __forceinline__ float group_reduce(float v, int lpg) { return qsf::group_sum_last(v, lpg); }
 #undef QSF_DPP
 
 struct GemvArgs {
@@ -394,9 +379,9 @@ struct GemvArgs {
     } mat[QK_MAX_GROUP];
     int n, cols, nb, lpg, lpg_log2, chunk, tpw;
     int xs_off;                    // LDS dword offset of fp32 x (main kernel)
-    int st_off, st_wave;           // LDS dword offset / doubles per wave of the result stash
+    int st_off, st_wave;           // LDS dword offset / floats per wave of the result stash
     const uint32_t* xq;            // prepared digits (stride DWS), or null: prepare here
-    const double2* xmeta;
+    const float2* xmeta;
     const float* x;
 };
 
@@ -425,68 +410,81 @@ template <int FMT, int BS, int R>
 __device__ __forceinline__ void load_block(const uint8_t* __restrict__ w, const uint32_t (&roff)[R],
                                            int b, uint32_t (&wv)[R][1 + Fmt<FMT, BS>::CW]) {
     using F = Fmt<FMT, BS>;
+    constexpr int NW = 1 + F::CW;
+    // dwordx4 pieces, then single dwords: the address unit takes 4 lanes a
+    // clock whatever the width, so a 20-byte 2-bit block costs 2 load
+    // instructions instead of 5 (the compiler does not merge dword loads of
+    // 4-byte aligned blocks by itself)
 #pragma unroll
     for (int r = 0; r < R; r++) {
         const uint32_t* p = reinterpret_cast<const uint32_t*>(w + (roff[r] + (uint32_t)b * F::BB));
 #pragma unroll
-        for (int i = 0; i < 1 + F::CW; i++) wv[r][i] = __builtin_nontemporal_load(p + i);
+        for (int i = 0; i + 4 <= NW; i += 4) {
+            const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_a4*>(p + i));
+            wv[r][i] = v.x;
+            wv[r][i + 1] = v.y;
+            wv[r][i + 2] = v.z;
+            wv[r][i + 3] = v.w;
+        }
+#pragma unroll
+        for (int i = NW & ~3; i < NW; i++) wv[r][i] = __builtin_nontemporal_load(p + i);
     }
 }
 
-// Dequant-dot of one block for R rows: rs[r] += s*sum(q*x) + z*sum(x), the
-// integer digit sums joined exactly and the row sums accumulated in fp64.
+// Dequant-dot of one block for R rows: rs[r] += s*sum(q*x) + z*sum(x).  The
+// digit sums are exact integers; each 3-digit group (< 2^23) converts to fp32
+// exactly and the two join with one rounding, so the block's one rounding
+// beyond x -> X is that of fp32 arithmetic on its partial sums.
 template <int FMT, int BS, int R>
 __device__ __forceinline__ void compute_block(const uint32_t (&wv)[R][1 + Fmt<FMT, BS>::CW],
-                                              const uint32_t* __restrict__ dg, double2 xm,
-                                              double (&rs)[R]) {
+                                              const uint32_t* __restrict__ dg, float2 xm,
+                                              float (&rs)[R]) {
     using F = Fmt<FMT, BS>;
-    {
-        int acc[R][F::NA][ND];
-        auto step = [&](auto wic) {
-            constexpr int wi = decltype(wic)::value;
-            uint32_t dd[F::NC][ND];
+    int acc[R][F::NA][ND];
+    auto step = [&](auto wic) __attribute__((always_inline)) {
+        constexpr int wi = decltype(wic)::value;
+        uint32_t dd[F::NC][ND];
 #pragma unroll
-            for (int c = 0; c < F::NC; c++)
+        for (int c = 0; c < F::NC; c++)
 #pragma unroll
-                for (int d = 0; d < ND; d++) dd[c][d] = dg[(wi * F::NC + c) * ND + d];
-#pragma unroll
-            for (int r = 0; r < R; r++) {
-#pragma unroll
-                for (int c = 0; c < F::NC; c++) {
-                    const uint32_t nib = extract<FMT, wi>(wv[r][1 + wi], c);
-                    const int s = F::NA == 2 ? c : 0;
-                    const bool first = wi == 0 && (F::NA == 2 || c == 0);
-#pragma unroll
-                    for (int d = 0; d < ND; d++)
-                        acc[r][s][d] = qsf::sdot8(nib, dd[c][d], first ? 0 : acc[r][s][d]);
-                }
-            }
-        };
-        [&]<int... I>(std::integer_sequence<int, I...>) {
-            (step(std::integral_constant<int, I>{}), ...);
-        }(std::make_integer_sequence<int, F::CW>{});
-
+            for (int d = 0; d < ND; d++) dd[c][d] = dg[(wi * F::NC + c) * ND + d];
 #pragma unroll
         for (int r = 0; r < R; r++) {
-            double sf = 0.0;
 #pragma unroll
-            for (int s = 0; s < F::NA; s++) {
-                uint32_t lo = (uint32_t)acc[r][s][ND_LO - 1];
+            for (int c = 0; c < F::NC; c++) {
+                const uint32_t nib = extract<FMT, wi>(wv[r][1 + wi], c);
+                const int s = F::NA == 2 ? c : 0;
+                const bool first = wi == 0 && (F::NA == 2 || c == 0);
 #pragma unroll
-                for (int d = ND_LO - 2; d >= 0; d--) lo = (lo << 4) + (uint32_t)acc[r][s][d];
-                uint32_t hi = (uint32_t)acc[r][s][ND - 1];
-#pragma unroll
-                for (int d = ND - 2; d >= ND_LO; d--) hi = (hi << 4) + (uint32_t)acc[r][s][d];
-                const double v = fma((double)(int)hi, 65536.0, (double)(int)lo);   // exact
-                sf = s == 0 ? v : fma(0.25, v, sf);                                 // exact
+                for (int d = 0; d < ND; d++)
+                    acc[r][s][d] = qsf::sdot8(nib, dd[c][d], first ? 0 : acc[r][s][d]);
             }
-            const double sc = (double)qsf::f16_lo(wv[r][0]);
-            rs[r] = fma(sc * xm.x, sf, rs[r]);             // sc * 2^-sh is exact
-            if constexpr (FMT != QK_FMT_4SYM) {
-                double z = (double)qsf::f16_hi(wv[r][0]);
-                if constexpr (FMT == QK_FMT_4) z = fma(8.0, sc, z);   // exact
-                rs[r] = fma(z, xm.y, rs[r]);
-            }
+        }
+    };
+    [&]<int... I>(std::integer_sequence<int, I...>) {
+        (step(std::integral_constant<int, I>{}), ...);
+    }(std::make_integer_sequence<int, F::CW>{});
+
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        float sf = 0.0f;
+#pragma unroll
+        for (int s = 0; s < F::NA; s++) {
+            uint32_t lo = (uint32_t)acc[r][s][ND_LO - 1];
+#pragma unroll
+            for (int d = ND_LO - 2; d >= 0; d--) lo = (lo << 4) + (uint32_t)acc[r][s][d];
+            uint32_t hi = (uint32_t)acc[r][s][ND - 1];
+#pragma unroll
+            for (int d = ND - 2; d >= ND_LO; d--) hi = (hi << 4) + (uint32_t)acc[r][s][d];
+            const float v = fmaf((float)(int)hi, 4096.0f, (float)(int)lo);
+            sf = s == 0 ? v : fmaf(0.25f, v, sf);
+        }
+        const float sc = qsf::f16_lo(wv[r][0]);
+        rs[r] = fmaf(sc, sf * xm.x, rs[r]);                // sf * 2^-sh is exact
+        if constexpr (FMT != QK_FMT_4SYM) {
+            float z = qsf::f16_hi(wv[r][0]);
+            if constexpr (FMT == QK_FMT_4) z = fmaf(8.0f, sc, z);
+            rs[r] = fmaf(z, xm.y, rs[r]);
         }
     }
 }
@@ -495,7 +493,7 @@ __device__ __forceinline__ void compute_block(const uint32_t (&wv)[R][1 + Fmt<FM
 // here, or copy the ones a stand-alone x-prep launch left in global memory.
 template <int FMT, int BS>
 __device__ __forceinline__ void stage_x(const GemvArgs& a, int c0, int c1, uint32_t* dig,
-                                        double2* meta) {
+                                        float2* meta) {
     using F = Fmt<FMT, BS>;
     if (a.xq) {
         for (int i = threadIdx.x; i < (c1 - c0) * F::DWS; i += WAVES * 64)
@@ -526,7 +524,7 @@ __device__ __forceinline__ void tile_of(const GemvArgs& a, int t, int rows_per_t
 // group reduction and store of one finished tile (chunked path).
 template <int R>
 __device__ __forceinline__ void flush_tile(const GemvArgs& a, int m, int row0, int lig, int lpg,
-                                           double (&rs)[R]) {
+                                           float (&rs)[R]) {
     const int rows = a.rows[m];
     const uint32_t* rp = a.rp[m];
     if (rp) {
@@ -538,7 +536,7 @@ __device__ __forceinline__ void flush_tile(const GemvArgs& a, int m, int row0, i
                 for (uint32_t e = rp[row] + lig; e < e1; e += lpg) {
                     uint32_t col, val;
                     entry_at(a, m, e, col, val);
-                    rs[r] = fma((double)qsf::f16_bits(val), (double)a.x[col], rs[r]);
+                    rs[r] = fmaf(qsf::f16_bits(val), a.x[col], rs[r]);
                 }
             }
         }
@@ -546,9 +544,9 @@ __device__ __forceinline__ void flush_tile(const GemvArgs& a, int m, int row0, i
     float* __restrict__ y = a.y[m];
 #pragma unroll
     for (int r = 0; r < R; r++) {
-        const double v = group_reduce(rs[r], lpg);
-        if (lig == lpg - 1 && row0 + r < rows) y[row0 + r] = (float)v;
-        rs[r] = 0.0;
+        const float v = group_reduce(rs[r], lpg);
+        if (lig == lpg - 1 && row0 + r < rows) y[row0 + r] = v;
+        rs[r] = 0.0f;
     }
 }
 
@@ -563,14 +561,20 @@ __device__ __forceinline__ void flush_tile(const GemvArgs& a, int m, int row0, i
 // wait for everything in flight).  So every load up to the end of the item
 // loop is issued unconditionally -- past a wave's last item at its last
 // tile's row starts, for absent outlier tables at the group's own row -- and
-// no global store happens before the end: finished rows park fp64 sums in
+// no global store happens before the end: finished rows park their sums in
 // LDS.  The setup avoids chains of dependent scalar loads (kernel-argument
 // arrays are read with static indices) and integer divisions, since every
 // such step waits behind the weight stream once it is in flight.
-// Issue order: x (coalesced), prepared digits, outlier row pointers, the first
-// D weight items, the first outlier entry per lane and row; then the prep
-// arithmetic, the item loop (the first entries join the row sums before the
-// one reduction a row), the remaining outlier entries and the stores.
+// A wave64 memory instruction occupies the CU's address unit for about 16
+// clocks whatever its width, and at the start every wave of the CU queues
+// there: the prologue keeps the count of vector loads low (one CSR-bound load
+// a lane, one first-entry load a tile).
+// Issue order: outlier row pointers; in the prep waves x and the digit
+// arithmetic of the first pass (the other waves skip it); prepared digits
+// and x; the first D weight items; then the later prep passes, the barrier,
+// the first outlier entries of each tile, the item loop (the first entries
+// join the row sums before the one reduction a row), the remaining outlier
+// entries and the stores.
 template <int FMT, int BS, int R, int D, bool OUT, bool PREP>
 __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
     constexpr int XV = kXvMax;
@@ -578,8 +582,8 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
     using WV = uint32_t[R][1 + F::CW];
     constexpr int NT = WAVES * 64;
     extern __shared__ __align__(16) uint32_t lds[];
-    double2* meta = reinterpret_cast<double2*>(lds);          // nb x 16 B
-    uint32_t* dig = lds + 4 * a.nb;                           // nb x DWS dwords (+ pad to 4)
+    float2* meta = reinterpret_cast<float2*>(lds);            // nb x 8 B (+ pad to 16 B)
+    uint32_t* dig = lds + ((2 * a.nb + 3) & ~3);              // nb x DWS dwords (+ pad to 4)
     float* xs = reinterpret_cast<float*>(lds + a.xs_off);     // nb*BS floats, zero past cols
     // wave index made provably uniform: tile -> matrix lookups then stay in
     // scalar registers (kernel arguments via s_load, no vector-memory waits)
@@ -642,10 +646,23 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
         }
     };
 
-    // 1. Preparing here: the prep waves load the x of their first pass of
-    //    blocks (before any weights, so it returns first); the other waves
-    //    start with their weights.  Prepared digits: digits and meta, and for
-    //    the outliers x, as whole float4s (the host guarantees cols >= 4) plus
+    // 1. CSR bounds of the wave's rows, one load a lane: lane lig < NBND of
+    //    a row group loads bound lig of its group (tile lig / (R+1), row
+    //    lig % (R+1)); the host sends row groups of fewer lanes to the chunked
+    //    kernel.  Matrices without outliers read their own row.
+    uint32_t rpl = 0;
+    if constexpr (OUT) {
+        const bool has = RP != nullptr;
+        const int bj = min(lig / (R + 1), MAXT - 1), br = lig % (R + 1);
+        const uint32_t* rp = has ? RP : own_of(bj);
+        rpl = rp[has ? min(row_of(bj) + br, rows) : min(br, (int)F::BB / 4 - 1)];
+    }
+
+    // 2. Preparing here: the prep waves load the x of their first pass of
+    //    blocks and turn it into digits in LDS before they issue any weights,
+    //    so that round trip and the digit arithmetic overlap the other waves'
+    //    weight stream.  Prepared digits: digits and meta, and for the
+    //    outliers x, as whole float4s (the host guarantees cols >= 4) plus
     //    the cols % 4 tail (threads 0-2).  Loads past the end re-read the
     //    thread's own first element (never one address for the whole chip:
     //    that serialises on one L2 channel).
@@ -653,8 +670,16 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
     const int t_id = (int)threadIdx.x;
     const int pw = t_id & (F::LPB - 1), pb = t_id / F::LPB;
     const bool prep_wave = !PREP && wave * (64 / F::LPB) < a.nb;
-    float xv0[F::NC * 8];
-    if (prep_wave) prep_load<FMT, BS, true>(a.x, a.cols, pb, pb < a.nb, pw, xv0);
+    float* xcopy = OUT ? xs : nullptr;
+    if constexpr (!PREP) {
+        if (prep_wave) {
+            float xv0[F::NC * 8];
+            const int b0 = pb < a.nb ? pb : 0;
+            prep_load<FMT, BS, true>(a.x, a.cols, pb, pb < a.nb, pw, xv0);
+            prep_settle<FMT, BS>(pb, pb < a.nb, pw, a.cols, xv0);
+            prep_finish<FMT, BS>(xv0, pb, pb < a.nb, pw, dig + b0 * F::DWS, meta + b0, xcopy, a.cols);
+        }
+    }
     constexpr bool XS = PREP && OUT;
     const int nf = a.cols >> 2;
     f32x4 xr[XV];
@@ -669,7 +694,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
     }
     const int nq = (a.nb * F::DWS + 3) >> 2;                  // dwordx4 of prepared digits
     u32x4 qr[DV];
-    double2 mr;
+    float2 mr;
     if constexpr (PREP) {
 #pragma unroll
         for (int i = 0; i < DV; i++) {
@@ -679,30 +704,17 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
         mr = a.xmeta[t_id < a.nb ? t_id : min(t_id & 63, a.nb - 1)];
     }
 
-    // 2. CSR bounds of this lane's rows: row r of tile j owns
-    //    [rpv[j][r], rpv[j][r+1]) (matrices without outliers read their own row)
-    uint32_t rpv[MAXT][R + 1];
-    if constexpr (OUT) {
-        const bool has = RP != nullptr;
-#pragma unroll
-        for (int j = 0; j < MAXT; j++) {
-            const int row0 = row_of(j);
-            const uint32_t* rp = has ? RP : own_of(j);
-#pragma unroll
-            for (int r = 0; r <= R; r++)
-                rpv[j][r] = rp[has ? min(row0 + r, rows) : min(r, (int)F::BB / 4 - 1)];
-        }
-    }
-
-    // 3. the first D weight items
+    // 3. the first weight item.  The rest of the first D follow the barrier:
+    //    once the memory system pushes back, each load waits at issue for
+    //    earlier data to return, and a wave that queued all of its items here
+    //    would hold the barrier (and every wave's first item) until the stream
+    //    had nearly drained.
     uint32_t wv[D][R][1 + F::CW];
-#pragma unroll
-    for (int k = 0; k < D; k++) issue(wv[k]);
+    issue(wv[0]);
 
-    // 5. LDS: prepared digits, meta and x as loaded; or the digits and meta
-    //    of every block prepared here, with x copied alongside for the
-    //    outliers.  Passes after the first load their x now, behind the
-    //    weights (only rows wider than one pass get there).
+    // 4. LDS: prepared digits, meta and x as loaded; or the passes of blocks
+    //    after the first, prepared here (only rows wider than one pass get
+    //    there; their x loads queue behind the weights).
     if constexpr (PREP) {
         if constexpr (XS) {
 #pragma unroll
@@ -719,12 +731,6 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
         }
         if (t_id < a.nb) meta[t_id] = mr;
     } else {
-        float* xcopy = OUT ? xs : nullptr;
-        if (prep_wave) {
-            const int b0 = pb < a.nb ? pb : 0;
-            prep_settle<FMT, BS>(pb, pb < a.nb, pw, a.cols, xv0);
-            prep_finish<FMT, BS>(xv0, pb, pb < a.nb, pw, dig + b0 * F::DWS, meta + b0, xcopy, a.cols);
-        }
         for (int base = PASS; base < a.nb; base += PASS) {
             if (base + wave * (64 / F::LPB) >= a.nb) break;     // whole wave past the end
             const int b = base + pb;
@@ -735,39 +741,50 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
     }
     __syncthreads();
 
-    // 4. first outlier entry of every row for this lane (packed tables).
-    //    Their addresses come from the CSR bounds loaded in step 2: issued
-    //    here, after the preparation, that round trip overlaps the digit
-    //    work instead of holding it up; they are first used at a tile's end.
-    uint32_t e0[MAXT][R];
+#pragma unroll
+    for (int k = 1; k < D; k++) issue(wv[k]);
+
+    // 5. CSR bounds to every lane of the group (ds_bpermute), then the first
+    //    outlier entries of each tile, one per lane: a tile's R rows own the
+    //    contiguous entries [rpv[j][0], rpv[j][R]).  Issued here, after the
+    //    preparation, that round trip overlaps the weight stream; the entries
+    //    are first used at a tile's end.
+    uint32_t rpv[MAXT][R + 1];
+    uint32_t e0[MAXT];
     if constexpr (OUT) {
+        const int gl = lane & ~(lpg - 1);                     // group's first lane
+#pragma unroll
+        for (int j = 0; j < MAXT; j++)
+#pragma unroll
+            for (int r = 0; r <= R; r++) rpv[j][r] = __shfl(rpl, gl + j * (R + 1) + r);
         const bool pk = OE != nullptr;
 #pragma unroll
         for (int j = 0; j < MAXT; j++) {
             const uint32_t* oe = pk ? OE : own_of(j);
-#pragma unroll
-            for (int r = 0; r < R; r++) e0[j][r] = oe[pk ? min(rpv[j][r] + lig, last) : 0u];
+            e0[j] = oe[pk ? min(rpv[j][0] + lig, last) : 0u];
         }
     }
 
     // 7. item loop.  At a tile's end the first outlier entry of each row joins
-    //    the lane sums (src/quant.c:481-494, fp64 value * x[col]), the row is
+    //    the lane sums (src/quant.c:481-494, value * x[col]), the row is
     //    reduced once and its sum parked in the stash.
-    double* stash = reinterpret_cast<double*>(lds + a.st_off) + wave * a.st_wave;
-    double rs[R];
+    float* stash = reinterpret_cast<float*>(lds + a.st_off) + wave * a.st_wave;
+    float rs[R];
 #pragma unroll
-    for (int r = 0; r < R; r++) rs[r] = 0.0;
+    for (int r = 0; r < R; r++) rs[r] = 0.0f;
     int cj = 0, cq = 0;                                       // compute cursor
-    // first outlier entry of each row of tile J (static J: no indexed arrays)
+    // first outlier entries of tile J (static J: no indexed arrays): entry
+    // rpv[J][0] + lig belongs to row r when it lies in [rpv[J][r], rpv[J][r+1])
     auto first_entries = [&](auto jc) __attribute__((always_inline)) {
         constexpr int J = decltype(jc)::value;
         const bool pk = OE != nullptr;
+        const uint32_t idx = rpv[J][0] + lig, e = e0[J];
+        const bool ok = pk && idx < rpv[J][R];
+        const float p = qsf::f16_bits(e >> 16) * xs[ok ? e & 0xFFFFu : 0u];
 #pragma unroll
         for (int r = 0; r < R; r++) {
-            const uint32_t e = e0[J][r];
-            const bool ok = pk && rpv[J][r] + lig < rpv[J][r + 1];
-            const double p = (double)qsf::f16_bits(e >> 16) * (double)xs[ok ? e & 0xFFFFu : 0u];
-            rs[r] += ok ? p : 0.0;
+            const bool mine = ok && idx >= rpv[J][r] && idx < rpv[J][r + 1];
+            rs[r] += mine ? p : 0.0f;
         }
     };
     auto tile_end = [&]() __attribute__((always_inline)) {
@@ -778,8 +795,8 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
         }
 #pragma unroll
         for (int r = 0; r < R; r++) {
-            const double v = group_reduce(rs[r], lpg);
-            rs[r] = 0.0;
+            const float v = group_reduce(rs[r], lpg);
+            rs[r] = 0.0f;
             if (lig == lpg - 1) stash[cj * rpt + grp * R + r] = v;
         }
     };
@@ -810,46 +827,43 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
             if ((nblk - 1) * D + k < ni) compute(wv[k]);
     }
 
-    // 8. remaining outlier entries, one per lane and row each step; every
-    //    slot loads (clamped index, own row where absent)
+    // 8. remaining outlier entries of each tile, one per lane each step;
+    //    every slot loads (clamped index, own row where absent)
     if constexpr (OUT) {
-        double orem[MAXT][R];
+        float orem[MAXT][R];
 #pragma unroll
         for (int j = 0; j < MAXT; j++)
 #pragma unroll
-            for (int r = 0; r < R; r++) orem[j][r] = 0.0;
+            for (int r = 0; r < R; r++) orem[j][r] = 0.0f;
         bool any_rem = false;
         for (uint32_t k = 1;; k++) {
-            bool ok[MAXT][R];
+            bool ok[MAXT];
             bool more = false;
 #pragma unroll
             for (int j = 0; j < MAXT; j++) {
-                const bool live = j < nt && OE != nullptr;
-#pragma unroll
-                for (int r = 0; r < R; r++) {
-                    ok[j][r] = live && rpv[j][r] + lig + (k << lgl) < rpv[j][r + 1];
-                    more |= ok[j][r];
-                }
+                ok[j] = j < nt && OE != nullptr && rpv[j][0] + lig + (k << lgl) < rpv[j][R];
+                more |= ok[j];
             }
             if (!__any(more)) break;
             any_rem = true;
-            uint32_t eu[MAXT][R];
+            uint32_t eu[MAXT];
             const bool pk = OE != nullptr;
 #pragma unroll
             for (int j = 0; j < MAXT; j++) {
                 const uint32_t* oe = pk ? OE : own_of(j);
-#pragma unroll
-                for (int r = 0; r < R; r++)
-                    eu[j][r] = oe[pk ? min(rpv[j][r] + lig + (k << lgl), last) : 0u];
+                eu[j] = oe[pk ? min(rpv[j][0] + lig + (k << lgl), last) : 0u];
             }
 #pragma unroll
-            for (int j = 0; j < MAXT; j++)
+            for (int j = 0; j < MAXT; j++) {
+                const uint32_t idx = rpv[j][0] + lig + (k << lgl);
+                const uint32_t col = ok[j] ? eu[j] & 0xFFFFu : 0u;
+                const float p = qsf::f16_bits(eu[j] >> 16) * xs[col];
 #pragma unroll
                 for (int r = 0; r < R; r++) {
-                    const uint32_t col = ok[j][r] ? eu[j][r] & 0xFFFFu : 0u;
-                    const double p = (double)qsf::f16_bits(eu[j][r] >> 16) * (double)xs[col];
-                    orem[j][r] += ok[j][r] ? p : 0.0;
+                    const bool mine = ok[j] && idx >= rpv[j][r] && idx < rpv[j][r + 1];
+                    orem[j][r] += mine ? p : 0.0f;
                 }
+            }
         }
         if (any_rem) {
 #pragma unroll
@@ -857,7 +871,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
                 if (j < nt) {
 #pragma unroll
                     for (int r = 0; r < R; r++) {
-                        const double v = group_reduce(orem[j][r], lpg);
+                        const float v = group_reduce(orem[j][r], lpg);
                         if (lig == lpg - 1) stash[j * rpt + grp * R + r] += v;
                     }
                 }
@@ -872,7 +886,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
 #pragma unroll
             for (int r = 0; r < R; r++) {
                 const int row = row0 + r;
-                if (lig == lpg - 1 && row < rows) Y[row] = (float)stash[j * rpt + grp * R + r];
+                if (lig == lpg - 1 && row < rows) Y[row] = stash[j * rpt + grp * R + r];
             }
         }
     }
@@ -884,8 +898,8 @@ template <int FMT, int BS, int R>
 __global__ __launch_bounds__(WAVES * 64) void gemv_chunked_kernel(GemvArgs a) {
     using F = Fmt<FMT, BS>;
     extern __shared__ __align__(16) uint32_t lds[];
-    double2* meta = reinterpret_cast<double2*>(lds);
-    uint32_t* dig = lds + 4 * a.chunk;
+    float2* meta = reinterpret_cast<float2*>(lds);
+    uint32_t* dig = lds + 2 * a.chunk;
     // wave index made provably uniform: tile -> matrix lookups then stay in
     // scalar registers (kernel arguments via s_load, no vector-memory waits)
     const int lane = threadIdx.x & 63;
@@ -896,11 +910,11 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_chunked_kernel(GemvArgs a) {
     const int t_end = min(a.tile0[a.n], t_begin + a.tpw);
     const uint32_t row_bytes = (uint32_t)a.nb * F::BB;
 
-    double rs[MAXT][R];
+    float rs[MAXT][R];
 #pragma unroll
     for (int j = 0; j < MAXT; j++)
 #pragma unroll
-        for (int r = 0; r < R; r++) rs[j][r] = 0.0;
+        for (int r = 0; r < R; r++) rs[j][r] = 0.0f;
 
     for (int c0 = 0; c0 < a.nb; c0 += a.chunk) {
         const int c1 = min(a.nb, c0 + a.chunk);
@@ -955,7 +969,7 @@ size_t xprep_bytes_t(int cols) {
     using F = Fmt<FMT, BS>;
     size_t nb = (size_t)((cols + BS - 1) / BS);
     size_t dig = nb * F::DWS * 4;
-    return ((dig + 255) & ~(size_t)255) + nb * sizeof(double2);
+    return ((dig + 255) & ~(size_t)255) + nb * sizeof(float2);
 }
 
 // Dynamic LDS a GEMV workgroup may use in total (digits, meta, staged x, stash).
@@ -1041,7 +1055,7 @@ int launch_t(const qsf_hip_tensor* const* t, int n, int cols, const float* d_x,
     const int nb = (cols + BS - 1) / BS;
     uint32_t* xq = (uint32_t*)d_ws;
     size_t dig = (size_t)nb * F::DWS * 4;
-    double2* xmeta = (double2*)((uint8_t*)d_ws + ((dig + 255) & ~(size_t)255));
+    float2* xmeta = (float2*)((uint8_t*)d_ws + ((dig + 255) & ~(size_t)255));
     if ((mode & QK_RUN_XPREP) && (!(mode & QK_RUN_GEMV) || (mode & QK_RUN_STANDALONE_PREP)))
         hipLaunchKernelGGL((xprep_kernel<FMT, BS>), dim3((nb + 256 / F::LPB - 1) / (256 / F::LPB)),
                            dim3(256), 0, s, d_x, cols, nb, xq, xmeta);
@@ -1058,7 +1072,7 @@ int launch_t(const qsf_hip_tensor* const* t, int n, int cols, const float* d_x,
     }
     a.lpg = lpg;
     a.lpg_log2 = lgl;
-    const int per_block = F::DWS * 4 + (int)sizeof(double2);
+    const int per_block = F::DWS * 4 + (int)sizeof(float2);
     a.chunk = nb < kLdsBudget / per_block ? nb : kLdsBudget / per_block;
     const int rows_per_tile = R * (64 / lpg);
     bool any_out = false, split = false;
@@ -1092,13 +1106,16 @@ int launch_t(const qsf_hip_tensor* const* t, int n, int cols, const float* d_x,
     a.x = d_x;
 
     // Main kernel LDS: [meta: nb x 16 B][digits: nb x DWS dwords, padded to
-    // 4][x: nb*BS floats][fp64 stash: a wave's tiles x rows_per_tile].  When
+    // 4][x: nb*BS floats][fp32 stash: a wave's tiles x rows_per_tile].  When
     // the stash would not fit, fewer tiles a workgroup.
     const size_t dig_dw = ((size_t)nb * F::DWS + 3) & ~(size_t)3;
-    const size_t main_fixed = (size_t)nb * 16 + dig_dw * 4 + (size_t)nb * BS * 4;
-    const size_t per_tile = (size_t)WAVES * rows_per_tile * sizeof(double);
+    const size_t meta_dw = ((size_t)nb * 2 + 3) & ~(size_t)3;
+    const size_t main_fixed = meta_dw * 4 + dig_dw * 4 + (size_t)nb * BS * 4;
+    const size_t per_tile = (size_t)WAVES * rows_per_tile * sizeof(float);
     // (the main kernel reads packed outlier tables only)
-    const bool whole = !split && cols >= 4 && cols <= 4 * kXvMax * WAVES * 64 && nb <= kMainMaxNb &&
+    // (the main kernel's outlier pass gathers a row group's CSR bounds from
+    // one load a lane: groups need MAXT * (R + 1) lanes)
+    const bool whole = !split && (!any_out || lpg >= MAXT * (R + 1)) && cols >= 4 && cols <= 4 * kXvMax * WAVES * 64 && nb <= kMainMaxNb &&
                        (!prepared || dig_dw <= (size_t)4 * DV * WAVES * 64) &&
                        main_fixed + per_tile <= lds_limit();
     size_t lds = (size_t)a.chunk * per_block;                 // chunked kernel
@@ -1109,7 +1126,7 @@ int launch_t(const qsf_hip_tensor* const* t, int n, int cols, const float* d_x,
         const size_t room = (lds_limit() - main_fixed) / per_tile;
         if ((size_t)a.tpw > WAVES * room) a.tpw = (int)(WAVES * room);
         const int ntc = (a.tpw + WAVES - 1) / WAVES;
-        a.xs_off = (int)((size_t)nb * 4 + dig_dw);
+        a.xs_off = (int)(meta_dw + dig_dw);
         a.st_off = a.xs_off + nb * BS;
         a.st_wave = ntc * rows_per_tile;
         lds = main_fixed + (size_t)ntc * per_tile;

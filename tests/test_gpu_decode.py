@@ -90,18 +90,20 @@ def _slots(qt, bs):
                                    (F.Q3, 32), (F.Q2, 256), (F.Q4, 256)])
 def test_xprep_digits_exact(hip, qt, bs):
     """x -> block-fixed-point X = rint(x * 2^sh) with amax * 2^sh < 2^XB, and
-    the seven balanced base-16 digit words of every multiplier X * 2^shift,
-    reconstructed exactly; block meta f = 2^-sh and sum(X) * f."""
+    the six balanced base-16 digit words of every multiplier X * 2^shift,
+    reconstructed exactly; block meta f = 2^-sh and sum(X) * f in fp32."""
     torch = torch_cuda()
     rng = np.random.default_rng(bs + qt)
     cols = 5 * bs + bs // 2 + 3                  # partial last block
     x = F.gaussian(rng, cols)
     x[bs:2 * bs] = 0.0                           # an all-zero block
     x[2 * bs:3 * bs] *= np.float32(1e-30)        # tiny scale
+    x[3 * bs:4 * bs] *= np.float32(2.0 ** 120)   # huge scale (negative shift)
     nb = (cols + bs - 1) // bs
     cw, nc, slots = _slots(qt, bs)
-    dws = (cw * nc * 7) | 1
-    xb = 24 if qt == F.Q3 else 26
+    nd = 6
+    dws = (cw * nc * nd) | 1
+    xb = 20 if qt == F.Q3 else 22
     nbytes = hip.xprep_bytes(qt, bs, cols)
     buf = torch.zeros(nbytes + 256, dtype=torch.uint8, device="cuda:0")
     addr = (buf.data_ptr() + 255) & ~255
@@ -109,24 +111,24 @@ def test_xprep_digits_exact(hip, qt, bs):
     raw = host(buf)[addr - buf.data_ptr():][:nbytes]
     dig = raw[:nb * dws * 4].view(np.uint32).reshape(nb, dws)
     moff = (nb * dws * 4 + 255) & ~255
-    meta = raw[moff:moff + nb * 16].view(np.float64).reshape(nb, 2)
+    meta = raw[moff:moff + nb * 8].view(np.float32).reshape(nb, 2)
     xp = np.zeros(nb * bs, np.float64)
     xp[:cols] = x
     for b in range(nb):
         blk = xp[b * bs:(b + 1) * bs]
         amax = np.abs(blk).max()
         sh = 0 if amax == 0 else xb - 1 - int(np.floor(np.log2(amax)))
-        sh = min(max(sh, -100), 126)
+        sh = min(sh, 126)
         X = np.rint(blk * 2.0 ** sh).astype(np.int64)
         assert np.abs(X).max() <= 2 ** xb
-        # meta = {2^-sh, 2^-sh * sum X} in fp64, both exact
-        assert meta[b, 0] == 2.0 ** -sh, (b, meta[b, 0], sh)
-        assert meta[b, 1] == float(X.sum()) * 2.0 ** -sh, (b, meta[b, 1])
+        # meta = {2^-sh exactly, 2^-sh * sum X rounded once to fp32}
+        assert meta[b, 0] == np.float32(2.0 ** -sh), (b, meta[b, 0], sh)
+        assert meta[b, 1] == np.float32(float(X.sum()) * 2.0 ** -sh), (b, meta[b, 1])
         for (w, c, m), (code, shift) in slots.items():
-            words = dig[b, (w * nc + c) * 7:(w * nc + c) * 7 + 7]
+            words = dig[b, (w * nc + c) * nd:(w * nc + c) * nd + nd]
             nib = (words >> np.uint32(4 * m)) & np.uint32(15)
             sd = np.where(nib >= 8, nib.astype(np.int64) - 16, nib.astype(np.int64))
-            rec = int(sum(int(sd[d]) * 16 ** d for d in range(7)))
+            rec = int(sum(int(sd[d]) * 16 ** d for d in range(nd)))
             assert rec == int(X[code]) * 2 ** shift, (b, w, c, m, rec, X[code])
 
 
@@ -246,7 +248,7 @@ def test_outlier_edge_cases(hip, oracle):
 @pytest.mark.parametrize("qt", ALL)
 def test_constant_x_large_blocks(hip, oracle, qt):
     """Same-sign x fills a 256-code block with |X| near 2^XB: the block sum of
-    X reaches 2^34 and must not wrap."""
+    X reaches 2^30 and must not wrap."""
     rows, cols, bs = 33, 1000, 256
     rng = np.random.default_rng(qt + 40)
     w = F.gaussian(rng, (rows, cols), 0.02)
@@ -256,6 +258,28 @@ def test_constant_x_large_blocks(hip, oracle, qt):
         out = np.full(rows, np.nan, np.float32)
         _slot(hip, qt)(payload, x, out, rows, cols, bs)
         assert rel_l2(out, ref) <= REL_L2, (qt, x[0])
+
+
+@pytest.mark.parametrize("qt,bs", [(F.Q2, 64), (F.Q3, 128), (F.Q4, 64), (F.Q4SYM, 64),
+                                   (F.Q2_OUTLIER, 64), (F.Q4_OUTLIER, 128)])
+def test_spiky_activations(hip, oracle, qt, bs):
+    """Decoder activations with a few channels 100-1000x the rest: the spike
+    sets its block's fixed-point scale, so the block's small entries keep
+    fewer bits.  The result must still meet the bar at a 7B shape."""
+    rows, cols = 512, 4096
+    rng = np.random.default_rng(qt * 7 + bs)
+    w = (F.heavy_tail_weights(rng, rows, cols) if qt in (F.Q2_OUTLIER, F.Q4_OUTLIER)
+         else F.gaussian(rng, (rows, cols), 0.02))
+    payload = F.quantize_matrix(w, qt, bs)
+    x = F.gaussian(rng, cols)
+    spikes = rng.choice(cols, 24, replace=False)
+    x[spikes] *= rng.uniform(100.0, 1000.0, 24).astype(np.float32)
+    ref = oracle.matvec(qt, payload, x, rows, cols, bs)
+    out = np.full(rows, np.nan, np.float32)
+    _slot(hip, qt)(payload, x, out, rows, cols, bs)
+    err = rel_l2(out, ref)
+    print(f"spiky x qt={qt} bs={bs}: rel_l2 = {err:.3e}")
+    assert err <= REL_L2, err
 
 
 @pytest.mark.parametrize("qt", [F.Q2_OUTLIER, F.Q4_OUTLIER])
