@@ -1031,27 +1031,28 @@ void launch_main(dim3 g, dim3 b, size_t lds, hipStream_t s, const GemvArgs& a) {
         hipLaunchKernelGGL(K, g, b, lds, s, a);
 }
 
-// rows per tile: 2 for 64-code-or-smaller blocks, else 1 (register budget);
-// prefetch depth: about 48 registers of weights in flight per lane
+// rows per tile: up to 2 for 64-code-or-smaller blocks, else 1 (register
+// budget); prefetch depth: about 48 registers of weights in flight per lane
 template <int FMT, int BS>
 constexpr int tile_rows() { return Fmt<FMT, BS>::CW <= 8 ? 2 : 1; }
 // (one item for 3-bit 256-code blocks: 25 dwords a row plus two accumulator
 // sets leave no room for a second set within 128 VGPRs)
-// (outlier kernels keep ~20 more registers of CSR state: 36)
-template <int FMT, int BS, bool OUT>
+// (outlier kernels keep ~20 more registers of CSR state, and their waves
+// have few items: 24, so that a wave computes its first item after issuing
+// the second rather than after issuing all of them)
+template <int FMT, int BS, int R, bool OUT>
 constexpr int prefetch_depth() {
-    constexpr int per = tile_rows<FMT, BS>() * (1 + Fmt<FMT, BS>::CW);
-    constexpr int budget = OUT ? 36 : 48;
+    constexpr int per = R * (1 + Fmt<FMT, BS>::CW);
+    constexpr int budget = OUT ? 24 : 48;
     if (FMT == QK_FMT_3 && Fmt<FMT, BS>::CW >= 24) return 1;
     if (OUT && per > 24) return 1;
     return budget / per < 2 ? 2 : (budget / per > 4 ? 4 : budget / per);
 }
 
-template <int FMT, int BS>
-int launch_t(const qsf_hip_tensor* const* t, int n, int cols, const float* d_x,
-             float* const* d_y, void* d_ws, int mode, hipStream_t s) {
+template <int FMT, int BS, int R>
+int launch_rt(const qsf_hip_tensor* const* t, int n, int cols, const float* d_x,
+              float* const* d_y, void* d_ws, int mode, hipStream_t s) {
     using F = Fmt<FMT, BS>;
-    constexpr int R = tile_rows<FMT, BS>();
     const int nb = (cols + BS - 1) / BS;
     uint32_t* xq = (uint32_t*)d_ws;
     size_t dig = (size_t)nb * F::DWS * 4;
@@ -1142,8 +1143,8 @@ int launch_t(const qsf_hip_tensor* const* t, int n, int cols, const float* d_x,
     }
     // only the 2-bit and 4-bit asymmetric formats have outlier variants
     constexpr bool kHasOut = FMT == QK_FMT_2 || FMT == QK_FMT_4;
-    constexpr int D = prefetch_depth<FMT, BS, false>();
-    constexpr int DO = prefetch_depth<FMT, BS, kHasOut>();
+    constexpr int D = prefetch_depth<FMT, BS, R, false>();
+    constexpr int DO = prefetch_depth<FMT, BS, R, kHasOut>();
     if (any_out && !kHasOut) return -2;
     const dim3 g(grid, whole ? n : 1), b(WAVES * 64);
     if (!whole)
@@ -1157,6 +1158,27 @@ int launch_t(const qsf_hip_tensor* const* t, int n, int cols, const float* d_x,
     else
         launch_main<gemv_kernel<FMT, BS, R, D, false, false>>(g, b, lds, s, a);
     return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+// Two-row tiles halve the digit reads a row, one-row tiles double the
+// parallelism: one row when two-row tiles would leave waves of the chip
+// without a tile (a 4096-row matrix fills half of it).
+template <int FMT, int BS>
+int launch_t(const qsf_hip_tensor* const* t, int n, int cols, const float* d_x,
+             float* const* d_y, void* d_ws, int mode, hipStream_t s) {
+    if constexpr (tile_rows<FMT, BS>() == 1) {
+        return launch_rt<FMT, BS, 1>(t, n, cols, d_x, d_y, d_ws, mode, s);
+    } else {
+        const int nb = (cols + BS - 1) / BS;
+        int lpg = 1;
+        while (lpg < nb && lpg < 64) lpg <<= 1;
+        const long rpt2 = 2L * (64 / lpg);
+        long tiles2 = 0;
+        for (int i = 0; i < n; i++) tiles2 += (t[i]->rows + rpt2 - 1) / rpt2;
+        if (tiles2 < (long)num_cus() * WAVES)
+            return launch_rt<FMT, BS, 1>(t, n, cols, d_x, d_y, d_ws, mode, s);
+        return launch_rt<FMT, BS, 2>(t, n, cols, d_x, d_y, d_ws, mode, s);
+    }
 }
 
 template <int FMT>
