@@ -672,12 +672,31 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
     const bool prep_wave = !PREP && wave * (64 / F::LPB) < a.nb;
     float* xcopy = OUT ? xs : nullptr;
     if constexpr (!PREP) {
+        // the first two passes load their x together (the second pass is the
+        // 7B down projection's: 172 4-bit or 86 3-bit blocks); passes past
+        // the second, for still wider rows, run one after another
+        constexpr int NS = F::NC * 8;
+        const int pb1 = pb + PASS;
+        const bool two = prep_wave && PASS + wave * (64 / F::LPB) < a.nb;
+        float xv0[NS], xv1[NS];
+        if (prep_wave) prep_load<FMT, BS, true>(a.x, a.cols, pb, pb < a.nb, pw, xv0);
+        if (two) prep_load<FMT, BS, true>(a.x, a.cols, pb1, pb1 < a.nb, pw, xv1);
         if (prep_wave) {
-            float xv0[F::NC * 8];
             const int b0 = pb < a.nb ? pb : 0;
-            prep_load<FMT, BS, true>(a.x, a.cols, pb, pb < a.nb, pw, xv0);
             prep_settle<FMT, BS>(pb, pb < a.nb, pw, a.cols, xv0);
             prep_finish<FMT, BS>(xv0, pb, pb < a.nb, pw, dig + b0 * F::DWS, meta + b0, xcopy, a.cols);
+        }
+        if (two) {
+            const int b1 = pb1 < a.nb ? pb1 : 0;
+            prep_settle<FMT, BS>(pb1, pb1 < a.nb, pw, a.cols, xv1);
+            prep_finish<FMT, BS>(xv1, pb1, pb1 < a.nb, pw, dig + b1 * F::DWS, meta + b1, xcopy, a.cols);
+        }
+        for (int base = 2 * PASS; base < a.nb; base += PASS) {
+            if (base + wave * (64 / F::LPB) >= a.nb) break;     // whole wave past the end
+            const int b = base + pb;
+            const bool live = b < a.nb;
+            const int bb = live ? b : 0;
+            prep_block<FMT, BS>(a.x, a.cols, b, live, pw, dig + bb * F::DWS, meta + bb, xcopy);
         }
     }
     constexpr bool XS = PREP && OUT;
@@ -712,9 +731,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
     uint32_t wv[D][R][1 + F::CW];
     issue(wv[0]);
 
-    // 4. LDS: prepared digits, meta and x as loaded; or the passes of blocks
-    //    after the first, prepared here (only rows wider than one pass get
-    //    there; their x loads queue behind the weights).
+    // 4. LDS: prepared digits, meta and x as loaded.
     if constexpr (PREP) {
         if constexpr (XS) {
 #pragma unroll
@@ -730,14 +747,6 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
             if (q < nq) reinterpret_cast<u32x4*>(dig)[q] = qr[i];
         }
         if (t_id < a.nb) meta[t_id] = mr;
-    } else {
-        for (int base = PASS; base < a.nb; base += PASS) {
-            if (base + wave * (64 / F::LPB) >= a.nb) break;     // whole wave past the end
-            const int b = base + pb;
-            const bool live = b < a.nb;
-            const int bb = live ? b : 0;
-            prep_block<FMT, BS>(a.x, a.cols, b, live, pw, dig + bb * F::DWS, meta + bb, xcopy);
-        }
     }
     __syncthreads();
 
@@ -1071,6 +1080,17 @@ int launch_rt(const qsf_hip_tensor* const* t, int n, int cols, const float* d_x,
         lpg <<= 1;
         lgl++;
     }
+    // Wider row groups (the lanes past a row's blocks idle) while the
+    // matrices have fewer tiles than the chip has waves: a 4096-row matrix
+    // of 32 blocks in 32-lane groups would fill half of it.
+    for (;;) {
+        long tl = 0;
+        const long rpt = (long)R * (64 / lpg);
+        for (int i = 0; i < n; i++) tl += (t[i]->rows + rpt - 1) / rpt;
+        if (lpg >= 64 || tl >= (long)num_cus() * WAVES) break;
+        lpg <<= 1;
+        lgl++;
+    }
     a.lpg = lpg;
     a.lpg_log2 = lgl;
     const int per_block = F::DWS * 4 + (int)sizeof(float2);
@@ -1126,18 +1146,26 @@ int launch_rt(const qsf_hip_tensor* const* t, int n, int cols, const float* d_x,
     if (whole) {
         const size_t room = (lds_limit() - main_fixed) / per_tile;
         if ((size_t)a.tpw > WAVES * room) a.tpw = (int)(WAVES * room);
+        // main kernel: workgroups (x, matrix y); a matrix with fewer tiles
+        // than the largest leaves its last workgroups without tiles
+        auto grid_of = [&](int tpw) {
+            int g = 0;
+            for (int i = 0; i < n; i++) {
+                const int gi = (a.mat[i].tiles + tpw - 1) / tpw;
+                g = gi > g ? gi : g;
+            }
+            return g;
+        };
+        // all workgroups in one round: a few past the CU count would run
+        // after the rest and double the time
+        const int tpw_max = WAVES * (int)(room < (size_t)MAXT ? room : (size_t)MAXT);
+        while (grid_of(a.tpw) * n > num_cus() && a.tpw < tpw_max) a.tpw++;
+        grid = grid_of(a.tpw);
         const int ntc = (a.tpw + WAVES - 1) / WAVES;
         a.xs_off = (int)(meta_dw + dig_dw);
         a.st_off = a.xs_off + nb * BS;
         a.st_wave = ntc * rows_per_tile;
         lds = main_fixed + (size_t)ntc * per_tile;
-        // main kernel: workgroups (x, matrix y); a matrix with fewer tiles
-        // than the largest leaves its last workgroups without tiles
-        grid = 0;
-        for (int i = 0; i < n; i++) {
-            const int g = (a.mat[i].tiles + a.tpw - 1) / a.tpw;
-            grid = g > grid ? g : grid;
-        }
     } else {
         grid = (tiles + a.tpw - 1) / a.tpw;
     }
