@@ -200,6 +200,16 @@ __device__ __forceinline__ void prep_load(const float* __restrict__ x, int cols,
             const f32x4 v = *reinterpret_cast<const f32x4_a4*>(x + min(col0 + 4 * k, cols - 4));
             xv[4 * k] = v.x; xv[4 * k + 1] = v.y; xv[4 * k + 2] = v.z; xv[4 * k + 3] = v.w;
         }
+    } else if constexpr (V4) {
+        // 3-bit, cols >= 4: the lane's slots lie in the 12 columns from
+        // floor(32 w / 3); three dwordx4 loads at clamped addresses, raw into
+        // xv[0..11], re-indexed by prep_settle()
+        const int col0 = b * BS + (32 * w) / 3;
+#pragma unroll
+        for (int k = 0; k < 3; k++) {
+            const f32x4 v = *reinterpret_cast<const f32x4_a4*>(x + min(col0 + 4 * k, cols - 4));
+            xv[4 * k] = v.x; xv[4 * k + 1] = v.y; xv[4 * k + 2] = v.z; xv[4 * k + 3] = v.w;
+        }
     } else {
 #pragma unroll
         for (int s = 0; s < NS; s++) {
@@ -207,8 +217,25 @@ __device__ __forceinline__ void prep_load(const float* __restrict__ x, int cols,
             slot_code<FMT>(w, s / 8, s % 8, code, shift);
             const int col = b * BS + code;
             const float v = x[min(max(col, 0), cols - 1)];
-            if constexpr (V4) xv[s] = v;                      // masked in prep_settle()
-            else xv[s] = (lane_live && col < cols) ? v : 0.0f;
+            xv[s] = (lane_live && col < cols) ? v : 0.0f;
+        }
+    }
+}
+
+// Re-index chunks loaded at base = min(col0 + 4k, cols - 4): column c sits at
+// c - base when c < cols; columns past the end and dead lanes read zero.
+template <int NCH, int N>
+__device__ __forceinline__ void settle_chunks(float (&xv)[N], int col0, int cols, bool lane_live) {
+    static_assert(4 * NCH <= N, "chunks past the array");
+#pragma unroll
+    for (int k = 0; k < NCH; k++) {
+        const int base = min(col0 + 4 * k, cols - 4);
+        const float v0 = xv[4 * k], v1 = xv[4 * k + 1], v2 = xv[4 * k + 2], v3 = xv[4 * k + 3];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int c = col0 + 4 * k + i, at = c - base;
+            const float v = at == 0 ? v0 : (at == 1 ? v1 : (at == 2 ? v2 : v3));
+            xv[4 * k + i] = (lane_live && c < cols) ? v : 0.0f;
         }
     }
 }
@@ -225,19 +252,7 @@ __device__ __forceinline__ void prep_settle(int b, bool live, int w, int cols,
     const bool lane_live = live && w < F::CW;
     if constexpr (FMT != QK_FMT_3) {
         const int col0 = b * BS + w * NS;
-        if (!lane_live || col0 + NS > cols) {
-#pragma unroll
-            for (int k = 0; k < NS / 4; k++) {
-                const int base = min(col0 + 4 * k, cols - 4);
-                const float v0 = xv[4 * k], v1 = xv[4 * k + 1], v2 = xv[4 * k + 2], v3 = xv[4 * k + 3];
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const int c = col0 + 4 * k + i, at = c - base;
-                    const float v = at == 0 ? v0 : (at == 1 ? v1 : (at == 2 ? v2 : v3));
-                    xv[4 * k + i] = (lane_live && c < cols) ? v : 0.0f;
-                }
-            }
-        }
+        if (!lane_live || col0 + NS > cols) settle_chunks<NS / 4>(xv, col0, cols, lane_live);
         float xr[NS];
 #pragma unroll
         for (int s = 0; s < NS; s++) xr[s] = xv[s];
@@ -248,11 +263,21 @@ __device__ __forceinline__ void prep_settle(int b, bool live, int w, int cols,
             xv[s] = xr[code];
         }
     } else {
+        // slot (c, m) of dword w = 3u + v pairs with column c0 + idx_v(m) + c,
+        // idx_v(m) = floor(4 (8v + m) / 3) - floor(32 v / 3)
+        const int col0 = b * BS + (32 * w) / 3;
+        if (!lane_live || col0 + 12 > cols) settle_chunks<3>(xv, col0, cols, lane_live);
+        float xr[12];
+#pragma unroll
+        for (int i = 0; i < 12; i++) xr[i] = xv[i];
+        const int v = w % 3;
 #pragma unroll
         for (int s = 0; s < NS; s++) {
-            int code, shift;
-            slot_code<FMT>(w, s / 8, s % 8, code, shift);
-            xv[s] = (lane_live && b * BS + code < cols) ? xv[s] : 0.0f;
+            const int c = s / 8, m = s % 8;
+            const float a0 = xr[(4 * m) / 3 + c];
+            const float a1 = xr[(4 * (8 + m)) / 3 - 10 + c];
+            const float a2 = xr[(4 * (16 + m)) / 3 - 21 + c];
+            xv[s] = v == 0 ? a0 : (v == 1 ? a1 : a2);
         }
     }
 }
