@@ -118,9 +118,9 @@ int qsf_hip_matvec_group_prepared_dev(const qsf_hip_tensor* const* t, int n,
                                       float* const* d_y, void* stream);
 
 /* Kernel timing (diagnostics; no counterpart in the reference).  While
- * enabled, each decode GEMV launch records a HIP event pair at the kernel's
- * own start and end on its stream (up to 4096 launches; enabling resets the
- * record).  _read waits for the recorded launches and writes their
+ * enabled, each decode GEMV, batched-prefill and MoE gate/up launch records a
+ * HIP event pair at the kernel's own start and end on its stream (up to 4096
+ * launches; enabling resets the record).  _read waits for the recorded launches and writes their
  * durations in microseconds; it returns how many it wrote, or a negative
  * status.  Do not enable it while a graph is being captured. */
 int qsf_hip_kernel_timing(int enable);

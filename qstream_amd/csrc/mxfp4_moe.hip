@@ -17,6 +17,8 @@
 #include "qsf_device.h"
 #include "qsf_hip_internal.h"
 
+#include <hip/hip_ext.h>
+
 namespace {
 
 typedef float f2 __attribute__((ext_vector_type(2)));
@@ -506,15 +508,21 @@ __global__ void moe_combine_kernel(MoeArgs a) {
 
 // Launch with `lds` bytes of dynamic LDS; the first launch of an
 // instantiation allows it up to 160 KB (inputs of 8 tokens exceed 64 KB).
+// Expert kernels with a dynamic LDS allowance; `timed` launches record the
+// library's kernel-timing event pair (diagnostics) when it is enabled.
 template <auto K>
-void launch_lds(dim3 g, dim3 b, size_t lds, hipStream_t s, const MoeArgs& a) {
+void launch_lds(dim3 g, dim3 b, size_t lds, hipStream_t s, const MoeArgs& a, bool timed = false) {
     static bool allowed = false;
     if (!allowed) {
         (void)hipFuncSetAttribute(reinterpret_cast<const void*>(K),
                                   hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024 - 8192);
         allowed = true;
     }
-    hipLaunchKernelGGL(K, g, b, lds, s, a);
+    hipEvent_t e0, e1;
+    if (timed && qk_timing_pair(&e0, &e1))
+        hipExtLaunchKernelGGL(K, g, b, (uint32_t)lds, s, e0, e1, 0, a);
+    else
+        hipLaunchKernelGGL(K, g, b, lds, s, a);
 }
 
 }  // namespace
@@ -569,10 +577,10 @@ extern "C" int qk_moe_launch(const qk_mx_expert* d_experts, int n_exp, int k, in
                  lds_dn = (size_t)ntok * ((eid + 31) / 32) * XBP * 4;
     const int ni_gu = (hidden + 1023) / 1024, ni_dn = (eid + 1023) / 1024;
     switch (ni_gu) {
-    case 1: launch_lds<moe_gate_up_kernel<1>>(g_gu, block, lds_gu, s, a); break;
-    case 2: launch_lds<moe_gate_up_kernel<2>>(g_gu, block, lds_gu, s, a); break;
-    case 3: launch_lds<moe_gate_up_kernel<3>>(g_gu, block, lds_gu, s, a); break;
-    default: launch_lds<moe_gate_up_kernel<4>>(g_gu, block, lds_gu, s, a); break;
+    case 1: launch_lds<moe_gate_up_kernel<1>>(g_gu, block, lds_gu, s, a, true); break;
+    case 2: launch_lds<moe_gate_up_kernel<2>>(g_gu, block, lds_gu, s, a, true); break;
+    case 3: launch_lds<moe_gate_up_kernel<3>>(g_gu, block, lds_gu, s, a, true); break;
+    default: launch_lds<moe_gate_up_kernel<4>>(g_gu, block, lds_gu, s, a, true); break;
     }
     switch (ni_dn) {
     case 1: launch_lds<moe_down_kernel<1>>(g_dn, block, lds_dn, s, a); break;
