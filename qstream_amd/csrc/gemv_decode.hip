@@ -58,6 +58,8 @@ constexpr int ND_LO = 3;               // digits 0-2 and 3-5 are recombined sepa
 constexpr uint32_t DIGIT_BIAS = 0x888888u;   // 8 * (16^6 - 1) / 15
 constexpr int WAVES = 16;              // waves per GEMV workgroup
 constexpr int MAXT = 4;                // tiles per wave (compile-time bound)
+// Main kernel with the digits in registers: one-row tiles, up to 8 a wave.
+constexpr int tiles_per_wave(bool dreg) { return dreg ? 8 : MAXT; }
 constexpr int kLdsBudget = 64 * 1024;  // block digits + meta held at once
 constexpr size_t kLdsLimit = 160 * 1024; // cap on a GEMV workgroup's dynamic LDS (gfx950 LDS)
 
@@ -460,10 +462,11 @@ __device__ __forceinline__ void load_block(const uint8_t* __restrict__ w, const 
 // digit sums are exact integers; each 3-digit group (< 2^23) converts to fp32
 // exactly and the two join with one rounding, so the block's one rounding
 // beyond x -> X is that of fp32 arithmetic on its partial sums.
-template <int FMT, int BS, int R>
+// `dg` is the block's digit words: an LDS pointer, or the lane's own copy in
+// registers (an array indexed with constants only).
+template <int FMT, int BS, int R, typename DG>
 __device__ __forceinline__ void compute_block(const uint32_t (&wv)[R][1 + Fmt<FMT, BS>::CW],
-                                              const uint32_t* __restrict__ dg, float2 xm,
-                                              float (&rs)[R]) {
+                                              const DG& dg, float2 xm, float (&rs)[R]) {
     using F = Fmt<FMT, BS>;
     int acc[R][F::NA][ND];
     auto step = [&](auto wic) __attribute__((always_inline)) {
@@ -600,9 +603,10 @@ __device__ __forceinline__ void flush_tile(const GemvArgs& a, int m, int row0, i
 // the first outlier entries of each tile, the item loop (the first entries
 // join the row sums before the one reduction a row), the remaining outlier
 // entries and the stores.
-template <int FMT, int BS, int R, int D, bool OUT, bool PREP>
+template <int FMT, int BS, int R, int D, bool OUT, bool PREP, bool DREG>
 __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
     constexpr int XV = kXvMax;
+    constexpr int MT = tiles_per_wave(DREG);
     using F = Fmt<FMT, BS>;
     using WV = uint32_t[R][1 + F::CW];
     constexpr int NT = WAVES * 64;
@@ -629,7 +633,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
     const int mtiles = M.tiles;
     const int tw = wgm * a.tpw + wave;                        // this wave's first tile
     const int t_end = min(mtiles, wgm * a.tpw + a.tpw);
-    const int nt = tw < t_end ? min(MAXT, (t_end - tw + WAVES - 1) / WAVES) : 0;
+    const int nt = tw < t_end ? min(MT, (t_end - tw + WAVES - 1) / WAVES) : 0;
     const int ipt = (a.nb + lpg - 1) >> lgl;                  // items per tile
     const int ni = nt * ipt;
     const int tl = nt > 0 ? tw : 0;                           // tile the loads are anchored on
@@ -678,7 +682,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
     uint32_t rpl = 0;
     if constexpr (OUT) {
         const bool has = RP != nullptr;
-        const int bj = min(lig / (R + 1), MAXT - 1), br = lig % (R + 1);
+        const int bj = min(lig / (R + 1), MT - 1), br = lig % (R + 1);
         const uint32_t* rp = has ? RP : own_of(bj);
         rpl = rp[has ? min(row_of(bj) + br, rows) : min(br, (int)F::BB / 4 - 1)];
     }
@@ -783,20 +787,33 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
     //    contiguous entries [rpv[j][0], rpv[j][R]).  Issued here, after the
     //    preparation, that round trip overlaps the weight stream; the entries
     //    are first used at a tile's end.
-    uint32_t rpv[MAXT][R + 1];
-    uint32_t e0[MAXT];
+    uint32_t rpv[MT][R + 1];
+    uint32_t e0[MT];
     if constexpr (OUT) {
         const int gl = lane & ~(lpg - 1);                     // group's first lane
 #pragma unroll
-        for (int j = 0; j < MAXT; j++)
+        for (int j = 0; j < MT; j++)
 #pragma unroll
             for (int r = 0; r <= R; r++) rpv[j][r] = __shfl(rpl, gl + j * (R + 1) + r);
         const bool pk = OE != nullptr;
 #pragma unroll
-        for (int j = 0; j < MAXT; j++) {
+        for (int j = 0; j < MT; j++) {
             const uint32_t* oe = pk ? OE : own_of(j);
             e0[j] = oe[pk ? min(rpv[j][0] + lig, last) : 0u];
         }
+    }
+
+    // 6. Digits in registers: with one block a lane (nb <= lpg) the lane's
+    //    block is the same in every item, so its digit words and meta are read
+    //    from LDS once (idle lanes past nb read block nb - 1).
+    constexpr int NDG = DREG ? F::CW * F::NC * ND : 1;
+    uint32_t dreg[NDG];
+    float2 mreg = make_float2(0.0f, 0.0f);
+    if constexpr (DREG) {
+        const uint32_t* dp = dig + min(lig, a.nb - 1) * F::DWS;
+#pragma unroll
+        for (int i = 0; i < NDG; i++) dreg[i] = dp[i];
+        mreg = meta[min(lig, a.nb - 1)];
     }
 
     // 7. item loop.  At a tile's end the first outlier entry of each row joins
@@ -825,7 +842,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
         if constexpr (OUT) {
             [&]<int... I>(std::integer_sequence<int, I...>) {
                 ((cj == I ? first_entries(std::integral_constant<int, I>{}) : void()), ...);
-            }(std::make_integer_sequence<int, MAXT>{});
+            }(std::make_integer_sequence<int, MT>{});
         }
 #pragma unroll
         for (int r = 0; r < R; r++) {
@@ -836,7 +853,11 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
     };
     auto compute = [&](const WV& w) __attribute__((always_inline)) {
         const int b = lig + (cq << lgl);
-        if (b < a.nb) compute_block<FMT, BS, R>(w, dig + b * F::DWS, meta[b], rs);
+        if constexpr (DREG) {
+            if (b < a.nb) compute_block<FMT, BS, R>(w, dreg, mreg, rs);
+        } else {
+            if (b < a.nb) compute_block<FMT, BS, R>(w, dig + b * F::DWS, meta[b], rs);
+        }
         if (++cq == ipt) {
             tile_end();
             cq = 0;
@@ -864,31 +885,31 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
     // 8. remaining outlier entries of each tile, one per lane each step;
     //    every slot loads (clamped index, own row where absent)
     if constexpr (OUT) {
-        float orem[MAXT][R];
+        float orem[MT][R];
 #pragma unroll
-        for (int j = 0; j < MAXT; j++)
+        for (int j = 0; j < MT; j++)
 #pragma unroll
             for (int r = 0; r < R; r++) orem[j][r] = 0.0f;
         bool any_rem = false;
         for (uint32_t k = 1;; k++) {
-            bool ok[MAXT];
+            bool ok[MT];
             bool more = false;
 #pragma unroll
-            for (int j = 0; j < MAXT; j++) {
+            for (int j = 0; j < MT; j++) {
                 ok[j] = j < nt && OE != nullptr && rpv[j][0] + lig + (k << lgl) < rpv[j][R];
                 more |= ok[j];
             }
             if (!__any(more)) break;
             any_rem = true;
-            uint32_t eu[MAXT];
+            uint32_t eu[MT];
             const bool pk = OE != nullptr;
 #pragma unroll
-            for (int j = 0; j < MAXT; j++) {
+            for (int j = 0; j < MT; j++) {
                 const uint32_t* oe = pk ? OE : own_of(j);
                 eu[j] = oe[pk ? min(rpv[j][0] + lig + (k << lgl), last) : 0u];
             }
 #pragma unroll
-            for (int j = 0; j < MAXT; j++) {
+            for (int j = 0; j < MT; j++) {
                 const uint32_t idx = rpv[j][0] + lig + (k << lgl);
                 const uint32_t col = ok[j] ? eu[j] & 0xFFFFu : 0u;
                 const float p = qsf::f16_bits(eu[j] >> 16) * xs[col];
@@ -901,7 +922,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
         }
         if (any_rem) {
 #pragma unroll
-            for (int j = 0; j < MAXT; j++)
+            for (int j = 0; j < MT; j++)
                 if (j < nt) {
 #pragma unroll
                     for (int r = 0; r < R; r++) {
@@ -914,7 +935,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
 
     // 9. stores
 #pragma unroll
-    for (int j = 0; j < MAXT; j++) {
+    for (int j = 0; j < MT; j++) {
         if (j < nt) {
             const int row0 = row_of(j);
 #pragma unroll
@@ -1083,9 +1104,10 @@ constexpr int prefetch_depth() {
     return budget / per < 2 ? 2 : (budget / per > 4 ? 4 : budget / per);
 }
 
-template <int FMT, int BS, int R>
+template <int FMT, int BS, int R, bool DREG = false>
 int launch_rt(const qsf_hip_tensor* const* t, int n, int cols, const float* d_x,
               float* const* d_y, void* d_ws, int mode, hipStream_t s) {
+    constexpr int MT = tiles_per_wave(DREG);
     using F = Fmt<FMT, BS>;
     const int nb = (cols + BS - 1) / BS;
     uint32_t* xq = (uint32_t*)d_ws;
@@ -1141,7 +1163,9 @@ int launch_rt(const qsf_hip_tensor* const* t, int n, int cols, const float* d_x,
     }
     const int tiles = a.tile0[n];
     if (tiles == 0) return 0;
-    // one workgroup per CU (fewer for small problems); at most MAXT tiles a wave
+    // one workgroup per CU (fewer for small problems); at most MAXT tiles a
+    // wave here (the chunked kernel's bound; the main kernel may take up to
+    // MT below, to fit its grid in one round)
     int grid = (tiles + WAVES - 1) / WAVES;
     grid = grid < num_cus() ? grid : num_cus();
     if ((tiles + grid - 1) / grid > WAVES * MAXT) grid = (tiles + WAVES * MAXT - 1) / (WAVES * MAXT);
@@ -1160,8 +1184,8 @@ int launch_rt(const qsf_hip_tensor* const* t, int n, int cols, const float* d_x,
     const size_t per_tile = (size_t)WAVES * rows_per_tile * sizeof(float);
     // (the main kernel reads packed outlier tables only)
     // (the main kernel's outlier pass gathers a row group's CSR bounds from
-    // one load a lane: groups need MAXT * (R + 1) lanes)
-    const bool whole = !split && (!any_out || lpg >= MAXT * (R + 1)) && cols >= 4 && cols <= 4 * kXvMax * WAVES * 64 && nb <= kMainMaxNb &&
+    // one load a lane: groups need MT * (R + 1) lanes)
+    const bool whole = !split && (!any_out || lpg >= MT * (R + 1)) && cols >= 4 && cols <= 4 * kXvMax * WAVES * 64 && nb <= kMainMaxNb &&
                        (!prepared || dig_dw <= (size_t)4 * DV * WAVES * 64) &&
                        main_fixed + per_tile <= lds_limit();
     size_t lds = (size_t)a.chunk * per_block;                 // chunked kernel
@@ -1183,7 +1207,7 @@ int launch_rt(const qsf_hip_tensor* const* t, int n, int cols, const float* d_x,
         };
         // all workgroups in one round: a few past the CU count would run
         // after the rest and double the time
-        const int tpw_max = WAVES * (int)(room < (size_t)MAXT ? room : (size_t)MAXT);
+        const int tpw_max = WAVES * (int)(room < (size_t)MT ? room : (size_t)MT);
         while (grid_of(a.tpw) * n > num_cus() && a.tpw < tpw_max) a.tpw++;
         grid = grid_of(a.tpw);
         const int ntc = (a.tpw + WAVES - 1) / WAVES;
@@ -1196,20 +1220,22 @@ int launch_rt(const qsf_hip_tensor* const* t, int n, int cols, const float* d_x,
     }
     // only the 2-bit and 4-bit asymmetric formats have outlier variants
     constexpr bool kHasOut = FMT == QK_FMT_2 || FMT == QK_FMT_4;
-    constexpr int D = prefetch_depth<FMT, BS, R, false>();
-    constexpr int DO = prefetch_depth<FMT, BS, R, kHasOut>();
+    // digits in registers: small items, two in flight, so that a wave
+    // alternates issue and compute
+    constexpr int D = DREG ? 2 : prefetch_depth<FMT, BS, R, false>();
+    constexpr int DO = DREG ? 2 : prefetch_depth<FMT, BS, R, kHasOut>();
     if (any_out && !kHasOut) return -2;
     const dim3 g(grid, whole ? n : 1), b(WAVES * 64);
     if (!whole)
         hipLaunchKernelGGL((gemv_chunked_kernel<FMT, BS, R>), g, b, lds, s, a);
     else if (prepared && any_out)
-        launch_main<gemv_kernel<FMT, BS, R, DO, kHasOut, true>>(g, b, lds, s, a);
+        launch_main<gemv_kernel<FMT, BS, R, DO, kHasOut, true, DREG>>(g, b, lds, s, a);
     else if (prepared)
-        launch_main<gemv_kernel<FMT, BS, R, D, false, true>>(g, b, lds, s, a);
+        launch_main<gemv_kernel<FMT, BS, R, D, false, true, DREG>>(g, b, lds, s, a);
     else if (any_out)
-        launch_main<gemv_kernel<FMT, BS, R, DO, kHasOut, false>>(g, b, lds, s, a);
+        launch_main<gemv_kernel<FMT, BS, R, DO, kHasOut, false, DREG>>(g, b, lds, s, a);
     else
-        launch_main<gemv_kernel<FMT, BS, R, D, false, false>>(g, b, lds, s, a);
+        launch_main<gemv_kernel<FMT, BS, R, D, false, false, DREG>>(g, b, lds, s, a);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
@@ -1219,6 +1245,16 @@ int launch_rt(const qsf_hip_tensor* const* t, int n, int cols, const float* d_x,
 template <int FMT, int BS>
 int launch_t(const qsf_hip_tensor* const* t, int n, int cols, const float* d_x,
              float* const* d_y, void* d_ws, int mode, hipStream_t s) {
+    // digits in registers when a row is one block a lane and the lane's
+    // digit words fit in 48 registers (2- and 4-bit blocks of <= 64 codes)
+    // (not the 4-bit 64-code outlier kernel: its CSR state on top spills)
+    constexpr bool kDreg = FMT != QK_FMT_3 && Fmt<FMT, BS>::CW * Fmt<FMT, BS>::NC * ND <= 48;
+    if constexpr (kDreg) {
+        bool out = false;
+        for (int i = 0; i < n; i++) out |= t[i]->d_row_ptr != nullptr;
+        if ((cols + BS - 1) / BS <= 64 && !(out && FMT == QK_FMT_4 && BS == 64))
+            return launch_rt<FMT, BS, 1, true>(t, n, cols, d_x, d_y, d_ws, mode, s);
+    }
     if constexpr (tile_rows<FMT, BS>() == 1) {
         return launch_rt<FMT, BS, 1>(t, n, cols, d_x, d_y, d_ws, mode, s);
     } else {
