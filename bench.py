@@ -269,6 +269,33 @@ def run_profile(torch, hip, cfg, steps, warmup):
     log(f"profile run: config {cfg}, {warmup} + {steps} launches done")
 
 
+def table_slot_step_us(hip, qt, bs, mats, x, calls=200):
+    """PCIe-inclusive latency of the drop-in path: the qsf_matvec_fn table
+    slot (host x and y, synchronous; pinned H2D copy of x, the GEMV launch,
+    D2H copy of y) called through ctypes with precomputed pointers, weights
+    already resident in the device arena (one copy, so they may sit in the
+    MALL).  Microseconds per step (all matrices of the step)."""
+    from qstream_amd import qsf_format as F
+    L = hip.load()
+    name = {F.Q2: "matvec_2bit", F.Q3: "matvec_3bit", F.Q4: "matvec_4bit",
+            F.Q4SYM: "matvec_4bit_sym", F.Q2_OUTLIER: "matvec_outlier_2bit",
+            F.Q4_OUTLIER: "matvec_outlier_4bit"}[qt]
+    fn = getattr(L, f"qsf_{name}_hip")
+    ws = [np.frombuffer(p, np.uint8) for _, p, _, _ in mats]
+    xh = np.ascontiguousarray(x, np.float32)
+    outs = [np.empty(r, np.float32) for _, _, r, _ in mats]
+    args = [(w.ctypes.data, xh.ctypes.data, o.ctypes.data, r, c, bs)
+            for w, o, (_, _, r, c) in zip(ws, outs, mats)]
+    for _ in range(10):
+        for a in args:
+            fn(*a)
+    t0 = time.perf_counter()
+    for _ in range(calls):
+        for a in args:
+            fn(*a)
+    return (time.perf_counter() - t0) / calls * 1e6
+
+
 def bench_dense(torch, hip, cfg, steps, warmup, with_cpu=True, split=False):
     qt, bs, mats, x = cfg1_data() if cfg == 1 else cfg0_data()
     log(f"config {cfg}: data ready ({len(mats)} matrices)")
@@ -292,6 +319,7 @@ def bench_dense(torch, hip, cfg, steps, warmup, with_cpu=True, split=False):
                      "launches_timed": res["kernel_us_n"]},
         "rotation_mib": res["rotation_mib"],
     }
+    out["table_slot_us_per_step"] = table_slot_step_us(hip, qt, bs, mats, x)
     if with_cpu:
         out["cpu_baseline"] = cpu_baseline_dense(qt, bs, mats, x)
     return out
@@ -752,6 +780,8 @@ def main():
                    "us_per_step_graph": round(r["ms_per_step"] * 1e3, 3),
                    "us_per_step_eager": round(r["us_per_step_eager"], 3),
                    "us_event_per_launch_eager": round(r["us_event_per_launch_eager"], 3),
+                   "table_slot_us_per_step_pcie": round(r["table_slot_us_per_step"], 3),
+                   "table_slot_gbs_pcie": round(r["bytes_per_step"] / (r["table_slot_us_per_step"] * 1e-6) / 1e9, 2),
                    "launch": "split x-prep + GEMV" if args.split else "one fused launch per step",
                    "bytes_per_step": r["bytes_per_step"],
                    "hbm_frac_of_8TBs": round(r["value"] / HBM_PEAK_GBS, 4),

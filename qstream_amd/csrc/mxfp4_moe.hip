@@ -491,6 +491,66 @@ __global__ __launch_bounds__(WAVES * 64) void moe_down_kernel(MoeArgs a) {
     });
 }
 
+// Down and combine in one launch for one token with at most FG experts
+// (batch-1 decode).  The FG wave groups of a workgroup each take one expert
+// (work item g = the token's rank g) over the workgroup's FROWS rows; the
+// rows' sums meet in LDS and the workgroup adds them in rank order like the
+// combine kernel below (src/engine.c:1021, 1104-1106).
+constexpr int FG = 4;                      // wave groups: experts of the token
+constexpr int FGW = 2;                     // waves a group (512 threads: 256 VGPRs a lane)
+constexpr int FMR = kMR<1>;                // rows per 32-lane group
+constexpr int FROWS = FGW * 2 * FMR;       // rows of a workgroup (16)
+template <int NI>
+__global__ __launch_bounds__(FG * FGW * 64) void moe_down_fused_kernel(MoeArgs a) {
+    extern __shared__ __align__(16) float xs[];  // [FG][eid, padded], then [FG][FROWS] row sums
+    const Route& rt = *a.route;
+    const int nwork = rt.nwork;
+    if (nwork == 0) {                            // no expert picked: out = 0, as the combine
+        const int row = blockIdx.x * FROWS + threadIdx.x;
+        if ((int)threadIdx.x < FROWS && row < a.hidden) a.out[row] = 0.0f;
+        return;
+    }
+    const int g = threadIdx.x / (FGW * 64);
+    const int wl = (threadIdx.x >> 6) & (FGW - 1);
+    const int lane = threadIdx.x & 63, lig = lane & 31;
+    const int gi = g < nwork ? g : 0;            // groups past the experts recompute item 0, store nothing
+    const Work& wk = rt.work[gi];
+    const MxExpert ex = a.experts[wk.expert];
+    const int nb = (a.eid + 31) / 32;
+    const MxMat mat[1] = {{ex.dc, ex.ds, a.hidden, a.eid, nb}};
+    const int tile0 = blockIdx.x * FROWS;
+    const int row0 = tile0 + wl * 2 * FMR + (lane >> 5) * FMR;
+    float* part = xs + (size_t)FG * nb * XBP;
+    const int nst = nwork < FG ? nwork : FG;
+    auto stage = [&]() {
+        stage_inputs(xs, nst, a.eid, nb,
+                     [&](int i) { return (const float*)(a.h + (size_t)rt.work[i].slot[0] * a.eid); });
+        __syncthreads();
+    };
+    mx_tile<1, NI, FMR>(mat, xs + (size_t)gi * nb * XBP, 1, row0, lig, stage,
+                        [&](int, const float (&acc)[1][FMR]) {
+#pragma unroll
+        for (int r = 0; r < FMR; r++) {
+            const float v = qsf::group_sum_last(acc[0][r], 32);
+            const int row = row0 + r;
+            if (lig == 31 && g < nwork && row < a.hidden)
+                part[g * FROWS + (row - tile0)] = ex.db ? v + qsf::f16_bits(ex.db[row]) : v;
+        }
+    });
+    __syncthreads();
+    if ((int)threadIdx.x < FROWS) {
+        const int row = tile0 + threadIdx.x;
+        if (row < a.hidden) {
+            float acc = 0.0f;
+            for (int q = 0; q < a.k; q++) {
+                if (rt.idx[q] < 0) continue;
+                acc += rt.w[q] * part[q * FROWS + threadIdx.x];
+            }
+            a.out[row] = acc;
+        }
+    }
+}
+
 // out[t] = sum over the token's ranks of w * d (src/engine.c:1021,
 // 1104-1106); slots without an expert are skipped.
 __global__ void moe_combine_kernel(MoeArgs a) {
@@ -506,10 +566,10 @@ __global__ void moe_combine_kernel(MoeArgs a) {
     a.out[(size_t)t * a.hidden + i] = acc;
 }
 
-// Launch with `lds` bytes of dynamic LDS; the first launch of an
-// instantiation allows it up to 160 KB (inputs of 8 tokens exceed 64 KB).
-// Expert kernels with a dynamic LDS allowance; `timed` launches record the
-// library's kernel-timing event pair (diagnostics) when it is enabled.
+// Expert kernels with dynamic LDS: the first launch of an instantiation
+// allows it up to 152 KB (inputs of 8 tokens exceed 64 KB).  `timed`
+// launches record the library's kernel-timing event pair (diagnostics) when
+// it is enabled.
 template <auto K>
 void launch_lds(dim3 g, dim3 b, size_t lds, hipStream_t s, const MoeArgs& a, bool timed = false) {
     static bool allowed = false;
@@ -581,6 +641,18 @@ extern "C" int qk_moe_launch(const qk_mx_expert* d_experts, int n_exp, int k, in
     case 2: launch_lds<moe_gate_up_kernel<2>>(g_gu, block, lds_gu, s, a, true); break;
     case 3: launch_lds<moe_gate_up_kernel<3>>(g_gu, block, lds_gu, s, a, true); break;
     default: launch_lds<moe_gate_up_kernel<4>>(g_gu, block, lds_gu, s, a, true); break;
+    }
+    if (ntok == 1 && k <= FG) {
+        // one token: down and combine in one launch
+        const dim3 g_f((hidden + FROWS - 1) / FROWS), b_f(FG * FGW * 64);
+        const size_t lds_f = (size_t)FG * ((eid + 31) / 32) * XBP * 4 + (size_t)FG * FROWS * 4;
+        switch (ni_dn) {
+        case 1: launch_lds<moe_down_fused_kernel<1>>(g_f, b_f, lds_f, s, a); break;
+        case 2: launch_lds<moe_down_fused_kernel<2>>(g_f, b_f, lds_f, s, a); break;
+        case 3: launch_lds<moe_down_fused_kernel<3>>(g_f, b_f, lds_f, s, a); break;
+        default: launch_lds<moe_down_fused_kernel<4>>(g_f, b_f, lds_f, s, a); break;
+        }
+        return hipGetLastError() == hipSuccess ? 0 : -1;
     }
     switch (ni_dn) {
     case 1: launch_lds<moe_down_kernel<1>>(g_dn, block, lds_dn, s, a); break;
