@@ -66,25 +66,6 @@ __device__ __forceinline__ float block_dot(uint4 c, const float* __restrict__ x,
     return acc;
 }
 
-// sum_{k<32} e2m1(code_k) * x[k] for a whole block (x 16-byte aligned).
-__device__ __forceinline__ float block_dot32(uint4 c, const float* __restrict__ x) {
-    float acc = 0.0f;
-    const uint32_t w[4] = {c.x, c.y, c.z, c.w};
-    const float4* x4 = reinterpret_cast<const float4*>(x);
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const float4 xa = x4[2 * i], xb = x4[2 * i + 1];
-        f2 v0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w[i], 1.0f, 0);
-        f2 v1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w[i], 1.0f, 1);
-        f2 v2 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w[i], 1.0f, 2);
-        f2 v3 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w[i], 1.0f, 3);
-        acc = fmaf(v0.x, xa.x, acc); acc = fmaf(v0.y, xa.y, acc);
-        acc = fmaf(v1.x, xa.z, acc); acc = fmaf(v1.y, xa.w, acc);
-        acc = fmaf(v2.x, xb.x, acc); acc = fmaf(v2.y, xb.y, acc);
-        acc = fmaf(v3.x, xb.z, acc); acc = fmaf(v3.y, xb.w, acc);
-    }
-    return acc;
-}
 
 // One MXFP4 matrix against up to 8 activation vectors (tokens).  XF(t)
 // returns token t's activation pointer; loops over tokens are unrolled to 8
@@ -185,9 +166,6 @@ struct Route {
     Work work[MAX_SLOTS];      // distinct experts in order of first pick
 };
 
-__device__ __forceinline__ float rdlane(float v, int l) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
-}
 
 __device__ __forceinline__ float act_fn(int act, float v) {
     if (act == 2) return v / (1.0f + expf(-v));                       // SiLU
@@ -210,53 +188,75 @@ struct MoeArgs {
 };
 
 // Routing of token t by one wave, into s_idx/s_w[t*K .. t*K+K-1]:
-// softmax (src/kernels_scalar.c:187-214) with the max and the sum taken in
-// index order as the reference does (lane values read back with readlane),
-// exps one expert per lane; top-K (src/engine.c:987-1018) as ranks: expert e
-// takes place r = #{q : p_q > p_e, or p_q == p_e and q < e} among those with
-// p > -1e30 (NaN never qualifies), which is the order the strict '>'
-// insertion from a -1e30 start produces; then optional renormalisation by
-// the rank-ordered sum.
-// RJ experts per lane: 1 for up to 64 experts, else MAX_EXP / 64.
+// softmax (src/kernels_scalar.c:187-214) and top-K (src/engine.c:987-1018).
+// - max: the reference's running max from x[0] keeps the largest non-NaN
+//   value (NaN never wins a '>') unless x[0] itself is NaN; a DPP max tree
+//   over the non-NaN values is the same number.
+// - sum: in index order as the reference adds, each lane running the same
+//   sequential fp32 sum over the wave's exps in LDS (broadcast reads).
+// - top-K as ranks: expert e takes place r = #{q : p_q > p_e, or p_q == p_e
+//   and q < e} among those with p > -1e30 (NaN never qualifies), the order
+//   the strict '>' insertion from a -1e30 start produces; each lane counts
+//   its rank against every p in LDS.
+// - optional renormalisation by the rank-ordered sum.
+// sp: this wave's LDS scratch of MAX_EXP floats.  RJ experts per lane: 1 for
+// up to 64 experts, else MAX_EXP / 64.
+__device__ __forceinline__ float wave_max_dpp(float v) {
+#define QSF_DPPM(x, ctrl, rmask) \
+    __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, -__builtin_inff()), \
+                                                          __builtin_bit_cast(int, (x)), (ctrl), (rmask), 0xF, false))
+    v = fmaxf(v, QSF_DPPM(v, 0xB1, 0xF));     // quad_perm [1,0,3,2]
+    v = fmaxf(v, QSF_DPPM(v, 0x4E, 0xF));     // quad_perm [2,3,0,1]
+    v = fmaxf(v, QSF_DPPM(v, 0x141, 0xF));    // row_half_mirror
+    v = fmaxf(v, QSF_DPPM(v, 0x140, 0xF));    // row_mirror
+    v = fmaxf(v, QSF_DPPM(v, 0x142, 0xA));    // row_bcast15
+    v = fmaxf(v, QSF_DPPM(v, 0x143, 0xC));    // row_bcast31
+#undef QSF_DPPM
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
 template <int RJ>
 __device__ void route_token(const float* __restrict__ lg, int n, int k, int norm, int t,
-                            int* s_idx, float* s_w) {
+                            int* s_idx, float* s_w, float* sp) {
     const int lane = threadIdx.x & 63;
     if (lane < k) { s_idx[t * k + lane] = -1; s_w[t * k + lane] = -1e30f; }
     float v[RJ];
 #pragma unroll
     for (int j = 0; j < RJ; j++) v[j] = lane + 64 * j < n ? lg[lane + 64 * j] : 0.0f;
-    float mx = rdlane(v[0], 0);
+    const float v0 = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, v[0])));
+    float m = -__builtin_inff();
 #pragma unroll
     for (int j = 0; j < RJ; j++)
-        for (int l = 0; l < 64 && 64 * j + l < n; l++) {
-            const float q = rdlane(v[j], l);
-            mx = q > mx ? q : mx;
-        }
+        if (lane + 64 * j < n) m = fmaxf(m, v[j]);          // fmaxf skips NaN
+    const float mx = v0 != v0 ? v0 : wave_max_dpp(m);
 #pragma unroll
-    for (int j = 0; j < RJ; j++) v[j] = expf(v[j] - mx);
+    for (int j = 0; j < RJ; j++) {
+        v[j] = expf(v[j] - mx);
+        if (lane + 64 * j < n) sp[lane + 64 * j] = v[j];
+    }
+    __builtin_amdgcn_wave_barrier();
     float sum = 0.0f;
-#pragma unroll
-    for (int j = 0; j < RJ; j++)
-        for (int l = 0; l < 64 && 64 * j + l < n; l++) sum += rdlane(v[j], l);
+    for (int i = 0; i < n; i++) sum += sp[i];
     const bool flat = sum < 1e-30f;
     const float inv = 1.0f / sum;
+    __builtin_amdgcn_wave_barrier();
 #pragma unroll
-    for (int j = 0; j < RJ; j++) v[j] = flat ? 1.0f / (float)n : v[j] * inv;
+    for (int j = 0; j < RJ; j++) {
+        v[j] = flat ? 1.0f / (float)n : v[j] * inv;
+        if (lane + 64 * j < n) sp[lane + 64 * j] = v[j];
+    }
+    __builtin_amdgcn_wave_barrier();
     int rank[RJ];
 #pragma unroll
     for (int j = 0; j < RJ; j++) rank[j] = 0;
+    for (int q = 0; q < n; q++) {
+        const float pq = sp[q];
 #pragma unroll
-    for (int jq = 0; jq < RJ; jq++)
-        for (int l = 0; l < 64 && 64 * jq + l < n; l++) {
-            const float pq = rdlane(v[jq], l);
-            const int q = 64 * jq + l;
-#pragma unroll
-            for (int j = 0; j < RJ; j++) {
-                const int e = lane + 64 * j;
-                rank[j] += pq > -1e30f && (pq > v[j] || (pq == v[j] && q < e)) ? 1 : 0;
-            }
+        for (int j = 0; j < RJ; j++) {
+            const int e = lane + 64 * j;
+            rank[j] += pq > -1e30f && (pq > v[j] || (pq == v[j] && q < e)) ? 1 : 0;
         }
+    }
     __builtin_amdgcn_wave_barrier();
 #pragma unroll
     for (int j = 0; j < RJ; j++) {
@@ -409,10 +409,12 @@ __device__ __forceinline__ void stage_inputs(float* xs, int n, int cols, int nb,
 __global__ __launch_bounds__(MAX_TOK * 64) void moe_route_kernel(MoeArgs a) {
     __shared__ int s_idx[MAX_SLOTS];
     __shared__ float s_w[MAX_SLOTS];
+    __shared__ float s_p[MAX_TOK][MAX_EXP];
     const int t = threadIdx.x >> 6;
     if (t < a.ntok) {
-        if (a.n_exp <= 64) route_token<1>(a.logits + (size_t)t * a.n_exp, a.n_exp, a.k, a.norm, t, s_idx, s_w);
-        else route_token<MAX_EXP / 64>(a.logits + (size_t)t * a.n_exp, a.n_exp, a.k, a.norm, t, s_idx, s_w);
+        const float* lg = a.logits + (size_t)t * a.n_exp;
+        if (a.n_exp <= 64) route_token<1>(lg, a.n_exp, a.k, a.norm, t, s_idx, s_w, s_p[t]);
+        else route_token<MAX_EXP / 64>(lg, a.n_exp, a.k, a.norm, t, s_idx, s_w, s_p[t]);
     }
     __syncthreads();
     if (t != 0) return;
