@@ -84,6 +84,11 @@ def _experts(rng, n_exp, hidden, eid, bias):
     (32, 4, 2880, 2880, 8, 1, 2, False),     # config 3, batch 8
     (8, 2, 256, 512, 3, 0, 0, True),         # GELU, biases, no renorm
     (4, 4, 128, 64, 8, 1, 3, True),          # every expert picked, ReLU
+    (8, 3, 256, 512, 1, 0, 0, True),         # one token (fused down + combine), biases, GELU
+    (3, 4, 64, 96, 1, 1, 2, False),          # top-4 of 3 experts: one rank stays empty
+    (64, 1, 320, 160, 1, 1, 2, True),        # top-1
+    (128, 8, 128, 64, 2, 1, 2, False),       # more experts than lanes: 2 per lane in routing
+    (200, 6, 64, 64, 3, 0, 3, True),         # expert count not a multiple of 64, ReLU
 ])
 def test_moe_forward(hip, oracle, n_exp, k, hidden, eid, ntok, norm, act, bias):
     torch = torch_cuda()
