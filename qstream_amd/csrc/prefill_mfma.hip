@@ -138,13 +138,16 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint3
 }
 
 // Workgroup id -> (m tile, n tile).  Workgroups are dealt to the 8 XCDs
-// round-robin; this numbering hands each XCD a contiguous run of tiles, so
-// the XCDs that share an m tile share its activation rows in their own L2.
+// round-robin; this numbering hands each XCD a contiguous run of tiles in
+// column-major order, so the M tiles of one N tile run side by side on one
+// XCD and the weight tile they share is fetched into that XCD's L2 once
+// (measured: 72 MB fetched a launch at config 4 instead of 91 MB).
 __device__ __forceinline__ void tile_of(int id, int nwg, int tiles_n, int& tm, int& tn) {
     const int q = nwg >> 3, r = nwg & 7, xcd = id & 7, slot = id >> 3;
     const int t = (xcd < r ? xcd * (q + 1) : r * (q + 1) + (xcd - r) * q) + slot;
-    tm = t / tiles_n;
-    tn = t - tm * tiles_n;
+    const int tiles_m = nwg / tiles_n;
+    tn = t / tiles_m;
+    tm = t - tn * tiles_m;
 }
 
 // RAGGED: k is not a multiple of 2 SK, so stages reach past the last column;
