@@ -70,11 +70,14 @@ __device__ __forceinline__ bf16x8 dequant8(uint32_t w, float s, float z) {
 // fma(16 s, 1 + q/16, c) with c = z - 16 s equals fp32(s q + z) exactly
 // whenever c is exact in fp32 (the caller checks that per block).
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
-__device__ __forceinline__ bf16x8 dequant8_m16(uint32_t w, float s16, float c) {
-    const uint32_t h[4] = {((w << 6) & 0x03C003C0u) | 0x3C003C00u,   // codes 0, 4
-                           ((w << 2) & 0x03C003C0u) | 0x3C003C00u,   // codes 1, 5
-                           ((w >> 2) & 0x03C003C0u) | 0x3C003C00u,   // codes 2, 6
-                           ((w >> 6) & 0x03C003C0u) | 0x3C003C00u};  // codes 3, 7
+// `one` is 0x3C003C00 (fp16 1.0 twice) held in a VGPR by the caller: with
+// the mask in an SGPR the and-or is one v_and_or_b32 (a VOP3 reads at most
+// one scalar operand here, and two literals would split it in two).
+__device__ __forceinline__ bf16x8 dequant8_m16(uint32_t w, float s16, float c, uint32_t one) {
+    const uint32_t h[4] = {((w << 6) & 0x03C003C0u) | one,   // codes 0, 4
+                           ((w << 2) & 0x03C003C0u) | one,   // codes 1, 5
+                           ((w >> 2) & 0x03C003C0u) | one,   // codes 2, 6
+                           ((w >> 6) & 0x03C003C0u) | one};  // codes 3, 7
     float x[8];
 #pragma unroll
     for (int j = 0; j < 4; j++) {
@@ -181,6 +184,8 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
         const uint32_t lane_code = lane_meta + 4 + (BS == 64 ? 0u : (uint32_t)h * 32);
         const uint32_t wv = (uint32_t)(n0 + col) * row_bytes;
         const int it_base = col * PITCH + 64 * h;
+        uint32_t one = 0x3C003C00u;
+        asm volatile("" : "+v"(one));                // kept in a VGPR (see dequant8_m16)
         auto load_codes = [&](int s, u32x4 (&code)[2], uint32_t& meta) __attribute__((always_inline)) {
             const uint32_t sm = BS <= SK ? (uint32_t)s * (SK / BS) * BB : (uint32_t)(s / (BS / SK)) * BB;
             const uint32_t sc = BS <= SK ? sm : sm + (uint32_t)(s % (BS / SK)) * (SK / 2);
@@ -198,7 +203,7 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
             if (__builtin_isfinite(cd) && (double)c == cd) {
 #pragma unroll
                 for (int j = 0; j < 8; j++) {
-                    bf16x8 v = dequant8_m16(code[j >> 2][j & 3], 16.0f * sc, c);
+                    bf16x8 v = dequant8_m16(code[j >> 2][j & 3], 16.0f * sc, c, one);
                     if (RAGGED && s * SK + 64 * h + 8 * j >= a.k) v = bf16x8{};
                     *reinterpret_cast<bf16x8*>(buf + it_base + 8 * j) = v;
                 }
