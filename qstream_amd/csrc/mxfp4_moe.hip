@@ -312,6 +312,10 @@ constexpr int XBP = 36;
 // two tokens), 4 for down; rows per workgroup WAVES * 2 * MR.
 template <int NM>
 constexpr int kMR = NM == 2 ? 2 : 4;
+// Inputs staged in LDS at a time: an expert averages one or two tokens, and
+// LDS sized for the whole batch (8 tokens: 103 KB at hidden 2880) would hold
+// a CU to one expert workgroup.
+constexpr int TCH = 2;
 
 template <int NM, int NI, int MR, typename STAGE, typename DONE>
 __device__ __forceinline__ void mx_tile(const MxMat (&mat)[NM], const float* xs, int n, int row0,
@@ -330,9 +334,15 @@ __device__ __forceinline__ void mx_tile(const MxMat (&mat)[NM], const float* xs,
                 sc[it][m][r] = e8m0(mat[m].scales[at]);
             }
     }
-    stage();                               // inputs to LDS while the codes load
+    // inputs TCH at a time (LDS for TCH inputs, not the batch): the first
+    // chunk stages while the codes load
+    stage(0, n < TCH ? n : TCH);
 #pragma unroll 1
     for (int i = 0; i < n; i++) {
+        if (i > 0 && i % TCH == 0) {
+            __syncthreads();               // every wave done with the previous chunk
+            stage(i, n - i < TCH ? n - i : TCH);
+        }
         float acc[NM][MR];
 #pragma unroll
         for (int m = 0; m < NM; m++)
@@ -343,7 +353,7 @@ __device__ __forceinline__ void mx_tile(const MxMat (&mat)[NM], const float* xs,
             const int b = lig + 32 * it;
             // inputs are zero-padded to whole blocks in LDS; lanes past the
             // last block add nothing
-            const float4* x4 = reinterpret_cast<const float4*>(xs + (size_t)i * XBP * mat[0].nb +
+            const float4* x4 = reinterpret_cast<const float4*>(xs + (size_t)(i % TCH) * XBP * mat[0].nb +
                                                                XBP * min(b, mat[0].nb - 1));
             const bool live = b < mat[0].nb;
             float dot[NM][MR];
@@ -443,8 +453,8 @@ __global__ __launch_bounds__(WAVES * 64) void moe_gate_up_kernel(MoeArgs a) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int lig = lane & 31;
     const int row0 = blockIdx.x * (WAVES * 2 * MR) + wave * 2 * MR + (lane >> 5) * MR;
-    auto stage = [&]() {
-        stage_inputs(xs, wk.n, a.hidden, nb, [&](int i) { return a.x + (size_t)(wk.slot[i] / a.k) * a.hidden; });
+    auto stage = [&](int i0, int cnt) {
+        stage_inputs(xs, cnt, a.hidden, nb, [&](int i) { return a.x + (size_t)(wk.slot[i0 + i] / a.k) * a.hidden; });
         __syncthreads();
     };
     mx_tile<2, NI, MR>(mat, xs, wk.n, row0, lig, stage, [&](int i, const float (&acc)[2][MR]) {
@@ -479,8 +489,8 @@ __global__ __launch_bounds__(WAVES * 64) void moe_down_kernel(MoeArgs a) {
     const int lig = lane & 31;
     constexpr int MR = kMR<1>;
     const int row0 = blockIdx.x * (WAVES * 2 * MR) + wave * 2 * MR + (lane >> 5) * MR;
-    auto stage = [&]() {
-        stage_inputs(xs, n, a.eid, nb, [&](int i) { return (const float*)(a.h + (size_t)wk.slot[i] * a.eid); });
+    auto stage = [&](int i0, int cnt) {
+        stage_inputs(xs, cnt, a.eid, nb, [&](int i) { return (const float*)(a.h + (size_t)wk.slot[i0 + i] * a.eid); });
         __syncthreads();
     };
     mx_tile<1, NI, MR>(mat, xs, n, row0, lig, stage, [&](int i, const float (&acc)[1][MR]) {
@@ -525,7 +535,7 @@ __global__ __launch_bounds__(FG * FGW * 64) void moe_down_fused_kernel(MoeArgs a
     const int row0 = tile0 + wl * 2 * FMR + (lane >> 5) * FMR;
     float* part = xs + (size_t)FG * nb * XBP;
     const int nst = nwork < FG ? nwork : FG;
-    auto stage = [&]() {
+    auto stage = [&](int, int) {                 // one input a group: all groups' at once
         stage_inputs(xs, nst, a.eid, nb,
                      [&](int i) { return (const float*)(a.h + (size_t)rt.work[i].slot[0] * a.eid); });
         __syncthreads();
@@ -637,8 +647,9 @@ extern "C" int qk_moe_launch(const qk_mx_expert* d_experts, int n_exp, int k, in
     constexpr int rows_dn = WAVES * 2 * kMR<1>;
     const dim3 g_gu((eid + rows_gu - 1) / rows_gu, items), g_dn((hidden + rows_dn - 1) / rows_dn, items);
     hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(MAX_TOK * 64), 0, s, a);
-    const size_t lds_gu = (size_t)ntok * ((hidden + 31) / 32) * XBP * 4,
-                 lds_dn = (size_t)ntok * ((eid + 31) / 32) * XBP * 4;
+    const int tch = ntok < TCH ? ntok : TCH;
+    const size_t lds_gu = (size_t)tch * ((hidden + 31) / 32) * XBP * 4,
+                 lds_dn = (size_t)tch * ((eid + 31) / 32) * XBP * 4;
     const int ni_gu = (hidden + 1023) / 1024, ni_dn = (eid + 1023) / 1024;
     switch (ni_gu * 2 + (few ? 0 : 1)) {
     case 2: launch_lds<moe_gate_up_kernel<1, 1>>(g_gu, block, lds_gu, s, a, true); break;
