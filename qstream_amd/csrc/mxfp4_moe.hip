@@ -308,10 +308,11 @@ constexpr int XBP = 36;
 // blocks of a lane are loaded before stage() stages the inputs.  The codes
 // stay in registers while a runtime loop walks the inputs; for each input
 // the lane partial sums acc[m][r] go to done(i, acc).
-// Rows per 32-lane group: 2 for the gate/up pair (1 for batches of one or
-// two tokens), 4 for down; rows per workgroup WAVES * 2 * MR.
-template <int NM>
-constexpr int kMR = NM == 2 ? 2 : 4;
+// Rows per 32-lane group (rows per workgroup WAVES * 2 * MR): 1 for the
+// gate/up pair (63 registers, so many workgroups stay resident; two rows
+// took 204), 2 for down, 4 for the batch-1 fused down (a workgroup there
+// carries four experts' rows).
+constexpr int GU_MR = 1, DN_MR = 2, FD_MR = 4;
 // Inputs staged in LDS at a time: an expert averages one or two tokens, and
 // LDS sized for the whole batch (8 tokens: 103 KB at hidden 2880) would hold
 // a CU to one expert workgroup.
@@ -439,11 +440,10 @@ __global__ __launch_bounds__(MAX_TOK * 64) void moe_route_kernel(MoeArgs a) {
 
 // Gate/up: workgroup (x, y) computes rows of row tile x of the gate and up
 // matrices of distinct expert y for the tokens that picked it:
-// h[slot] = act(gate + b) * (up + b).  MR rows a 32-lane group: 1 for one or
-// two tokens (63 registers, more workgroups resident), 2 for more tokens
-// (half the workgroups, so half the input staging).
-template <int NI, int MR>
+// h[slot] = act(gate + b) * (up + b).
+template <int NI>
 __global__ __launch_bounds__(WAVES * 64) void moe_gate_up_kernel(MoeArgs a) {
+    constexpr int MR = GU_MR;
     extern __shared__ __align__(16) float xs[];           // [n][hidden, padded]
     if ((int)blockIdx.y >= a.route->nwork) return;
     const Work& wk = a.route->work[blockIdx.y];
@@ -487,7 +487,7 @@ __global__ __launch_bounds__(WAVES * 64) void moe_down_kernel(MoeArgs a) {
     const MxMat mat[1] = {{ex.dc, ex.ds, a.hidden, a.eid, nb}};
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int lig = lane & 31;
-    constexpr int MR = kMR<1>;
+    constexpr int MR = DN_MR;
     const int row0 = blockIdx.x * (WAVES * 2 * MR) + wave * 2 * MR + (lane >> 5) * MR;
     auto stage = [&](int i0, int cnt) {
         stage_inputs(xs, cnt, a.eid, nb, [&](int i) { return (const float*)(a.h + (size_t)wk.slot[i0 + i] * a.eid); });
@@ -511,7 +511,7 @@ __global__ __launch_bounds__(WAVES * 64) void moe_down_kernel(MoeArgs a) {
 // combine kernel below (src/engine.c:1021, 1104-1106).
 constexpr int FG = 4;                      // wave groups: experts of the token
 constexpr int FGW = 2;                     // waves a group (512 threads: 256 VGPRs a lane)
-constexpr int FMR = kMR<1>;                // rows per 32-lane group
+constexpr int FMR = FD_MR;                 // rows per 32-lane group
 constexpr int FROWS = FGW * 2 * FMR;       // rows of a workgroup (16)
 template <int NI>
 __global__ __launch_bounds__(FG * FGW * 64) void moe_down_fused_kernel(MoeArgs a) {
@@ -642,24 +642,19 @@ extern "C" int qk_moe_launch(const qk_mx_expert* d_experts, int n_exp, int k, in
     // work items: distinct experts, at most min(n_exp, ntok*k)
     const int items = ntok * k < n_exp ? ntok * k : n_exp;
     const dim3 block(WAVES * 64);
-    const bool few = ntok <= 2;                  // gate/up rows a 32-lane group: 1, else 2
-    const int rows_gu = WAVES * 2 * (few ? 1 : 2);
-    constexpr int rows_dn = WAVES * 2 * kMR<1>;
+    constexpr int rows_gu = WAVES * 2 * GU_MR;
+    constexpr int rows_dn = WAVES * 2 * DN_MR;
     const dim3 g_gu((eid + rows_gu - 1) / rows_gu, items), g_dn((hidden + rows_dn - 1) / rows_dn, items);
     hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(MAX_TOK * 64), 0, s, a);
     const int tch = ntok < TCH ? ntok : TCH;
     const size_t lds_gu = (size_t)tch * ((hidden + 31) / 32) * XBP * 4,
                  lds_dn = (size_t)tch * ((eid + 31) / 32) * XBP * 4;
     const int ni_gu = (hidden + 1023) / 1024, ni_dn = (eid + 1023) / 1024;
-    switch (ni_gu * 2 + (few ? 0 : 1)) {
-    case 2: launch_lds<moe_gate_up_kernel<1, 1>>(g_gu, block, lds_gu, s, a, true); break;
-    case 3: launch_lds<moe_gate_up_kernel<1, 2>>(g_gu, block, lds_gu, s, a, true); break;
-    case 4: launch_lds<moe_gate_up_kernel<2, 1>>(g_gu, block, lds_gu, s, a, true); break;
-    case 5: launch_lds<moe_gate_up_kernel<2, 2>>(g_gu, block, lds_gu, s, a, true); break;
-    case 6: launch_lds<moe_gate_up_kernel<3, 1>>(g_gu, block, lds_gu, s, a, true); break;
-    case 7: launch_lds<moe_gate_up_kernel<3, 2>>(g_gu, block, lds_gu, s, a, true); break;
-    case 8: launch_lds<moe_gate_up_kernel<4, 1>>(g_gu, block, lds_gu, s, a, true); break;
-    default: launch_lds<moe_gate_up_kernel<4, 2>>(g_gu, block, lds_gu, s, a, true); break;
+    switch (ni_gu) {
+    case 1: launch_lds<moe_gate_up_kernel<1>>(g_gu, block, lds_gu, s, a, true); break;
+    case 2: launch_lds<moe_gate_up_kernel<2>>(g_gu, block, lds_gu, s, a, true); break;
+    case 3: launch_lds<moe_gate_up_kernel<3>>(g_gu, block, lds_gu, s, a, true); break;
+    default: launch_lds<moe_gate_up_kernel<4>>(g_gu, block, lds_gu, s, a, true); break;
     }
     if (ntok == 1 && k <= FG) {
         // one token: down and combine in one launch
