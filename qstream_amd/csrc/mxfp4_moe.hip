@@ -313,6 +313,9 @@ constexpr int XBP = 36;
 // took 204), 2 for down, 4 for the batch-1 fused down (a workgroup there
 // carries four experts' rows).
 constexpr int GU_MR = 1, DN_MR = 2, FD_MR = 4;
+// Waves a gate/up workgroup: 8 (16 rows, so each workgroup's input staging
+// serves twice the rows of a 4-wave one; down keeps WAVES).
+constexpr int GU_WAVES = 8;
 // Inputs staged in LDS at a time: an expert averages one or two tokens, and
 // LDS sized for the whole batch (8 tokens: 103 KB at hidden 2880) would hold
 // a CU to one expert workgroup.
@@ -442,7 +445,7 @@ __global__ __launch_bounds__(MAX_TOK * 64) void moe_route_kernel(MoeArgs a) {
 // matrices of distinct expert y for the tokens that picked it:
 // h[slot] = act(gate + b) * (up + b).
 template <int NI>
-__global__ __launch_bounds__(WAVES * 64) void moe_gate_up_kernel(MoeArgs a) {
+__global__ __launch_bounds__(GU_WAVES * 64) void moe_gate_up_kernel(MoeArgs a) {
     constexpr int MR = GU_MR;
     extern __shared__ __align__(16) float xs[];           // [n][hidden, padded]
     if ((int)blockIdx.y >= a.route->nwork) return;
@@ -452,7 +455,7 @@ __global__ __launch_bounds__(WAVES * 64) void moe_gate_up_kernel(MoeArgs a) {
     const MxMat mat[2] = {{ex.gc, ex.gs, a.eid, a.hidden, nb}, {ex.uc, ex.us, a.eid, a.hidden, nb}};
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int lig = lane & 31;
-    const int row0 = blockIdx.x * (WAVES * 2 * MR) + wave * 2 * MR + (lane >> 5) * MR;
+    const int row0 = blockIdx.x * (GU_WAVES * 2 * MR) + wave * 2 * MR + (lane >> 5) * MR;
     auto stage = [&](int i0, int cnt) {
         stage_inputs(xs, cnt, a.hidden, nb, [&](int i) { return a.x + (size_t)(wk.slot[i0 + i] / a.k) * a.hidden; });
         __syncthreads();
@@ -641,8 +644,8 @@ extern "C" int qk_moe_launch(const qk_mx_expert* d_experts, int n_exp, int k, in
     a.d = (float*)ws;
     // work items: distinct experts, at most min(n_exp, ntok*k)
     const int items = ntok * k < n_exp ? ntok * k : n_exp;
-    const dim3 block(WAVES * 64);
-    constexpr int rows_gu = WAVES * 2 * GU_MR;
+    const dim3 block(WAVES * 64), block_gu(GU_WAVES * 64);
+    constexpr int rows_gu = GU_WAVES * 2 * GU_MR;
     constexpr int rows_dn = WAVES * 2 * DN_MR;
     const dim3 g_gu((eid + rows_gu - 1) / rows_gu, items), g_dn((hidden + rows_dn - 1) / rows_dn, items);
     hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(MAX_TOK * 64), 0, s, a);
@@ -651,10 +654,10 @@ extern "C" int qk_moe_launch(const qk_mx_expert* d_experts, int n_exp, int k, in
                  lds_dn = (size_t)tch * ((eid + 31) / 32) * XBP * 4;
     const int ni_gu = (hidden + 1023) / 1024, ni_dn = (eid + 1023) / 1024;
     switch (ni_gu) {
-    case 1: launch_lds<moe_gate_up_kernel<1>>(g_gu, block, lds_gu, s, a, true); break;
-    case 2: launch_lds<moe_gate_up_kernel<2>>(g_gu, block, lds_gu, s, a, true); break;
-    case 3: launch_lds<moe_gate_up_kernel<3>>(g_gu, block, lds_gu, s, a, true); break;
-    default: launch_lds<moe_gate_up_kernel<4>>(g_gu, block, lds_gu, s, a, true); break;
+    case 1: launch_lds<moe_gate_up_kernel<1>>(g_gu, block_gu, lds_gu, s, a, true); break;
+    case 2: launch_lds<moe_gate_up_kernel<2>>(g_gu, block_gu, lds_gu, s, a, true); break;
+    case 3: launch_lds<moe_gate_up_kernel<3>>(g_gu, block_gu, lds_gu, s, a, true); break;
+    default: launch_lds<moe_gate_up_kernel<4>>(g_gu, block_gu, lds_gu, s, a, true); break;
     }
     if (ntok == 1 && k <= FG) {
         // one token: down and combine in one launch
