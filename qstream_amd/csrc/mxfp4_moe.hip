@@ -308,14 +308,14 @@ constexpr int XBP = 36;
 // blocks of a lane are loaded before stage() stages the inputs.  The codes
 // stay in registers while a runtime loop walks the inputs; for each input
 // the lane partial sums acc[m][r] go to done(i, acc).
-// Rows per 32-lane group (rows per workgroup WAVES * 2 * MR): 1 for the
-// gate/up pair (63 registers, so many workgroups stay resident; two rows
-// took 204), 2 for down, 4 for the batch-1 fused down (a workgroup there
-// carries four experts' rows).
-constexpr int GU_MR = 1, DN_MR = 2, FD_MR = 4;
-// Waves a gate/up workgroup: 8 (16 rows, so each workgroup's input staging
-// serves twice the rows of a 4-wave one; down keeps WAVES).
-constexpr int GU_WAVES = 8;
+// Rows per 32-lane group (rows per workgroup waves * 2 * MR): 1 for gate/up
+// and down (about 64 registers, so many workgroups stay resident; two rows
+// took 158-206), 4 for the batch-1 fused down (a workgroup there carries
+// four experts' rows).
+constexpr int GU_MR = 1, DN_MR = 1, FD_MR = 4;
+// Waves an expert workgroup: 8, so the 16 rows of a workgroup share one
+// staging of its inputs (4-wave workgroups staged them for 8 rows).
+constexpr int GU_WAVES = 8, DN_WAVES = 8;
 // Inputs staged in LDS at a time: an expert averages one or two tokens, and
 // LDS sized for the whole batch (8 tokens: 103 KB at hidden 2880) would hold
 // a CU to one expert workgroup.
@@ -480,7 +480,7 @@ __global__ __launch_bounds__(GU_WAVES * 64) void moe_gate_up_kernel(MoeArgs a) {
 // Down: workgroup (x, y) computes rows of row tile x of expert y's down
 // matrix for its slots, d[slot] = down h[slot] + b.
 template <int NI>
-__global__ __launch_bounds__(WAVES * 64) void moe_down_kernel(MoeArgs a) {
+__global__ __launch_bounds__(DN_WAVES * 64) void moe_down_kernel(MoeArgs a) {
     extern __shared__ __align__(16) float xs[];           // [n][eid, padded]
     if ((int)blockIdx.y >= a.route->nwork) return;
     const Work& wk = a.route->work[blockIdx.y];
@@ -491,7 +491,7 @@ __global__ __launch_bounds__(WAVES * 64) void moe_down_kernel(MoeArgs a) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int lig = lane & 31;
     constexpr int MR = DN_MR;
-    const int row0 = blockIdx.x * (WAVES * 2 * MR) + wave * 2 * MR + (lane >> 5) * MR;
+    const int row0 = blockIdx.x * (DN_WAVES * 2 * MR) + wave * 2 * MR + (lane >> 5) * MR;
     auto stage = [&](int i0, int cnt) {
         stage_inputs(xs, cnt, a.eid, nb, [&](int i) { return (const float*)(a.h + (size_t)wk.slot[i0 + i] * a.eid); });
         __syncthreads();
@@ -644,9 +644,9 @@ extern "C" int qk_moe_launch(const qk_mx_expert* d_experts, int n_exp, int k, in
     a.d = (float*)ws;
     // work items: distinct experts, at most min(n_exp, ntok*k)
     const int items = ntok * k < n_exp ? ntok * k : n_exp;
-    const dim3 block(WAVES * 64), block_gu(GU_WAVES * 64);
+    const dim3 block_dn(DN_WAVES * 64), block_gu(GU_WAVES * 64);
     constexpr int rows_gu = GU_WAVES * 2 * GU_MR;
-    constexpr int rows_dn = WAVES * 2 * DN_MR;
+    constexpr int rows_dn = DN_WAVES * 2 * DN_MR;
     const dim3 g_gu((eid + rows_gu - 1) / rows_gu, items), g_dn((hidden + rows_dn - 1) / rows_dn, items);
     hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(MAX_TOK * 64), 0, s, a);
     const int tch = ntok < TCH ? ntok : TCH;
@@ -672,10 +672,10 @@ extern "C" int qk_moe_launch(const qk_mx_expert* d_experts, int n_exp, int k, in
         return hipGetLastError() == hipSuccess ? 0 : -1;
     }
     switch (ni_dn) {
-    case 1: launch_lds<moe_down_kernel<1>>(g_dn, block, lds_dn, s, a); break;
-    case 2: launch_lds<moe_down_kernel<2>>(g_dn, block, lds_dn, s, a); break;
-    case 3: launch_lds<moe_down_kernel<3>>(g_dn, block, lds_dn, s, a); break;
-    default: launch_lds<moe_down_kernel<4>>(g_dn, block, lds_dn, s, a); break;
+    case 1: launch_lds<moe_down_kernel<1>>(g_dn, block_dn, lds_dn, s, a); break;
+    case 2: launch_lds<moe_down_kernel<2>>(g_dn, block_dn, lds_dn, s, a); break;
+    case 3: launch_lds<moe_down_kernel<3>>(g_dn, block_dn, lds_dn, s, a); break;
+    default: launch_lds<moe_down_kernel<4>>(g_dn, block_dn, lds_dn, s, a); break;
     }
     hipLaunchKernelGGL(moe_combine_kernel, dim3((hidden + 255) / 256, ntok), dim3(256), 0, s, a);
     return hipGetLastError() == hipSuccess ? 0 : -1;
