@@ -152,6 +152,7 @@ constexpr int MAX_TOK = 8;
 constexpr int MAX_K = 8;
 constexpr int MAX_EXP = 256;
 constexpr int MAX_SLOTS = MAX_TOK * MAX_K;     // slot s = t*K + rank; one lane each
+static_assert(MAX_SLOTS <= 64 && MAX_TOK <= 32, "one wave routes every slot; token masks are 32-bit");
 
 // A distinct expert and the slots that picked it, in slot order (a token
 // picks an expert at most once, so at most MAX_TOK slots).
@@ -273,25 +274,31 @@ __device__ void route_token(const float* __restrict__ lg, int n, int k, int norm
 }
 
 // The distinct experts of the routed slots, in order of first pick, each
-// with the slots that picked it (wave 0, after every token is routed).
-__device__ void build_work(const int* s_idx, int ns, Route& rt) {
+// with the slots that picked it in slot order (wave 0, lane = slot, after
+// every token is routed).  A token picks an expert at most once, so the mask
+// of the tokens that picked expert e (an LDS OR, whatever the lane order)
+// gives its slot count, its first slot and each slot's place in its list,
+// all in one pass over the lanes.  s_tok, s_item: LDS, MAX_EXP each.
+__device__ void build_work(const int* s_idx, int ns, int k, unsigned* s_tok, int* s_item, Route& rt) {
     const int lane = threadIdx.x & 63;
     const int e = lane < ns ? s_idx[lane] : -1;
-    bool first = e >= 0;
-    for (int q = 0; q < ns; q++) {
-        const int eq = __builtin_amdgcn_readlane(e, q);
-        if (q < lane && eq == e) first = false;
-    }
+    const int t = lane / k;
+    if (e >= 0) s_tok[e] = 0u;
+    __builtin_amdgcn_wave_barrier();
+    if (e >= 0) atomicOr(&s_tok[e], 1u << t);
+    __builtin_amdgcn_wave_barrier();
+    const unsigned m = e >= 0 ? s_tok[e] : 0u;
+    const bool first = e >= 0 && __builtin_ctz(m) == t;  // the earliest token's slot
     const uint64_t owners = __ballot(first);
-    const int wi = __popcll(owners & ((1ull << lane) - 1));
-    int cnt = 0;
-    for (int q = 0; q < ns; q++) {
-        const int eq = __builtin_amdgcn_readlane(e, q);
-        if (first && q >= lane && eq == e) rt.work[wi].slot[cnt++] = q;
-    }
-    if (first) {
-        rt.work[wi].expert = e;
-        rt.work[wi].n = cnt;
+    if (first) s_item[e] = __popcll(owners & ((1ull << lane) - 1));
+    __builtin_amdgcn_wave_barrier();
+    if (e >= 0) {
+        Work& w = rt.work[s_item[e]];
+        w.slot[__popc(m & ((1u << t) - 1))] = lane;
+        if (first) {
+            w.expert = e;
+            w.n = __popc(m);
+        }
     }
     if (lane == 0) rt.nwork = __popcll(owners);
 }
@@ -424,6 +431,8 @@ __global__ __launch_bounds__(MAX_TOK * 64) void moe_route_kernel(MoeArgs a) {
     __shared__ int s_idx[MAX_SLOTS];
     __shared__ float s_w[MAX_SLOTS];
     __shared__ float s_p[MAX_TOK][MAX_EXP];
+    __shared__ unsigned s_tok[MAX_EXP];
+    __shared__ int s_item[MAX_EXP];
     const int t = threadIdx.x >> 6;
     if (t < a.ntok) {
         const float* lg = a.logits + (size_t)t * a.n_exp;
@@ -438,7 +447,7 @@ __global__ __launch_bounds__(MAX_TOK * 64) void moe_route_kernel(MoeArgs a) {
         rt.idx[lane] = s_idx[lane];
         rt.w[lane] = s_w[lane];
     }
-    build_work(s_idx, ns, rt);
+    build_work(s_idx, ns, a.k, s_tok, s_item, rt);
 }
 
 // Gate/up: workgroup (x, y) computes rows of row tile x of the gate and up
