@@ -578,16 +578,29 @@ __global__ __launch_bounds__(FG * FGW * 64) void moe_down_fused_kernel(MoeArgs a
 
 // out[t] = sum over the token's ranks of w * d (src/engine.c:1021,
 // 1104-1106); slots without an expert are skipped.
+// Every rank's index, weight and output is loaded before the sum, without
+// branches (slots are clamped into the workspace's MAX_SLOTS rows; ranks
+// past k and empty ranks are then left out), so the loads overlap instead of
+// each waiting on the rank's expert index.
 __global__ void moe_combine_kernel(MoeArgs a) {
     const Route& rt = *a.route;
     const int t = blockIdx.y;
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= a.hidden) return;
-    float acc = 0.0f;
-    for (int q = 0; q < a.k; q++) {
-        if (rt.idx[t * a.k + q] < 0) continue;
-        acc += rt.w[t * a.k + q] * a.d[(size_t)(t * a.k + q) * a.hidden + i];
+    bool on[MAX_K];
+    float wv[MAX_K], dv[MAX_K];
+#pragma unroll
+    for (int q = 0; q < MAX_K; q++) {
+        const int s = min(t * a.k + q, MAX_SLOTS - 1);
+        on[q] = (q < a.k) & (rt.idx[s] >= 0);            // '&': the load is not skipped
+        wv[q] = rt.w[s];
+        dv[q] = a.d[(size_t)s * a.hidden + i];
     }
+    __builtin_amdgcn_sched_barrier(0);                    // every load issued before the sum
+    float acc = 0.0f;
+#pragma unroll
+    for (int q = 0; q < MAX_K; q++)
+        if (on[q]) acc += wv[q] * dv[q];
     a.out[(size_t)t * a.hidden + i] = acc;
 }
 

@@ -137,7 +137,7 @@ def test_moe_tie_keeps_lower_expert(hip, oracle):
 
 def test_moe_repeated_calls_reuse_workspace(hip, oracle):
     """One expert table, calls with different token counts and K in a row:
-    the workspace (routing, per-tile completion counters) is reused and
+    the workspace (routing list, gate/up and down outputs) is reused and
     every call must still match the oracle."""
     torch = torch_cuda()
     rng = np.random.default_rng(7)
