@@ -597,12 +597,12 @@ __device__ __forceinline__ void flush_tile(const GemvArgs& a, int m, int row0, i
 // clocks whatever its width, and at the start every wave of the CU queues
 // there: the prologue keeps the count of vector loads low (one CSR-bound load
 // a lane, one first-entry load a tile).
-// Issue order: outlier row pointers; in the prep waves x and the digit
-// arithmetic of the first pass (the other waves skip it); prepared digits
-// and x; the first D weight items; then the later prep passes, the barrier,
-// the first outlier entries of each tile, the item loop (the first entries
-// join the row sums before the one reduction a row), the remaining outlier
-// entries and the stores.
+// Issue order: outlier row pointers; in the prep waves the x of the first
+// two passes; the first weight item; the prep waves' digit arithmetic and
+// later passes; prepared digits and x; the barrier; the rest of the first D
+// weight items; then the first outlier entries of each tile, the item loop
+// (the first entries join the row sums before the one reduction a row), the
+// remaining outlier entries and the stores.
 template <int FMT, int BS, int R, int D, bool OUT, bool PREP, bool DREG>
 __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
     constexpr int XV = kXvMax;
@@ -687,10 +687,14 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
         rpl = rp[has ? min(row_of(bj) + br, rows) : min(br, (int)F::BB / 4 - 1)];
     }
 
-    // 2. Preparing here: the prep waves load the x of their first pass of
-    //    blocks and turn it into digits in LDS before they issue any weights,
-    //    so that round trip and the digit arithmetic overlap the other waves'
-    //    weight stream.  Prepared digits: digits and meta, and for the
+    // 2. Preparing here: the prep waves load the x of their first two passes
+    //    of blocks, issue their first weight item, and then turn x into
+    //    digits in LDS.  The x loads go ahead of every weight load of the
+    //    wave (queued behind weights, x arrives late and holds the barrier),
+    //    while the digit arithmetic overlaps the wave's own first item as
+    //    well as the other waves' weight stream (measured: config 0 5.25 ->
+    //    5.04 us, config 1 12.7 -> 12.45 us against digits before the first
+    //    item).  Prepared digits: digits and meta, and for the
     //    outliers x, as whole float4s (the host guarantees cols >= 4) plus
     //    the cols % 4 tail (threads 0-2).  Loads past the end re-read the
     //    thread's own first element (never one address for the whole chip:
@@ -700,6 +704,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
     const int pw = t_id & (F::LPB - 1), pb = t_id / F::LPB;
     const bool prep_wave = !PREP && wave * (64 / F::LPB) < a.nb;
     float* xcopy = OUT ? xs : nullptr;
+    uint32_t wv[D][R][1 + F::CW];
     if constexpr (!PREP) {
         // the first two passes load their x together (the second pass is the
         // 7B down projection's: 172 4-bit or 86 3-bit blocks); passes past
@@ -710,6 +715,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
         float xv0[NS], xv1[NS];
         if (prep_wave) prep_load<FMT, BS, true>(a.x, a.cols, pb, pb < a.nb, pw, xv0);
         if (two) prep_load<FMT, BS, true>(a.x, a.cols, pb1, pb1 < a.nb, pw, xv1);
+        issue(wv[0]);                                        // 3. the first weight item
         if (prep_wave) {
             const int b0 = pb < a.nb ? pb : 0;
             prep_settle<FMT, BS>(pb, pb < a.nb, pw, a.cols, xv0);
@@ -752,13 +758,12 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
         mr = a.xmeta[t_id < a.nb ? t_id : min(t_id & 63, a.nb - 1)];
     }
 
-    // 3. the first weight item.  The rest of the first D follow the barrier:
-    //    once the memory system pushes back, each load waits at issue for
-    //    earlier data to return, and a wave that queued all of its items here
-    //    would hold the barrier (and every wave's first item) until the stream
-    //    had nearly drained.
-    uint32_t wv[D][R][1 + F::CW];
-    issue(wv[0]);
+    // 3. the first weight item (issued in step 2 unless prepared).  The rest
+    //    of the first D follow the barrier: once the memory system pushes
+    //    back, each load waits at issue for earlier data to return, and a
+    //    wave that queued all of its items before it would hold the barrier
+    //    (and every wave's first item) until the stream had nearly drained.
+    if constexpr (PREP) issue(wv[0]);
 
     // 4. LDS: prepared digits, meta and x as loaded.
     if constexpr (PREP) {
