@@ -286,6 +286,24 @@ __device__ __forceinline__ void prep_settle(int b, bool live, int w, int cols,
 
 // Block meta: f = 2^-sh (exact) and sx = f * sum_k X_k (rounded once), fp32.
 // xs (optional): the lane's x values copied to LDS (columns < cols).
+// op over aligned groups of W lanes (power of two, <= 64) with the result
+// in every lane of the group: quad_perm exchanges within quads, then
+// row_half_mirror (lane i <-> 7 - i) and row_mirror (i <-> 15 - i) pair each
+// lane with one of the other half of its group; groups wider than a 16-lane
+// row finish with one shuffle per doubling.  DPP instead of __shfl_xor: no
+// LDS crossbar round trip per step.  Every lane of the wave must be active.
+template <int W, typename OP>
+__device__ __forceinline__ int group_allreduce(int v, OP op) {
+    static_assert(W >= 1 && W <= 64 && (W & (W - 1)) == 0, "power-of-two groups within a wave");
+    if constexpr (W >= 2) v = op(v, __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false));
+    if constexpr (W >= 4) v = op(v, __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false));
+    if constexpr (W >= 8) v = op(v, __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false));
+    if constexpr (W >= 16) v = op(v, __builtin_amdgcn_update_dpp(0, v, 0x140, 0xF, 0xF, false));
+    if constexpr (W >= 32) v = op(v, __shfl_xor(v, 16, 64));
+    if constexpr (W >= 64) v = op(v, __shfl_xor(v, 32, 64));
+    return v;
+}
+
 template <int FMT, int BS>
 __device__ __forceinline__ void prep_finish(const float (&xv)[Fmt<FMT, BS>::NC * 8], int b,
                                             bool live, int w, uint32_t* dst, float2* meta,
@@ -304,20 +322,19 @@ __device__ __forceinline__ void prep_finish(const float (&xv)[Fmt<FMT, BS>::NC *
             if (own) xs[col] = xv[s];
         }
     }
-    float amax = 0.0f;
-    int bad = 0;
+    // block max of |x| as fp32 bits (non-negative floats order like their
+    // bits), Inf or NaN counted as +Inf: one integer max over the group
+    int amax_b = 0;
 #pragma unroll
     for (int s = 0; s < NS; s++) {
-        if (!(fabsf(xv[s]) <= 3.402823466e38f)) bad = 1;   // Inf or NaN
-        else amax = fmaxf(amax, fabsf(xv[s]));
+        const float ax = fabsf(xv[s]);
+        amax_b = max(amax_b, ax <= 3.402823466e38f ? __builtin_bit_cast(int, ax) : 0x7F800000);
     }
-#pragma unroll
-    for (int off = F::LPB / 2; off > 0; off >>= 1) {
-        amax = fmaxf(amax, __shfl_xor(amax, off, F::LPB));
-        bad |= __shfl_xor(bad, off, F::LPB);
-    }
+    amax_b = group_allreduce<F::LPB>(amax_b, [](int u, int v) { return max(u, v); });
+    const bool bad = amax_b == 0x7F800000;
+    const float amax = __builtin_bit_cast(float, amax_b);
     int sh = 0;
-    if (amax > 0.0f) {
+    if (!bad && amax > 0.0f) {
         sh = F::XB - 1 - ilogbf(amax);                 // amax * 2^sh < 2^XB
         sh = sh > 126 ? 126 : sh;                      // f = 2^-sh stays a normal fp32
     }
@@ -336,10 +353,9 @@ __device__ __forceinline__ void prep_finish(const float (&xv)[Fmt<FMT, BS>::NC *
             sum += X;
         }
     }
-    // per-lane |sum| <= NS * 2^XB < 2^31; the block total (up to 2^30) in fp64
-    double dsum = (double)sum;
-#pragma unroll
-    for (int off = F::LPB / 2; off > 0; off >>= 1) dsum += __shfl_xor(dsum, off, F::LPB);
+    // |block total| <= BS * 2^XB <= 2^29: exact in int32
+    sum = group_allreduce<F::LPB>(sum, [](int u, int v) { return u + v; });
+    const double dsum = (double)sum;
     if (lane_live) {
 #pragma unroll
         for (int c = 0; c < F::NC; c++) {
