@@ -328,9 +328,12 @@ constexpr int GU_WAVES = 8, DN_WAVES = 8;
 // a CU to one expert workgroup.
 constexpr int TCH = 2;
 
-template <int NM, int NI, int MR, typename STAGE, typename DONE>
+template <int NM, int NI, int MR, typename PRE, typename STAGE, typename DONE>
 __device__ __forceinline__ void mx_tile(const MxMat (&mat)[NM], const float* xs, int n, int row0,
-                                        int lig, STAGE stage, DONE done) {
+                                        int lig, PRE pre, STAGE stage, DONE done) {
+    // the first chunk's inputs into registers ahead of the code loads, so
+    // they do not queue behind the weights
+    pre();
     uint4 c[NI][NM][MR];
     float sc[NI][NM][MR];
 #pragma unroll
@@ -346,7 +349,7 @@ __device__ __forceinline__ void mx_tile(const MxMat (&mat)[NM], const float* xs,
             }
     }
     // inputs TCH at a time (LDS for TCH inputs, not the batch): the first
-    // chunk stages while the codes load
+    // chunk is written to LDS from the registers pre() filled
     stage(0, n < TCH ? n : TCH);
 #pragma unroll 1
     for (int i = 0; i < n; i++) {
@@ -425,6 +428,35 @@ __device__ __forceinline__ void stage_inputs(float* xs, int n, int cols, int nb,
     }
 }
 
+// Inputs of the first chunk in registers: vectors i < n (n <= T) of cols
+// <= 4096 floats over 512 threads, XR float4s a thread; put_inputs writes
+// them in stage_inputs' LDS layout.
+constexpr int XR = 2;
+static_assert(GU_WAVES * 64 * XR * 4 >= 4096 && DN_WAVES * 64 * XR * 4 >= 4096,
+              "one register chunk holds a 4096-float input");
+template <int T, typename SRC>
+__device__ __forceinline__ void load_inputs(float4 (&xr)[T][XR], int n, int cols, SRC src) {
+#pragma unroll
+    for (int i = 0; i < T; i++)
+#pragma unroll
+        for (int q = 0; q < XR; q++) {
+            const int j = threadIdx.x + q * blockDim.x;
+            xr[i][q] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (i < n && j < cols / 4) xr[i][q] = reinterpret_cast<const float4*>(src(i))[j];
+        }
+}
+template <int T>
+__device__ __forceinline__ void put_inputs(float* xs, const float4 (&xr)[T][XR], int n, int nb) {
+#pragma unroll
+    for (int i = 0; i < T; i++)
+#pragma unroll
+        for (int q = 0; q < XR; q++) {
+            const int j = threadIdx.x + q * blockDim.x;
+            if (i < n && j < nb * 8)
+                *reinterpret_cast<float4*>(xs + (size_t)i * nb * XBP + (j >> 3) * XBP + 4 * (j & 7)) = xr[i][q];
+        }
+}
+
 // Routing once per step: one wave per token, then the distinct-expert list
 // (one launch of MAX_TOK waves; the expert kernels read the result).
 __global__ __launch_bounds__(MAX_TOK * 64) void moe_route_kernel(MoeArgs a) {
@@ -465,11 +497,15 @@ __global__ __launch_bounds__(GU_WAVES * 64) void moe_gate_up_kernel(MoeArgs a) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int lig = lane & 31;
     const int row0 = blockIdx.x * (GU_WAVES * 2 * MR) + wave * 2 * MR + (lane >> 5) * MR;
+    auto src = [&](int i) { return a.x + (size_t)(wk.slot[i] / a.k) * a.hidden; };
+    float4 xr[TCH][XR];
+    auto pre = [&]() { load_inputs<TCH>(xr, wk.n, a.hidden, src); };
     auto stage = [&](int i0, int cnt) {
-        stage_inputs(xs, cnt, a.hidden, nb, [&](int i) { return a.x + (size_t)(wk.slot[i0 + i] / a.k) * a.hidden; });
+        if (i0 == 0) put_inputs<TCH>(xs, xr, cnt, nb);
+        else stage_inputs(xs, cnt, a.hidden, nb, [&](int i) { return src(i0 + i); });
         __syncthreads();
     };
-    mx_tile<2, NI, MR>(mat, xs, wk.n, row0, lig, stage, [&](int i, const float (&acc)[2][MR]) {
+    mx_tile<2, NI, MR>(mat, xs, wk.n, row0, lig, pre, stage, [&](int i, const float (&acc)[2][MR]) {
         const int s2 = wk.slot[i];
 #pragma unroll
         for (int r = 0; r < MR; r++) {
@@ -501,11 +537,15 @@ __global__ __launch_bounds__(DN_WAVES * 64) void moe_down_kernel(MoeArgs a) {
     const int lig = lane & 31;
     constexpr int MR = DN_MR;
     const int row0 = blockIdx.x * (DN_WAVES * 2 * MR) + wave * 2 * MR + (lane >> 5) * MR;
+    auto src = [&](int i) { return (const float*)(a.h + (size_t)wk.slot[i] * a.eid); };
+    float4 xr[TCH][XR];
+    auto pre = [&]() { load_inputs<TCH>(xr, n, a.eid, src); };
     auto stage = [&](int i0, int cnt) {
-        stage_inputs(xs, cnt, a.eid, nb, [&](int i) { return (const float*)(a.h + (size_t)wk.slot[i0 + i] * a.eid); });
+        if (i0 == 0) put_inputs<TCH>(xs, xr, cnt, nb);
+        else stage_inputs(xs, cnt, a.eid, nb, [&](int i) { return src(i0 + i); });
         __syncthreads();
     };
-    mx_tile<1, NI, MR>(mat, xs, n, row0, lig, stage, [&](int i, const float (&acc)[1][MR]) {
+    mx_tile<1, NI, MR>(mat, xs, n, row0, lig, pre, stage, [&](int i, const float (&acc)[1][MR]) {
         float* y = a.d + (size_t)wk.slot[i] * a.hidden;
 #pragma unroll
         for (int r = 0; r < MR; r++) {
@@ -552,7 +592,7 @@ __global__ __launch_bounds__(FG * FGW * 64) void moe_down_fused_kernel(MoeArgs a
                      [&](int i) { return (const float*)(a.h + (size_t)rt.work[i].slot[0] * a.eid); });
         __syncthreads();
     };
-    mx_tile<1, NI, FMR>(mat, xs + (size_t)gi * nb * XBP, 1, row0, lig, stage,
+    mx_tile<1, NI, FMR>(mat, xs + (size_t)gi * nb * XBP, 1, row0, lig, [] {}, stage,
                         [&](int, const float (&acc)[1][FMR]) {
 #pragma unroll
         for (int r = 0; r < FMR; r++) {
