@@ -587,12 +587,17 @@ __global__ __launch_bounds__(FG * FGW * 64) void moe_down_fused_kernel(MoeArgs a
     const int row0 = tile0 + wl * 2 * FMR + (lane >> 5) * FMR;
     float* part = xs + (size_t)FG * nb * XBP;
     const int nst = nwork < FG ? nwork : FG;
-    auto stage = [&](int, int) {                 // one input a group: all groups' at once
-        stage_inputs(xs, nst, a.eid, nb,
-                     [&](int i) { return (const float*)(a.h + (size_t)rt.work[i].slot[0] * a.eid); });
+    // one input a group, all groups' at once, loaded ahead of the codes
+    static_assert(FG * FGW * 64 * XR * 4 >= 4096, "one register chunk holds a 4096-float input");
+    float4 xr[FG][XR];
+    auto pre = [&]() {
+        load_inputs<FG>(xr, nst, a.eid, [&](int i) { return (const float*)(a.h + (size_t)rt.work[i].slot[0] * a.eid); });
+    };
+    auto stage = [&](int, int) {
+        put_inputs<FG>(xs, xr, nst, nb);
         __syncthreads();
     };
-    mx_tile<1, NI, FMR>(mat, xs + (size_t)gi * nb * XBP, 1, row0, lig, [] {}, stage,
+    mx_tile<1, NI, FMR>(mat, xs + (size_t)gi * nb * XBP, 1, row0, lig, pre, stage,
                         [&](int, const float (&acc)[1][FMR]) {
 #pragma unroll
         for (int r = 0; r < FMR; r++) {
