@@ -615,8 +615,8 @@ __device__ __forceinline__ void flush_tile(const GemvArgs& a, int m, int row0, i
 // a lane, one first-entry load a tile).
 // Issue order: outlier row pointers; in the prep waves the x of the first
 // two passes; the first weight item; the prep waves' digit arithmetic and
-// later passes; prepared digits and x; the barrier; the rest of the first D
-// weight items; then the first outlier entries of each tile, the item loop
+// later passes; prepared digits and x; the first outlier entries of each
+// tile; the barrier; the rest of the first D weight items; then the item loop
 // (the first entries join the row sums before the one reduction a row), the
 // remaining outlier entries and the stores.
 template <int FMT, int BS, int R, int D, bool OUT, bool PREP, bool DREG>
@@ -798,16 +798,13 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
         }
         if (t_id < a.nb) meta[t_id] = mr;
     }
-    __syncthreads();
-
-#pragma unroll
-    for (int k = 1; k < D; k++) issue(wv[k]);
-
     // 5. CSR bounds to every lane of the group (ds_bpermute), then the first
     //    outlier entries of each tile, one per lane: a tile's R rows own the
-    //    contiguous entries [rpv[j][0], rpv[j][R]).  Issued here, after the
-    //    preparation, that round trip overlaps the weight stream; the entries
-    //    are first used at a tile's end.
+    //    contiguous entries [rpv[j][0], rpv[j][R]).  Issued before the
+    //    barrier: the bounds (loaded first thing) are back by then, and the
+    //    entries, first used at the wave's first tile end, queue ahead of the
+    //    rest of its weights instead of behind them (config 1 12.64 ->
+    //    11.98 us against issuing them after the barrier).
     uint32_t rpv[MT][R + 1];
     uint32_t e0[MT];
     if constexpr (OUT) {
@@ -823,6 +820,11 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
             e0[j] = oe[pk ? min(rpv[j][0] + lig, last) : 0u];
         }
     }
+
+    __syncthreads();
+
+#pragma unroll
+    for (int k = 1; k < D; k++) issue(wv[k]);
 
     // 6. Digits in registers: with one block a lane (nb <= lpg) the lane's
     //    block is the same in every item, so its digit words and meta are read
