@@ -805,20 +805,33 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
     //    entries, first used at the wave's first tile end, queue ahead of the
     //    rest of its weights instead of behind them (config 1 12.64 ->
     //    11.98 us against issuing them after the barrier).
-    uint32_t rpv[MT][R + 1];
+    //    Only what the item loop needs stays live: the entries, a mask of
+    //    the row each lane's first entry belongs to (bit J*R + r), and
+    //    whether any tile has entries past its first lpg.  The bounds
+    //    themselves (R+1 registers a tile) held through the loop cost
+    //    config 1 about 0.5 us; step 8 rebuilds them when it has work.
     uint32_t e0[MT];
+    uint32_t omask = 0;
+    bool orest = false;
+    static_assert(MT * R <= 32, "one mask bit a tile row");
     if constexpr (OUT) {
         const int gl = lane & ~(lpg - 1);                     // group's first lane
-#pragma unroll
-        for (int j = 0; j < MT; j++)
-#pragma unroll
-            for (int r = 0; r <= R; r++) rpv[j][r] = __shfl(rpl, gl + j * (R + 1) + r);
         const bool pk = OE != nullptr;
+        bool more = false;
 #pragma unroll
         for (int j = 0; j < MT; j++) {
+            uint32_t rb[R + 1];
+#pragma unroll
+            for (int r = 0; r <= R; r++) rb[r] = __shfl(rpl, gl + j * (R + 1) + r);
             const uint32_t* oe = pk ? OE : own_of(j);
-            e0[j] = oe[pk ? min(rpv[j][0] + lig, last) : 0u];
+            const uint32_t idx = rb[0] + lig;
+            e0[j] = oe[pk ? min(idx, last) : 0u];
+#pragma unroll
+            for (int r = 0; r < R; r++)
+                if (pk && idx >= rb[r] && idx < rb[r + 1]) omask |= 1u << (j * R + r);
+            more |= j < nt && pk && idx + lpg < rb[R];
         }
+        orest = __any(more);
     }
 
     __syncthreads();
@@ -847,19 +860,14 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
 #pragma unroll
     for (int r = 0; r < R; r++) rs[r] = 0.0f;
     int cj = 0, cq = 0;                                       // compute cursor
-    // first outlier entries of tile J (static J: no indexed arrays): entry
-    // rpv[J][0] + lig belongs to row r when it lies in [rpv[J][r], rpv[J][r+1])
+    // first outlier entries of tile J (static J: no indexed arrays): the
+    // lane's entry belongs to row r when mask bit J*R + r is set
     auto first_entries = [&](auto jc) __attribute__((always_inline)) {
         constexpr int J = decltype(jc)::value;
-        const bool pk = OE != nullptr;
-        const uint32_t idx = rpv[J][0] + lig, e = e0[J];
-        const bool ok = pk && idx < rpv[J][R];
-        const float p = qsf::f16_bits(e >> 16) * xs[ok ? e & 0xFFFFu : 0u];
+        const uint32_t e = e0[J], mb = (omask >> (J * R)) & ((1u << R) - 1);
+        const float p = qsf::f16_bits(e >> 16) * xs[mb ? e & 0xFFFFu : 0u];
 #pragma unroll
-        for (int r = 0; r < R; r++) {
-            const bool mine = ok && idx >= rpv[J][r] && idx < rpv[J][r + 1];
-            rs[r] += mine ? p : 0.0f;
-        }
+        for (int r = 0; r < R; r++) rs[r] += (mb >> r) & 1u ? p : 0.0f;
     };
     auto tile_end = [&]() __attribute__((always_inline)) {
         if constexpr (OUT) {
@@ -907,7 +915,13 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
 
     // 8. remaining outlier entries of each tile, one per lane each step;
     //    every slot loads (clamped index, own row where absent)
-    if constexpr (OUT) {
+    if constexpr (OUT) if (orest) {
+        uint32_t rpv[MT][R + 1];
+        const int gl = lane & ~(lpg - 1);
+#pragma unroll
+        for (int j = 0; j < MT; j++)
+#pragma unroll
+            for (int r = 0; r <= R; r++) rpv[j][r] = __shfl(rpl, gl + j * (R + 1) + r);
         float orem[MT][R];
 #pragma unroll
         for (int j = 0; j < MT; j++)
