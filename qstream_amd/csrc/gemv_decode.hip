@@ -312,14 +312,24 @@ __device__ __forceinline__ void prep_finish(const float (&xv)[Fmt<FMT, BS>::NC *
     constexpr int NS = F::NC * 8;
     const bool lane_live = live && w < F::CW;
     if (xs && lane_live) {
+        if constexpr (FMT == QK_FMT_3) {
 #pragma unroll
-        for (int s = 0; s < NS; s++) {
-            int code, shift;
-            slot_code<FMT>(w, s / 8, s % 8, code, shift);
-            const int col = b * BS + code;
-            bool own = col < cols;
-            if constexpr (FMT == QK_FMT_3) own = own && (3 * code) / 4 == 8 * w + s % 8;
-            if (own) xs[col] = xv[s];
+            for (int s = 0; s < NS; s++) {
+                int code, shift;
+                slot_code<FMT>(w, s / 8, s % 8, code, shift);
+                const int col = b * BS + code;
+                if (col < cols && (3 * code) / 4 == 8 * w + s % 8) xs[col] = xv[s];
+            }
+        } else {
+            // 2/4-bit: the lane's slots are the NS consecutive columns from
+            // b*BS + NS*w (zero past cols, as the copy must hold there),
+            // written back in column order as 16-byte LDS stores
+            constexpr auto slot_of = [](int k) { return FMT == QK_FMT_2 ? (k & 1) * 8 + (k >> 1) : k; };
+            f32x4* d4 = reinterpret_cast<f32x4*>(xs + b * BS + NS * w);
+#pragma unroll
+            for (int q = 0; q < NS / 4; q++)
+                d4[q] = f32x4{xv[slot_of(4 * q)], xv[slot_of(4 * q + 1)], xv[slot_of(4 * q + 2)],
+                              xv[slot_of(4 * q + 3)]};
         }
     }
     // block max of |x| as fp32 bits (non-negative floats order like their
