@@ -870,21 +870,22 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
 #pragma unroll
     for (int r = 0; r < R; r++) rs[r] = 0.0f;
     int cj = 0, cq = 0;                                       // compute cursor
-    // first outlier entries of tile J (static J: no indexed arrays): the
-    // lane's entry belongs to row r when mask bit J*R + r is set
-    auto first_entries = [&](auto jc) __attribute__((always_inline)) {
-        constexpr int J = decltype(jc)::value;
-        const uint32_t e = e0[J], mb = (omask >> (J * R)) & ((1u << R) - 1);
+    // first outlier entries of the tile ending now.  Tiles end in order, so
+    // its entry and mask bits are always at the front: consumed there, then
+    // the rest shift down (a few moves, where a per-tile selection over a
+    // runtime tile index cost a chain of branches: config 1 11.25 -> 10.74
+    // us).  The lane's entry belongs to row r when mask bit r is set.
+    auto first_entries = [&]() __attribute__((always_inline)) {
+        const uint32_t e = e0[0], mb = omask & ((1u << R) - 1);
         const float p = qsf::f16_bits(e >> 16) * xs[mb ? e & 0xFFFFu : 0u];
 #pragma unroll
         for (int r = 0; r < R; r++) rs[r] += (mb >> r) & 1u ? p : 0.0f;
+#pragma unroll
+        for (int j = 0; j + 1 < MT; j++) e0[j] = e0[j + 1];
+        omask >>= R;
     };
     auto tile_end = [&]() __attribute__((always_inline)) {
-        if constexpr (OUT) {
-            [&]<int... I>(std::integer_sequence<int, I...>) {
-                ((cj == I ? first_entries(std::integral_constant<int, I>{}) : void()), ...);
-            }(std::make_integer_sequence<int, MT>{});
-        }
+        if constexpr (OUT) first_entries();
 #pragma unroll
         for (int r = 0; r < R; r++) {
             const float v = group_reduce(rs[r], lpg);
