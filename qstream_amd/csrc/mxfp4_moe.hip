@@ -486,12 +486,44 @@ __global__ __launch_bounds__(MAX_TOK * 64) void moe_route_kernel(MoeArgs a) {
 // Gate/up: workgroup (x, y) computes rows of row tile x of the gate and up
 // matrices of distinct expert y for the tokens that picked it:
 // h[slot] = act(gate + b) * (up + b).
-template <int NI>
+// RT (one token): every workgroup routes the token itself (one wave; what
+// the route kernel does) instead of waiting for a routing launch, and
+// workgroup (0, 0) stores the result for the down kernel.
+template <int NI, bool RT>
 __global__ __launch_bounds__(GU_WAVES * 64) void moe_gate_up_kernel(MoeArgs a) {
     constexpr int MR = GU_MR;
     extern __shared__ __align__(16) float xs[];           // [n][hidden, padded]
-    if ((int)blockIdx.y >= a.route->nwork) return;
-    const Work& wk = a.route->work[blockIdx.y];
+    float4 xr[TCH][XR];
+    const Route* rtp = a.route;
+    if constexpr (RT) {
+        // the one token's input does not depend on the routing: loaded first
+        load_inputs<TCH>(xr, 1, a.hidden, [&](int) { return a.x; });
+        __shared__ int s_idx[MAX_K];
+        __shared__ float s_w[MAX_K];
+        __shared__ float s_p[MAX_EXP];
+        __shared__ unsigned s_tok[MAX_EXP];
+        __shared__ int s_item[MAX_EXP];
+        __shared__ Route s_rt;
+        if (threadIdx.x < 64) {
+            if (a.n_exp <= 64) route_token<1>(a.logits, a.n_exp, a.k, a.norm, 0, s_idx, s_w, s_p);
+            else route_token<MAX_EXP / 64>(a.logits, a.n_exp, a.k, a.norm, 0, s_idx, s_w, s_p);
+            __builtin_amdgcn_wave_barrier();
+            if ((int)threadIdx.x < a.k) {
+                s_rt.idx[threadIdx.x] = s_idx[threadIdx.x];
+                s_rt.w[threadIdx.x] = s_w[threadIdx.x];
+            }
+            build_work(s_idx, a.k, a.k, s_tok, s_item, s_rt);
+        }
+        __syncthreads();
+        if (blockIdx.x == 0 && blockIdx.y == 0) {
+            const uint32_t* src = reinterpret_cast<const uint32_t*>(&s_rt);
+            uint32_t* dst = reinterpret_cast<uint32_t*>(a.route);
+            for (int i = threadIdx.x; i < (int)(sizeof(Route) / 4); i += blockDim.x) dst[i] = src[i];
+        }
+        rtp = &s_rt;
+    }
+    if ((int)blockIdx.y >= rtp->nwork) return;
+    const Work& wk = rtp->work[blockIdx.y];
     const MxExpert ex = a.experts[wk.expert];
     const int nb = (a.hidden + 31) / 32;
     const MxMat mat[2] = {{ex.gc, ex.gs, a.eid, a.hidden, nb}, {ex.uc, ex.us, a.eid, a.hidden, nb}};
@@ -499,8 +531,9 @@ __global__ __launch_bounds__(GU_WAVES * 64) void moe_gate_up_kernel(MoeArgs a) {
     const int lig = lane & 31;
     const int row0 = blockIdx.x * (GU_WAVES * 2 * MR) + wave * 2 * MR + (lane >> 5) * MR;
     auto src = [&](int i) { return a.x + (size_t)(wk.slot[i] / a.k) * a.hidden; };
-    float4 xr[TCH][XR];
-    auto pre = [&]() { load_inputs<TCH>(xr, wk.n, a.hidden, src); };
+    auto pre = [&]() {
+        if constexpr (!RT) load_inputs<TCH>(xr, wk.n, a.hidden, src);
+    };
     auto stage = [&](int i0, int cnt) {
         if (i0 == 0) put_inputs<TCH>(xs, xr, cnt, nb);
         else stage_inputs(xs, cnt, a.hidden, nb, [&](int i) { return src(i0 + i); });
@@ -716,18 +749,24 @@ extern "C" int qk_moe_launch(const qk_mx_expert* d_experts, int n_exp, int k, in
     constexpr int rows_gu = GU_WAVES * 2 * GU_MR;
     constexpr int rows_dn = DN_WAVES * 2 * DN_MR;
     const dim3 g_gu((eid + rows_gu - 1) / rows_gu, items), g_dn((hidden + rows_dn - 1) / rows_dn, items);
-    hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(MAX_TOK * 64), 0, s, a);
+    // one token with the fused down: gate/up routes in-kernel (no route launch)
+    const bool one = ntok == 1 && k <= FG;
+    if (!one) hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(MAX_TOK * 64), 0, s, a);
     const int tch = ntok < TCH ? ntok : TCH;
     const size_t lds_gu = (size_t)tch * ((hidden + 31) / 32) * XBP * 4,
                  lds_dn = (size_t)tch * ((eid + 31) / 32) * XBP * 4;
     const int ni_gu = (hidden + 1023) / 1024, ni_dn = (eid + 1023) / 1024;
+#define QK_GU(NI)                                                                        \
+    if (one) launch_lds<moe_gate_up_kernel<NI, true>>(g_gu, block_gu, lds_gu, s, a, true); \
+    else launch_lds<moe_gate_up_kernel<NI, false>>(g_gu, block_gu, lds_gu, s, a, true);
     switch (ni_gu) {
-    case 1: launch_lds<moe_gate_up_kernel<1>>(g_gu, block_gu, lds_gu, s, a, true); break;
-    case 2: launch_lds<moe_gate_up_kernel<2>>(g_gu, block_gu, lds_gu, s, a, true); break;
-    case 3: launch_lds<moe_gate_up_kernel<3>>(g_gu, block_gu, lds_gu, s, a, true); break;
-    default: launch_lds<moe_gate_up_kernel<4>>(g_gu, block_gu, lds_gu, s, a, true); break;
+    case 1: QK_GU(1) break;
+    case 2: QK_GU(2) break;
+    case 3: QK_GU(3) break;
+    default: QK_GU(4) break;
     }
-    if (ntok == 1 && k <= FG) {
+#undef QK_GU
+    if (one) {
         // one token: down and combine in one launch
         const dim3 g_f((hidden + FROWS - 1) / FROWS), b_f(FG * FGW * 64);
         const size_t lds_f = (size_t)FG * ((eid + 31) / 32) * XBP * 4 + (size_t)FG * FROWS * 4;
