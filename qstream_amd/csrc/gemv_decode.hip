@@ -846,8 +846,13 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
 
     __syncthreads();
 
+    // (outlier kernels: only the items the wave has.  Measured with the
+    // guard: config 1 10.83 -> 10.59 us, although its waves all have more
+    // than D items, so the difference is in the generated code; in the
+    // 3-bit kernels the same guard cost 0.9 us, so they issue all D.)
 #pragma unroll
-    for (int k = 1; k < D; k++) issue(wv[k]);
+    for (int k = 1; k < D; k++)
+        if (!OUT || k < ni) issue(wv[k]);
 
     // 6. Digits in registers: with one block a lane (nb <= lpg) the lane's
     //    block is the same in every item, so its digit words and meta are read
