@@ -2,7 +2,7 @@
 """Benchmark of QStream's quantized matvec hot path on one MI355X.
 
 Metric: quant matvec HBM GB/s (% of ~8 TB/s peak) + us/call
-at 7B decode shapes.  The default workload is BASELINE config 1: the
+at 7B decode shapes.  The default workload is BASELINE.json config 1: the
 2-bit+outlier FFN gate and up projections (11008x4096 each, block 64), batch-1
 decode.  A step is one pass over one activation vector: x-prep + one grouped
 GEMV launch over gate and up.  Weights rotate over >= 512 MiB of distinct

@@ -203,7 +203,7 @@ def random_mxfp4(rng: np.random.Generator, rows: int, cols: int,
     return codes.tobytes() + scales.tobytes()
 
 
-# ---- seeded synthetic inputs of the BASELINE configs -----------------------
+# ---- seeded synthetic inputs of the benchmark configs -----------------------
 def gaussian(rng: np.random.Generator, shape, std: float = 1.0) -> np.ndarray:
     return (rng.standard_normal(shape, dtype=np.float32) * np.float32(std)).astype(np.float32)
 

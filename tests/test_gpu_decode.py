@@ -4,7 +4,7 @@ Every case calls libqsf_hip through its C ABI (ctypes) on cuda:0 and compares
 with oracle/ (a strict restatement of src/kernels_scalar.c and src/quant.c,
 itself pinned bit-exactly to the compiled reference in test_oracle.py):
   * unpack: codes, block meta and dequantised values bit-exact;
-  * matvec: relative L2 error <= 1e-5, fp32 accumulate.
+  * matvec: relative L2 error <= 1e-5 (the tolerance the path is held to), fp32 accumulate.
 """
 from __future__ import annotations
 

@@ -99,7 +99,7 @@ def test_prefill_vs_scalar_oracle(hip, oracle, m, n, k, bs):
 
 
 def test_prefill_config4_rows(hip, oracle):
-    """BASELINE config 4 (M=512, K=4096, N=14336, block 64): all outputs
+    """Benchmark config 4 (M=512, K=4096, N=14336, block 64): all outputs
     against the exact-weight fp64 reference."""
     m, n, k, bs = 512, 14336, 4096, 64
     payload, xb = case(4, m, n, k, bs)
