@@ -684,15 +684,21 @@ __global__ void moe_combine_kernel(MoeArgs a) {
 }
 
 // Expert kernels with dynamic LDS: the first launch of an instantiation
-// allows it up to 152 KB (inputs of 8 tokens exceed 64 KB).  `timed`
+// allows it what its static LDS leaves of 160 KB (inputs of 8 tokens exceed
+// 64 KB).  `timed`
 // launches record the library's kernel-timing event pair (diagnostics) when
 // it is enabled.
 template <auto K>
 void launch_lds(dim3 g, dim3 b, size_t lds, hipStream_t s, const MoeArgs& a, bool timed = false) {
     static bool allowed = false;
     if (!allowed) {
+        // what the kernel's static LDS leaves of the CU's 160 KB (asking for
+        // more fails the call, and its error would be reported at the launch)
+        hipFuncAttributes fa = {};
+        const size_t st = hipFuncGetAttributes(&fa, reinterpret_cast<const void*>(K)) == hipSuccess
+                              ? fa.sharedSizeBytes : (size_t)16384;
         (void)hipFuncSetAttribute(reinterpret_cast<const void*>(K),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024 - 8192);
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)(160 * 1024 - st));
         allowed = true;
     }
     hipEvent_t e0, e1;
