@@ -160,3 +160,40 @@ def test_moe_repeated_calls_reuse_workspace(hip, oracle):
     for ts in tens.values():
         for t in ts:
             t.free()
+
+
+@pytest.mark.parametrize("ntok,all_nan", [(1, False), (3, False), (3, True)])
+def test_moe_nan_logits_pick_nothing(hip, oracle, ntok, all_nan):
+    """A NaN router logit makes every softmax probability NaN (the sum
+    carries it, src/kernels_scalar.c:187-214), and the strict '>' top-K from
+    its -1e30 start then picks no expert (src/engine.c:987-1018): that
+    token's output is zero.  Token 0 (or every token) has one NaN logit; the
+    others are routed as usual.  Covers the no-work paths: the batch-1 fused
+    down and the combine."""
+    torch = torch_cuda()
+    rng = np.random.default_rng(11 + ntok + 5 * all_nan)
+    n_exp, k, hidden, eid = 8, 2, 128, 64
+    ex = _experts(rng, n_exp, hidden, eid, True)
+    x = F.gaussian(rng, (ntok, hidden))
+    logits = F.gaussian(rng, (ntok, n_exp))
+    for t in range(ntok if all_nan else 1):
+        logits[t, 3] = np.nan
+    ref = np.stack([oracle.moe_token(ex, k, 1, 2, hidden, eid, x[t], logits[t])
+                    for t in range(ntok)])
+    assert (ref[0] == 0).all()
+    tens = {n: [hip.Tensor(e[n], F.MXFP4, *((eid, hidden) if n != "down" else (hidden, eid)), 32)
+                for e in ex] for n in ("gate", "up", "down")}
+    biases = {n: [e[n] for e in ex] for n in ("gate_bias", "up_bias", "down_bias")}
+    moe = hip.Moe(tens["gate"], tens["up"], tens["down"], hidden, eid, **biases)
+    out = torch.full((ntok, hidden), float("nan"), device="cuda:0")
+    moe.forward(k, 1, 2, ntok, dev(x), dev(logits), out, stream=_stream())
+    got = host(out)
+    for t in range(ntok):
+        if (ref[t] == 0).all():
+            assert (got[t] == 0).all(), t
+        else:
+            assert rel_l2(got[t], ref[t]) <= REL_L2, t
+    moe.free()
+    for ts in tens.values():
+        for t in ts:
+            t.free()
