@@ -1293,7 +1293,7 @@ int launch_rt(const qsf_hip_tensor* const* t, int n, int cols, const float* d_x,
         launch_main<gemv_kernel<FMT, BS, R, D, false, true, DREG>>(g, b, lds, s, a);
     else if (any_out)
         launch_main<gemv_kernel<FMT, BS, R, DO, kHasOut, false, DREG>>(g, b, lds, s, a);
-    else if (DREG && single)
+    else if (single)
         launch_main<gemv_kernel<FMT, BS, R, 1, false, false, DREG>>(g, b, lds, s, a);
     else
         launch_main<gemv_kernel<FMT, BS, R, D, false, false, DREG>>(g, b, lds, s, a);
