@@ -1242,7 +1242,7 @@ int launch_rt(const qsf_hip_tensor* const* t, int n, int cols, const float* d_x,
                        (!prepared || dig_dw <= (size_t)4 * DV * WAVES * 64) &&
                        main_fixed + per_tile <= lds_limit();
     size_t lds = (size_t)a.chunk * per_block;                 // chunked kernel
-    bool single = false;                                      // at most one item a wave
+    int most = 1 << 30;                                       // items a wave at most
     a.xs_off = 0;
     a.st_off = 0;
     a.st_wave = 0;
@@ -1265,7 +1265,7 @@ int launch_rt(const qsf_hip_tensor* const* t, int n, int cols, const float* d_x,
         while (grid_of(a.tpw) * n > num_cus() && a.tpw < tpw_max) a.tpw++;
         grid = grid_of(a.tpw);
         const int ntc = (a.tpw + WAVES - 1) / WAVES;
-        single = ntc * ((nb + lpg - 1) / lpg) <= 1;
+        most = ntc * ((nb + lpg - 1) / lpg);
         a.xs_off = (int)(meta_dw + dig_dw);
         a.st_off = a.xs_off + nb * BS;
         a.st_wave = ntc * rows_per_tile;
@@ -1278,7 +1278,8 @@ int launch_rt(const qsf_hip_tensor* const* t, int n, int cols, const float* d_x,
     // one item a wave at most (a 4096-row matrix of up to 64 blocks): one
     // item in flight.  A second would only re-read a row for nothing, and
     // its wave could not retire before that load returned (4096x4096 4-bit
-    // 5.05 -> 4.70 us, 3-bit 6.85 -> 6.44 us).
+    // 5.05 -> 4.70 us, 3-bit 6.85 -> 6.44 us).  Likewise at most two items
+    // keep two in flight (3-bit q/k/v 9.3 -> 9.0 us, down 12.86 -> 12.72).
     // digits in registers: small items, two in flight, so that a wave
     // alternates issue and compute
     constexpr int D = DREG ? 2 : prefetch_depth<FMT, BS, R, false>();
@@ -1293,8 +1294,10 @@ int launch_rt(const qsf_hip_tensor* const* t, int n, int cols, const float* d_x,
         launch_main<gemv_kernel<FMT, BS, R, D, false, true, DREG>>(g, b, lds, s, a);
     else if (any_out)
         launch_main<gemv_kernel<FMT, BS, R, DO, kHasOut, false, DREG>>(g, b, lds, s, a);
-    else if (single)
+    else if (most <= 1)
         launch_main<gemv_kernel<FMT, BS, R, 1, false, false, DREG>>(g, b, lds, s, a);
+    else if (D > 2 && most <= 2)
+        launch_main<gemv_kernel<FMT, BS, R, (D > 2 ? 2 : D), false, false, DREG>>(g, b, lds, s, a);
     else
         launch_main<gemv_kernel<FMT, BS, R, D, false, false, DREG>>(g, b, lds, s, a);
     return hipGetLastError() == hipSuccess ? 0 : -1;
