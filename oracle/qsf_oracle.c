@@ -329,13 +329,54 @@ void orc_moe_token(const orc_expert* ex, int n_exp, int k, int norm_topk, int ac
     free(probs); free(idx); free(w); free(g); free(u); free(d);
 }
 
+/* M token-by-token src/kernels_scalar.c:64-85 matvecs on float(bf16 x)
+ * (the engine prefills one token at a time, src/engine.c:1289-1295).
+ * The weights are dequantised once (the same values matvec_dense makes per
+ * call) and four rows run as independent chains; each row keeps
+ * matvec_dense's sequential order, so y is bit-identical to the token loop
+ * (tests/test_oracle.py checks that). */
 void orc_prefill_4bit(const void* w, const uint16_t* x_bf16, float* y,
                       int m, int n, int k, int bs) {
+    if (m <= 0 || n <= 0) return;
+    size_t bb = orc_block_bytes(ORC_Q4, bs);
+    int nb = k > 0 ? (k + bs - 1) / bs : 0;
     float* xf = (float*)malloc(sizeof(float) * (size_t)(k > 0 ? k : 1));
+    float* wd = (float*)malloc(sizeof(float) * (size_t)n * (size_t)(k > 0 ? k : 1));
+    const uint8_t* wp = (const uint8_t*)w;
+    for (int r = 0; r < n; r++)
+        for (int b = 0, col = 0; b < nb; b++, col += bs) {
+            int count = (col + bs <= k) ? bs : k - col;
+            orc_dequant_block(ORC_Q4, wp, wd + (size_t)r * k + col, count);
+            wp += bb;
+        }
     for (int t = 0; t < m; t++) {
         for (int i = 0; i < k; i++)
             xf[i] = bits_to_f32((uint32_t)x_bf16[(size_t)t * k + i] << 16);
-        matvec_dense(ORC_Q4, w, xf, y + (size_t)t * n, n, k, bs);
+        float* yt = y + (size_t)t * n;
+        int r = 0;
+        for (; r + 4 <= n; r += 4) {
+            const float* w0 = wd + (size_t)r * k;
+            const float* w1 = w0 + k;
+            const float* w2 = w1 + k;
+            const float* w3 = w2 + k;
+            float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+            for (int i = 0; i < k; i++) {
+                float p0 = w0[i] * xf[i], p1 = w1[i] * xf[i];
+                float p2 = w2[i] * xf[i], p3 = w3[i] * xf[i];
+                a0 = a0 + p0; a1 = a1 + p1; a2 = a2 + p2; a3 = a3 + p3;
+            }
+            yt[r] = a0; yt[r + 1] = a1; yt[r + 2] = a2; yt[r + 3] = a3;
+        }
+        for (; r < n; r++) {
+            const float* w0 = wd + (size_t)r * k;
+            float a0 = 0.0f;
+            for (int i = 0; i < k; i++) {
+                float p0 = w0[i] * xf[i];
+                a0 = a0 + p0;
+            }
+            yt[r] = a0;
+        }
     }
+    free(wd);
     free(xf);
 }

@@ -3,28 +3,41 @@
 //
 // There is no reference kernel: the engine runs one matvec per token
 // (src/engine.c:1289-1295), so the specification is M independent
-// src/kernels_scalar.c:64-85 matvecs on float(bf16(x_m)).  Here the weights
-// are dequantised in registers, w = s*q + z (exact in fp32: s*q has at most
-// 15 significant bits), rounded to bf16 (round-to-nearest-even,
-// v_cvt_pk_bf16_f32) and contracted with v_mfma_f32_16x16x32_bf16 in fp32.
-// The one rounding beyond fp32 accumulation is that of w to bf16.
+// src/kernels_scalar.c:64-85 matvecs on float(bf16(x_m)), with
+// w = s*q + z per block (src/quant.c:136-155).
+//
+// Arithmetic.  Nothing is rounded below fp32.  Per block b of a weight row,
+//   sum_k (s q_k + z) x_k = s * (sum_k q_k x_k) + z * X_b,   X_b = sum_k x_k.
+//  * The codes q (0..15) are exact bf16 integers, x is bf16, so every MFMA
+//    product q*x is exact; v_mfma_f32_16x16x32_bf16 sums them in fp32.  The
+//    sum restarts every 64 k (a "sub-block"; the scale is constant inside
+//    one) and is folded into the output in fp32: out = fma(s, acc, out).
+//  * The zero-point term sum_b z_b X_b is itself a small contraction over
+//    the blocks.  It runs on the same MFMA as extra k-steps ahead of the
+//    codes, on exact bf16 splits: z = zh + zl (fp16 has 11 significant
+//    bits, bf16 8, so the remainder has at most 3) and X_b = X1 + X2 + X3
+//    (fp32 sum of the block, 24 bits in three 8-bit parts).  Each block
+//    takes 8 extra k positions, {X1, X2, X3, X1, X2, 0, 0, 0} against
+//    {zh, zh, zh, zl, zl, 0, 0, 0}: every product is exact and only
+//    zl*X3 (2^-26 of z X_b) is left out.
+// Against the scalar oracle this is at the level of fp32 accumulation
+// order (about 1e-6 rel-L2), not of bf16 weights.
 //
 // Tiling.  One 512-thread workgroup per 256 (m) x 112 (n) tile of Y; at
 // config-4 shape (M 512, N 14336) that is exactly one workgroup per CU.  K
-// advances in stages of 128 codes (4 MFMA k-steps).  The waves split by role,
-// one of each per SIMD, so dequantisation (VALU) and MFMAs overlap in the
-// hardware rather than in one instruction stream:
-//  * 4 producer waves dequantise stage s+1's 112 x 128 codes into a bf16 LDS
-//    tile ([112][128 + 8 pad], two buffers) while stage s is contracted;
-//    codes are loaded two stages ahead;
-//  * 4 consumer waves each own 64 rows x 112 columns (4 x 7 MFMA tiles, 112
-//    fp32 accumulators per lane).  A fragments come from x repacked into
-//    fragment order (xpack_kernel: one contiguous 1 KB load per fragment),
-//    one stage ahead in registers; B fragments come from LDS one k-step
-//    ahead.
+// advances in stages of 128 (4 MFMA k-steps): first the zero-point stages
+// (8 k positions per block, padded to an even stage count), then the code
+// stages.  The waves split by role, one of each per SIMD, so the VALU work
+// (code conversion, scale epilogue) and MFMAs overlap in the hardware:
+//  * 4 producer waves write stage s+1's 112 x 128 B tile into LDS (bf16,
+//    [112][128 + 8 pad], two buffers) with each column's sub-block scales,
+//    while stage s is contracted; their loads run two stages ahead;
+//  * 4 consumer waves each own 64 rows x 112 columns (4 x 7 MFMA tiles).
+//    A fragments come from x repacked into fragment order (xpack_kernel:
+//    one contiguous 1 KB load per fragment), one stage ahead in registers;
+//    B fragments come from LDS one n-tile ahead.
 // One barrier per stage.  Loads go through raw buffer descriptors: offsets
-// past a tensor read zeros, so prefetches past the end need no clamps and
-// all loads are issued unconditionally (exact compiler wait counts).
+// past a tensor read zeros, so prefetches past the end need no clamps.
 //
 #include "qsf_device.h"
 #include "qsf_hip_internal.h"
@@ -43,12 +56,27 @@ constexpr int BM = 256, BN = 112;      // workgroup tile: 4 waves x 64 m, 7 x 16
 constexpr int MT = 4, NT = 7;          // 16x16 MFMA tiles per wave
 constexpr int SK = 128;                // k per stage (4 MFMA k-steps)
 constexpr int PITCH = SK + 8;          // LDS row pitch of the B tile, bf16
+constexpr int BUF = BN * PITCH;        // bf16 per B buffer
+constexpr int SCN = 2 * BN;            // fp32 scales per buffer: [sub-block][column]
 constexpr int EP_PITCH = BN + 4;       // LDS row pitch of the output staging tile, fp32
 constexpr int EP_FLOATS = 4 * 64 * EP_PITCH;
+constexpr int LDS_MAIN = 2 * BUF * 2 + 2 * SCN * 4;
+constexpr int LDS_BYTES = LDS_MAIN > EP_FLOATS * 4 ? LDS_MAIN : EP_FLOATS * 4;
+constexpr int ZK = 8;                  // zero-point k positions per block
 
-// Eight codes (one dword, low nibble = even code) -> bf16(s*q + z) x 8.
-__device__ __forceinline__ bf16x8 dequant8(uint32_t w, float s, float z) {
-    // (byte extracts to float become v_cvt_f32_ubyte0..3)
+__device__ __forceinline__ float bf16_f32(__bf16 v) {
+    return __builtin_bit_cast(float, (uint32_t)__builtin_bit_cast(uint16_t, v) << 16);
+}
+
+// Round two fp32 to bf16 (round-to-nearest-even, v_cvt_pk_bf16_f32).
+__device__ __forceinline__ bf16x2 to_bf16x2(float a, float b) {
+    const f32x2 v = {a, b};
+    return __builtin_convertvector(v, bf16x2);
+}
+
+// Eight codes (one dword, low nibble = even code) -> the integers 0..15 as
+// bf16, exact (byte extracts to float become v_cvt_f32_ubyte0..3).
+__device__ __forceinline__ bf16x8 codes8(uint32_t w) {
     const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
     const float q[8] = {(float)(lo & 0xFFu),         (float)(hi & 0xFFu),
                         (float)((lo >> 8) & 0xFFu),  (float)((hi >> 8) & 0xFFu),
@@ -57,66 +85,81 @@ __device__ __forceinline__ bf16x8 dequant8(uint32_t w, float s, float z) {
     bf16x8 r;
 #pragma unroll
     for (int j = 0; j < 8; j += 2) {
-        const f32x2 v = {fmaf(s, q[j], z), fmaf(s, q[j + 1], z)};
-        const bf16x2 b = __builtin_convertvector(v, bf16x2);
+        const bf16x2 b = to_bf16x2(q[j], q[j + 1]);
         r[j] = b[0];
         r[j + 1] = b[1];
     }
     return r;
 }
 
-// The same with one shift and one and-or per pair of codes: code q becomes
-// the fp16 value 1 + q/16 (q in mantissa bits 6..9 of 1.0), and
-// fma(16 s, 1 + q/16, c) with c = z - 16 s equals fp32(s q + z) exactly
-// whenever c is exact in fp32 (the caller checks that per block).
-typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
-// `one` is 0x3C003C00 (fp16 1.0 twice) held in a VGPR by the caller: with
-// the mask in an SGPR the and-or is one v_and_or_b32 (a VOP3 reads at most
-// one scalar operand here, and two literals would split it in two).
-__device__ __forceinline__ bf16x8 dequant8_m16(uint32_t w, float s16, float c, uint32_t one) {
-    const uint32_t h[4] = {((w << 6) & 0x03C003C0u) | one,   // codes 0, 4
-                           ((w << 2) & 0x03C003C0u) | one,   // codes 1, 5
-                           ((w >> 2) & 0x03C003C0u) | one,   // codes 2, 6
-                           ((w >> 6) & 0x03C003C0u) | one};  // codes 3, 7
-    float x[8];
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const f16x2 p = __builtin_bit_cast(f16x2, h[j]);
-        x[j] = (float)p[0];
-        x[j + 4] = (float)p[1];
-    }
-    bf16x8 r;
-#pragma unroll
-    for (int j = 0; j < 8; j += 2) {
-        const f32x2 v = {fmaf(s16, x[j], c), fmaf(s16, x[j + 1], c)};
-        const bf16x2 b = __builtin_convertvector(v, bf16x2);
-        r[j] = b[0];
-        r[j + 1] = b[1];
-    }
-    return r;
+// Zero-point chunk of one block from its meta dword (fp16 scale | fp16 zero
+// << 16): {zh, zh, zh, zl, zl, 0, 0, 0}, zh = bf16(z), zl = z - zh (exact).
+__device__ __forceinline__ bf16x8 zchunk(uint32_t meta) {
+    const float z = qsf::f16_hi(meta);
+    const bf16x2 h = to_bf16x2(z, 0.f);
+    const bf16x2 l = to_bf16x2(z - bf16_f32(h[0]), 0.f);
+    const __bf16 zero = h[1];
+    return bf16x8{h[0], h[0], h[0], l[0], l[0], zero, zero, zero};
 }
 
 struct PrefillArgs {
     const uint8_t* w;        // QSF 4-bit blocks, rows n, row stride nb*BB
-    const u32x4* xp;         // x in A-fragment order (xpack_kernel)
+    const u32x4* xp;         // [X parts | x] in A-fragment order (xpack_kernel)
     float* y;                // fp32 [m][n]
     int m, n, k, nb;
-    int tiles_n, pairs;      // n tiles; stage pairs (ceil(k / 2 SK))
+    int tiles_n;
+    int sz, s;               // zero-point stages; all stages (both even)
     uint32_t w_bytes, xp_bytes;
 };
 
-// x bf16 [m][k] -> A-fragment order: for each group of 16 rows and each
-// 32-wide k-step kk < ksp, 64 chunks of 16 bytes, chunk l holding row
-// 16 g + l%16, columns 32 kk + 8 (l/16)..+7 (zero past m or k).  The GEMM
-// then loads each fragment as one contiguous 1 KB read instead of 64
-// scattered 16-byte pieces.  One workgroup per (row group, 8 k-steps): the
-// 16 x 256 tile is read row-contiguously into LDS and written back in
-// fragment order, both coalesced.
+// x bf16 [m][k] -> A-fragment order.  For each group of 16 rows, ksp_total
+// k-steps of 64 chunks of 16 bytes; chunk l of k-step kk holds row
+// 16 g + l%16:
+//  * k-steps kk < kz: the zero-point part, one chunk per block
+//    b = 4 kk + l/16: {X1, X2, X3, X1, X2, 0, 0, 0}, the bf16 split of the
+//    block's fp32 sum X_b = X1 + X2 + X3 (exact);
+//  * k-steps kz + kk: columns 32 kk + 8 (l/16)..+7 of x.
+// Zeros past m, k and nb.  The GEMM then loads each fragment as one
+// contiguous 1 KB read instead of 64 scattered 16-byte pieces.  One
+// workgroup per (row group, 8 k-steps): the code part reads a 16 x 256 tile
+// row-contiguously into LDS and writes it back in fragment order.
 constexpr int XP_PITCH = 256 + 8;      // LDS row pitch of the pack tile, bf16
 __global__ __launch_bounds__(256) void xpack_kernel(const uint16_t* __restrict__ x, u32x4* xp,
-                                                   int m, int k, int ksp) {
+                                                   int m, int k, int ksp_total, int kz,
+                                                   int bs, int nb) {
     __shared__ __align__(16) uint16_t tile[16 * XP_PITCH];
-    const int g = blockIdx.y, kk0 = blockIdx.x * 8, t = threadIdx.x;
+    const int g = blockIdx.y, t = threadIdx.x;
+    if ((int)blockIdx.x < kz / 8) {
+        // 32 blocks of each of the 16 rows; a lane sums one block in order
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const int r = (t >> 5) + 8 * h, row = g * 16 + r;
+            const int b = (int)blockIdx.x * 32 + (t & 31);
+            float X = 0.f;
+            if (row < m && b < nb) {
+                const uint16_t* xr = x + (size_t)row * k + (size_t)b * bs;
+                const int cnt = min(bs, k - b * bs);       // a multiple of 8
+                for (int e = 0; e < cnt; e += 8) {
+                    const u32x4 v = *reinterpret_cast<const u32x4*>(xr + e);
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        X += __builtin_bit_cast(float, v[j] << 16);
+                        X += __builtin_bit_cast(float, v[j] & 0xFFFF0000u);
+                    }
+                }
+            }
+            const bf16x2 p1 = to_bf16x2(X, 0.f);
+            const float r1 = X - bf16_f32(p1[0]);
+            const bf16x2 p2 = to_bf16x2(r1, 0.f);
+            const bf16x2 p3 = to_bf16x2(r1 - bf16_f32(p2[0]), 0.f);
+            const __bf16 zero = p1[1];
+            const bf16x8 c = {p1[0], p2[0], p3[0], p1[0], p2[0], zero, zero, zero};
+            xp[((size_t)g * ksp_total + (b >> 2)) * 64 + r + 16 * (b & 3)] =
+                __builtin_bit_cast(u32x4, c);
+        }
+        return;
+    }
+    const int kk0 = ((int)blockIdx.x - kz / 8) * 8;
     const int c = t & 31;                      // 16-byte chunk of a 256-wide row piece
 #pragma unroll
     for (int h = 0; h < 2; h++) {
@@ -129,7 +172,7 @@ __global__ __launch_bounds__(256) void xpack_kernel(const uint16_t* __restrict__
 #pragma unroll
     for (int h = 0; h < 2; h++) {
         const int j = t + 256 * h, kk = j >> 6, l = j & 63;
-        xp[((size_t)g * ksp + kk0 + kk) * 64 + l] =
+        xp[((size_t)g * ksp_total + kz + kk0 + kk) * 64 + l] =
             *reinterpret_cast<const u32x4*>(&tile[(l & 15) * XP_PITCH + kk * 32 + 8 * (l >> 4)]);
     }
 }
@@ -143,8 +186,7 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint3
 // Workgroup id -> (m tile, n tile).  Workgroups are dealt to the 8 XCDs
 // round-robin; this numbering hands each XCD a contiguous run of tiles in
 // column-major order, so the M tiles of one N tile run side by side on one
-// XCD and the weight tile they share is fetched into that XCD's L2 once
-// (measured: 72 MB fetched a launch at config 4 instead of 91 MB).
+// XCD and the weight tile they share is fetched into that XCD's L2 once.
 __device__ __forceinline__ void tile_of(int id, int nwg, int tiles_n, int& tm, int& tn) {
     const int q = nwg >> 3, r = nwg & 7, xcd = id & 7, slot = id >> 3;
     const int t = (xcd < r ? xcd * (q + 1) : r * (q + 1) + (xcd - r) * q) + slot;
@@ -153,83 +195,95 @@ __device__ __forceinline__ void tile_of(int id, int nwg, int tiles_n, int& tm, i
     tm = t - tn * tiles_m;
 }
 
-// RAGGED: k is not a multiple of 2 SK, so stages reach past the last column;
-// their B items and A fragments are zeroed.
+// RAGGED: k is not a multiple of 2 SK, so code stages reach past the last
+// column; their B items are zeroed (and x is zero there).
 template <int BS, bool RAGGED>
 __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
     constexpr int BB = 4 + BS / 2;             // block bytes
-    constexpr int BUF = BN * PITCH;            // bf16 per B buffer
-    // two B buffers during the main loop; the output staging tile after it
-    __shared__ __align__(16) __bf16 lds[2 * BUF > EP_FLOATS * 2 ? 2 * BUF : EP_FLOATS * 2];
+    // two B buffers and their scales during the main loop; the output
+    // staging tile after it
+    __shared__ __align__(16) uint8_t lds_raw[LDS_BYTES];
+    __bf16* const lds = reinterpret_cast<__bf16*>(lds_raw);
+    float* const scl = reinterpret_cast<float*>(lds_raw + 2 * BUF * 2);
 
     const int t = threadIdx.x, lane = t & 63;
     const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
     int tm, tn;
     tile_of(blockIdx.x, gridDim.x, a.tiles_n, tm, tn);
     const int n0 = tn * BN;
-    const int S = 2 * a.pairs;                 // stages
 
     if (wave >= 4) {
-        // ---- producer waves: dequantise stage s+1's B tile during stage s.
-        // Item p < 2 BN: column p/2, codes 64 (p%2)..+63 of the stage, read
-        // as one meta dword and two 16-byte loads; each becomes 8 LDS
-        // writes of 8 bf16.  Byte offsets in a row: the lane part is fixed,
-        // the stage part uniform; columns past n read zeros.
+        // ---- producer waves: write stage s+1's B tile during stage s.
+        // Item p < 2 BN: column p/2, k positions 64 (p%2)..+63 of the stage.
+        //  * zero-point stage: the 8 blocks 16 s + 8 (p%2) + j of the
+        //    column, one meta dword each -> one 16-byte chunk each;
+        //  * code stage: one meta dword and two 16-byte code loads; the
+        //    codes become 8 chunks of 8 bf16 integers and the scale goes to
+        //    the stage's scale row (p%2 = the stage's 64-wide sub-block).
+        // Byte offsets in a row: the lane part is fixed, the stage part
+        // uniform; columns past n read zeros.
         const uint32_t row_bytes = (uint32_t)a.nb * BB;
         const __amdgpu_buffer_rsrc_t wr = make_rsrc(a.w, a.w_bytes);
         const int p = t - 256, col = p >> 1, h = p & 1;
         const bool active = p < 2 * BN;
-        // 64 codes (p%2) of the stage: block offset and the codes' offset in it
         const uint32_t lane_meta = BS == 64 ? (uint32_t)h * BB : 0u;
         const uint32_t lane_code = lane_meta + 4 + (BS == 64 ? 0u : (uint32_t)h * 32);
         const uint32_t wv = (uint32_t)(n0 + col) * row_bytes;
         const int it_base = col * PITCH + 64 * h;
-        uint32_t one = 0x3C003C00u;
-        asm volatile("" : "+v"(one));                // kept in a VGPR (see dequant8_m16)
-        auto load_codes = [&](int s, u32x4 (&code)[2], uint32_t& meta) __attribute__((always_inline)) {
-            const uint32_t sm = BS <= SK ? (uint32_t)s * (SK / BS) * BB : (uint32_t)(s / (BS / SK)) * BB;
-            const uint32_t sc = BS <= SK ? sm : sm + (uint32_t)(s % (BS / SK)) * (SK / 2);
-            meta = __builtin_amdgcn_raw_buffer_load_b32(wr, wv + lane_meta + sm, 0, 0);
-            code[0] = __builtin_amdgcn_raw_buffer_load_b128(wr, wv + lane_code + sc, 0, 0);
-            code[1] = __builtin_amdgcn_raw_buffer_load_b128(wr, wv + lane_code + sc + 16, 0, 0);
+        auto load = [&](int s, u32x4 (&c)[2], uint32_t& meta) __attribute__((always_inline)) {
+            if (s < a.sz) {
+                const uint32_t b0 = (uint32_t)(16 * s + 8 * h);
+#pragma unroll
+                for (int j = 0; j < 8; j++)
+                    c[j >> 2][j & 3] = __builtin_amdgcn_raw_buffer_load_b32(wr, wv + (b0 + j) * BB, 0, 0);
+                meta = 0;
+            } else {
+                const int sc = s - a.sz;
+                const uint32_t sm = BS <= SK ? (uint32_t)sc * (SK / BS) * BB : (uint32_t)(sc / (BS / SK)) * BB;
+                const uint32_t so = BS <= SK ? sm : sm + (uint32_t)(sc % (BS / SK)) * (SK / 2);
+                meta = __builtin_amdgcn_raw_buffer_load_b32(wr, wv + lane_meta + sm, 0, 0);
+                c[0] = __builtin_amdgcn_raw_buffer_load_b128(wr, wv + lane_code + so, 0, 0);
+                c[1] = __builtin_amdgcn_raw_buffer_load_b128(wr, wv + lane_code + so + 16, 0, 0);
+            }
         };
-        auto dequant = [&](int s, const u32x4 (&code)[2], uint32_t meta, __bf16* buf) __attribute__((always_inline)) {
+        auto produce = [&](int s, const u32x4 (&c)[2], uint32_t meta, __bf16* buf, float* sc)
+            __attribute__((always_inline)) {
             if (!active) return;
-            const float sc = qsf::f16_lo(meta), zp = qsf::f16_hi(meta);
-            // z - 16 s is exact in fp64 (fp16 operands); the short form
-            // applies when it is also exact (and finite) in fp32
-            const double cd = (double)zp - 16.0 * (double)sc;
-            const float c = (float)cd;
-            if (__builtin_isfinite(cd) && (double)c == cd) {
+            if (s < a.sz) {
 #pragma unroll
                 for (int j = 0; j < 8; j++) {
-                    bf16x8 v = dequant8_m16(code[j >> 2][j & 3], 16.0f * sc, c, one);
-                    if (RAGGED && s * SK + 64 * h + 8 * j >= a.k) v = bf16x8{};
+                    const int b = 16 * s + 8 * h + j;
+                    bf16x8 v = zchunk(c[j >> 2][j & 3]);
+                    if (b >= a.nb) v = bf16x8{};
                     *reinterpret_cast<bf16x8*>(buf + it_base + 8 * j) = v;
                 }
             } else {
+                const int k0 = (s - a.sz) * SK + 64 * h;
+                // a sub-block wholly past k has zero codes and x; a zero
+                // scale keeps junk meta (Inf, NaN) out of the sum
+                sc[h * BN + col] = RAGGED && k0 >= a.k ? 0.f : qsf::f16_lo(meta);
 #pragma unroll
                 for (int j = 0; j < 8; j++) {
-                    bf16x8 v = dequant8(code[j >> 2][j & 3], sc, zp);
-                    if (RAGGED && s * SK + 64 * h + 8 * j >= a.k) v = bf16x8{};
+                    bf16x8 v = codes8(c[j >> 2][j & 3]);
+                    if (RAGGED && k0 + 8 * j >= a.k) v = bf16x8{};
                     *reinterpret_cast<bf16x8*>(buf + it_base + 8 * j) = v;
                 }
             }
         };
-        // codes double-buffered two stages ahead
+        // loads double-buffered two stages ahead
         u32x4 ca[2], cb[2];
         uint32_t ma, mb;
-        load_codes(0, ca, ma);
-        load_codes(1, cb, mb);
-        dequant(0, ca, ma, lds);
-        load_codes(2, ca, ma);
+        load(0, ca, ma);
+        load(1, cb, mb);
+        produce(0, ca, ma, lds, scl);
+        load(2, ca, ma);
         __syncthreads();
-        for (int s = 0; s < S; s += 2) {
-            dequant(s + 1, cb, mb, lds + BUF);
-            load_codes(s + 3, cb, mb);
+        for (int s = 0; s < a.s; s += 2) {
+            produce(s + 1, cb, mb, lds + BUF, scl + SCN);
+            load(s + 3, cb, mb);
             __syncthreads();
-            dequant(s + 2, ca, ma, lds);
-            load_codes(s + 4, ca, ma);
+            produce(s + 2, ca, ma, lds, scl);
+            load(s + 4, ca, ma);
             __syncthreads();
         }
         __syncthreads();                           // the consumers' epilogue barrier
@@ -242,7 +296,7 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(a.xp, a.xp_bytes);
     // A fragment (rows m0 + 16 mt.., k-step kk): 1 KB at (group * ksp + kk)
     // KB of the packed x, 16 bytes per lane; groups past m read zeros
-    const uint32_t ksp = 8u * (uint32_t)a.pairs;
+    const uint32_t ksp = 4u * (uint32_t)a.s;
     uint32_t xv[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; mt++) xv[mt] = ((uint32_t)(m0 / 16 + mt) * ksp * 64u + lane) * 16u;
@@ -254,65 +308,98 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
         for (int mt = 0; mt < MT; mt++)
             A[mt][ks] = __builtin_amdgcn_raw_buffer_load_b128(xr, xv[mt] + (uint32_t)(s * 4 + ks) * 1024u, 0, 0);
     };
-    f32x4 acc[MT][NT];
+    auto load_b = [&](const __bf16* src, int nt, int ks) __attribute__((always_inline)) {
+        return *reinterpret_cast<const bf16x8*>(src + bf_base + nt * 16 * PITCH + ks * 32);
+    };
+    f32x4 out[MT][NT];
 #pragma unroll
     for (int mt = 0; mt < MT; mt++)
 #pragma unroll
-        for (int nt = 0; nt < NT; nt++) acc[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int nt = 0; nt < NT; nt++) out[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
     u32x4 A[MT][4];
-    bf16x8 bf[NT];
-    // k-step ks of a stage: for each n-tile, its 4 MFMAs, then that B
-    // fragment register is refilled with the next k-step's (from `src`,
-    // k-step kn); then the A fragments used are refilled with stage s+1's.
-    auto kstep = [&](int s, int ks, const __bf16* src, int kn) __attribute__((always_inline)) {
+    bf16x8 b0, b1;                             // the next n-tile's two B fragments
+
+    // One stage.  ZS (zero-point stages): the MFMAs accumulate into the
+    // outputs.  Code stages: per 64-wide sub-block j and n-tile, a fresh
+    // two-MFMA sum per m-tile, folded in as out = fma(scale, sum, out).
+    // The B fragments are read one n-tile ahead; the last n-tile of a stage
+    // reads the next stage's first ones after the stage barrier.
+    auto stage = [&]<bool ZS>(int s, const __bf16* cur, const float* sc, const __bf16* nxt)
+        __attribute__((always_inline)) {
 #pragma unroll
-        for (int nt = 0; nt < NT; nt++) {
+        for (int j = 0; j < 2; j++) {
+            float scv[NT];
+            if constexpr (!ZS) {
 #pragma unroll
-            for (int mt = 0; mt < MT; mt++)
-                acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                    __builtin_bit_cast(bf16x8, A[mt][ks]), bf[nt], acc[mt][nt], 0, 0, 0);
-            bf[nt] = *reinterpret_cast<const bf16x8*>(src + bf_base + nt * 16 * PITCH + kn * 32);
+                for (int nt = 0; nt < NT; nt++) scv[nt] = sc[j * BN + nt * 16 + l16];
+            }
+#pragma unroll
+            for (int nt = 0; nt < NT; nt++) {
+                const bf16x8 f0 = b0, f1 = b1;
+                f32x4 acc[MT];
+#pragma unroll
+                for (int mt = 0; mt < MT; mt++) {
+                    const bf16x8 a0 = __builtin_bit_cast(bf16x8, A[mt][2 * j]);
+                    const bf16x8 a1 = __builtin_bit_cast(bf16x8, A[mt][2 * j + 1]);
+                    if constexpr (ZS) {
+                        out[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, f0, out[mt][nt], 0, 0, 0);
+                        out[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, f1, out[mt][nt], 0, 0, 0);
+                    } else {
+                        acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, f0, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                        acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, f1, acc[mt], 0, 0, 0);
+                    }
+                }
+                if (nt < NT - 1) {
+                    b0 = load_b(cur, nt + 1, 2 * j);
+                    b1 = load_b(cur, nt + 1, 2 * j + 1);
+                } else if (j == 0) {
+                    b0 = load_b(cur, 0, 2);
+                    b1 = load_b(cur, 0, 3);
+                } else {
+                    // the producers finish stage s+1's tile before this barrier
+                    __syncthreads();
+                    b0 = load_b(nxt, 0, 0);
+                    b1 = load_b(nxt, 0, 1);
+                }
+                if constexpr (!ZS) {
+#pragma unroll
+                    for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+                        for (int i = 0; i < 4; i++)
+                            out[mt][nt][i] = __builtin_fmaf(scv[nt], acc[mt][i], out[mt][nt][i]);
+                }
+            }
+            // this sub-block's A fragments are refilled with stage s+1's
+            load_a(s + 1, 2 * j, A);
+            load_a(s + 1, 2 * j + 1, A);
         }
-        load_a(s + 1, ks, A);
-        // keep the machine scheduler from sliding these loads into the next
-        // k-step
-        __builtin_amdgcn_sched_barrier(0);
-    };
-    // The producers finish stage s+1's tile before the barrier inside stage
-    // s, whose last k-step already reads its first fragments.
-    auto stage = [&](int s, const __bf16* cur, const __bf16* nxt) __attribute__((always_inline)) {
-        kstep(s, 0, cur, 1);
-        kstep(s, 1, cur, 2);
-        kstep(s, 2, cur, 3);
-        __syncthreads();
-        kstep(s, 3, nxt, 0);
-        // the next stage's first fragments are loaded here, not re-read in
-        // front of their MFMAs (which would expose the LDS latency per tile)
-#pragma unroll
-        for (int nt = 0; nt < NT; nt++) asm volatile("" : "+v"(bf[nt]));
     };
 #pragma unroll
     for (int ks = 0; ks < 4; ks++) load_a(0, ks, A);
     __syncthreads();
-#pragma unroll
-    for (int nt = 0; nt < NT; nt++)
-        bf[nt] = *reinterpret_cast<const bf16x8*>(lds + bf_base + nt * 16 * PITCH);
-    for (int s = 0; s < S; s += 2) {
-        stage(s, lds, lds + BUF);
-        stage(s + 1, lds + BUF, lds);
+    b0 = load_b(lds, 0, 0);
+    b1 = load_b(lds, 0, 1);
+    int s = 0;
+    for (; s < a.sz; s += 2) {
+        stage.template operator()<true>(s, lds, scl, lds + BUF);
+        stage.template operator()<true>(s + 1, lds + BUF, scl + SCN, lds);
+    }
+    for (; s < a.s; s += 2) {
+        stage.template operator()<false>(s, lds, scl, lds + BUF);
+        stage.template operator()<false>(s + 1, lds + BUF, scl + SCN, lds);
     }
 
     // Epilogue: each wave stages its 64 x 112 fp32 tile in LDS (once every
     // wave is past its last B read) and writes whole row pieces with 16-byte
     // stores, instead of 4-byte stores scattered over four rows each.
     __syncthreads();
-    float* ep = reinterpret_cast<float*>(lds) + wave * 64 * EP_PITCH;
+    float* ep = reinterpret_cast<float*>(lds_raw) + wave * 64 * EP_PITCH;
 #pragma unroll
     for (int mt = 0; mt < MT; mt++)
 #pragma unroll
         for (int nt = 0; nt < NT; nt++)
 #pragma unroll
-            for (int i = 0; i < 4; i++) ep[(mt * 16 + 4 * g4 + i) * EP_PITCH + nt * 16 + l16] = acc[mt][nt][i];
+            for (int i = 0; i < 4; i++) ep[(mt * 16 + 4 * g4 + i) * EP_PITCH + nt * 16 + l16] = out[mt][nt][i];
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -343,14 +430,23 @@ void launch(dim3 g, dim3 b, hipStream_t s, const PrefillArgs& a) {
         hipLaunchKernelGGL(K, g, b, 0, s, a);
 }
 
+// Stage counts of a (cols, block size) prefill: zero-point stages (8 k
+// positions per block, rounded up to an even stage count) and code stages
+// (cols rounded up to an even stage count).
+struct Stages { int sz, sc; };
+Stages stages_of(int cols, int bs) {
+    const int nb = (cols + bs - 1) / bs;
+    return {2 * ((ZK * nb + 2 * SK - 1) / (2 * SK)), 2 * ((cols + 2 * SK - 1) / (2 * SK))};
+}
+
 }  // namespace
 
-// Packed-x layout of qk_prefill_4bit: ceil(m/16) row groups of ksp k-steps.
-static int packed_ksp(int cols) { return 8 * ((cols + 2 * SK - 1) / (2 * SK)); }
-
-extern "C" size_t qk_prefill_ws_bytes(int m, int cols) {
-    if (m <= 0 || cols <= 0) return 0;
-    return (size_t)((m + 15) / 16) * (size_t)packed_ksp(cols) * 1024;
+// Packed-x layout of qk_prefill_4bit: ceil(m/16) row groups of 4 (sz + sc)
+// k-steps of 1 KB.
+extern "C" size_t qk_prefill_ws_bytes(int m, int cols, int bs) {
+    if (m <= 0 || cols <= 0 || bs <= 0) return 0;
+    const Stages st = stages_of(cols, bs);
+    return (size_t)((m + 15) / 16) * (size_t)(4 * (st.sz + st.sc)) * 1024;
 }
 
 extern "C" int qk_prefill_4bit(const qsf_hip_tensor* t, const uint16_t* d_x_bf16, int m,
@@ -359,21 +455,25 @@ extern "C" int qk_prefill_4bit(const qsf_hip_tensor* t, const uint16_t* d_x_bf16
     if (m <= 0 || t->rows <= 0) return 0;
     if (t->cols < 32 || t->cols % 8) return -2;
     const int bb = 4 + t->bs / 2;
-    const size_t xp_bytes = qk_prefill_ws_bytes(m, t->cols);
+    const Stages st = stages_of(t->cols, t->bs);
+    const int ksp_total = 4 * (st.sz + st.sc), kz = 4 * st.sz;
+    const size_t xp_bytes = qk_prefill_ws_bytes(m, t->cols, t->bs);
     // 32-bit byte offsets inside the weight payload (including the columns
-    // of the last tile past the end) and the packed activations (including
-    // the row groups of the last tile and the prefetch past the last stage)
+    // of the last tile past the end, and the zero-point stages' block reads
+    // up to 16 sz blocks a row) and the packed activations (including the
+    // row groups of the last tile and the prefetch past the last stage)
     const int tiles_m = (m + BM - 1) / BM;
-    if ((uint64_t)(t->rows + BN) * (uint64_t)t->nb * bb >= (1ull << 32) ||
-        (uint64_t)tiles_m * (BM / 16) * packed_ksp(t->cols) * 1024 + 8 * 1024 >= (1ull << 32))
+    const uint64_t row_bytes = (uint64_t)t->nb * bb;
+    if ((uint64_t)(t->rows + BN) * row_bytes + (uint64_t)16 * st.sz * bb >= (1ull << 32) ||
+        (uint64_t)tiles_m * (BM / 16) * ksp_total * 1024 + 8 * 1024 >= (1ull << 32))
         return -2;
     const int tiles_n = (t->rows + BN - 1) / BN;
-    const int pairs = (t->cols + 2 * SK - 1) / (2 * SK);
     const bool ragged = t->cols % (2 * SK) != 0;
-    hipLaunchKernelGGL(xpack_kernel, dim3(packed_ksp(t->cols) / 8, (m + 15) / 16), dim3(256), 0, s,
-                       d_x_bf16, static_cast<u32x4*>(d_ws), m, t->cols, packed_ksp(t->cols));
+    hipLaunchKernelGGL(xpack_kernel, dim3(ksp_total / 8, (m + 15) / 16), dim3(256), 0, s,
+                       d_x_bf16, static_cast<u32x4*>(d_ws), m, t->cols, ksp_total, kz, t->bs, t->nb);
     PrefillArgs a = {t->d_blocks, static_cast<const u32x4*>(d_ws), d_y, m, t->rows, t->cols, t->nb,
-                     tiles_n, pairs, (uint32_t)((uint64_t)t->rows * t->nb * bb), (uint32_t)xp_bytes};
+                     tiles_n, st.sz, st.sz + st.sc, (uint32_t)((uint64_t)t->rows * row_bytes),
+                     (uint32_t)xp_bytes};
     const dim3 grid(tiles_n * tiles_m), block(512);
 #define QK_PREFILL_CASE(B)                                                   \
     case B:                                                                  \

@@ -92,9 +92,9 @@ int qk_moe_launch(const qk_mx_expert* d_experts, int n_exp, int k, int norm, int
                   float* d_out, void* d_ws, hipStream_t s);
 
 /* 4-bit prefill on MFMA: y[m][n] = W[n] . float(x_bf16[m]).  d_ws holds
- * x repacked into MFMA fragment order: qk_prefill_ws_bytes(m, cols) bytes,
- * 16-byte aligned. */
-size_t qk_prefill_ws_bytes(int m, int cols);
+ * the per-block sums of x and x itself in MFMA fragment order:
+ * qk_prefill_ws_bytes(m, cols, bs) bytes, 16-byte aligned. */
+size_t qk_prefill_ws_bytes(int m, int cols, int bs);
 int qk_prefill_4bit(const qsf_hip_tensor* t, const uint16_t* d_x_bf16, int m,
                     float* d_y, void* d_ws, hipStream_t s);
 

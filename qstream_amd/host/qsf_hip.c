@@ -85,14 +85,38 @@ int qsf_hip_init(int device) {
     return rc;
 }
 
+/* Buffers a grow-only device buffer has outgrown.  A caller may have
+ * captured a graph whose kernels hold the old address (the device-pointer
+ * entry points run on the caller's stream), so an outgrown buffer is never
+ * freed before qsf_hip_shutdown; growth is by 1.5x, so the retired buffers
+ * together stay below twice the live one. */
+static void** g_retired;
+static size_t g_retired_n, g_retired_cap;
+
+static int retire_dev(void* p) {
+    if (!p) return E_OK;
+    if (g_retired_n == g_retired_cap) {
+        size_t cap = g_retired_cap ? 2 * g_retired_cap : 16;
+        void** nr = realloc(g_retired, cap * sizeof *nr);
+        if (!nr) return fail(E_OOM, "qsf_hip: retired-buffer list");
+        g_retired = nr;
+        g_retired_cap = cap;
+    }
+    g_retired[g_retired_n++] = p;
+    return E_OK;
+}
+
 /* grow-only device buffer */
 static int ensure_dev(void** p, size_t* have, size_t need) {
     if (*have >= need) return E_OK;
-    if (*p) hipFree(*p);
-    *p = NULL;
-    *have = 0;
     size_t sz = need < 4096 ? 4096 : need + need / 2;
-    HIPCHK(hipMalloc(p, sz), E_OOM);
+    void* np = NULL;
+    HIPCHK(hipMalloc(&np, sz), E_OOM);
+    if (retire_dev(*p) != E_OK) {
+        hipFree(np);
+        return E_OOM;
+    }
+    *p = np;
     *have = sz;
     return E_OK;
 }
@@ -438,8 +462,12 @@ void qsf_hip_shutdown(void) {
         if (g_dev.d_y) hipFree(g_dev.d_y);
         if (g_dev.h_x) hipHostFree(g_dev.h_x);
         if (g_dev.h_y) hipHostFree(g_dev.h_y);
+        for (size_t i = 0; i < g_retired_n; i++) hipFree(g_retired[i]);
         hipStreamDestroy(g_dev.stream);
     }
+    free(g_retired);
+    g_retired = NULL;
+    g_retired_n = g_retired_cap = 0;
     memset(&g_dev, 0, sizeof g_dev);
     pthread_mutex_unlock(&g_lock);
 }
@@ -538,7 +566,7 @@ int qsf_hip_prefill_4bit_dev(const qsf_hip_tensor* t, const uint16_t* d_x_bf16, 
                                "and a 16-byte aligned x are required");
     pthread_mutex_lock(&g_lock);
     int rc = g_dev.ready ? E_OK : fail(E_INVALID, "qsf_hip: not initialised");
-    if (rc == E_OK) rc = ensure_dev(&g_dev.ws, &g_dev.ws_bytes, qk_prefill_ws_bytes(m, t->cols));
+    if (rc == E_OK) rc = ensure_dev(&g_dev.ws, &g_dev.ws_bytes, qk_prefill_ws_bytes(m, t->cols, t->bs));
     if (rc == E_OK && qk_prefill_4bit(t, d_x_bf16, m, d_y, g_dev.ws, pick_stream(stream)))
         rc = fail(E_INTERNAL, "qsf_hip_prefill_4bit_dev: launch failed");
     pthread_mutex_unlock(&g_lock);

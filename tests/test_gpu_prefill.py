@@ -1,25 +1,19 @@
 """Batched prefill (config 4) on MFMA: Y[m] = W float(bf16 x[m]).
 
-Two references:
-* exact-weights: fp64 products of the same bf16 weights the kernel builds
-  (w = fp32(s*q + z), rounded to bf16 with round-to-nearest-even) and bf16 x.
-  The kernel only adds fp32 accumulation error: rel-L2 <= 1e-5.
-* the scalar oracle (M token-by-token src/kernels_scalar.c:64-85 matvecs on
-  float(bf16(x)), fp32 weights): the difference is the bf16 rounding of the
-  weights that the prefill design prescribes.  bf16 keeps 8 significant bits,
-  so each weight moves by at most 2^-8 of itself (about 1.6e-3 rms for
-  uniformly spread rounding errors); the bound is that worst case, 2^-8.
+The specification is M token-by-token src/kernels_scalar.c:64-85 matvecs on
+float(bf16(x)) (the engine prefills one token at a time,
+src/engine.c:1289-1295): oracle.prefill_4bit.  The bar is north_star's
+1e-5 rel-L2 against it, on every shape, and at config-4 shape on row slices
+of the full launch.  A second reference, fp64 products of the fp32
+dequantised weights, shows how far each side is from exact.
 """
 import numpy as np
 import pytest
 
 from qstream_amd import qsf_format as F
-from gpu_util import rel_l2, torch_cuda
+from gpu_util import REL_L2, rel_l2, torch_cuda
 
 pytestmark = pytest.mark.gpu
-
-REL_EXACT = 1e-5
-REL_BF16 = 2.0 ** -8
 
 
 @pytest.fixture(scope="module")
@@ -39,8 +33,9 @@ def bf16_to_f64(h: np.ndarray) -> np.ndarray:
     return (h.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
 
 
-def dequant_bf16(oracle, payload, n, k, bs) -> np.ndarray:
-    """The kernel's weights: bf16(fp32(s*q + z)) as fp64 [n][k]."""
+def dequant_f64(oracle, payload, n, k, bs) -> np.ndarray:
+    """The reference's weights, fp32(s*q + z) (src/quant.c:136-155), as fp64
+    [n][k]."""
     nb = (k + bs - 1) // bs
     bb = 4 + bs // 2
     raw = np.frombuffer(payload, np.uint8)[:n * nb * bb]
@@ -48,9 +43,8 @@ def dequant_bf16(oracle, payload, n, k, bs) -> np.ndarray:
     meta = raw.reshape(n * nb, bb)[:, :4].copy().view(np.uint16)
     s = oracle.fp16_to_fp32_bits(meta[:, 0]).view(np.float32)[:, None]
     z = oracle.fp16_to_fp32_bits(meta[:, 1]).view(np.float32)[:, None]
-    w32 = (s * q.reshape(n * nb, bs)) + z            # s*q exact; one rounding in +
-    w = bf16_to_f64(bf16_rne(w32.astype(np.float32))).reshape(n, nb * bs)
-    return w[:, :k]
+    w32 = ((s * q.reshape(n * nb, bs)) + z).astype(np.float32)   # s*q exact; one rounding in +
+    return w32.astype(np.float64).reshape(n, nb * bs)[:, :k]
 
 
 def case(seed, m, n, k, bs=64):
@@ -73,42 +67,82 @@ def run(hip, payload, xb, m, n, k, bs):
     return out
 
 
+def row_slice(payload, r0, r1, k, bs):
+    """Payload bytes of rows r0..r1-1 (rows are contiguous runs of blocks)."""
+    rb = ((k + bs - 1) // bs) * (4 + bs // 2)
+    return bytes(payload[r0 * rb:r1 * rb])
+
+
+# (m, n, k, bs): single tile, ragged k and partial blocks, several m and n
+# tiles, every block size, n and m past a tile edge
 SHAPES = [(1, 64, 64, 64), (37, 100, 256, 64), (128, 64, 512, 64), (200, 300, 1000, 64),
-          (130, 70, 512, 128), (64, 96, 768, 256), (513, 129, 4096, 64)]
+          (130, 70, 512, 128), (64, 96, 768, 256), (513, 129, 4096, 64), (16, 112, 200, 128),
+          (300, 224, 1280, 256)]
 
 
 @pytest.mark.parametrize("m,n,k,bs", SHAPES)
-def test_prefill_exact_weights(hip, oracle, m, n, k, bs):
-    payload, xb = case(m * 7 + n + k, m, n, k, bs)
-    got = run(hip, payload, xb, m, n, k, bs)
-    w = dequant_bf16(oracle, payload, n, k, bs)
-    ref = bf16_to_f64(xb) @ w.T
-    err = rel_l2(got, ref)
-    print(f"prefill {m}x{n}x{k} bs{bs}: rel_l2 vs exact-weight fp64 = {err:.3e}")
-    assert err <= REL_EXACT, err
-
-
-@pytest.mark.parametrize("m,n,k,bs", SHAPES[:5])
 def test_prefill_vs_scalar_oracle(hip, oracle, m, n, k, bs):
     payload, xb = case(m * 7 + n + k, m, n, k, bs)
     got = run(hip, payload, xb, m, n, k, bs)
     ref = oracle.prefill_4bit(payload, xb, m, n, k, bs)
     err = rel_l2(got, ref)
-    print(f"prefill {m}x{n}x{k} bs{bs}: rel_l2 vs scalar oracle = {err:.3e}")
-    assert err <= REL_BF16, err
+    exact = bf16_to_f64(xb) @ dequant_f64(oracle, payload, n, k, bs).T
+    print(f"prefill {m}x{n}x{k} bs{bs}: rel_l2 vs scalar oracle {err:.3e}, "
+          f"vs fp64 {rel_l2(got, exact):.3e} (oracle vs fp64 {rel_l2(ref, exact):.3e})")
+    assert np.all(np.isfinite(got))
+    assert err <= REL_L2, err
 
 
-def test_prefill_config4_rows(hip, oracle):
-    """Benchmark config 4 (M=512, K=4096, N=14336, block 64): all outputs
-    against the exact-weight fp64 reference."""
+def test_prefill_config4_slices(hip, oracle):
+    """Benchmark config 4 (M=512, K=4096, N=14336, block 64) as one launch;
+    two 1024-row slices (the first and the last n tiles) against the
+    scalar oracle, and every output finite."""
     m, n, k, bs = 512, 14336, 4096, 64
     payload, xb = case(4, m, n, k, bs)
     got = run(hip, payload, xb, m, n, k, bs)
-    w = dequant_bf16(oracle, payload, n, k, bs)
-    ref = bf16_to_f64(xb) @ w.T
-    err = rel_l2(got, ref)
-    print(f"prefill config 4: rel_l2 = {err:.3e}")
-    assert err <= REL_EXACT, err
+    assert np.all(np.isfinite(got))
+    for r0, r1 in ((0, 1024), (n - 1024, n)):
+        ref = oracle.prefill_4bit(row_slice(payload, r0, r1, k, bs), xb, m, r1 - r0, k, bs)
+        err = rel_l2(got[:, r0:r1], ref)
+        print(f"prefill config 4 rows {r0}..{r1}: rel_l2 vs scalar oracle = {err:.3e}")
+        assert err <= REL_L2, err
+
+
+def test_prefill_graph_survives_workspace_growth(hip, oracle):
+    """A graph captured at small m keeps its workspace address: a later,
+    larger eager call that grows the library workspace must not free it.
+    Each replay (with eager work and a synchronisation between) matches the
+    oracle."""
+    torch = torch_cuda()
+    n, k, bs = 128, 512, 64
+    small, big = 16, 512
+    payload, xb = case(11, big, n, k, bs)
+    t = hip.Tensor(payload, F.Q4, n, k, bs)
+    dx = torch.from_numpy(xb.view(np.int16).copy()).to("cuda:0")
+    y_small = torch.full((small, n), float("nan"), device="cuda:0")
+    y_big = torch.full((big, n), float("nan"), device="cuda:0")
+    ref = oracle.prefill_4bit(payload, xb, big, n, k, bs)
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        t.prefill(dx, small, y_small, stream=stream)        # sizes the workspace
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        t.prefill(dx, small, y_small, stream=stream)
+    torch.cuda.synchronize()
+    t.prefill(dx, big, y_big, stream=torch.cuda.current_stream())   # grows it
+    torch.cuda.synchronize()
+    assert rel_l2(y_big.cpu().numpy(), ref) <= REL_L2
+    for rep in range(3):
+        y_small.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        err = rel_l2(y_small.cpu().numpy(), ref[:small])
+        print(f"replay {rep}: rel_l2 {err:.3e}")
+        assert err <= REL_L2, err
+    del g
+    t.free()
 
 
 def test_prefill_rejects_bad_input(hip):

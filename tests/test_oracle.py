@@ -291,9 +291,12 @@ def test_activations(oracle):
     assert np.array_equal(oracle.act(3, v), np.maximum(v, 0))
 
 
-def test_prefill_oracle_is_token_loop(oracle):
-    rng = np.random.default_rng(4)
-    m, n, k, bs = 3, 20, 128, 64
+@pytest.mark.parametrize("m,n,k,bs", [(3, 20, 128, 64), (2, 7, 200, 64), (2, 9, 384, 256)])
+def test_prefill_oracle_is_token_loop(oracle, m, n, k, bs):
+    """The prefill oracle (weights dequantised once, rows interleaved) equals
+    M calls of the scalar matvec bit for bit, odd row counts and partial
+    blocks included."""
+    rng = np.random.default_rng(4 + n)
     p = F.quantize_matrix(F.gaussian(rng, (n, k), 0.02), F.Q4, bs)
     xb = F.bf16_bits(F.gaussian(rng, (m, k)))
     y = oracle.prefill_4bit(p, xb, m, n, k, bs)
