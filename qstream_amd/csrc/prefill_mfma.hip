@@ -74,22 +74,28 @@ __device__ __forceinline__ bf16x2 to_bf16x2(float a, float b) {
     return __builtin_convertvector(v, bf16x2);
 }
 
-// Eight codes (one dword, low nibble = even code) -> the integers 0..15 as
-// bf16, exact (byte extracts to float become v_cvt_f32_ubyte0..3).
+// Eight codes (one dword; code 2i is the low nibble of byte i, code 2i+1
+// the high one) -> the integers 0..15 as exact bf16, in the k order
+// {0, 2, 4, 6, 1, 3, 5, 7} (xpack_kernel orders x the same way).  A byte
+// 0000qqqq read as OCP FP8 E4M3 is q * 2^-9 (subnormal for q < 8, exponent
+// field 1 for q >= 8), so one v_cvt_scalef32_pk_bf16_fp8 with scale 2^9
+// (only the scale's exponent is used) turns two nibble bytes into two exact
+// bf16 integers: 7 VALU operations per 8 codes.
 __device__ __forceinline__ bf16x8 codes8(uint32_t w) {
     const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
-    const float q[8] = {(float)(lo & 0xFFu),         (float)(hi & 0xFFu),
-                        (float)((lo >> 8) & 0xFFu),  (float)((hi >> 8) & 0xFFu),
-                        (float)((lo >> 16) & 0xFFu), (float)((hi >> 16) & 0xFFu),
-                        (float)(lo >> 24),           (float)(hi >> 24)};
-    bf16x8 r;
-#pragma unroll
-    for (int j = 0; j < 8; j += 2) {
-        const bf16x2 b = to_bf16x2(q[j], q[j + 1]);
-        r[j] = b[0];
-        r[j + 1] = b[1];
-    }
-    return r;
+    const bf16x2 a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 512.0f, false);   // codes 0, 2
+    const bf16x2 b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 512.0f, true);    // codes 4, 6
+    const bf16x2 c = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 512.0f, false);   // codes 1, 3
+    const bf16x2 d = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 512.0f, true);    // codes 5, 7
+    return bf16x8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+}
+
+// Eight bf16 of x in k order 0..7 -> the codes8 order {0, 2, 4, 6, 1, 3, 5, 7}.
+__device__ __forceinline__ u32x4 x_order(u32x4 v) {
+    return u32x4{__builtin_amdgcn_perm(v[1], v[0], 0x05040100u),   // x0, x2
+                 __builtin_amdgcn_perm(v[3], v[2], 0x05040100u),   // x4, x6
+                 __builtin_amdgcn_perm(v[1], v[0], 0x07060302u),   // x1, x3
+                 __builtin_amdgcn_perm(v[3], v[2], 0x07060302u)};  // x5, x7
 }
 
 // Zero-point chunk of one block from its meta dword (fp16 scale | fp16 zero
@@ -118,7 +124,8 @@ struct PrefillArgs {
 //  * k-steps kk < kz: the zero-point part, one chunk per block
 //    b = 4 kk + l/16: {X1, X2, X3, X1, X2, 0, 0, 0}, the bf16 split of the
 //    block's fp32 sum X_b = X1 + X2 + X3 (exact);
-//  * k-steps kz + kk: columns 32 kk + 8 (l/16)..+7 of x.
+//  * k-steps kz + kk: columns 32 kk + 8 (l/16)..+7 of x, in the k order
+//    {0, 2, 4, 6, 1, 3, 5, 7} of the codes (codes8).
 // Zeros past m, k and nb.  The GEMM then loads each fragment as one
 // contiguous 1 KB read instead of 64 scattered 16-byte pieces.  One
 // workgroup per (row group, 8 k-steps): the code part reads a 16 x 256 tile
@@ -165,7 +172,7 @@ __global__ __launch_bounds__(256) void xpack_kernel(const uint16_t* __restrict__
     for (int h = 0; h < 2; h++) {
         const int r = (t >> 5) + 8 * h, row = g * 16 + r, col = kk0 * 32 + 8 * c;
         u32x4 v = {0u, 0u, 0u, 0u};
-        if (row < m && col < k) v = *reinterpret_cast<const u32x4*>(x + (size_t)row * k + col);
+        if (row < m && col < k) v = x_order(*reinterpret_cast<const u32x4*>(x + (size_t)row * k + col));
         *reinterpret_cast<u32x4*>(&tile[r * XP_PITCH + 8 * c]) = v;
     }
     __syncthreads();
@@ -318,12 +325,21 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
         for (int nt = 0; nt < NT; nt++) out[mt][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
     u32x4 A[MT][4];
     bf16x8 b0, b1;                             // the next n-tile's two B fragments
+    // Sums of the previous n-tile and their scale, folded into `out` while
+    // the MFMAs of the current one run (the previous n-tile is always the
+    // last one, NT-1, when the current one is the first of a sub-block).
+    f32x4 accp[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++) accp[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float scp = 0.f;
 
     // One stage.  ZS (zero-point stages): the MFMAs accumulate into the
     // outputs.  Code stages: per 64-wide sub-block j and n-tile, a fresh
-    // two-MFMA sum per m-tile, folded in as out = fma(scale, sum, out).
-    // The B fragments are read one n-tile ahead; the last n-tile of a stage
-    // reads the next stage's first ones after the stage barrier.
+    // two-MFMA sum per m-tile, folded in as out = fma(scale, sum, out) one
+    // n-tile later.  The next n-tile's B fragments are read before the
+    // current MFMAs; the last n-tile of a stage reads the next stage's first
+    // ones after the stage barrier (the producers finish stage s+1's tile
+    // before it, and no wave reads this stage's tile after it).
     auto stage = [&]<bool ZS>(int s, const __bf16* cur, const float* sc, const __bf16* nxt)
         __attribute__((always_inline)) {
 #pragma unroll
@@ -336,19 +352,6 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
 #pragma unroll
             for (int nt = 0; nt < NT; nt++) {
                 const bf16x8 f0 = b0, f1 = b1;
-                f32x4 acc[MT];
-#pragma unroll
-                for (int mt = 0; mt < MT; mt++) {
-                    const bf16x8 a0 = __builtin_bit_cast(bf16x8, A[mt][2 * j]);
-                    const bf16x8 a1 = __builtin_bit_cast(bf16x8, A[mt][2 * j + 1]);
-                    if constexpr (ZS) {
-                        out[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, f0, out[mt][nt], 0, 0, 0);
-                        out[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, f1, out[mt][nt], 0, 0, 0);
-                    } else {
-                        acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, f0, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                        acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, f1, acc[mt], 0, 0, 0);
-                    }
-                }
                 if (nt < NT - 1) {
                     b0 = load_b(cur, nt + 1, 2 * j);
                     b1 = load_b(cur, nt + 1, 2 * j + 1);
@@ -356,17 +359,46 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
                     b0 = load_b(cur, 0, 2);
                     b1 = load_b(cur, 0, 3);
                 } else {
-                    // the producers finish stage s+1's tile before this barrier
                     __syncthreads();
                     b0 = load_b(nxt, 0, 0);
                     b1 = load_b(nxt, 0, 1);
                 }
-                if constexpr (!ZS) {
+                const int pnt = nt == 0 ? NT - 1 : nt - 1;
+                f32x4 acc[MT];
 #pragma unroll
-                    for (int mt = 0; mt < MT; mt++)
+                for (int mt = 0; mt < MT; mt++) {
+                    const bf16x8 a0 = __builtin_bit_cast(bf16x8, A[mt][2 * j]);
+                    if constexpr (ZS) {
+                        out[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, f0, out[mt][nt], 0, 0, 0);
+                    } else {
+                        acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, f0, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
 #pragma unroll
                         for (int i = 0; i < 4; i++)
-                            out[mt][nt][i] = __builtin_fmaf(scv[nt], acc[mt][i], out[mt][nt][i]);
+                            out[mt][pnt][i] = __builtin_fmaf(scp, accp[mt][i], out[mt][pnt][i]);
+                    }
+                }
+#pragma unroll
+                for (int mt = 0; mt < MT; mt++) {
+                    const bf16x8 a1 = __builtin_bit_cast(bf16x8, A[mt][2 * j + 1]);
+                    if constexpr (ZS)
+                        out[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, f1, out[mt][nt], 0, 0, 0);
+                    else
+                        accp[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, f1, acc[mt], 0, 0, 0);
+                }
+                if constexpr (!ZS) {
+                    scp = scv[nt];
+                    // one n-tile per scheduling region: the B reads first,
+                    // then each MFMA followed by two of the previous
+                    // n-tile's folds, which the wave issues while the
+                    // matrix core runs (in-order issue: a run of MFMAs
+                    // would hold the folds back until the core drains)
+                    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);      // DS reads
+#pragma unroll
+                    for (int i = 0; i < 2 * MT; i++) {
+                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+                        __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // VALU
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
                 }
             }
             // this sub-block's A fragments are refilled with stage s+1's
@@ -388,6 +420,11 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
         stage.template operator()<false>(s, lds, scl, lds + BUF);
         stage.template operator()<false>(s + 1, lds + BUF, scl + SCN, lds);
     }
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            out[mt][NT - 1][i] = __builtin_fmaf(scp, accp[mt][i], out[mt][NT - 1][i]);
 
     // Epilogue: each wave stages its 64 x 112 fp32 tile in LDS (once every
     // wave is past its last B read) and writes whole row pieces with 16-byte
