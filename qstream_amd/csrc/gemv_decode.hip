@@ -1163,9 +1163,11 @@ int launch_rt(const qsf_hip_tensor* const* t, int n, int cols, const float* d_x,
     constexpr int MT = tiles_per_wave(DREG);
     using F = Fmt<FMT, BS>;
     const int nb = (cols + BS - 1) / BS;
+    // prepared digits and block meta (QK_RUN_XPREP / a prepared run only)
     uint32_t* xq = (uint32_t*)d_ws;
     size_t dig = (size_t)nb * F::DWS * 4;
-    float2* xmeta = (float2*)((uint8_t*)d_ws + ((dig + 255) & ~(size_t)255));
+    float2* xmeta = d_ws ? (float2*)((uint8_t*)d_ws + ((dig + 255) & ~(size_t)255)) : nullptr;
+    if (!d_ws && (mode != QK_RUN_BOTH)) return -2;
     if ((mode & QK_RUN_XPREP) && (!(mode & QK_RUN_GEMV) || (mode & QK_RUN_STANDALONE_PREP)))
         hipLaunchKernelGGL((xprep_kernel<FMT, BS>), dim3((nb + 256 / F::LPB - 1) / (256 / F::LPB)),
                            dim3(256), 0, s, d_x, cols, nb, xq, xmeta);

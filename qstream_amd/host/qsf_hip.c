@@ -488,10 +488,9 @@ static int group_locked(const qsf_hip_tensor* const* t, int n, const float* d_x,
             return fail(E_INVALID, "qsf_hip: grouped tensors differ in type/cols/block");
     }
     if (t[0]->cols > 0 && !d_x) return fail(E_INVALID, "qsf_hip: null input");
-    size_t ws = qk_xprep_bytes(t[0]->fmt, t[0]->bs, t[0]->cols);
-    int rc = ensure_dev(&g_dev.ws, &g_dev.ws_bytes, ws);
-    if (rc) return rc;
-    rc = qk_gemv_group(t, n, d_x, d_y, g_dev.ws, QK_RUN_BOTH, pick_stream(stream));
+    /* the one-launch form prepares x inside the GEMV workgroups: no
+     * workspace, so nothing is allocated on this path */
+    int rc = qk_gemv_group(t, n, d_x, d_y, NULL, QK_RUN_BOTH, pick_stream(stream));
     if (rc) return fail(E_INTERNAL, "qsf_hip: GEMV launch failed (%d)", rc);
     return E_OK;
 }
