@@ -161,6 +161,21 @@ int qsf_hip_moe_forward_dev(qsf_hip_moe* m, int top_k, int norm_topk, int activa
 int qsf_hip_prefill_4bit_dev(const qsf_hip_tensor* t, const uint16_t* d_x_bf16, int m,
                              float* d_y, void* stream);
 
+/* Allocation-free form of qsf_hip_prefill_4bit_dev (no counterpart in the
+ * reference).  For callers that cannot allocate device memory: code under
+ * HIP graph capture and serving loops that forbid hipMalloc.  Same inputs,
+ * outputs and results; the packed activations go to a static per-GPU
+ * scratch array of QSF_HIP_PREFILL_SCRATCH_BYTES instead of the library
+ * workspace, and nothing is allocated or freed.  A call that needs more
+ * scratch than that (about 2 * m * (cols + 8 * cols / block_size) bytes,
+ * m rounded up to 16 and both column counts to 256; config 4's 512 x 4096
+ * at block 64 needs 4.7 MB) fails with QSF_ERR_INVALID_INPUT.  Every call on one GPU shares that GPU's
+ * array: calls that overlap on one GPU (different streams, or graphs
+ * replayed concurrently) race on it. */
+#define QSF_HIP_PREFILL_SCRATCH_BYTES (16 << 20)
+int qsf_hip_prefill_4bit_dev_noalloc(const qsf_hip_tensor* t, const uint16_t* d_x_bf16, int m,
+                                     float* d_y, void* stream);
+
 /* Bit-exact unpack of `nblocks` QSF blocks already in device memory (the
  * same device code paths the GEMV uses): codes int8[nblocks*bs] (2/3/4-bit
  * field values; 4-bit sym as two's complement), meta u32[nblocks] (first

@@ -526,3 +526,33 @@ extern "C" int qk_prefill_4bit(const qsf_hip_tensor* t, const uint16_t* d_x_bf16
 #undef QK_PREFILL_CASE
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
+
+// ---- allocation-free form -------------------------------------------------
+// The packed activations live in one file-scope device array per GPU
+// (QK_PREFILL_SCRATCH_BYTES; every GPU the library runs on holds it until the
+// process ends).  In host code `scratch` names a host-side stand-in, so its
+// device address is looked up once per device (with that device current)
+// and only that address is ever passed to kernels.  xpack_kernel rewrites
+// every byte the GEMM reads from it, so nothing needs clearing between
+// calls; calls that overlap on one GPU race on it.
+static __device__ __align__(256) uint8_t scratch[QK_PREFILL_SCRATCH_BYTES];
+static void* g_scratch[QK_MAX_DEVICES];
+
+extern "C" int qk_prefill_scratch_init(void) {
+    int d = -1;
+    if (hipGetDevice(&d) != hipSuccess || d < 0 || d >= QK_MAX_DEVICES) return -1;
+    if (g_scratch[d]) return 0;
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return -1;
+    g_scratch[d] = p;
+    return 0;
+}
+
+extern "C" int qk_prefill_4bit_noalloc(const qsf_hip_tensor* t, const uint16_t* d_x_bf16, int m,
+                                       float* d_y, hipStream_t s) {
+    if (qk_prefill_ws_bytes(m, t->cols, t->bs) > (size_t)QK_PREFILL_SCRATCH_BYTES) return -3;
+    int d = -1;
+    if (hipGetDevice(&d) != hipSuccess || d < 0 || d >= QK_MAX_DEVICES) return -1;
+    if (!g_scratch[d] && qk_prefill_scratch_init() != 0) return -1;
+    return qk_prefill_4bit(t, d_x_bf16, m, d_y, g_scratch[d], s);
+}

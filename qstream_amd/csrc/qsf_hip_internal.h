@@ -95,6 +95,17 @@ int qk_moe_launch(const qk_mx_expert* d_experts, int n_exp, int k, int norm, int
  * the per-block sums of x and x itself in MFMA fragment order:
  * qk_prefill_ws_bytes(m, cols, bs) bytes, 16-byte aligned. */
 size_t qk_prefill_ws_bytes(int m, int cols, int bs);
+
+/* The same prefill with the packed activations in a file-scope device array
+ * of QK_PREFILL_SCRATCH_BYTES per GPU instead of a caller workspace: no
+ * allocation.  qk_prefill_scratch_init looks up the current device's address
+ * of that array (once per device); qk_prefill_4bit_noalloc returns -3 when
+ * the call needs more than the array holds. */
+#define QK_PREFILL_SCRATCH_BYTES (16 << 20)
+#define QK_MAX_DEVICES 64
+int qk_prefill_scratch_init(void);
+int qk_prefill_4bit_noalloc(const qsf_hip_tensor* t, const uint16_t* d_x_bf16, int m,
+                            float* d_y, hipStream_t s);
 int qk_prefill_4bit(const qsf_hip_tensor* t, const uint16_t* d_x_bf16, int m,
                     float* d_y, void* d_ws, hipStream_t s);
 

@@ -73,6 +73,10 @@ static int init_locked(int device) {
     if (device < 0 || device >= n) return fail(E_INVALID, "qsf_hip: device %d of %d", device, n);
     HIPCHK(hipSetDevice(device), E_INTERNAL);
     HIPCHK(hipStreamCreateWithFlags(&g_dev.stream, hipStreamNonBlocking), E_INTERNAL);
+    /* device address of the allocation-free prefill's scratch array; a
+     * failure here surfaces as that entry point's error (it retries the
+     * lookup on its first call on a device) */
+    (void)qk_prefill_scratch_init();
     g_dev.device = device;
     g_dev.ready = 1;
     return E_OK;
@@ -554,20 +558,48 @@ int qsf_hip_matvec_dev(const qsf_hip_tensor* t, const float* d_x, float* d_y, vo
     return rc;
 }
 
+_Static_assert(QSF_HIP_PREFILL_SCRATCH_BYTES == QK_PREFILL_SCRATCH_BYTES,
+               "public and kernel-side scratch sizes differ");
+
+static int prefill_check(const char* who, const qsf_hip_tensor* t, const uint16_t* d_x_bf16, int m) {
+    if (!t) return fail(E_INVALID, "%s: null tensor", who);
+    if (t->fmt != QK_FMT_4 || t->n_outliers || !(t->bs == 64 || t->bs == 128 || t->bs == 256))
+        return fail(E_INVALID, "%s: needs a 4-bit asymmetric tensor with "
+                               "block 64, 128 or 256 and no outliers", who);
+    if (m < 0 || t->cols < 32 || t->cols % 8 != 0 || ((uintptr_t)d_x_bf16 & 15u) != 0)
+        return fail(E_INVALID, "%s: m >= 0, cols >= 32, cols %% 8 == 0 "
+                               "and a 16-byte aligned x are required", who);
+    return E_OK;
+}
+
 int qsf_hip_prefill_4bit_dev(const qsf_hip_tensor* t, const uint16_t* d_x_bf16, int m,
                              float* d_y, void* stream) {
-    if (!t) return fail(E_INVALID, "qsf_hip_prefill_4bit_dev: null tensor");
-    if (t->fmt != QK_FMT_4 || t->n_outliers || !(t->bs == 64 || t->bs == 128 || t->bs == 256))
-        return fail(E_INVALID, "qsf_hip_prefill_4bit_dev: needs a 4-bit asymmetric tensor with "
-                               "block 64, 128 or 256 and no outliers");
-    if (m < 0 || t->cols < 32 || t->cols % 8 != 0 || ((uintptr_t)d_x_bf16 & 15u) != 0)
-        return fail(E_INVALID, "qsf_hip_prefill_4bit_dev: m >= 0, cols >= 32, cols %% 8 == 0 "
-                               "and a 16-byte aligned x are required");
+    if (prefill_check("qsf_hip_prefill_4bit_dev", t, d_x_bf16, m)) return g_err;
     pthread_mutex_lock(&g_lock);
     int rc = g_dev.ready ? E_OK : fail(E_INVALID, "qsf_hip: not initialised");
     if (rc == E_OK) rc = ensure_dev(&g_dev.ws, &g_dev.ws_bytes, qk_prefill_ws_bytes(m, t->cols, t->bs));
     if (rc == E_OK && qk_prefill_4bit(t, d_x_bf16, m, d_y, g_dev.ws, pick_stream(stream)))
         rc = fail(E_INTERNAL, "qsf_hip_prefill_4bit_dev: launch failed");
+    pthread_mutex_unlock(&g_lock);
+    return rc;
+}
+
+int qsf_hip_prefill_4bit_dev_noalloc(const qsf_hip_tensor* t, const uint16_t* d_x_bf16, int m,
+                                     float* d_y, void* stream) {
+    if (prefill_check("qsf_hip_prefill_4bit_dev_noalloc", t, d_x_bf16, m)) return g_err;
+    const size_t need = qk_prefill_ws_bytes(m, t->cols, t->bs);
+    if (need > (size_t)QSF_HIP_PREFILL_SCRATCH_BYTES)
+        return fail(E_INVALID, "qsf_hip_prefill_4bit_dev_noalloc: %d tokens x %d columns need "
+                               "%zu bytes of scratch, more than its %d (use "
+                               "qsf_hip_prefill_4bit_dev, or split the tokens)",
+                    m, t->cols, need, QSF_HIP_PREFILL_SCRATCH_BYTES);
+    pthread_mutex_lock(&g_lock);
+    int rc = g_dev.ready ? E_OK : fail(E_INVALID, "qsf_hip: not initialised");
+    if (rc == E_OK) {
+        int r = qk_prefill_4bit_noalloc(t, d_x_bf16, m, d_y, pick_stream(stream));
+        if (r) rc = fail(E_INTERNAL, "qsf_hip_prefill_4bit_dev_noalloc: %s",
+                         r == -1 ? "no address for this device's scratch array" : "launch failed");
+    }
     pthread_mutex_unlock(&g_lock);
     return rc;
 }

@@ -34,7 +34,7 @@ EXPORTS = (
     "qsf_hip_xprep_dev", "qsf_hip_matvec_group_prepared_dev",
     "qsf_hip_moe_create", "qsf_hip_moe_free", "qsf_hip_moe_forward_dev",
     "qsf_hip_unpack_dev", "qsf_hip_kernel_timing", "qsf_hip_kernel_timing_read",
-    "qsf_hip_prefill_4bit_dev",
+    "qsf_hip_prefill_4bit_dev", "qsf_hip_prefill_4bit_dev_noalloc",
 )
 
 _lib = None
@@ -96,6 +96,8 @@ def load(path: str = LIB_PATH) -> C.CDLL:
     L.qsf_hip_unpack_dev.restype = _i
     L.qsf_hip_prefill_4bit_dev.argtypes = [_vp, _vp, _i, _vp, _vp]
     L.qsf_hip_prefill_4bit_dev.restype = _i
+    L.qsf_hip_prefill_4bit_dev_noalloc.argtypes = [_vp, _vp, _i, _vp, _vp]
+    L.qsf_hip_prefill_4bit_dev_noalloc.restype = _i
     L.qsf_hip_kernel_timing.argtypes = [_i]
     L.qsf_hip_kernel_timing.restype = _i
     L.qsf_hip_kernel_timing_read.argtypes = [C.POINTER(C.c_float), _i]
@@ -193,6 +195,13 @@ class Tensor:
         """y[m][rows] = W . float(x_bf16[m][cols]) on MFMA (4-bit tensors)."""
         _check(load().qsf_hip_prefill_4bit_dev(self.handle, _addr(x_bf16), m, _addr(y),
                                                _stream(stream)), "qsf_hip_prefill_4bit_dev")
+
+    def prefill_noalloc(self, x_bf16, m: int, y, stream=None) -> None:
+        """The same through the allocation-free entry point (static per-GPU
+        scratch; safe to capture into a graph without a first eager call)."""
+        _check(load().qsf_hip_prefill_4bit_dev_noalloc(self.handle, _addr(x_bf16), m, _addr(y),
+                                                       _stream(stream)),
+               "qsf_hip_prefill_4bit_dev_noalloc")
 
     def matvec(self, x, y, stream=None) -> None:
         _check(load().qsf_hip_matvec_dev(self.handle, _addr(x), _addr(y), _stream(stream)),
