@@ -4,23 +4,28 @@
 Metric: quant matvec HBM GB/s (% of ~8 TB/s peak) + us/call
 at 7B decode shapes.  The default workload is BASELINE.json config 1: the
 2-bit+outlier FFN gate and up projections (11008x4096 each, block 64), batch-1
-decode.  A step is one pass over one activation vector: x-prep + one grouped
-GEMV launch over gate and up.  Weights rotate over >= 512 MiB of distinct
-copies in HBM so the 256 MB Infinity Cache cannot serve them; inputs are
-resident in HBM before the timed region.
+decode.  A step is one pass over one activation vector: one grouped GEMV
+launch over gate and up that prepares x inside its workgroups.  Weights
+rotate over >= 512 MiB of distinct copies in HBM so the 256 MB Infinity Cache
+cannot serve them; inputs are resident in HBM before the timed region.
 
-    python bench.py [--steps K] [--warmup W] [--config 1|0|2|3|all]
+    python bench.py [--steps K] [--warmup W] [--config 1|0|2|3|4|all]
 
 Prints one JSON line.  `value` is algorithmic bytes per step (on-disk QSF
 payload + x read once + y written, per matrix) / wall time per step, over K
-steps replayed from one HIP graph between two synchronisations.
-`roofline.achieved` is the same bytes / the GEMV kernel's mean duration, from
-HIP event pairs recorded at the kernel's own start and end on its launch
-stream (hipExtLaunchKernel, via qsf_hip_kernel_timing).  `roofline.traffic`
-is the HBM bytes per launch measured with rocprofv3 counters
-(profiles/traffic.json), or null.  `cpu_baseline` times QStream's own AVX2
-kernel (oracle/_ref, reference release flags, 1 thread) on a bounded sample.
-`--profile` runs eager launches only, for rocprofv3 counter passes.
+steps captured once into a HIP graph and replayed between two HIP events on
+the replay stream.  For the one-launch decode steps (configs 0 and 1) that
+timed region is also the kernel's time: `roofline.kernel_us` is the region
+time per launch, so it never exceeds the step.  Configs 2-4 time their
+dominant kernel separately (see each function).  `roofline.traffic` is the
+HBM bytes per launch measured with rocprofv3 counters (profiles/traffic.json),
+used only while the kernel source it was measured on is unchanged, else
+null.  `cpu_baseline` times QStream's own AVX2 kernel (oracle/_ref,
+reference release flags, 1 thread) on a bounded sample.
+The default line also carries config 0 (the 4-bit matvec north_star's
+target names) under "config0"; `--config all` nests every config under
+"configs".  `--profile` runs eager launches only, for rocprofv3 counter
+passes; `--no-slot` skips the PCIe-inclusive table-slot timing.
 """
 from __future__ import annotations
 
@@ -49,24 +54,12 @@ def log(*a):
 # ---------------------------------------------------------------------------
 def cfg1_data(seed=1):
     from qstream_amd import qsf_format as F
-    rng = np.random.default_rng(seed)
-    rows, cols, bs = 11008, 4096, 64
-    mats = []
-    for name in ("gate", "up"):
-        w = F.heavy_tail_weights(rng, rows, cols)
-        mats.append((name, np.frombuffer(F.quantize_matrix(w, F.Q2_OUTLIER, bs), np.uint8), rows, cols))
-        del w
-    x = F.gaussian(rng, cols)
-    return F.Q2_OUTLIER, bs, mats, x
+    return F.config1_matrices(seed)
 
 
 def cfg0_data(seed=0):
     from qstream_amd import qsf_format as F
-    rng = np.random.default_rng(seed)
-    rows, cols, bs = 4096, 4096, 64
-    w = F.gaussian(rng, (rows, cols), 0.02)
-    mats = [("w", np.frombuffer(F.quantize_matrix(w, F.Q4, bs), np.uint8), rows, cols)]
-    return F.Q4, bs, mats, F.gaussian(rng, cols)
+    return F.config0_matrix(seed)
 
 
 def cfg4_data(seed=4):
@@ -81,36 +74,46 @@ def cfg4_data(seed=4):
 
 
 def cfg2_layer(seed=2):
-    """One 7B decoder layer at 3-bit, block 128: q/k/v/o 4096x4096, gate/up
-    11008x4096, down 4096x11008 (N(0,0.02) weights, quantised).  The 32
-    layers of config 2 are distinct device copies of these payloads."""
+    """One 7B decoder layer at 3-bit, block 128 (qsf_format.config2_layer);
+    the 32 layers of config 2 are distinct device copies of these payloads."""
     from qstream_amd import qsf_format as F
-    rng = np.random.default_rng(seed)
-    shapes = [("q", 4096, 4096), ("k", 4096, 4096), ("v", 4096, 4096), ("o", 4096, 4096),
-              ("gate", 11008, 4096), ("up", 11008, 4096), ("down", 4096, 11008)]
-    mats = []
-    for name, r, c in shapes:
-        w = F.gaussian(rng, (r, c), 0.02)
-        mats.append((name, np.frombuffer(F.quantize_matrix(w, F.Q3, 128), np.uint8), r, c))
-        del w
-    return F.Q3, 128, mats
+    return F.config2_layer(seed)
 
 
 def cfg3_experts(seed=3, n_exp=32, dim=2880):
-    """32 MXFP4 experts (gate, up [2880][2880], down [2880][2880]) with
-    random E2M1 codes and E8M0 scales around 2^-6 (|w| ~ 0.02)."""
+    """32 MXFP4 experts (gate, up [2880][2880], down [2880][2880]) quantised
+    from N(0, 0.02) weights, one seed per matrix (qsf_format.moe_experts;
+    the config-3 parity tests build the same experts)."""
     from qstream_amd import qsf_format as F
-    rng = np.random.default_rng(seed)
-    return [{n: F.random_mxfp4(rng, dim, dim) for n in ("gate", "up", "down")} for _ in range(n_exp)]
+    return F.moe_experts(seed, n_exp, dim, dim)
 
 
 def algo_bytes(mats) -> int:
     return sum(len(p) + 4 * c + 4 * r for _, p, r, c in mats)
 
 
-class Events:
-    def __init__(self, torch, n):
-        self.ev = [torch.cuda.Event(enable_timing=True) for _ in range(n)]
+def graph_ms(torch, fn, steps):
+    """Mean ms per step of `fn(i, stream)` for i < steps, captured once into a
+    HIP graph and replayed between two HIP events on the replay stream (two
+    untimed replays first)."""
+    graph = torch.cuda.CUDAGraph()
+    cap = torch.cuda.Stream()
+    cap.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(cap):
+        with torch.cuda.graph(graph, stream=cap):
+            for i in range(steps):
+                fn(i, cap)
+    stream = torch.cuda.current_stream()
+    for _ in range(2):
+        graph.replay()
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    graph.replay()
+    t1.record(stream)
+    torch.cuda.synchronize()
+    del graph
+    return t0.elapsed_time(t1) / steps
 
 
 def run_dense(torch, hip, qt, bs, mats, x, steps, warmup, split=False):
@@ -121,87 +124,27 @@ def run_dense(torch, hip, qt, bs, mats, x, steps, warmup, split=False):
     n_copies = max(2, math.ceil(ROTATE_BYTES / per_copy))
     copies = [[hip.Tensor(p, qt, r, c, bs) for _, p, r, c in mats] for _ in range(n_copies)]
     cols = mats[0][3]
-    stream = torch.cuda.current_stream()
     dx = torch.from_numpy(x).to("cuda:0")
     xq = torch.empty(hip.xprep_bytes(qt, bs, cols) + 256, dtype=torch.uint8, device="cuda:0")
     xq_addr = (xq.data_ptr() + 255) & ~255
     ys = [torch.empty(r, device="cuda:0") for _, _, r, _ in mats]
 
-    def step(i, ev=None):
+    def step(i, stream):
         ts = copies[i % n_copies]
-        if ev is not None:
-            ev[0].record(stream)
         if split:
             hip.xprep(qt, bs, cols, dx, xq_addr, stream=stream)
-        if ev is not None:
-            ev[1].record(stream)
-        if split:
             hip.matvec_group_prepared(ts, dx, xq_addr, ys, stream=stream)
         else:
             hip.matvec_group(ts, dx, ys, stream=stream)
-        if ev is not None:
-            ev[2].record(stream)
 
     for i in range(warmup):
-        step(i)
+        step(i, torch.cuda.current_stream())
     torch.cuda.synchronize()
-
-    def timed(fn):
-        t0 = torch.cuda.Event(enable_timing=True)
-        t1 = torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        t0.record(stream)
-        fn()
-        t1.record(stream)
-        torch.cuda.synchronize()
-        return t0.elapsed_time(t1)
-
-    # Eager: K steps launched one by one from Python (host launch rate bound
-    # for these few-microsecond kernels).
-    ms_eager = timed(lambda: [step(i) for i in range(steps)])
-    # Graph: the same K launches captured once and replayed (the way a decode
-    # loop submits them); K steps between two synchronisations.
-    graph = torch.cuda.CUDAGraph()
-    cap = torch.cuda.Stream()
-    cap.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(cap):
-        stream = cap
-        with torch.cuda.graph(graph, stream=cap):
-            for i in range(steps):
-                step(i)
-    stream = torch.cuda.current_stream()
-    for _ in range(2):
-        graph.replay()
-    ms_graph = timed(graph.replay)
-    # per-launch event timing (eager, events around each launch)
-    evs = [Events(torch, 3).ev for _ in range(steps)]
-    for i in range(steps):
-        step(i, evs[i])
-    torch.cuda.synchronize()
-    gemv_ms = [e[1].elapsed_time(e[2]) for e in evs]
-    xprep_ms = [e[0].elapsed_time(e[1]) for e in evs]
-    # kernel durations: HIP event pairs recorded at each GEMV kernel's own
-    # start and end on the launch stream (no launch gaps)
-    hip.kernel_timing(True)
-    for i in range(steps):
-        step(i)
-    torch.cuda.synchronize()
-    kern_us = hip.kernel_timing_read(steps)
-    hip.kernel_timing(False)
-    del graph
+    ms = graph_ms(torch, step, steps)
     for ts in copies:
         for t in ts:
             t.free()
-    return {
-        "ms_per_step": ms_graph / steps,
-        "ms_per_step_eager": ms_eager / steps,
-        "gemv_ms_event_mean": float(np.mean(gemv_ms)),
-        "xprep_ms_event_mean": float(np.mean(xprep_ms)),
-        "kernel_us_mean": float(np.mean(kern_us)) if len(kern_us) else float("nan"),
-        "kernel_us_n": int(len(kern_us)),
-        "n_copies": n_copies,
-        "rotation_mib": n_copies * per_copy / (1 << 20),
-    }
+    return {"ms_per_step": ms, "n_copies": n_copies, "rotation_mib": n_copies * per_copy / (1 << 20)}
 
 
 def cpu_baseline_dense(qt, bs, mats, x, budget_s=10.0):
@@ -213,7 +156,7 @@ def cpu_baseline_dense(qt, bs, mats, x, budget_s=10.0):
     if ref is not None:
         def fn(p, r, c):
             return ref.matvec(qt, p, x, r, c, bs, isa="avx2")
-        name = "qsf_matvec_outlier_2bit_avx2" if qt == 9 else "qsf_matvec_4bit_avx2"
+        name = {9: "qsf_matvec_outlier_2bit_avx2", 3: "qsf_matvec_4bit_avx2"}[qt]
     else:
         kind = "port"
         o = Oracle()
@@ -237,20 +180,35 @@ def cpu_baseline_dense(qt, bs, mats, x, budget_s=10.0):
             break
     med = float(np.median(times))
     return {"value": per_step / med / 1e9, "unit": "GB/s", "cores": 1, "kind": kind,
-            "sample": f"{name}, {len(times)} steps (gate+up per step) over 4 host copies, "
-                      f"median {med * 1e3:.1f} ms/step, {time.perf_counter() - t_start:.1f} s"}
+            "sample": f"{name}, {len(times)} steps ({len(mats)} matrices per step) over 4 host "
+                      f"copies, median {med * 1e3:.1f} ms/step, {time.perf_counter() - t_start:.1f} s"}
+
+
+def _sha16(path: str):
+    import hashlib
+    try:
+        with open(path, "rb") as f:
+            return hashlib.sha256(f.read()).hexdigest()[:16]
+    except OSError:
+        return None
 
 
 def measured_traffic(key: str):
     """HBM bytes per launch measured with rocprofv3 FETCH_SIZE / WRITE_SIZE
     (scaled by the copy-kernel calibration), as recorded in
-    profiles/traffic.json; None when not measured."""
+    profiles/traffic.json, or None when not measured or when the kernel
+    source it was measured on (`kernel_src`, sha256 prefix
+    `kernel_src_sha16`) has changed since."""
     path = os.path.join(ROOT, "profiles", "traffic.json")
     try:
         with open(path) as f:
-            return json.load(f)[key]["traffic_bytes"]
+            rec = json.load(f)[key]
     except (OSError, KeyError, ValueError):
         return None
+    src, sha = rec.get("kernel_src"), rec.get("kernel_src_sha16")
+    if not src or not sha or _sha16(os.path.join(ROOT, src)) != sha:
+        return None
+    return rec.get("traffic_bytes")
 
 
 def run_profile(torch, hip, cfg, steps, warmup):
@@ -296,32 +254,34 @@ def table_slot_step_us(hip, qt, bs, mats, x, calls=200):
     return (time.perf_counter() - t0) / calls * 1e6
 
 
-def bench_dense(torch, hip, cfg, steps, warmup, with_cpu=True, split=False):
+def bench_dense(torch, hip, cfg, steps, warmup, with_cpu=True, split=False, slot=True,
+                cpu_budget=10.0):
     qt, bs, mats, x = cfg1_data() if cfg == 1 else cfg0_data()
     log(f"config {cfg}: data ready ({len(mats)} matrices)")
     res = run_dense(torch, hip, qt, bs, mats, x, steps, warmup, split)
     bytes_step = algo_bytes(mats)
-    value = bytes_step / (res["ms_per_step"] * 1e-3) / 1e9
-    # one GEMV launch per step: algorithmic bytes / its mean kernel duration
-    achieved = bytes_step / (res["kernel_us_mean"] * 1e-6) / 1e9
+    us_step = res["ms_per_step"] * 1e3
+    value = bytes_step / (us_step * 1e-6) / 1e9
     out = {
         "value": value,
         "ms_per_step": res["ms_per_step"],
-        "us_per_call": res["ms_per_step"] * 1e3 / len(mats),
-        "us_per_step_eager": res["ms_per_step_eager"] * 1e3,
-        "us_event_per_launch_eager": res["gemv_ms_event_mean"] * 1e3,
-        "us_kernel": res["kernel_us_mean"],
+        "us_per_call": us_step / len(mats),
         "bytes_per_step": bytes_step,
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": measured_traffic(f"cfg{cfg}"),
-                     "kernel_us": round(res["kernel_us_mean"], 3),
-                     "launches_timed": res["kernel_us_n"]},
         "rotation_mib": res["rotation_mib"],
     }
-    out["table_slot_us_per_step"] = table_slot_step_us(hip, qt, bs, mats, x)
+    if not split:
+        # one GEMV launch per step: the graph-replayed timed region per
+        # launch is the kernel's time (launch gaps included, so it errs low)
+        out["roofline"] = {"bound": "hbm", "kernel": "gemv_kernel (one launch per step)",
+                           "achieved": round(value, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                           "frac": round(value / HBM_PEAK_GBS, 4),
+                           "traffic": measured_traffic(f"cfg{cfg}"),
+                           "kernel_us": round(us_step, 3), "launches_timed": steps,
+                           "bytes_per_launch": bytes_step}
+    if slot:
+        out["table_slot_us_per_step"] = table_slot_step_us(hip, qt, bs, mats, x)
     if with_cpu:
-        out["cpu_baseline"] = cpu_baseline_dense(qt, bs, mats, x)
+        out["cpu_baseline"] = cpu_baseline_dense(qt, bs, mats, x, cpu_budget)
     return out
 
 
@@ -367,8 +327,11 @@ def profile_prefill(torch, hip, steps, warmup):
     log(f"profile run: config 4, {warmup} + {steps} launches done")
 
 
-def bench_prefill(torch, hip, steps, warmup, with_cpu=True):
-    """Config 4: one MFMA prefill launch per step over a rotating weight copy."""
+def bench_prefill(torch, hip, steps, warmup, with_cpu=True, cpu_budget=10.0):
+    """Config 4: one MFMA prefill (x repack + GEMM launch) per step over a
+    rotating weight copy.  The GEMM's own time comes from HIP event pairs
+    at its start and end on its launch stream (qsf_hip_kernel_timing), over
+    eager steps after the graph-timed region."""
     from qstream_amd import qsf_format as F
     payload, xb, m, n, k, bs = cfg4_data()
     log(f"config 4: data ready ({m}x{n}x{k}, block {bs})")
@@ -376,73 +339,36 @@ def bench_prefill(torch, hip, steps, warmup, with_cpu=True):
     copies = [hip.Tensor(payload, F.Q4, n, k, bs) for _ in range(n_copies)]
     dx = torch.from_numpy(xb.view(np.int16).copy()).to("cuda:0")
     y = torch.empty((m, n), device="cuda:0")
-    stream = torch.cuda.current_stream()
 
-    def step(i):
+    def step(i, stream):
         copies[i % n_copies].prefill(dx, m, y, stream=stream)
 
     for i in range(warmup):
-        step(i)
+        step(i, torch.cuda.current_stream())
     torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    cap = torch.cuda.Stream()
-    cap.wait_stream(stream)
-    with torch.cuda.stream(cap):
-        with torch.cuda.graph(graph, stream=cap):
-            for i in range(steps):
-                copies[i % n_copies].prefill(dx, m, y, stream=cap)
-    graph.replay()
-    torch.cuda.synchronize()
-    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t0.record(stream)
-    graph.replay()
-    t1.record(stream)
-    torch.cuda.synchronize()
-    ms = t0.elapsed_time(t1) / steps
+    ms = graph_ms(torch, step, steps)
     hip.kernel_timing(True)
     for i in range(steps):
-        step(i)
+        step(i, torch.cuda.current_stream())
     torch.cuda.synchronize()
     kern_us = hip.kernel_timing_read(steps)
     hip.kernel_timing(False)
-    del graph
     for t in copies:
         t.free()
     flops = 2.0 * m * n * k
     kus = float(np.mean(kern_us))
     out = {"value": flops / (ms * 1e-3) / 1e12, "ms_per_step": ms, "us_kernel": kus,
            "flops_per_step": flops, "weight_bytes": len(payload),
-           "roofline": {"bound": "mfma", "achieved": round(flops / (kus * 1e-6) / 1e12, 2),
+           "roofline": {"bound": "mfma", "kernel": "prefill_kernel",
+                        "achieved": round(flops / (kus * 1e-6) / 1e12, 2),
                         "peak": BF16_MFMA_PEAK_TFS, "unit": "TFLOP/s",
                         "frac": round(flops / (kus * 1e-6) / 1e12 / BF16_MFMA_PEAK_TFS, 4),
                         "traffic": measured_traffic("cfg4"), "kernel_us": round(kus, 3),
                         "launches_timed": len(kern_us)},
            "rotation_mib": n_copies * len(payload) / (1 << 20), "m": m, "n": n, "k": k}
     if with_cpu:
-        out["cpu_baseline"] = cpu_baseline_prefill(payload, xb, m, n, k, bs)
+        out["cpu_baseline"] = cpu_baseline_prefill(payload, xb, m, n, k, bs, cpu_budget)
     return out
-
-
-def _graph_ms(torch, fn, steps):
-    """Mean ms per step of `fn(i)` for i < steps, captured once into a HIP
-    graph and replayed between two synchronisations."""
-    graph = torch.cuda.CUDAGraph()
-    cap = torch.cuda.Stream()
-    cap.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(cap):
-        with torch.cuda.graph(graph, stream=cap):
-            for i in range(steps):
-                fn(i, cap)
-    graph.replay()
-    torch.cuda.synchronize()
-    stream = torch.cuda.current_stream()
-    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t0.record(stream)
-    graph.replay()
-    t1.record(stream)
-    torch.cuda.synchronize()
-    del graph
-    return t0.elapsed_time(t1) / steps
 
 
 def profile_layers(torch, hip, steps, warmup):
@@ -462,7 +388,7 @@ def profile_layers(torch, hip, steps, warmup):
     log(f"profile run: config 2 gate/up, {warmup} + {steps} launches done")
 
 
-def bench_layers(torch, hip, steps, warmup, with_cpu=True):
+def bench_layers(torch, hip, steps, warmup, with_cpu=True, cpu_budget=10.0):
     """Config 2: 32 decoder layers at 3-bit back to back.  A step is the
     whole stack: per layer q/k/v in one grouped launch, o, gate/up grouped,
     down -- 128 launches, each on its own fresh x."""
@@ -485,7 +411,7 @@ def bench_layers(torch, hip, steps, warmup, with_cpu=True):
     for i in range(warmup):
         step(i, torch.cuda.current_stream())
     torch.cuda.synchronize()
-    ms = _graph_ms(torch, step, steps)
+    ms = graph_ms(torch, step, steps)
     # Dominant kernel: the gate/up launch (45% of a layer's bytes).  Its
     # duration is the time per launch of a graph of 32 back-to-back gate/up
     # launches on the 32 layers' copies, HIP events around the replay on the
@@ -494,7 +420,7 @@ def bench_layers(torch, hip, steps, warmup, with_cpu=True):
     def gu_step(i, stream):
         hip.matvec_group(layers[i][4:6], xs[i][2, :4096], [ys["gate"], ys["up"]], stream=stream)
 
-    gu_us = _graph_ms(torch, gu_step, 32) * 1e3
+    gu_us = graph_ms(torch, gu_step, 32) * 1e3
     for ts in layers:
         for t in ts:
             t.free()
@@ -509,7 +435,7 @@ def bench_layers(torch, hip, steps, warmup, with_cpu=True):
                        "traffic": measured_traffic("cfg2"), "kernel_us": round(gu_us, 3),
                        "bytes_per_launch": gu_bytes}
     if with_cpu:
-        out["cpu_baseline"] = cpu_baseline_layer(qt, bs, mats)
+        out["cpu_baseline"] = cpu_baseline_layer(qt, bs, mats, cpu_budget)
     return out
 
 
@@ -563,13 +489,14 @@ def profile_moe(torch, hip, steps, warmup, ntok):
             t.free()
 
 
-def bench_moe(torch, hip, steps, warmup, ntok, with_cpu=True):
+def bench_moe(torch, hip, steps, warmup, ntok, with_cpu=True, cpu_budget=10.0, ex=None):
     """Config 3: MXFP4 MoE FFN, 32 experts, hidden = expert dim = 2880,
     top-4 softmax routing, ntok tokens per step.  Each step draws new router
     logits (64 seeded sets in rotation), so the experts read change."""
     from qstream_amd import qsf_format as F
     n_exp, dim, k = 32, 2880, 4
-    ex = cfg3_experts()
+    if ex is None:
+        ex = cfg3_experts()
     log(f"config 3: experts ready (batch {ntok})")
     tens = {n: [hip.Tensor(e[n], F.MXFP4, dim, dim, 32) for e in ex] for n in ("gate", "up", "down")}
     moe = hip.Moe(tens["gate"], tens["up"], tens["down"], dim, dim)
@@ -587,7 +514,7 @@ def bench_moe(torch, hip, steps, warmup, ntok, with_cpu=True):
     for i in range(warmup):
         step(i, torch.cuda.current_stream())
     torch.cuda.synchronize()
-    ms = _graph_ms(torch, step, steps)
+    ms = graph_ms(torch, step, steps)
     # algorithmic bytes per step: distinct experts x 3 matrices + activations
     per_mat = dim * (dim // 32) * 17
     distinct = []
@@ -623,7 +550,8 @@ def bench_moe(torch, hip, steps, warmup, ntok, with_cpu=True):
                        "kernel_us": round(float(np.mean(gu_us)), 3),
                        "bytes_per_launch": round(float(np.mean(gu_bytes)))}
     if with_cpu:
-        res["cpu_baseline"] = cpu_baseline_moe(ex, ntok, k, dim, logits_h, xs.cpu().numpy())
+        res["cpu_baseline"] = cpu_baseline_moe(ex, ntok, k, dim, logits_h, xs.cpu().numpy(),
+                                               cpu_budget)
     return res
 
 
@@ -669,13 +597,98 @@ def copy_calibration(torch, steps, warmup, mib=512):
     return {"copy_mib": mib, "ms_per_copy": ms, "read_plus_write_GBs": moved / (ms * 1e-3) / 1e9}
 
 
+DENSE_WORKLOAD = {1: "cfg1: 2-bit+outlier FFN gate+up, 2x 11008x4096, block 64, batch-1 decode",
+                  0: "cfg0: 4-bit asym 4096x4096, block 64, batch-1 decode"}
+DIGIT_DTYPE = "i4xi4->i32 digit dot, f32 accumulate"
+
+
+def run_config(torch, hip, key: str, args, cpu_budget: float, cache: dict) -> dict:
+    """One config's full JSON object (as printed when it runs alone)."""
+    base = {"metric": METRIC, "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None}
+    with_cpu = not args.no_cpu
+    if key in ("0", "1"):
+        cfg = int(key)
+        r = bench_dense(torch, hip, cfg, args.steps, args.warmup, with_cpu=with_cpu,
+                        split=args.split, slot=not args.no_slot, cpu_budget=cpu_budget)
+        conf = {"workload": DENSE_WORKLOAD[cfg], "us_per_call": round(r["us_per_call"], 3),
+                "us_per_step_graph": round(r["ms_per_step"] * 1e3, 3),
+                "launch": "split x-prep + GEMV" if args.split else "one fused launch per step",
+                "bytes_per_step": r["bytes_per_step"],
+                "hbm_frac_of_8TBs": round(r["value"] / HBM_PEAK_GBS, 4),
+                "rotation_mib": round(r["rotation_mib"], 1)}
+        if "table_slot_us_per_step" in r:
+            conf["table_slot_us_per_step_pcie"] = round(r["table_slot_us_per_step"], 3)
+            conf["table_slot_gbs_pcie"] = round(
+                r["bytes_per_step"] / (r["table_slot_us_per_step"] * 1e-6) / 1e9, 2)
+        line = dict(base, value=round(r["value"], 2), ms_per_step=round(r["ms_per_step"], 5),
+                    dtype=DIGIT_DTYPE,
+                    data="synthetic (seeded N(0,0.02)" + (" + Student-t outliers" if cfg == 1 else "")
+                         + ", converter-semantics quantisation)",
+                    config=conf)
+    elif key == "2":
+        r = bench_layers(torch, hip, args.steps, args.warmup, with_cpu=with_cpu, cpu_budget=cpu_budget)
+        line = dict(base, value=round(r["value"], 2), ms_per_step=round(r["ms_per_step"], 5),
+                    dtype=DIGIT_DTYPE, data="synthetic (seeded N(0,0.02), quantised to 3-bit block 128)",
+                    config={"workload": "cfg2: 32 x 7B decoder layer at 3-bit block 128, batch-1 "
+                                        "decode, back to back",
+                            "launches_per_step": 128, "us_per_step_graph": round(r["ms_per_step"] * 1e3, 3),
+                            "bytes_per_step": r["bytes_per_step"],
+                            "hbm_frac_of_8TBs": round(r["value"] / HBM_PEAK_GBS, 4)})
+    elif key in ("3", "3b1", "3b8"):
+        ntok = args.moe_batch if key == "3" else int(key[2:])
+        if "experts" not in cache:
+            cache["experts"] = cfg3_experts()
+        r = bench_moe(torch, hip, args.steps, args.warmup, ntok, with_cpu=with_cpu,
+                      cpu_budget=cpu_budget, ex=cache["experts"])
+        line = dict(base, value=round(r["value"], 2), ms_per_step=round(r["ms_per_step"], 5),
+                    dtype="e2m1 x f32, f32 accumulate",
+                    data="synthetic (seeded N(0,0.02) experts quantised to MXFP4; N(0,1) router logits "
+                         "and activations)",
+                    config={"workload": f"cfg3: MXFP4 MoE FFN, 32 experts 2880x2880, top-4, batch {ntok}",
+                            "distinct_experts_mean": round(r["distinct_experts_mean"], 2),
+                            "us_per_step_graph": round(r["ms_per_step"] * 1e3, 3),
+                            "bytes_per_step": r["bytes_per_step"],
+                            "hbm_frac_of_8TBs": round(r["value"] / HBM_PEAK_GBS, 4)})
+    elif key == "4":
+        r = bench_prefill(torch, hip, args.steps, args.warmup, with_cpu=with_cpu, cpu_budget=cpu_budget)
+        line = dict(base, metric="batched 4-bit prefill TFLOP/s (bf16 MFMA, % of 2.5 PFLOP/s dense peak)",
+                    value=round(r["value"], 2), unit="TFLOP/s", ms_per_step=round(r["ms_per_step"], 5),
+                    dtype="bf16 x bf16 -> f32 MFMA (4-bit codes as exact bf16 integers, fp32 "
+                          "per-block scale and zero-point)",
+                    data="synthetic (seeded N(0,0.02) weights, converter-semantics quantisation; "
+                         "bf16 N(0,1) activations)",
+                    config={"workload": f"cfg4: 4-bit asym prefill M={r['m']} x K={r['k']} x "
+                                        f"N={r['n']}, block 64",
+                            "us_kernel": round(r["us_kernel"], 3),
+                            "us_per_step_graph": round(r["ms_per_step"] * 1e3, 3),
+                            "mfma_util_of_peak": round(r["value"] / BF16_MFMA_PEAK_TFS, 4),
+                            "flops_per_step": r["flops_per_step"],
+                            "rotation_mib": round(r["rotation_mib"], 1)})
+    else:
+        raise SystemExit(f"unknown --config {key}")
+    if "roofline" in r:
+        line["roofline"] = r["roofline"]
+    if "cpu_baseline" in r:
+        line["cpu_baseline"] = r["cpu_baseline"]
+    return line
+
+
+def nested(line: dict) -> dict:
+    """A config's result as a nested field of the headline line."""
+    keep = ("metric", "value", "unit", "ms_per_step", "dtype", "config", "roofline", "cpu_baseline")
+    return {k: line[k] for k in keep if k in line}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--config", default="1")
+    ap.add_argument("--config", default="1", help="1 (default), 0, 2, 3, 4, all, or copy")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-slot", action="store_true", help="skip the table-slot (PCIe) timing")
     ap.add_argument("--moe-batch", type=int, default=1, help="tokens per step for --config 3")
     ap.add_argument("--split", action="store_true",
                     help="stand-alone x-prep launch + GEMV on prepared digits")
@@ -693,103 +706,27 @@ def main():
     if args.config == "copy":
         print(json.dumps(copy_calibration(torch, args.steps, args.warmup, args.copy_mib)), flush=True)
         return
-    cfg = int(args.config) if args.config != "all" else 1
-    if cfg in (2, 3) and args.profile:
+    if args.profile:
+        cfg = int(args.config)
         if cfg == 2:
             profile_layers(torch, qsf_hip, args.steps, args.warmup)
-        else:
+        elif cfg == 3:
             profile_moe(torch, qsf_hip, args.steps, args.warmup, args.moe_batch)
-        return
-    if cfg in (2, 3):
-        if cfg == 2:
-            r = bench_layers(torch, qsf_hip, args.steps, args.warmup, with_cpu=not args.no_cpu)
-            workload = "cfg2: 32 x 7B decoder layer at 3-bit block 128, batch-1 decode, back to back"
-            extra = {"launches_per_step": 128, "us_per_step_graph": round(r["ms_per_step"] * 1e3, 3)}
+        elif cfg == 4:
+            profile_prefill(torch, qsf_hip, args.steps, args.warmup)
         else:
-            r = bench_moe(torch, qsf_hip, args.steps, args.warmup, args.moe_batch, with_cpu=not args.no_cpu)
-            workload = (f"cfg3: MXFP4 MoE FFN, 32 experts 2880x2880, top-4, batch {args.moe_batch}")
-            extra = {"distinct_experts_mean": round(r["distinct_experts_mean"], 2),
-                     "us_per_step_graph": round(r["ms_per_step"] * 1e3, 3)}
-        line = {
-            "metric": METRIC, "value": round(r["value"], 2), "unit": "GB/s", "n_gpus": 1,
-            "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(r["ms_per_step"], 5),
-            "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-            "dtype": "i4xi4->i32 digit dot, f32 accumulate" if cfg == 2 else "e2m1 x f32, f32 accumulate",
-            "data": "synthetic (seeded; cfg2 N(0,0.02) quantised, cfg3 random E2M1 codes / E8M0 scales)",
-            "config": dict({"workload": workload, "bytes_per_step": r["bytes_per_step"],
-                            "hbm_frac_of_8TBs": round(r["value"] / HBM_PEAK_GBS, 4)}, **extra),
-        }
-        if "roofline" in r:
-            line["roofline"] = r["roofline"]
-        if "cpu_baseline" in r:
-            line["cpu_baseline"] = r["cpu_baseline"]
-        print(json.dumps(line), flush=True)
+            run_profile(torch, qsf_hip, cfg, args.steps, args.warmup)
         return
-    if cfg == 4 and args.profile:
-        profile_prefill(torch, qsf_hip, args.steps, args.warmup)
-        return
-    if cfg == 4:
-        r = bench_prefill(torch, qsf_hip, args.steps, args.warmup, with_cpu=not args.no_cpu)
-        line = {
-            "metric": "batched 4-bit prefill TFLOP/s (bf16 MFMA, % of 2.5 PFLOP/s dense peak)",
-            "value": round(r["value"], 2),
-            "unit": "TFLOP/s",
-            "n_gpus": 1,
-            "steps": args.steps,
-            "warmup": args.warmup,
-            "ms_per_step": round(r["ms_per_step"], 5),
-            "higher_is_better": True,
-            "scaling": "weak",
-            "vs_baseline": None,
-            "dtype": "bf16 x bf16 -> f32 MFMA (weights dequantised from 4-bit in registers)",
-            "data": "synthetic (seeded N(0,0.02) weights, converter-semantics quantisation; "
-                    "bf16 N(0,1) activations)",
-            "config": {"workload": f"cfg4: 4-bit asym prefill M={r['m']} x K={r['k']} x "
-                                   f"N={r['n']}, block 64", "us_kernel": round(r["us_kernel"], 3),
-                       "us_per_step_graph": round(r["ms_per_step"] * 1e3, 3),
-                       "mfma_util_of_peak": round(r["value"] / BF16_MFMA_PEAK_TFS, 4),
-                       "flops_per_step": r["flops_per_step"],
-                       "rotation_mib": round(r["rotation_mib"], 1)},
-            "roofline": r["roofline"],
-        }
-        if "cpu_baseline" in r:
-            line["cpu_baseline"] = r["cpu_baseline"]
-        print(json.dumps(line), flush=True)
-        return
-    if args.profile:
-        run_profile(torch, qsf_hip, cfg, args.steps, args.warmup)
-        return
-    r = bench_dense(torch, qsf_hip, cfg, args.steps, args.warmup, with_cpu=not args.no_cpu,
-                    split=args.split)
-    workload = {1: "cfg1: 2-bit+outlier FFN gate+up, 2x 11008x4096, block 64, batch-1 decode",
-                0: "cfg0: 4-bit asym 4096x4096, block 64, batch-1 decode"}[cfg]
-    line = {
-        "metric": METRIC,
-        "value": round(r["value"], 2),
-        "unit": "GB/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(r["ms_per_step"], 5),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "i4xi4->i32 digit dot, f32 accumulate",
-        "data": "synthetic (seeded N(0,0.02) + Student-t outliers, converter-semantics quantisation)",
-        "config": {"workload": workload, "us_per_call": round(r["us_per_call"], 3),
-                   "us_per_step_graph": round(r["ms_per_step"] * 1e3, 3),
-                   "us_per_step_eager": round(r["us_per_step_eager"], 3),
-                   "us_event_per_launch_eager": round(r["us_event_per_launch_eager"], 3),
-                   "table_slot_us_per_step_pcie": round(r["table_slot_us_per_step"], 3),
-                   "table_slot_gbs_pcie": round(r["bytes_per_step"] / (r["table_slot_us_per_step"] * 1e-6) / 1e9, 2),
-                   "launch": "split x-prep + GEMV" if args.split else "one fused launch per step",
-                   "bytes_per_step": r["bytes_per_step"],
-                   "hbm_frac_of_8TBs": round(r["value"] / HBM_PEAK_GBS, 4),
-                   "rotation_mib": round(r["rotation_mib"], 1)},
-        "roofline": r["roofline"],
-    }
-    if "cpu_baseline" in r:
-        line["cpu_baseline"] = r["cpu_baseline"]
+    cache: dict = {}
+    if args.config == "all":
+        line = run_config(torch, qsf_hip, "1", args, 10.0, cache)
+        line["configs"] = {k.replace("3b", "3_b"): nested(run_config(torch, qsf_hip, k, args, 4.0, cache))
+                           for k in ("0", "2", "3b1", "3b8", "4")}
+    elif args.config == "1":
+        line = run_config(torch, qsf_hip, "1", args, 10.0, cache)
+        line["config0"] = nested(run_config(torch, qsf_hip, "0", args, 5.0, cache))
+    else:
+        line = run_config(torch, qsf_hip, args.config, args, 10.0, cache)
     print(json.dumps(line), flush=True)
 
 

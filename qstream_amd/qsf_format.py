@@ -162,17 +162,20 @@ def outlier_payload(n_idx: np.ndarray, vals_f16_bits: np.ndarray, blocks: bytes)
 E2M1_MAG = np.array([0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0], np.float32)
 
 
+# Rounding boundaries between consecutive E2M1 magnitudes; at a tie the
+# even code wins, so the boundary above an even code is exclusive (>) and
+# the one above an odd code inclusive (>=).
+_E2M1_UP = ((0.25, False), (0.75, True), (1.25, False), (1.75, True),
+            (2.5, False), (3.5, True), (5.0, False))
+
+
 def _e2m1_encode(v: np.ndarray) -> np.ndarray:
-    """Round fp32 to the nearest E2M1 value, ties to even code, saturating."""
-    mag = np.minimum(np.abs(v), 6.0)
-    # candidate codes below/above; nearest with ties to the even mantissa
-    idx = np.searchsorted(E2M1_MAG, mag, side="left")
-    idx = np.clip(idx, 0, 7)
-    lo = np.clip(idx - 1, 0, 7)
-    d_hi = np.abs(E2M1_MAG[idx] - mag)
-    d_lo = np.abs(mag - E2M1_MAG[lo])
-    pick_lo = (d_lo < d_hi) | ((d_lo == d_hi) & (lo % 2 == 0))
-    code = np.where(pick_lo, lo, idx).astype(np.uint8)
+    """Round fp32 to the nearest E2M1 value, ties to even code, saturating
+    at 6 (codes: bit 3 sign, bits 2..0 the index into E2M1_MAG)."""
+    mag = np.abs(v)
+    code = np.zeros(v.shape, np.uint8)
+    for edge, inclusive in _E2M1_UP:
+        code += (mag >= edge) if inclusive else (mag > edge)
     sign = (np.signbit(v) & (code != 0)).astype(np.uint8) << 3
     return code | sign
 
@@ -190,6 +193,33 @@ def quantize_mxfp4(w: np.ndarray) -> bytes:
     packed = (codes[:, 0::2] | (codes[:, 1::2] << 4)).astype(np.uint8)
     scales = (e + 127).astype(np.uint8)
     return packed.tobytes() + scales.tobytes()
+
+
+def _mx_matrix(job) -> bytes:
+    seed, e, i, rows, cols = job
+    rng = np.random.default_rng([seed, e, i])
+    return quantize_mxfp4(gaussian(rng, (rows, cols), 0.02))
+
+
+def moe_experts(seed: int, n_exp: int, hidden: int, eid: int, workers: int | None = None):
+    """Benchmark config 3's experts: per expert gate and up [eid][hidden] and
+    down [hidden][eid], MXFP4-quantised N(0, 0.02) weights.  Each matrix has
+    its own seed (seed, expert, matrix), so the result does not depend on
+    how many worker processes (spawned, so safe beside an initialised GPU)
+    build it."""
+    import os
+    jobs = [(seed, e, i, eid if i < 2 else hidden, hidden if i < 2 else eid)
+            for e in range(n_exp) for i in range(3)]
+    if workers is None:
+        workers = min(16, os.cpu_count() or 1)
+    if workers > 1 and len(jobs) > 4:
+        import multiprocessing as mp
+        with mp.get_context("spawn").Pool(min(workers, len(jobs))) as pool:
+            mats = pool.map(_mx_matrix, jobs, chunksize=1)
+    else:
+        mats = [_mx_matrix(j) for j in jobs]
+    return [{"gate": mats[3 * e], "up": mats[3 * e + 1], "down": mats[3 * e + 2]}
+            for e in range(n_exp)]
 
 
 def random_mxfp4(rng: np.random.Generator, rows: int, cols: int,
@@ -225,3 +255,40 @@ def bf16_bits(x: np.ndarray) -> np.ndarray:
     rounded = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
     nan = np.isnan(x)
     return np.where(nan, ((u >> 16) | 0x40).astype(np.uint16), rounded).astype(np.uint16)
+
+
+# ---- the benchmark configs' seeded data --------
+# bench.py times these and the GPU parity tests check the same bytes.
+def config0_matrix(seed: int = 0):
+    """Config 0: one 4-bit asymmetric 4096x4096 matrix, block 64, and x."""
+    rng = np.random.default_rng(seed)
+    w = gaussian(rng, (4096, 4096), 0.02)
+    mats = [("w", np.frombuffer(quantize_matrix(w, Q4, 64), np.uint8), 4096, 4096)]
+    return Q4, 64, mats, gaussian(rng, 4096)
+
+
+def config1_matrices(seed: int = 1):
+    """Config 1: the 2-bit+outlier gate and up projections, 11008x4096 each,
+    block 64, with 0.5 % Student-t outliers, and x."""
+    rng = np.random.default_rng(seed)
+    mats = []
+    for name in ("gate", "up"):
+        w = heavy_tail_weights(rng, 11008, 4096)
+        mats.append((name, np.frombuffer(quantize_matrix(w, Q2_OUTLIER, 64), np.uint8), 11008, 4096))
+        del w
+    return Q2_OUTLIER, 64, mats, gaussian(rng, 4096)
+
+
+def config2_layer(seed: int = 2):
+    """Config 2: one 7B decoder layer at 3-bit, block 128 -- q/k/v/o
+    4096x4096, gate/up 11008x4096, down 4096x11008 (N(0, 0.02) weights)."""
+    rng = np.random.default_rng(seed)
+    shapes = [("q", 4096, 4096), ("k", 4096, 4096), ("v", 4096, 4096), ("o", 4096, 4096),
+              ("gate", 11008, 4096), ("up", 11008, 4096), ("down", 4096, 11008)]
+    mats = []
+    for name, r, c in shapes:
+        w = gaussian(rng, (r, c), 0.02)
+        mats.append((name, np.frombuffer(quantize_matrix(w, Q3, 128), np.uint8), r, c))
+        del w
+    return Q3, 128, mats
+

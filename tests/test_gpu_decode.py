@@ -339,12 +339,22 @@ def test_degenerate_shapes(hip, oracle):
     assert np.all(out == 0.0)
 
 
-def test_nonfinite_input_gives_nan(hip):
+@pytest.mark.parametrize("qt", [F.Q2, F.Q3, F.Q4, F.Q4SYM, F.Q2_OUTLIER])
+@pytest.mark.parametrize("bad", [np.inf, -np.inf, np.nan])
+def test_nonfinite_input_gives_nan(hip, qt, bad):
+    """Documented divergence: a non-finite x value makes every output row
+    NaN.  The scalar reference gives +-Inf for rows whose weight at that
+    column is nonzero (NaN only for 0 * Inf or Inf - Inf); the block
+    fixed-point x cannot carry an infinity, so the whole result is marked
+    invalid instead, which the engine's NaN check catches
+    (src/engine.c:1174-1187)."""
     rows, cols, bs = 8, 256, 64
     rng = np.random.default_rng(3)
-    p = F.quantize_matrix(F.gaussian(rng, (rows, cols), 0.02), F.Q4, bs)
+    p = F.quantize_matrix(F.heavy_tail_weights(rng, rows, cols), qt, bs)
     x = F.gaussian(rng, cols)
-    x[70] = np.inf
+    x[70] = bad
     out = np.zeros(rows, np.float32)
-    hip.KernelTable().matvec_4bit(p, x, out, rows, cols, bs)
-    assert np.all(~np.isfinite(out))
+    slot = {F.Q2: "matvec_2bit", F.Q3: "matvec_3bit", F.Q4: "matvec_4bit",
+            F.Q4SYM: "matvec_4bit_sym", F.Q2_OUTLIER: "matvec_outlier_2bit"}[qt]
+    getattr(hip.KernelTable(), slot)(p, x, out, rows, cols, bs)
+    assert np.all(np.isnan(out)), out
