@@ -439,6 +439,67 @@ def bench_layers(torch, hip, steps, warmup, with_cpu=True, cpu_budget=10.0):
     return out
 
 
+def bench_decode_layer(torch, hip, steps, warmup, position=1023):
+    """One device-resident 7B decoder layer step per step (LLaMA-7B shapes:
+    hidden 4096, 32 heads of 128, intermediate 11008, 3-bit block 128
+    weights): RMSNorm, q/k/v (one grouped launch), RoPE, int8 KV store,
+    attention over `position` + 1 cached positions, o, residual, RMSNorm,
+    gate/up (grouped), SiLU x up, down, residual + NaN check -- 12 launches,
+    no host round trip.  Steps cycle over 32 layers' distinct weights and
+    KV caches (2.9 GB), so neither stays in the MALL.  Bytes per step: the
+    layer's weight payloads, the KV rows attention reads, activations."""
+    qt, bs, mats = cfg2_layer()
+    log("layer: weights quantised")
+    hid, nh, hd, eid, max_seq, n_layers = 4096, 32, 128, 11008, position + 1, 32
+    layers = [[hip.Tensor(p, qt, r, c, bs) for _, p, r, c in mats] for _ in range(n_layers)]
+    g = torch.Generator(device="cuda:0").manual_seed(40)
+    kcs = [torch.randint(-127, 128, (nh, max_seq, hd), dtype=torch.int8, device="cuda:0", generator=g)
+           for _ in range(n_layers)]
+    vcs = [torch.randint(-127, 128, (nh, max_seq, hd), dtype=torch.int8, device="cuda:0", generator=g)
+           for _ in range(n_layers)]
+    kss = [torch.rand((nh, max_seq), device="cuda:0", generator=g) * 0.02 for _ in range(n_layers)]
+    vss = [torch.rand((nh, max_seq), device="cuda:0", generator=g) * 0.02 for _ in range(n_layers)]
+    an_w = torch.ones(hid, device="cuda:0")
+    fn_w = torch.ones(hid, device="cuda:0")
+    rope = hip.Rope(hd, 10000.0)
+    res = torch.randn(hid, device="cuda:0", generator=g)
+    x = torch.empty(hid, device="cuda:0")
+    ys = {n: torch.empty(r, device="cuda:0") for n, _, r, _ in mats}
+    attn = torch.empty(nh * hd, device="cuda:0")
+    bad = torch.zeros(1, dtype=torch.int32, device="cuda:0")
+
+    def step(i, stream):
+        li = i % n_layers
+        ts = layers[li]
+        hip.rms_norm(res, x, an_w, 1e-5, stream=stream)
+        hip.matvec_group(ts[0:3], x, [ys["q"], ys["k"], ys["v"]], stream=stream)
+        rope.apply(ys["q"], ys["k"], nh, nh, position, stream=stream)
+        hip.kv_store(kcs[li], vcs[li], kss[li], vss[li], max_seq, nh, hd, position, ys["k"], ys["v"],
+                     stream=stream)
+        hip.attention(ys["q"], kcs[li], vcs[li], kss[li], vss[li], max_seq, nh, nh, hd, position, attn,
+                      stream=stream)
+        hip.matvec_group(ts[3:4], attn, [ys["o"]], stream=stream)
+        hip.residual(res, ys["o"], None, stream=stream)
+        hip.rms_norm(res, x, fn_w, 1e-5, stream=stream)
+        hip.matvec_group(ts[4:6], x, [ys["gate"], ys["up"]], stream=stream)
+        hip.act_mul(ys["gate"], ys["up"], 2, stream=stream)
+        hip.matvec_group(ts[6:7], ys["gate"], [ys["down"]], stream=stream)
+        hip.residual(res, ys["down"], bad, stream=stream)
+
+    for i in range(warmup):
+        step(i, torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    ms = graph_ms(torch, step, steps)
+    rope.free()
+    for ts in layers:
+        for t in ts:
+            t.free()
+    kv_bytes = 2 * nh * max_seq * (hd + 4)
+    total = algo_bytes(mats) + kv_bytes
+    return {"value": total / (ms * 1e-3) / 1e9, "ms_per_step": ms, "bytes_per_step": total,
+            "weight_bytes": algo_bytes(mats), "kv_bytes": kv_bytes, "position": position}
+
+
 def cpu_baseline_layer(qt, bs, mats, budget_s=10.0):
     """The reference's 3-bit matvec is scalar on every ISA
     (src/kernels.c:10): qsf_matvec_3bit_scalar from oracle/_ref (reference
@@ -651,6 +712,19 @@ def run_config(torch, hip, key: str, args, cpu_budget: float, cache: dict) -> di
                             "us_per_step_graph": round(r["ms_per_step"] * 1e3, 3),
                             "bytes_per_step": r["bytes_per_step"],
                             "hbm_frac_of_8TBs": round(r["value"] / HBM_PEAK_GBS, 4)})
+    elif key == "layer":
+        r = bench_decode_layer(torch, hip, args.steps, args.warmup)
+        line = dict(base, value=round(r["value"], 2), ms_per_step=round(r["ms_per_step"], 5),
+                    dtype=DIGIT_DTYPE + "; glue fp32",
+                    data="synthetic (seeded N(0,0.02) weights quantised to 3-bit block 128; random "
+                         "int8 KV cache)",
+                    config={"workload": f"device-resident 7B decoder layer step (3-bit block 128), "
+                                        f"attention over {r['position'] + 1} cached positions, "
+                                        f"12 launches",
+                            "us_per_layer": round(r["ms_per_step"] * 1e3, 3),
+                            "bytes_per_step": r["bytes_per_step"], "weight_bytes": r["weight_bytes"],
+                            "kv_bytes": r["kv_bytes"],
+                            "hbm_frac_of_8TBs": round(r["value"] / HBM_PEAK_GBS, 4)})
     elif key == "4":
         r = bench_prefill(torch, hip, args.steps, args.warmup, with_cpu=with_cpu, cpu_budget=cpu_budget)
         line = dict(base, metric="batched 4-bit prefill TFLOP/s (bf16 MFMA, % of 2.5 PFLOP/s dense peak)",
@@ -686,7 +760,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--config", default="1", help="1 (default), 0, 2, 3, 4, all, or copy")
+    ap.add_argument("--config", default="1", help="1 (default), 0, 2, 3, 4, layer, all, or copy")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-slot", action="store_true", help="skip the table-slot (PCIe) timing")
     ap.add_argument("--moe-batch", type=int, default=1, help="tokens per step for --config 3")
@@ -721,7 +795,7 @@ def main():
     if args.config == "all":
         line = run_config(torch, qsf_hip, "1", args, 10.0, cache)
         line["configs"] = {k.replace("3b", "3_b"): nested(run_config(torch, qsf_hip, k, args, 4.0, cache))
-                           for k in ("0", "2", "3b1", "3b8", "4")}
+                           for k in ("0", "2", "3b1", "3b8", "4", "layer")}
     elif args.config == "1":
         line = run_config(torch, qsf_hip, "1", args, 10.0, cache)
         line["config0"] = nested(run_config(torch, qsf_hip, "0", args, 5.0, cache))

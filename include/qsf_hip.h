@@ -176,6 +176,55 @@ int qsf_hip_prefill_4bit_dev(const qsf_hip_tensor* t, const uint16_t* d_x_bf16, 
 int qsf_hip_prefill_4bit_dev_noalloc(const qsf_hip_tensor* t, const uint16_t* d_x_bf16, int m,
                                      float* d_y, void* stream);
 
+/* ---- device-resident decode glue ------------------------------------------
+ * The per-layer work between the projections of one decode step
+ * (src/engine.c:709-1187), so an engine that keeps its activations in HBM
+ * needs no host round trip.  All take device pointers and are asynchronous
+ * on `stream`.  Layouts: q [n_heads][head_dim], k and v [n_kv][head_dim];
+ * one layer's KV cache [n_kv][max_seq][head_dim] int8 with per-position
+ * scales [n_kv][max_seq] (src/engine.c:240-327). */
+/* src/kernels_scalar.c:172-185 (called at src/engine.c:805-815, 940-948, 1190-1196) */
+int qsf_hip_rms_norm_dev(const float* d_in, float* d_out, const float* d_w, int dim, float eps,
+                         void* stream);
+/* src/kernels_scalar.c:148-169; d_b may be NULL */
+int qsf_hip_layer_norm_dev(const float* d_in, float* d_out, const float* d_w, const float* d_b,
+                           int dim, float eps, void* stream);
+/* apply_rope, src/engine.c:204-235.  The frequency table 1/theta^(2j/head_dim)
+ * is computed once on the host with the C library's powf, as the reference
+ * does (theta <= 0 means 10000, src/engine.c:873). */
+typedef struct qsf_hip_rope qsf_hip_rope;
+qsf_hip_rope* qsf_hip_rope_create(int head_dim, float theta);
+void qsf_hip_rope_free(qsf_hip_rope* r);
+int qsf_hip_rope_dev(const qsf_hip_rope* r, float* d_q, float* d_k, int n_heads, int n_kv_heads,
+                     int position, void* stream);
+/* kv_cache_store, src/engine.c:240-300: row `position` of one layer's cache;
+ * int8 codes and scales bit-exact. */
+int qsf_hip_kv_store_dev(int8_t* d_kc, int8_t* d_vc, float* d_ks, float* d_vs, int max_seq,
+                         int n_kv_heads, int head_dim, int position, const float* d_k,
+                         const float* d_v, void* stream);
+/* The attention loop of src/engine.c:879-923 over positions 0..position
+ * (grouped-query heads: head h reads KV head h / (n_heads / n_kv_heads));
+ * d_out [n_heads][head_dim].  head_dim a multiple of 16 up to 256,
+ * position < 16384.  Uses a library workspace for per-chunk partial
+ * results (grown on first use: run once eagerly before capturing a graph;
+ * calls must not overlap on different streams). */
+int qsf_hip_attention_dev(const float* d_q, const int8_t* d_kc, const int8_t* d_vc,
+                          const float* d_ks, const float* d_vs, int max_seq, int n_heads,
+                          int n_kv_heads, int head_dim, int position, float* d_out, void* stream);
+/* gate = act(gate) * up, src/engine.c:1128-1140 (QSFActivation: 2 SiLU,
+ * 0/1 GELU, else ReLU) */
+int qsf_hip_act_mul_dev(float* d_gate, const float* d_up, int n, int activation, void* stream);
+/* res += x, src/engine.c:937 and 1174; with d_bad, the NaN/Inf check of
+ * src/engine.c:1176-1187: *d_bad = first index holding NaN or |v| > 1e30,
+ * or -1 (written on every call; nothing to clear beforehand). */
+int qsf_hip_residual_dev(float* d_res, const float* d_x, int n, int* d_bad, void* stream);
+/* Embedding lookup, src/engine.c:709-765: row `token` of a blockwise table
+ * uploaded with qsf_hip_tensor_upload (rows = vocab, cols = hidden),
+ * dequantised bit-exactly; or of an FP16 table [vocab][hd] in device memory. */
+int qsf_hip_embed_row_dev(const qsf_hip_tensor* table, int token, float* d_out, void* stream);
+int qsf_hip_embed_row_fp16_dev(const uint16_t* d_table, int hd, int token, float* d_out,
+                               void* stream);
+
 /* Bit-exact unpack of `nblocks` QSF blocks already in device memory (the
  * same device code paths the GEMV uses): codes int8[nblocks*bs] (2/3/4-bit
  * field values; 4-bit sym as two's complement), meta u32[nblocks] (first

@@ -56,6 +56,16 @@ class Oracle:
         L.orc_topk.argtypes = [_vp, _i, _i, _i, _vp, _vp]
         L.orc_moe_token.argtypes = [_vp, _i, _i, _i, _i, _i, _i, _vp, _vp, _vp]
         L.orc_prefill_4bit.argtypes = [_vp, _vp, _vp, _i, _i, _i, _i]
+        L.orc_rms_norm.argtypes = [_vp, _vp, _vp, _i, C.c_float]
+        L.orc_layer_norm.argtypes = [_vp, _vp, _vp, _vp, _i, C.c_float]
+        L.orc_vec_add.argtypes = [_vp, _vp, _vp, _i]
+        L.orc_vec_mul.argtypes = [_vp, _vp, _vp, _i]
+        L.orc_rope.argtypes = [_vp, _vp, _i, _i, C.c_float, _i, _i]
+        L.orc_kv_store.argtypes = [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _vp]
+        L.orc_attention.argtypes = [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp]
+        L.orc_residual_check.argtypes = [_vp, _vp, _i]
+        L.orc_residual_check.restype = _i
+        L.orc_embed_row.argtypes = [_i, _vp, _i, _i, _i, _vp]
 
     def fp16_to_fp32_bits(self, h: np.ndarray) -> np.ndarray:
         # bulk C call: a ctypes float return would quiet signalling NaNs
@@ -146,6 +156,70 @@ class Oracle:
         return y
 
 
+    # ---- decode glue (src/engine.c, src/kernels_scalar.c) ----------------
+    def rms_norm(self, x, w, eps):
+        x = np.ascontiguousarray(x, np.float32)
+        w = np.ascontiguousarray(w, np.float32)
+        out = np.empty_like(x)
+        self.lib.orc_rms_norm(_ptr(x), _ptr(out), _ptr(w), len(x), eps)
+        return out
+
+    def layer_norm(self, x, w, b, eps):
+        x = np.ascontiguousarray(x, np.float32)
+        w = np.ascontiguousarray(w, np.float32)
+        bb = None if b is None else np.ascontiguousarray(b, np.float32)
+        out = np.empty_like(x)
+        self.lib.orc_layer_norm(_ptr(x), _ptr(out), _ptr(w), None if bb is None else _ptr(bb),
+                                len(x), eps)
+        return out
+
+    def rope(self, q, k, head_dim, position, theta, n_heads, n_kv):
+        q = np.array(q, np.float32, copy=True)
+        k = np.array(k, np.float32, copy=True)
+        self.lib.orc_rope(_ptr(q), _ptr(k), head_dim, position, theta, n_heads, n_kv)
+        return q, k
+
+    def kv_store(self, kc, vc, ks, vs, max_seq, n_kv, head_dim, position, k, v):
+        """Writes row `position` of the layer's int8 caches in place."""
+        k = np.ascontiguousarray(k, np.float32)
+        v = np.ascontiguousarray(v, np.float32)
+        self.lib.orc_kv_store(_ptr(kc), _ptr(vc), _ptr(ks), _ptr(vs), max_seq, n_kv, head_dim,
+                              position, _ptr(k), _ptr(v))
+
+    def attention(self, q, kc, vc, ks, vs, max_seq, n_heads, n_kv, head_dim, position):
+        q = np.ascontiguousarray(q, np.float32)
+        out = np.zeros(n_heads * head_dim, np.float32)
+        self.lib.orc_attention(_ptr(q), _ptr(kc), _ptr(vc), _ptr(ks), _ptr(vs), max_seq, n_heads,
+                               n_kv, head_dim, position, _ptr(out))
+        return out
+
+    def residual_check(self, res, x):
+        res = np.array(res, np.float32, copy=True)
+        x = np.ascontiguousarray(x, np.float32)
+        bad = self.lib.orc_residual_check(_ptr(res), _ptr(x), len(res))
+        return res, bad
+
+    def embed_row(self, qt, table, bs, hd, token):
+        keep, p = _buf(table)
+        out = np.zeros(hd, np.float32)
+        self.lib.orc_embed_row(qt, p, bs, hd, token, _ptr(out))
+        return out
+
+    def vec_add(self, a, b):
+        a = np.ascontiguousarray(a, np.float32)
+        b = np.ascontiguousarray(b, np.float32)
+        out = np.empty_like(a)
+        self.lib.orc_vec_add(_ptr(a), _ptr(b), _ptr(out), len(a))
+        return out
+
+    def vec_mul(self, a, b):
+        a = np.ascontiguousarray(a, np.float32)
+        b = np.ascontiguousarray(b, np.float32)
+        out = np.empty_like(a)
+        self.lib.orc_vec_mul(_ptr(a), _ptr(b), _ptr(out), len(a))
+        return out
+
+
 _MATVEC_SYMS = ("qsf_matvec_2bit_scalar", "qsf_matvec_3bit_scalar",
                 "qsf_matvec_4bit_scalar", "qsf_matvec_4bit_sym_scalar")
 _AVX2_SYMS = ("qsf_matvec_2bit_avx2", "qsf_matvec_4bit_avx2",
@@ -177,6 +251,14 @@ class RefLib:
         if self.has_avx2:
             for n in _AVX2_SYMS:
                 getattr(L, n).argtypes = [_vp, _vp, _vp, _i, _i, _i]
+        # the elementwise kernels of src/kernels_scalar.c:112-214
+        L.qsf_rms_norm_scalar.argtypes = [_vp, _vp, _vp, _vp, _i, C.c_float]
+        L.qsf_layer_norm_scalar.argtypes = [_vp, _vp, _vp, _vp, _i, C.c_float]
+        L.qsf_softmax_scalar.argtypes = [_vp, _vp, _i]
+        for n in ("qsf_silu_scalar", "qsf_gelu_scalar", "qsf_relu_scalar"):
+            getattr(L, n).argtypes = [_vp, _i]
+        for n in ("qsf_vec_add_scalar_impl", "qsf_vec_mul_scalar_impl"):
+            getattr(L, n).argtypes = [_vp, _vp, _vp, _i]
         L.qsf_quant_block_2bit.argtypes = [_vp, _vp, _i]
         L.qsf_quant_block_3bit.argtypes = [_vp, _vp, _i]
         L.qsf_quant_block_4bit.argtypes = [_vp, _vp, _i]

@@ -380,3 +380,160 @@ void orc_prefill_4bit(const void* w, const uint16_t* x_bf16, float* y,
     free(wd);
     free(xf);
 }
+
+/* ---- decode glue ---------------------------------------------------------- */
+void orc_rms_norm(const float* in, float* out, const float* w, int dim, float eps) {
+    float ss = 0.0f;
+    for (int i = 0; i < dim; i++) {
+        float sq = in[i] * in[i];
+        ss = ss + sq;
+    }
+    float rms = sqrtf(ss / (float)dim + eps);
+    float inv = 1.0f / rms;
+    for (int i = 0; i < dim; i++) {
+        float t = in[i] * inv;
+        out[i] = t * w[i];
+    }
+}
+
+void orc_layer_norm(const float* in, float* out, const float* w, const float* b,
+                    int dim, float eps) {
+    float mean = 0.0f;
+    for (int i = 0; i < dim; i++) mean = mean + in[i];
+    mean = mean / (float)dim;
+    float var = 0.0f;
+    for (int i = 0; i < dim; i++) {
+        float d = in[i] - mean;
+        float sq = d * d;
+        var = var + sq;
+    }
+    var = var / (float)dim;
+    float inv_std = 1.0f / sqrtf(var + eps);
+    for (int i = 0; i < dim; i++) {
+        float t = (in[i] - mean) * inv_std;
+        out[i] = t * w[i];
+        if (b) out[i] = out[i] + b[i];
+    }
+}
+
+void orc_vec_add(const float* a, const float* b, float* o, int n) {
+    for (int i = 0; i < n; i++) o[i] = a[i] + b[i];
+}
+
+void orc_vec_mul(const float* a, const float* b, float* o, int n) {
+    for (int i = 0; i < n; i++) o[i] = a[i] * b[i];
+}
+
+/* One head's rotation; the angle is reduced in double as the reference
+ * does (fmod by 2 pi), then cos/sin in float. */
+static void rope_head(float* h, int head_dim, int position, float theta) {
+    for (int i = 0; i < head_dim; i += 2) {
+        float freq = 1.0f / powf(theta, (float)i / (float)head_dim);
+        double angle = (double)position * (double)freq;
+        angle = fmod(angle, 2.0 * 3.14159265358979323846);
+        float c = cosf((float)angle), s = sinf((float)angle);
+        float a0 = h[i], a1 = h[i + 1];
+        float p0 = a0 * c, p1 = a1 * s, p2 = a0 * s, p3 = a1 * c;
+        h[i] = p0 - p1;
+        h[i + 1] = p2 + p3;
+    }
+}
+
+void orc_rope(float* q, float* k, int head_dim, int position, float theta,
+              int n_heads, int n_kv_heads) {
+    for (int h = 0; h < n_heads; h++) rope_head(q + (size_t)h * head_dim, head_dim, position, theta);
+    for (int h = 0; h < n_kv_heads; h++) rope_head(k + (size_t)h * head_dim, head_dim, position, theta);
+}
+
+/* absmax int8 with round half away from zero and a +-127 clamp */
+static float kv_quant_row(const float* src, int8_t* dst, int n) {
+    float amax = 0.0f;
+    for (int i = 0; i < n; i++) {
+        float a = src[i] < 0 ? -src[i] : src[i];
+        if (a > amax) amax = a;
+    }
+    float scale = amax / 127.0f;
+    if (amax > 1e-30f) {
+        float inv = 127.0f / amax;
+        for (int i = 0; i < n; i++) {
+            float v = src[i] * inv;
+            if (v > 127.0f) v = 127.0f;
+            if (v < -127.0f) v = -127.0f;
+            float r = v + (v >= 0 ? 0.5f : -0.5f);
+            dst[i] = (int8_t)r;
+        }
+    } else {
+        memset(dst, 0, (size_t)n);
+    }
+    return scale;
+}
+
+void orc_kv_store(int8_t* kc, int8_t* vc, float* ks, float* vs, int max_seq,
+                  int n_kv, int head_dim, int position, const float* k, const float* v) {
+    for (int h = 0; h < n_kv; h++) {
+        size_t row = (size_t)h * max_seq + position;
+        ks[row] = kv_quant_row(k + (size_t)h * head_dim, kc + row * head_dim, head_dim);
+        vs[row] = kv_quant_row(v + (size_t)h * head_dim, vc + row * head_dim, head_dim);
+    }
+}
+
+void orc_attention(const float* q, const int8_t* kc, const int8_t* vc, const float* ks,
+                   const float* vs, int max_seq, int n_heads, int n_kv, int head_dim,
+                   int position, float* out) {
+    int seq = position + 1, groups = n_heads / n_kv;
+    float* scores = (float*)malloc(sizeof(float) * (size_t)seq);
+    float inv_sqrt_d = 1.0f / sqrtf((float)head_dim);
+    for (int h = 0; h < n_heads; h++) {
+        int kvh = h / groups;
+        const float* qh = q + (size_t)h * head_dim;
+        for (int p = 0; p < seq; p++) {
+            size_t row = (size_t)kvh * max_seq + p;
+            const int8_t* kr = kc + row * head_dim;
+            float sc = ks[row], dot = 0.0f;
+            for (int d = 0; d < head_dim; d++) {
+                float kv = (float)kr[d] * sc;
+                float prod = qh[d] * kv;
+                dot = dot + prod;
+            }
+            scores[p] = dot * inv_sqrt_d;
+        }
+        orc_softmax(scores, scores, seq);
+        float* oh = out + (size_t)h * head_dim;
+        for (int d = 0; d < head_dim; d++) oh[d] = 0.0f;
+        for (int p = 0; p < seq; p++) {
+            size_t row = (size_t)kvh * max_seq + p;
+            const int8_t* vr = vc + row * head_dim;
+            float sv = scores[p] * vs[row];
+            for (int d = 0; d < head_dim; d++) {
+                float prod = sv * (float)vr[d];
+                oh[d] = oh[d] + prod;
+            }
+        }
+    }
+    free(scores);
+}
+
+int orc_residual_check(float* res, const float* x, int n) {
+    int bad = -1;
+    for (int i = 0; i < n; i++) res[i] = res[i] + x[i];
+    for (int i = 0; i < n; i++)
+        if (res[i] != res[i] || res[i] > 1e30f || res[i] < -1e30f) { bad = i; break; }
+    return bad;
+}
+
+void orc_embed_row(int qt, const void* table, int bs, int hd, int token, float* out) {
+    if (qt == 7) {   /* QSF_QUANT_FP16: hd halfs per row */
+        const uint8_t* r = (const uint8_t*)table + (size_t)token * hd * 2;
+        for (int i = 0; i < hd; i++) out[i] = orc_fp16_to_fp32(rd_u16(r + 2 * (size_t)i));
+        return;
+    }
+    int dt = dense_type(qt);
+    size_t bb = orc_block_bytes(dt, bs);
+    int nb = (hd + bs - 1) / bs;
+    const uint8_t* bp = (const uint8_t*)table + (size_t)token * nb * bb;
+    for (int b = 0; b < nb; b++, bp += bb) {
+        int count = (b + 1 < nb) ? bs : hd - b * bs;
+        orc_dequant_block(dt, bp, out + (size_t)b * bs, count);
+    }
+}
+

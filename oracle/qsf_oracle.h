@@ -86,6 +86,35 @@ void     orc_moe_token(const orc_expert* experts, int n_exp, int k,
 void     orc_prefill_4bit(const void* w, const uint16_t* x_bf16, float* y,
                           int m, int n, int k, int bs);
 
+/* ---- decode glue around the matvecs (device-resident decode step) ----- */
+/* src/kernels_scalar.c:172-185 (bias ignored, as there) */
+void     orc_rms_norm(const float* in, float* out, const float* w, int dim, float eps);
+/* src/kernels_scalar.c:148-169; b may be NULL */
+void     orc_layer_norm(const float* in, float* out, const float* w, const float* b,
+                        int dim, float eps);
+/* src/kernels_scalar.c:112-118 */
+void     orc_vec_add(const float* a, const float* b, float* o, int n);
+void     orc_vec_mul(const float* a, const float* b, float* o, int n);
+/* apply_rope, src/engine.c:204-235: q [n_heads][head_dim], k [n_kv][head_dim]
+ * rotated in place, pair (i, i+1) by position * theta^(-i/head_dim). */
+void     orc_rope(float* q, float* k, int head_dim, int position, float theta,
+                  int n_heads, int n_kv_heads);
+/* kv_cache_store, src/engine.c:240-300, for one layer: caches
+ * [n_kv][max_seq][head_dim] int8, scales [n_kv][max_seq]; row `position`. */
+void     orc_kv_store(int8_t* kc, int8_t* vc, float* ks, float* vs, int max_seq,
+                      int n_kv, int head_dim, int position, const float* k, const float* v);
+/* The attention loop of src/engine.c:879-923 for one layer over positions
+ * 0..position: out [n_heads][head_dim]. */
+void     orc_attention(const float* q, const int8_t* kc, const int8_t* vc, const float* ks,
+                       const float* vs, int max_seq, int n_heads, int n_kv, int head_dim,
+                       int position, float* out);
+/* Residual add and the NaN/Inf check, src/engine.c:1172-1187: res += x;
+ * returns the first index with NaN or |res| > 1e30, or -1. */
+int      orc_residual_check(float* res, const float* x, int n);
+/* Embedding row dequantisation, src/engine.c:709-765: row `token` of a
+ * [vocab][ceil(hd/bs) blocks] table of type qt (FP16 = 7: hd halfs). */
+void     orc_embed_row(int qt, const void* table, int bs, int hd, int token, float* out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,368 @@
+// decode_glue.hip - the per-layer work around the matvecs of a batch-1
+// decode step, on gfx950, so a device-resident engine needs no host round
+// trip between its projections (src/engine.c:709-1187):
+//   RMS / layer norm          src/kernels_scalar.c:148-185 (engine.c:805-815)
+//   RoPE                      apply_rope, src/engine.c:204-235
+//   int8 KV-cache store       kv_cache_store, src/engine.c:240-300
+//   attention over the cache  src/engine.c:879-923
+//   activation x up           src/engine.c:1128-1140
+//   residual add + NaN check  src/engine.c:1172-1187
+//   embedding row             src/engine.c:709-765
+// Where the reference's result is integer (int8 KV codes) or follows one
+// fixed sequence of fp32 roundings (KV scales, embedding values, the
+// residual add) the kernels use the same operations in the same order with
+// explicitly rounded multiplies and adds, so they match bit for bit; sums
+// the kernels spread over lanes differ only in fp32 rounding order.
+#include "qsf_device.h"
+#include "qsf_hip_internal.h"
+
+namespace {
+
+constexpr int NORM_THREADS = 1024;
+
+// Sum over the workgroup (blockDim.x a multiple of 64, <= 1024); every
+// thread gets the total.  `red` holds one float per wave.
+__device__ __forceinline__ float block_sum(float v, float* red) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    __syncthreads();                       // `red` free from any earlier use
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float t = 0.f;
+    for (int w = 0; w < nw; w++) t += red[w];
+    return t;
+}
+
+// RMS norm (LAYER = false) or layer norm over one vector of `dim` floats,
+// one workgroup.  Output rounding order as src/kernels_scalar.c:148-185:
+// (x * inv) * w, and (x - mean) * inv_std * w + b.
+template <bool LAYER>
+__global__ __launch_bounds__(NORM_THREADS) void norm_kernel(const float* __restrict__ in, float* out,
+                                                            const float* __restrict__ w,
+                                                            const float* __restrict__ b, int dim,
+                                                            float eps) {
+    __shared__ float red[NORM_THREADS / 64];
+    if (!LAYER) {
+        float ss = 0.f;
+        for (int i = threadIdx.x; i < dim; i += blockDim.x) ss = fmaf(in[i], in[i], ss);
+        ss = block_sum(ss, red);
+        const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)dim), eps)));
+        for (int i = threadIdx.x; i < dim; i += blockDim.x) out[i] = __fmul_rn(__fmul_rn(in[i], inv), w[i]);
+    } else {
+        float s = 0.f;
+        for (int i = threadIdx.x; i < dim; i += blockDim.x) s += in[i];
+        const float mean = __fdiv_rn(block_sum(s, red), (float)dim);
+        float v = 0.f;
+        for (int i = threadIdx.x; i < dim; i += blockDim.x) {
+            const float d = in[i] - mean;
+            v = fmaf(d, d, v);
+        }
+        const float var = __fdiv_rn(block_sum(v, red), (float)dim);
+        const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(var, eps)));
+        for (int i = threadIdx.x; i < dim; i += blockDim.x) {
+            float o = __fmul_rn(__fmul_rn(__fsub_rn(in[i], mean), inv), w[i]);
+            if (b) o = __fadd_rn(o, b[i]);
+            out[i] = o;
+        }
+    }
+}
+
+// RoPE: one thread per (head, pair).  freq[j] = 1 / powf(theta, 2j/hd) is
+// computed by the host C library once (qsf_hip_rope_create), so every
+// angle position * freq matches the reference's; the angle is reduced in
+// double as there, then rotated in fp32.
+__global__ __launch_bounds__(256) void rope_kernel(float* q, float* k, const float* __restrict__ freq,
+                                                   int head_dim, int nq_pairs, int nk_pairs,
+                                                   int position) {
+    const int t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= nq_pairs + nk_pairs) return;
+    float* v = t < nq_pairs ? q + 2 * t : k + 2 * (t - nq_pairs);
+    const int j = (t < nq_pairs ? t : t - nq_pairs) % (head_dim / 2);
+    double ang = (double)position * (double)freq[j];
+    ang = fmod(ang, 2.0 * 3.14159265358979323846);
+    const float c = cosf((float)ang), s = sinf((float)ang);
+    const float a0 = v[0], a1 = v[1];
+    v[0] = __fsub_rn(__fmul_rn(a0, c), __fmul_rn(a1, s));
+    v[1] = __fadd_rn(__fmul_rn(a0, s), __fmul_rn(a1, c));
+}
+
+// int8 KV store: one wave per (kv head, K or V).  absmax, scale =
+// amax / 127, codes = trunc(clamp(x * (127 / amax)) +- 0.5) with every
+// operation rounded as in src/engine.c:252-296: bit-exact.
+__global__ __launch_bounds__(64) void kv_store_kernel(int8_t* kc, int8_t* vc, float* ks, float* vs,
+                                                      const float* __restrict__ k,
+                                                      const float* __restrict__ v, int max_seq,
+                                                      int head_dim, int position) {
+    const int h = blockIdx.x >> 1, isv = blockIdx.x & 1, lane = threadIdx.x;
+    const float* src = (isv ? v : k) + (size_t)h * head_dim;
+    const size_t row = (size_t)h * max_seq + position;
+    int8_t* dst = (isv ? vc : kc) + row * head_dim;
+    float amax = 0.f;
+    for (int i = lane; i < head_dim; i += 64) {
+        const float a = src[i] < 0 ? -src[i] : src[i];
+        amax = a > amax ? a : amax;
+    }
+    for (int off = 32; off > 0; off >>= 1) {
+        const float o = __shfl_xor(amax, off, 64);
+        amax = o > amax ? o : amax;
+    }
+    if (lane == 0) (isv ? vs : ks)[row] = __fdiv_rn(amax, 127.0f);
+    if (amax > 1e-30f) {
+        const float inv = __fdiv_rn(127.0f, amax);
+        for (int i = lane; i < head_dim; i += 64) {
+            float x = __fmul_rn(src[i], inv);
+            if (x > 127.0f) x = 127.0f;
+            if (x < -127.0f) x = -127.0f;
+            dst[i] = (int8_t)(int)__fadd_rn(x, x >= 0 ? 0.5f : -0.5f);
+        }
+    } else {
+        for (int i = lane; i < head_dim; i += 64) dst[i] = 0;
+    }
+}
+
+// Attention over positions 0..position, split over positions so a short
+// decode step still fills the chip: workgroup (head, chunk) handles
+// ATT_CHUNK positions and leaves its local max m, its sum l of
+// exp(score - m) and its unnormalised output o[d] = sum exp(score - m) *
+// v_scale * v[d] in the workspace; attention_combine_kernel rescales the
+// chunks to the global max and normalises.  This is the reference's
+// softmax(q . k * scale / sqrt(hd)) . v (src/engine.c:879-923), regrouped:
+// the fp32 sums run in a different order.
+constexpr int ATT_THREADS = 256;
+constexpr int ATT_CHUNK = 128;
+constexpr int ATT_MAX_SEQ = QK_ATT_MAX_SEQ;
+typedef uint32_t att_u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float sbyte(uint32_t w, int i) {
+    return (float)(int8_t)(uint8_t)(w >> (8 * i));
+}
+
+__global__ __launch_bounds__(ATT_THREADS) void attention_part_kernel(
+    const float* __restrict__ q, const int8_t* __restrict__ kc, const int8_t* __restrict__ vc,
+    const float* __restrict__ ks, const float* __restrict__ vs, int max_seq, int groups,
+    int head_dim, int seq, int nsplit, float* __restrict__ ws) {
+    __shared__ float qs[256];
+    __shared__ float ew[ATT_CHUNK];                      // exp(score - m) * v_scale per position
+    __shared__ float parts[ATT_THREADS];
+    __shared__ float red[ATT_THREADS / 64];
+    const int h = blockIdx.x, chunk = blockIdx.y, kvh = h / groups, t = threadIdx.x;
+    const int p0 = chunk * ATT_CHUNK, np = min(ATT_CHUNK, seq - p0);
+    for (int d = t; d < head_dim; d += ATT_THREADS) qs[d] = q[(size_t)h * head_dim + d];
+    __syncthreads();
+    // scores: one thread per position; the row's int8 codes 16 at a time
+    const float inv_sqrt_d = __fdiv_rn(1.0f, __fsqrt_rn((float)head_dim));
+    float sc = -INFINITY;
+    if (t < np) {
+        const size_t row = (size_t)kvh * max_seq + p0 + t;
+        const att_u32x4* kr = reinterpret_cast<const att_u32x4*>(kc + row * head_dim);
+        const float kscale = ks[row];
+        float dot = 0.f;
+        for (int c = 0; c < head_dim / 16; c++) {
+            const att_u32x4 w = kr[c];
+#pragma unroll
+            for (int j = 0; j < 16; j++)
+                dot = fmaf(qs[16 * c + j], __fmul_rn(sbyte(w[j >> 2], j & 3), kscale), dot);
+        }
+        sc = __fmul_rn(dot, inv_sqrt_d);
+    }
+    float m = sc;
+    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+    if ((t & 63) == 0) red[t >> 6] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    const float e = t < np ? expf(sc - m) : 0.f;
+    if (t < np) ew[t] = __fmul_rn(e, vs[(size_t)kvh * max_seq + p0 + t]);
+    const float l = block_sum(e, red);                   // also orders the ew writes
+    // weighted V: thread (d, part) over positions part, part + P, ...
+    const int P = ATT_THREADS / head_dim, d = t % head_dim, part = t / head_dim;
+    float acc = 0.f;
+    if (part < P) {
+        const int8_t* vr = vc + ((size_t)kvh * max_seq + p0) * head_dim + d;
+        for (int p = part; p < np; p += P) acc = fmaf(ew[p], (float)vr[(size_t)p * head_dim], acc);
+    }
+    parts[t] = acc;
+    __syncthreads();
+    float* rec = ws + ((size_t)h * nsplit + chunk) * (head_dim + 2);
+    if (t < head_dim) {
+        float o = 0.f;
+        for (int i = 0; i < P; i++) o += parts[i * head_dim + t];
+        rec[2 + t] = o;
+    }
+    if (t == 0) {
+        rec[0] = m;
+        rec[1] = l;
+    }
+}
+
+__global__ __launch_bounds__(256) void attention_combine_kernel(const float* __restrict__ ws,
+                                                                int head_dim, int nsplit,
+                                                                float* __restrict__ out) {
+    const int h = blockIdx.x, d = threadIdx.x;
+    if (d >= head_dim) return;
+    const float* base = ws + (size_t)h * nsplit * (head_dim + 2);
+    float M = -INFINITY;
+    for (int c = 0; c < nsplit; c++) M = fmaxf(M, base[(size_t)c * (head_dim + 2)]);
+    float L = 0.f, O = 0.f;
+    for (int c = 0; c < nsplit; c++) {
+        const float* rec = base + (size_t)c * (head_dim + 2);
+        const float f = expf(rec[0] - M);
+        L = fmaf(f, rec[1], L);
+        O = fmaf(f, rec[2 + d], O);
+    }
+    out[(size_t)h * head_dim + d] = __fdiv_rn(O, L);
+}
+
+// gate = act(gate) * up (QSFActivation: 2 SiLU, 0/1 GELU tanh form, else
+// ReLU), src/kernels_scalar.c:129-147 and src/engine.c:1128-1140.
+__global__ __launch_bounds__(256) void act_mul_kernel(float* gate, const float* __restrict__ up,
+                                                      int n, int act) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    float x = gate[i];
+    if (act == 2) {
+        x = __fdiv_rn(x, __fadd_rn(1.0f, expf(-x)));
+    } else if (act == 0 || act == 1) {
+        const float inner = __fmul_rn(0.7978845608f, __fadd_rn(x, __fmul_rn(__fmul_rn(__fmul_rn(0.044715f, x), x), x)));
+        x = __fmul_rn(__fmul_rn(0.5f, x), __fadd_rn(1.0f, tanhf(inner)));
+    } else if (x < 0.0f) {
+        x = 0.0f;
+    }
+    gate[i] = __fmul_rn(x, up[i]);
+}
+
+// res += x, then the first index whose value is NaN or beyond +-1e30 (or
+// -1) into *bad when bad is given.  One workgroup: the minimum is reduced
+// in LDS, so nothing has to be cleared before the launch.
+__global__ __launch_bounds__(1024) void residual_kernel(float* res, const float* __restrict__ x, int n,
+                                                        int* bad) {
+    __shared__ int red[1024 / 64];
+    int first = n;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        const float r = __fadd_rn(res[i], x[i]);
+        res[i] = r;
+        if ((r != r || r > 1e30f || r < -1e30f) && i < first) first = i;
+    }
+    if (!bad) return;
+    for (int off = 32; off > 0; off >>= 1) first = min(first, __shfl_xor(first, off, 64));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = first;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int f = n;
+        for (int w = 0; w < (int)(blockDim.x >> 6); w++) f = min(f, red[w]);
+        *bad = f < n ? f : -1;
+    }
+}
+
+// One row of a blockwise table: value i = scale * q + zero (4-bit sym:
+// scale * q), each product and sum rounded as in src/quant.c:95-177.
+__device__ __forceinline__ unsigned code_of(int fmt, const uint8_t* packed, int i) {
+    if (fmt == QK_FMT_2) return (packed[i >> 2] >> ((i & 3) * 2)) & 3u;
+    if (fmt == QK_FMT_3) {
+        const int bit = 3 * i, byte = bit >> 3, off = bit & 7;
+        unsigned v = packed[byte] >> off;
+        if (off > 5) v |= (unsigned)packed[byte + 1] << (8 - off);
+        return v & 7u;
+    }
+    return (packed[i >> 1] >> ((i & 1) * 4)) & 15u;
+}
+
+__global__ __launch_bounds__(256) void embed_row_kernel(const uint8_t* __restrict__ blocks, int fmt,
+                                                        int bs, int bb, int hd, float* out) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= hd) return;
+    const uint8_t* blk = blocks + (size_t)(i / bs) * bb;
+    const uint32_t meta = (uint32_t)blk[0] | ((uint32_t)blk[1] << 8) | ((uint32_t)blk[2] << 16) |
+                          ((uint32_t)blk[3] << 24);
+    const unsigned c = code_of(fmt, blk + 4, i % bs);
+    const float s = qsf::f16_lo(meta);
+    if (fmt == QK_FMT_4SYM) {
+        out[i] = __fmul_rn(s, (float)(c >= 8u ? (int)c - 16 : (int)c));
+    } else {
+        out[i] = __fadd_rn(__fmul_rn(s, (float)c), qsf::f16_hi(meta));
+    }
+}
+
+__global__ __launch_bounds__(256) void embed_row_fp16_kernel(const uint16_t* __restrict__ row, int hd,
+                                                             float* out) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < hd) out[i] = qsf::f16_bits(row[i]);
+}
+
+}  // namespace
+
+extern "C" int qk_norm(const float* in, float* out, const float* w, const float* b, int dim,
+                       float eps, int layer, hipStream_t s) {
+    if (dim <= 0) return 0;
+    if (layer)
+        hipLaunchKernelGGL(norm_kernel<true>, dim3(1), dim3(NORM_THREADS), 0, s, in, out, w, b, dim, eps);
+    else
+        hipLaunchKernelGGL(norm_kernel<false>, dim3(1), dim3(NORM_THREADS), 0, s, in, out, w, b, dim, eps);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+extern "C" int qk_rope(float* q, float* k, const float* freq, int head_dim, int n_heads,
+                       int n_kv, int position, hipStream_t s) {
+    const int nq = n_heads * head_dim / 2, nk = n_kv * head_dim / 2;
+    if (nq + nk == 0) return 0;
+    hipLaunchKernelGGL(rope_kernel, dim3((nq + nk + 255) / 256), dim3(256), 0, s, q, k, freq, head_dim,
+                       nq, nk, position);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+extern "C" int qk_kv_store(int8_t* kc, int8_t* vc, float* ks, float* vs, int max_seq, int n_kv,
+                           int head_dim, int position, const float* k, const float* v,
+                           hipStream_t s) {
+    if (n_kv <= 0) return 0;
+    hipLaunchKernelGGL(kv_store_kernel, dim3(2 * n_kv), dim3(64), 0, s, kc, vc, ks, vs, k, v, max_seq,
+                       head_dim, position);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+extern "C" size_t qk_attention_ws_bytes(int n_heads, int head_dim, int position) {
+    const int nsplit = (position + 1 + ATT_CHUNK - 1) / ATT_CHUNK;
+    return sizeof(float) * (size_t)n_heads * nsplit * (head_dim + 2);
+}
+
+extern "C" int qk_attention(const float* q, const int8_t* kc, const int8_t* vc, const float* ks,
+                            const float* vs, int max_seq, int n_heads, int n_kv, int head_dim,
+                            int position, float* out, void* ws, hipStream_t s) {
+    const int seq = position + 1;
+    if (head_dim > ATT_THREADS || head_dim % 16 || seq > ATT_MAX_SEQ || n_kv <= 0 ||
+        n_heads % n_kv)
+        return -2;
+    const int nsplit = (seq + ATT_CHUNK - 1) / ATT_CHUNK;
+    hipLaunchKernelGGL(attention_part_kernel, dim3(n_heads, nsplit), dim3(ATT_THREADS), 0, s, q, kc, vc,
+                       ks, vs, max_seq, n_heads / n_kv, head_dim, seq, nsplit, (float*)ws);
+    hipLaunchKernelGGL(attention_combine_kernel, dim3(n_heads), dim3(256), 0, s, (const float*)ws,
+                       head_dim, nsplit, out);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+extern "C" int qk_act_mul(float* gate, const float* up, int n, int act, hipStream_t s) {
+    if (n <= 0) return 0;
+    hipLaunchKernelGGL(act_mul_kernel, dim3((n + 255) / 256), dim3(256), 0, s, gate, up, n, act);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+extern "C" int qk_residual(float* res, const float* x, int n, int* bad, hipStream_t s) {
+    if (n <= 0) return 0;
+    hipLaunchKernelGGL(residual_kernel, dim3(1), dim3(1024), 0, s, res, x, n, bad);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+extern "C" int qk_embed_row(const qsf_hip_tensor* t, int token, float* out, hipStream_t s) {
+    if (t->fmt < 0 || token < 0 || token >= t->rows) return -2;
+    if (t->cols <= 0) return 0;
+    const uint8_t* row = t->d_blocks + (size_t)token * t->nb * t->block_bytes;
+    hipLaunchKernelGGL(embed_row_kernel, dim3((t->cols + 255) / 256), dim3(256), 0, s, row, t->fmt, t->bs,
+                       t->block_bytes, t->cols, out);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+extern "C" int qk_embed_row_fp16(const uint16_t* table, int hd, int token, float* out,
+                                 hipStream_t s) {
+    if (hd <= 0) return 0;
+    hipLaunchKernelGGL(embed_row_fp16_kernel, dim3((hd + 255) / 256), dim3(256), 0, s,
+                       table + (size_t)token * hd, hd, out);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}

@@ -109,6 +109,29 @@ int qk_prefill_4bit_noalloc(const qsf_hip_tensor* t, const uint16_t* d_x_bf16, i
 int qk_prefill_4bit(const qsf_hip_tensor* t, const uint16_t* d_x_bf16, int m,
                     float* d_y, void* d_ws, hipStream_t s);
 
+/* Decode glue (decode_glue.hip), all asynchronous on `s`.  Layouts: q
+ * [n_heads][head_dim], k/v [n_kv][head_dim]; one layer's KV cache
+ * [n_kv][max_seq][head_dim] int8 with scales [n_kv][max_seq].  freq is the
+ * head_dim/2 RoPE frequency table.  qk_attention returns -2 for a head_dim
+ * above 256 or not a multiple of 16, more than QK_ATT_MAX_SEQ positions
+ * or n_heads not a multiple
+ * of n_kv; ws holds qk_attention_ws_bytes of per-chunk partial results. */
+#define QK_ATT_MAX_SEQ 16384
+int qk_norm(const float* in, float* out, const float* w, const float* b, int dim, float eps,
+            int layer, hipStream_t s);
+int qk_rope(float* q, float* k, const float* freq, int head_dim, int n_heads, int n_kv,
+            int position, hipStream_t s);
+int qk_kv_store(int8_t* kc, int8_t* vc, float* ks, float* vs, int max_seq, int n_kv,
+                int head_dim, int position, const float* k, const float* v, hipStream_t s);
+size_t qk_attention_ws_bytes(int n_heads, int head_dim, int position);
+int qk_attention(const float* q, const int8_t* kc, const int8_t* vc, const float* ks,
+                 const float* vs, int max_seq, int n_heads, int n_kv, int head_dim,
+                 int position, float* out, void* ws, hipStream_t s);
+int qk_act_mul(float* gate, const float* up, int n, int act, hipStream_t s);
+int qk_residual(float* res, const float* x, int n, int* bad, hipStream_t s);
+int qk_embed_row(const qsf_hip_tensor* t, int token, float* out, hipStream_t s);
+int qk_embed_row_fp16(const uint16_t* table, int hd, int token, float* out, hipStream_t s);
+
 #ifdef __cplusplus
 }
 #endif

@@ -47,7 +47,8 @@ const char* qsf_hip_last_error_detail(void) { return g_err_detail; }
 typedef struct {
     int ready, device;
     hipStream_t stream;
-    void* ws;          size_t ws_bytes;       /* x-prep / MoE workspace */
+    void* ws;          size_t ws_bytes;       /* prefill workspace */
+    void* att_ws;      size_t att_ws_bytes;   /* attention partials */
     float* d_x;        size_t d_x_n;          /* staging for host-pointer calls */
     float* d_y;        size_t d_y_n;
     float* h_x;        size_t h_x_n;          /* pinned host staging */
@@ -462,6 +463,7 @@ void qsf_hip_shutdown(void) {
     if (g_dev.ready) {
         hipStreamSynchronize(g_dev.stream);
         if (g_dev.ws) hipFree(g_dev.ws);
+        if (g_dev.att_ws) hipFree(g_dev.att_ws);
         if (g_dev.d_x) hipFree(g_dev.d_x);
         if (g_dev.d_y) hipFree(g_dev.d_y);
         if (g_dev.h_x) hipHostFree(g_dev.h_x);
@@ -629,6 +631,133 @@ int qsf_hip_kernel_timing_read(float* us, int max) {
     int n = qk_timing_read(us, max);
     pthread_mutex_unlock(&g_lock);
     return n < 0 ? -fail(E_INTERNAL, "qsf_hip_kernel_timing_read: event query failed") : n;
+}
+
+/* ---- device-resident decode glue (src/engine.c:709-1187) ------------------ */
+static int glue_rc(const char* who, int r) {
+    if (r == 0) return E_OK;
+    return fail(r == -2 ? E_INVALID : E_INTERNAL, "%s: %s", who,
+                r == -2 ? "unsupported shape" : "launch failed");
+}
+
+int qsf_hip_rms_norm_dev(const float* d_in, float* d_out, const float* d_w, int dim, float eps,
+                         void* stream) {
+    if (dim < 0 || (dim > 0 && (!d_in || !d_out || !d_w)))
+        return fail(E_INVALID, "qsf_hip_rms_norm_dev: bad arguments");
+    return glue_rc("qsf_hip_rms_norm_dev", qk_norm(d_in, d_out, d_w, NULL, dim, eps, 0, pick_stream(stream)));
+}
+
+int qsf_hip_layer_norm_dev(const float* d_in, float* d_out, const float* d_w, const float* d_b,
+                           int dim, float eps, void* stream) {
+    if (dim < 0 || (dim > 0 && (!d_in || !d_out || !d_w)))
+        return fail(E_INVALID, "qsf_hip_layer_norm_dev: bad arguments");
+    return glue_rc("qsf_hip_layer_norm_dev", qk_norm(d_in, d_out, d_w, d_b, dim, eps, 1, pick_stream(stream)));
+}
+
+struct qsf_hip_rope {
+    int head_dim;
+    float* d_freq;     /* head_dim/2 frequencies */
+};
+
+qsf_hip_rope* qsf_hip_rope_create(int head_dim, float theta) {
+    if (head_dim <= 0 || head_dim % 2) {
+        fail(E_INVALID, "qsf_hip_rope_create: head_dim %d must be even and positive", head_dim);
+        return NULL;
+    }
+    if (theta <= 0) theta = 10000.0f;          /* src/engine.c:873 */
+    int n = head_dim / 2;
+    float* f = malloc(sizeof(float) * (size_t)n);
+    qsf_hip_rope* r = calloc(1, sizeof *r);
+    if (!f || !r) {
+        free(f); free(r);
+        fail(E_OOM, "qsf_hip_rope_create");
+        return NULL;
+    }
+    /* the reference's frequency, by the host C library (src/engine.c:210) */
+    for (int j = 0; j < n; j++) f[j] = 1.0f / powf(theta, (float)(2 * j) / (float)head_dim);
+    r->head_dim = head_dim;
+    if (hipMalloc((void**)&r->d_freq, sizeof(float) * (size_t)n) != hipSuccess ||
+        hipMemcpy(r->d_freq, f, sizeof(float) * (size_t)n, hipMemcpyHostToDevice) != hipSuccess) {
+        if (r->d_freq) hipFree(r->d_freq);
+        free(f); free(r);
+        fail(E_OOM, "qsf_hip_rope_create: device table");
+        return NULL;
+    }
+    free(f);
+    return r;
+}
+
+void qsf_hip_rope_free(qsf_hip_rope* r) {
+    if (!r) return;
+    hipFree(r->d_freq);
+    free(r);
+}
+
+int qsf_hip_rope_dev(const qsf_hip_rope* r, float* d_q, float* d_k, int n_heads, int n_kv_heads,
+                     int position, void* stream) {
+    if (!r || n_heads < 0 || n_kv_heads < 0 || position < 0 ||
+        (n_heads > 0 && !d_q) || (n_kv_heads > 0 && !d_k))
+        return fail(E_INVALID, "qsf_hip_rope_dev: bad arguments");
+    return glue_rc("qsf_hip_rope_dev", qk_rope(d_q, d_k, r->d_freq, r->head_dim, n_heads, n_kv_heads,
+                                               position, pick_stream(stream)));
+}
+
+int qsf_hip_kv_store_dev(int8_t* d_kc, int8_t* d_vc, float* d_ks, float* d_vs, int max_seq,
+                         int n_kv_heads, int head_dim, int position, const float* d_k,
+                         const float* d_v, void* stream) {
+    if (!d_kc || !d_vc || !d_ks || !d_vs || !d_k || !d_v || n_kv_heads < 0 || head_dim <= 0 ||
+        position < 0 || position >= max_seq)
+        return fail(E_INVALID, "qsf_hip_kv_store_dev: bad arguments (position %d of %d)",
+                    position, max_seq);
+    return glue_rc("qsf_hip_kv_store_dev", qk_kv_store(d_kc, d_vc, d_ks, d_vs, max_seq, n_kv_heads,
+                                                       head_dim, position, d_k, d_v,
+                                                       pick_stream(stream)));
+}
+
+int qsf_hip_attention_dev(const float* d_q, const int8_t* d_kc, const int8_t* d_vc,
+                          const float* d_ks, const float* d_vs, int max_seq, int n_heads,
+                          int n_kv_heads, int head_dim, int position, float* d_out,
+                          void* stream) {
+    if (!d_q || !d_kc || !d_vc || !d_ks || !d_vs || !d_out || n_heads <= 0 || n_kv_heads <= 0 ||
+        head_dim <= 0 || position < 0 || position >= max_seq)
+        return fail(E_INVALID, "qsf_hip_attention_dev: bad arguments");
+    pthread_mutex_lock(&g_lock);
+    int rc = g_dev.ready ? E_OK : fail(E_INVALID, "qsf_hip: not initialised");
+    if (rc == E_OK)
+        rc = ensure_dev(&g_dev.att_ws, &g_dev.att_ws_bytes,
+                        qk_attention_ws_bytes(n_heads, head_dim, position));
+    if (rc == E_OK)
+        rc = glue_rc("qsf_hip_attention_dev",
+                     qk_attention(d_q, d_kc, d_vc, d_ks, d_vs, max_seq, n_heads, n_kv_heads, head_dim,
+                                  position, d_out, g_dev.att_ws, pick_stream(stream)));
+    pthread_mutex_unlock(&g_lock);
+    return rc;
+}
+
+int qsf_hip_act_mul_dev(float* d_gate, const float* d_up, int n, int activation, void* stream) {
+    if (n < 0 || (n > 0 && (!d_gate || !d_up)))
+        return fail(E_INVALID, "qsf_hip_act_mul_dev: bad arguments");
+    return glue_rc("qsf_hip_act_mul_dev", qk_act_mul(d_gate, d_up, n, activation, pick_stream(stream)));
+}
+
+int qsf_hip_residual_dev(float* d_res, const float* d_x, int n, int* d_bad, void* stream) {
+    if (n < 0 || (n > 0 && (!d_res || !d_x)))
+        return fail(E_INVALID, "qsf_hip_residual_dev: bad arguments");
+    return glue_rc("qsf_hip_residual_dev", qk_residual(d_res, d_x, n, d_bad, pick_stream(stream)));
+}
+
+int qsf_hip_embed_row_dev(const qsf_hip_tensor* t, int token, float* d_out, void* stream) {
+    if (!t || !d_out || t->fmt < 0 || token < 0 || token >= t->rows)
+        return fail(E_INVALID, "qsf_hip_embed_row_dev: bad arguments (token %d)", token);
+    return glue_rc("qsf_hip_embed_row_dev", qk_embed_row(t, token, d_out, pick_stream(stream)));
+}
+
+int qsf_hip_embed_row_fp16_dev(const uint16_t* d_table, int hd, int token, float* d_out,
+                               void* stream) {
+    if (!d_table || !d_out || hd < 0 || token < 0)
+        return fail(E_INVALID, "qsf_hip_embed_row_fp16_dev: bad arguments");
+    return glue_rc("qsf_hip_embed_row_fp16_dev",
+                   qk_embed_row_fp16(d_table, hd, token, d_out, pick_stream(stream)));
 }
 
 /* ---- MoE ------------------------------------------------------------------- */

@@ -35,6 +35,9 @@ EXPORTS = (
     "qsf_hip_moe_create", "qsf_hip_moe_free", "qsf_hip_moe_forward_dev",
     "qsf_hip_unpack_dev", "qsf_hip_kernel_timing", "qsf_hip_kernel_timing_read",
     "qsf_hip_prefill_4bit_dev", "qsf_hip_prefill_4bit_dev_noalloc",
+    "qsf_hip_rms_norm_dev", "qsf_hip_layer_norm_dev", "qsf_hip_rope_create", "qsf_hip_rope_free",
+    "qsf_hip_rope_dev", "qsf_hip_kv_store_dev", "qsf_hip_attention_dev", "qsf_hip_act_mul_dev",
+    "qsf_hip_residual_dev", "qsf_hip_embed_row_dev", "qsf_hip_embed_row_fp16_dev",
 )
 
 _lib = None
@@ -98,6 +101,23 @@ def load(path: str = LIB_PATH) -> C.CDLL:
     L.qsf_hip_prefill_4bit_dev.restype = _i
     L.qsf_hip_prefill_4bit_dev_noalloc.argtypes = [_vp, _vp, _i, _vp, _vp]
     L.qsf_hip_prefill_4bit_dev_noalloc.restype = _i
+    _f = C.c_float
+    L.qsf_hip_rms_norm_dev.argtypes = [_vp, _vp, _vp, _i, _f, _vp]
+    L.qsf_hip_layer_norm_dev.argtypes = [_vp, _vp, _vp, _vp, _i, _f, _vp]
+    L.qsf_hip_rope_create.argtypes = [_i, _f]
+    L.qsf_hip_rope_create.restype = _vp
+    L.qsf_hip_rope_free.argtypes = [_vp]
+    L.qsf_hip_rope_dev.argtypes = [_vp, _vp, _vp, _i, _i, _i, _vp]
+    L.qsf_hip_kv_store_dev.argtypes = [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _vp, _vp]
+    L.qsf_hip_attention_dev.argtypes = [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp, _vp]
+    L.qsf_hip_act_mul_dev.argtypes = [_vp, _vp, _i, _i, _vp]
+    L.qsf_hip_residual_dev.argtypes = [_vp, _vp, _i, _vp, _vp]
+    L.qsf_hip_embed_row_dev.argtypes = [_vp, _i, _vp, _vp]
+    L.qsf_hip_embed_row_fp16_dev.argtypes = [_vp, _i, _i, _vp, _vp]
+    for n in ("qsf_hip_rms_norm_dev", "qsf_hip_layer_norm_dev", "qsf_hip_rope_dev",
+              "qsf_hip_kv_store_dev", "qsf_hip_attention_dev", "qsf_hip_act_mul_dev",
+              "qsf_hip_residual_dev", "qsf_hip_embed_row_dev", "qsf_hip_embed_row_fp16_dev"):
+        getattr(L, n).restype = _i
     L.qsf_hip_kernel_timing.argtypes = [_i]
     L.qsf_hip_kernel_timing.restype = _i
     L.qsf_hip_kernel_timing_read.argtypes = [C.POINTER(C.c_float), _i]
@@ -276,3 +296,67 @@ class Moe:
         if self.handle:
             load().qsf_hip_moe_free(self.handle)
             self.handle = None
+
+
+# ---- device-resident decode glue (src/engine.c:709-1187) --------------------
+def rms_norm(x, out, w, eps, stream=None) -> None:
+    _check(load().qsf_hip_rms_norm_dev(_addr(x), _addr(out), _addr(w), x.numel(), eps,
+                                       _stream(stream)), "qsf_hip_rms_norm_dev")
+
+
+def layer_norm(x, out, w, b, eps, stream=None) -> None:
+    _check(load().qsf_hip_layer_norm_dev(_addr(x), _addr(out), _addr(w), _addr(b), x.numel(), eps,
+                                         _stream(stream)), "qsf_hip_layer_norm_dev")
+
+
+class Rope:
+    """RoPE frequency table on the device (qsf_hip_rope_create)."""
+
+    def __init__(self, head_dim: int, theta: float):
+        self.head_dim = head_dim
+        self.handle = load().qsf_hip_rope_create(head_dim, theta)
+        if not self.handle:
+            _check(-1, "qsf_hip_rope_create")
+
+    def apply(self, q, k, n_heads, n_kv, position, stream=None) -> None:
+        _check(load().qsf_hip_rope_dev(self.handle, _addr(q), _addr(k), n_heads, n_kv, position,
+                                       _stream(stream)), "qsf_hip_rope_dev")
+
+    def free(self) -> None:
+        if self.handle:
+            load().qsf_hip_rope_free(self.handle)
+            self.handle = None
+
+
+def kv_store(kc, vc, ks, vs, max_seq, n_kv, head_dim, position, k, v, stream=None) -> None:
+    _check(load().qsf_hip_kv_store_dev(_addr(kc), _addr(vc), _addr(ks), _addr(vs), max_seq, n_kv,
+                                       head_dim, position, _addr(k), _addr(v), _stream(stream)),
+           "qsf_hip_kv_store_dev")
+
+
+def attention(q, kc, vc, ks, vs, max_seq, n_heads, n_kv, head_dim, position, out,
+              stream=None) -> None:
+    _check(load().qsf_hip_attention_dev(_addr(q), _addr(kc), _addr(vc), _addr(ks), _addr(vs),
+                                        max_seq, n_heads, n_kv, head_dim, position, _addr(out),
+                                        _stream(stream)), "qsf_hip_attention_dev")
+
+
+def act_mul(gate, up, activation, stream=None) -> None:
+    _check(load().qsf_hip_act_mul_dev(_addr(gate), _addr(up), gate.numel(), activation,
+                                      _stream(stream)), "qsf_hip_act_mul_dev")
+
+
+def residual(res, x, bad=None, stream=None) -> None:
+    _check(load().qsf_hip_residual_dev(_addr(res), _addr(x), res.numel(), _addr(bad),
+                                       _stream(stream)), "qsf_hip_residual_dev")
+
+
+def embed_row(table: "Tensor", token: int, out, stream=None) -> None:
+    _check(load().qsf_hip_embed_row_dev(table.handle, token, _addr(out), _stream(stream)),
+           "qsf_hip_embed_row_dev")
+
+
+def embed_row_fp16(d_table, hd: int, token: int, out, stream=None) -> None:
+    _check(load().qsf_hip_embed_row_fp16_dev(_addr(d_table), hd, token, _addr(out),
+                                             _stream(stream)), "qsf_hip_embed_row_fp16_dev")
+

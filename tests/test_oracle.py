@@ -303,3 +303,22 @@ def test_prefill_oracle_is_token_loop(oracle, m, n, k, bs):
     for t in range(m):
         xf = (xb[t].astype(np.uint32) << 16).view(np.float32)
         assert np.array_equal(y[t], oracle.matvec(F.Q4, p, xf, n, k, bs))
+
+
+def test_e2m1_encoder_matches_brute_force():
+    """qsf_format's threshold E2M1 encoder equals nearest-value rounding with
+    ties to the even code, saturating at 6 (OCP MX v1.0), on random values,
+    every rounding boundary and its neighbours, and specials."""
+    rng = np.random.default_rng(17)
+    edges = np.array([0.25, 0.75, 1.25, 1.75, 2.5, 3.5, 5.0], np.float32)
+    v = np.concatenate([rng.standard_normal(20000).astype(np.float32) * 3, edges, -edges,
+                        np.nextafter(edges, np.float32(0)), np.nextafter(edges, np.float32(10)),
+                        np.float32([0.0, -0.0, 6.0, 7.0, 100.0, -100.0, np.inf, -np.inf])])
+    mags = F.E2M1_MAG.astype(np.float64)
+    mag = np.minimum(np.abs(v.astype(np.float64)), 6.0)
+    d = np.abs(mags[None, :] - mag[:, None])
+    best = d == d.min(axis=1, keepdims=True)
+    even = best & (np.arange(8)[None, :] % 2 == 0)
+    idx = np.where(even.any(axis=1), even.argmax(axis=1), best.argmax(axis=1)).astype(np.uint8)
+    want = idx | ((np.signbit(v) & (idx != 0)).astype(np.uint8) << 3)
+    assert np.array_equal(F._e2m1_encode(v), want)
