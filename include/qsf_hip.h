@@ -126,6 +126,49 @@ int qsf_hip_matvec_group_prepared_dev(const qsf_hip_tensor* const* t, int n,
 int qsf_hip_kernel_timing(int enable);
 int qsf_hip_kernel_timing_read(float* us, int max);
 
+/* ---- QSF model file -> device arena (src/format.c:11-284, engine.c:183-202) */
+/* qsf_crc32 of src/format.c:11-34 (ISO 3309 CRC-32). */
+uint32_t qsf_hip_crc32(const void* data, size_t len);
+
+typedef struct qsf_hip_model qsf_hip_model;   /* opaque */
+/* Header fields (include/qsf/types.h:185-245, zero defaults resolved as
+ * src/format.c:37-99 and 137-160 do) and what the load found. */
+typedef struct {
+    uint32_t num_layers, hidden_dim, num_heads, num_kv_heads, vocab_size, max_seq_len,
+             intermediate_dim, head_dim, block_size;
+    uint32_t quant_type, activation, norm_type, pos_enc_type, ffn_type, attn_type;
+    uint32_t has_bias, weight_tied, num_experts, num_active_experts, expert_intermediate_dim;
+    float    rope_theta, norm_epsilon;
+    uint32_t num_tensors;        /* tensor records in all layers */
+    uint32_t has_embedding;
+    uint32_t crc_mismatches;     /* header, layers, embedding, final section */
+    uint32_t size_mismatch;      /* total_file_size differs from the file */
+    size_t   device_bytes;       /* bytes uploaded to HBM */
+} qsf_hip_model_info;
+/* Load an uncompressed QSF file: validate the header (src/format.c:37-99),
+ * check every CRC (a mismatch is counted and warned about, as the
+ * reference only warns, src/format.c:129-135, 226-233), walk each layer's
+ * tensor records (src/engine.c:183-202) and upload every matrix to HBM and
+ * every FP16 vector (norms, biases) as fp32, plus the embedding table and
+ * the final norm / output head (src/engine.c:403-420, 664-679).  The file
+ * is fully checked before any device work.  NULL on error
+ * (qsf_hip_last_error: 1 not found, 2 corrupted, 3 version, 6 invalid
+ * model, 15 LZ4-compressed layers, which this build does not read). */
+qsf_hip_model* qsf_hip_model_load(const char* path);
+void qsf_hip_model_free(qsf_hip_model* m);
+int qsf_hip_model_get_info(const qsf_hip_model* m, qsf_hip_model_info* out);
+/* Matrix (tensor_type of include/qsf/types.h:118-162) of a layer, or NULL. */
+const qsf_hip_tensor* qsf_hip_model_tensor(const qsf_hip_model* m, int layer, int tensor_type);
+/* FP16 vector tensor of a layer as device fp32 (*n elements), or NULL. */
+const float* qsf_hip_model_vector(const qsf_hip_model* m, int layer, int tensor_type, int* n);
+/* Embedding table: blockwise (for qsf_hip_embed_row_dev), or FP16. */
+const qsf_hip_tensor* qsf_hip_model_embedding(const qsf_hip_model* m);
+const uint16_t* qsf_hip_model_embedding_fp16(const qsf_hip_model* m);
+/* Output head for the logits matvec: the embedding table when tied. */
+const qsf_hip_tensor* qsf_hip_model_output_head(const qsf_hip_model* m);
+/* Final norm weight (and bias, NULL when absent) as device fp32. */
+const float* qsf_hip_model_final_norm(const qsf_hip_model* m, const float** bias);
+
 /* ---- MoE FFN with MXFP4 experts (src/engine.c:951-1107) ------------------ */
 typedef struct qsf_hip_moe qsf_hip_moe;         /* opaque device expert table */
 /* gate/up: [expert_dim][hidden], down: [hidden][expert_dim], all MXFP4

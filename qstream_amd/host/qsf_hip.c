@@ -12,6 +12,7 @@
  * additively with out-of-range rows skipped (src/quant.c:423-444).
  */
 #include "qsf_hip.h"
+#include "qsf_host.h"
 #include "../csrc/qsf_hip_internal.h"
 
 #include <math.h>
@@ -31,6 +32,16 @@ static _Thread_local int g_err;
 static _Thread_local char g_err_detail[256];
 
 static int fail(int code, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err_detail, sizeof g_err_detail, fmt, ap);
+    va_end(ap);
+    g_err = code;
+    if (qsf_set_error) qsf_set_error(code, g_err_detail);
+    return code;
+}
+
+int qsf_host_fail(int code, const char* fmt, ...) {
     va_list ap;
     va_start(ap, fmt);
     vsnprintf(g_err_detail, sizeof g_err_detail, fmt, ap);
@@ -424,6 +435,58 @@ qsf_hip_tensor* qsf_hip_tensor_upload(const void* host, int qt, int rows, int co
     }
     pthread_mutex_unlock(&g_lock);
     return t;
+}
+
+qsf_hip_tensor* qsf_host_upload_owned(const void* host, int qt, int rows, int cols, int bs) {
+    pthread_mutex_lock(&g_lock);
+    qsf_hip_tensor* t = upload_locked(host, qt, rows, cols, bs);
+    pthread_mutex_unlock(&g_lock);
+    return t;
+}
+
+void* qsf_host_device_bytes(const void* host, size_t n) {
+    pthread_mutex_lock(&g_lock);
+    void* d = NULL;
+    int rc = init_locked(g_dev.ready ? g_dev.device : 0);
+    if (!rc && hipMalloc(&d, n ? n : 1) != hipSuccess) {
+        fail(E_OOM, "qsf_hip: device buffer of %zu bytes", n);
+        d = NULL;
+    }
+    if (d && n && hipMemcpy(d, host, n, hipMemcpyHostToDevice) != hipSuccess) {
+        hipFree(d);
+        d = NULL;
+        fail(E_INTERNAL, "qsf_hip: device buffer upload");
+    }
+    pthread_mutex_unlock(&g_lock);
+    return d;
+}
+
+float* qsf_host_device_floats(const float* host, size_t n) {
+    return (float*)qsf_host_device_bytes(host, sizeof(float) * n);
+}
+
+void qsf_host_device_free(void* p) {
+    if (p) hipFree(p);
+}
+
+float qsf_host_fp16(uint16_t h) {
+    uint32_t sign = ((uint32_t)h & 0x8000u) << 16, e = (h >> 10) & 0x1Fu, m = h & 0x3FFu, u;
+    if (e == 31u) {
+        u = sign | 0x7F800000u | (m << 13);
+    } else if (e == 0u) {
+        if (m == 0u) {
+            u = sign;
+        } else {
+            int sh = 0;
+            while (!(m & 0x400u)) { m <<= 1; sh++; }
+            u = sign | ((uint32_t)(113 - sh) << 23) | ((m & 0x3FFu) << 13);
+        }
+    } else {
+        u = sign | ((e + 112u) << 23) | (m << 13);
+    }
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
 }
 
 qsf_hip_tensor* qsf_hip_tensor_lookup(const void* host) {

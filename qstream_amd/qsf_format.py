@@ -292,3 +292,90 @@ def config2_layer(seed: int = 2):
         del w
     return Q3, 128, mats
 
+
+# ---- QSF container (include/qsf/types.h:185-312) -----------------------------
+# A test-data writer: the struct layouts the converter writes
+# (tools/convert_hf.py:875-1258), packed little-endian, so the device
+# loader can be checked on real files without a HuggingFace checkpoint.
+QSF_MAGIC = 0x51534631
+T_ATTN_Q, T_ATTN_K, T_ATTN_V, T_ATTN_O = 0, 1, 2, 3
+T_FFN_GATE, T_FFN_UP, T_FFN_DOWN = 4, 5, 6
+T_ATTN_NORM_W, T_FFN_NORM_W = 7, 9
+FP16 = 7
+
+
+def _crc32(b: bytes) -> int:
+    import zlib
+    return zlib.crc32(b) & 0xFFFFFFFF
+
+
+def tensor_record(tensor_type: int, qt: int, rows: int, cols: int, payload: bytes) -> bytes:
+    """[24-byte QSFTensorHeader][payload] (types.h:264-273)."""
+    import struct
+    return struct.pack("<HBBIIIII", tensor_type, qt, 0, rows, cols, len(payload), 0, 0) + bytes(payload)
+
+
+def write_qsf(path: str, *, hidden: int, heads: int, vocab: int, inter: int, layers,
+              quant_type: int, block_size: int = 64, kv_heads: int = 0, head_dim: int = 0,
+              embedding=None, final_norm=None, output_head=None, tied: bool = False,
+              activation: int = 2, norm_type: int = 2, pos_enc: int = 1, ffn_type: int = 1,
+              rope_theta: float = 10000.0, eps: float = 1e-5, layer_crc: bool = True,
+              header_crc: bool = True, compression=None) -> dict:
+    """Write a QSF file.  layers: per layer a list of (tensor_type, qt, rows,
+    cols, payload); embedding: (qt, payload) of a [vocab][hidden] table;
+    final_norm: fp16 array [hidden]; output_head: payload of a separate
+    [vocab][hidden] head in quant_type.  Returns the section offsets."""
+    import struct
+    body = bytearray(b"\0" * 256)
+
+    def align():
+        while len(body) % 64:
+            body.append(0)
+
+    index = []
+    for li, recs in enumerate(layers):
+        align()
+        off = len(body)
+        data = b"".join(tensor_record(*r) for r in recs)
+        body += data
+        comp = (compression or {}).get(li, 0)
+        crc = _crc32(data) if layer_crc else 0
+        index.append(struct.pack("<QIIBBHIIfII8s", off, len(data), len(data), quant_type, comp,
+                                 len(recs), crc, crc, 0.0, len(data), 0, b"\0" * 8))
+    align()
+    li_off = len(body)
+    for e in index:
+        body += e
+    emb_off = 0
+    if embedding is not None:
+        align()
+        emb_off = len(body)
+        eqt, epay = embedding
+        body += struct.pack("<IIIIBBBBIII", eqt, 0, vocab, hidden, 0, 0, 0, 0, _crc32(bytes(epay)), 1,
+                            vocab)
+        body += bytes(epay)
+    fin_off = 0
+    if final_norm is not None:
+        align()
+        fin_off = len(body)
+        norm = np.ascontiguousarray(final_norm, np.float16).tobytes()
+        head = b"" if (tied or output_head is None) else bytes(output_head)
+        body += struct.pack("<IIII", 1 if tied else 0, len(norm), len(head), _crc32(norm + head))
+        body += norm + head
+    h = bytearray(256)
+    struct.pack_into("<IIIIIIIIIIII", h, 0, QSF_MAGIC, 1, 256, 1, len(layers), hidden, heads,
+                     kv_heads, vocab, 4096, inter, head_dim)
+    struct.pack_into("<BBBBffI", h, 48, quant_type, activation, norm_type, pos_enc, rope_theta, eps,
+                     block_size)
+    struct.pack_into("<QQQQQQQ", h, 64, li_off, emb_off, fin_off, 0, 0, 0, 0)
+    struct.pack_into("<BBBB", h, 140, 0, ffn_type, 0, 1 if tied else 0)
+    struct.pack_into("<I", h, 156, 1 if tied else 0)
+    struct.pack_into("<Q", h, 160, len(body))
+    struct.pack_into("<I", h, 168, _crc32(bytes(h[:168])) if header_crc else 0)
+    h[172] = 1
+    body[:256] = h
+    with open(path, "wb") as f:
+        f.write(body)
+    return {"layer_index": li_off, "embedding": emb_off, "final": fin_off, "size": len(body),
+            "layer_offsets": [struct.unpack_from("<Q", e)[0] for e in index]}
+

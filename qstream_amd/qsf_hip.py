@@ -38,6 +38,9 @@ EXPORTS = (
     "qsf_hip_rms_norm_dev", "qsf_hip_layer_norm_dev", "qsf_hip_rope_create", "qsf_hip_rope_free",
     "qsf_hip_rope_dev", "qsf_hip_kv_store_dev", "qsf_hip_attention_dev", "qsf_hip_act_mul_dev",
     "qsf_hip_residual_dev", "qsf_hip_embed_row_dev", "qsf_hip_embed_row_fp16_dev",
+    "qsf_hip_crc32", "qsf_hip_model_load", "qsf_hip_model_free", "qsf_hip_model_get_info",
+    "qsf_hip_model_tensor", "qsf_hip_model_vector", "qsf_hip_model_embedding",
+    "qsf_hip_model_embedding_fp16", "qsf_hip_model_output_head", "qsf_hip_model_final_norm",
 )
 
 _lib = None
@@ -118,6 +121,22 @@ def load(path: str = LIB_PATH) -> C.CDLL:
               "qsf_hip_kv_store_dev", "qsf_hip_attention_dev", "qsf_hip_act_mul_dev",
               "qsf_hip_residual_dev", "qsf_hip_embed_row_dev", "qsf_hip_embed_row_fp16_dev"):
         getattr(L, n).restype = _i
+    L.qsf_hip_crc32.argtypes = [_vp, C.c_size_t]
+    L.qsf_hip_crc32.restype = C.c_uint32
+    L.qsf_hip_model_load.argtypes = [C.c_char_p]
+    L.qsf_hip_model_load.restype = _vp
+    L.qsf_hip_model_free.argtypes = [_vp]
+    L.qsf_hip_model_get_info.argtypes = [_vp, _vp]
+    L.qsf_hip_model_get_info.restype = _i
+    L.qsf_hip_model_tensor.argtypes = [_vp, _i, _i]
+    L.qsf_hip_model_tensor.restype = _vp
+    L.qsf_hip_model_vector.argtypes = [_vp, _i, _i, C.POINTER(_i)]
+    L.qsf_hip_model_vector.restype = _vp
+    for n in ("qsf_hip_model_embedding", "qsf_hip_model_embedding_fp16", "qsf_hip_model_output_head"):
+        getattr(L, n).argtypes = [_vp]
+        getattr(L, n).restype = _vp
+    L.qsf_hip_model_final_norm.argtypes = [_vp, C.POINTER(_vp)]
+    L.qsf_hip_model_final_norm.restype = _vp
     L.qsf_hip_kernel_timing.argtypes = [_i]
     L.qsf_hip_kernel_timing.restype = _i
     L.qsf_hip_kernel_timing_read.argtypes = [C.POINTER(C.c_float), _i]
@@ -359,4 +378,73 @@ def embed_row(table: "Tensor", token: int, out, stream=None) -> None:
 def embed_row_fp16(d_table, hd: int, token: int, out, stream=None) -> None:
     _check(load().qsf_hip_embed_row_fp16_dev(_addr(d_table), hd, token, _addr(out),
                                              _stream(stream)), "qsf_hip_embed_row_fp16_dev")
+
+
+# ---- QSF model file -> device arena ------------------------------------------
+class ModelInfo(C.Structure):
+    """qsf_hip_model_info (include/qsf_hip.h)."""
+    _fields_ = [(n, C.c_uint32) for n in (
+        "num_layers", "hidden_dim", "num_heads", "num_kv_heads", "vocab_size", "max_seq_len",
+        "intermediate_dim", "head_dim", "block_size", "quant_type", "activation", "norm_type",
+        "pos_enc_type", "ffn_type", "attn_type", "has_bias", "weight_tied", "num_experts",
+        "num_active_experts", "expert_intermediate_dim")] + [
+        ("rope_theta", C.c_float), ("norm_epsilon", C.c_float), ("num_tensors", C.c_uint32),
+        ("has_embedding", C.c_uint32), ("crc_mismatches", C.c_uint32),
+        ("size_mismatch", C.c_uint32), ("device_bytes", C.c_size_t)]
+
+
+def crc32(data: bytes) -> int:
+    buf = np.frombuffer(data, np.uint8)
+    return load().qsf_hip_crc32(buf.ctypes.data, len(buf))
+
+
+class _Ref:
+    """A tensor the model owns (no free)."""
+
+    def __init__(self, handle):
+        self.handle = handle
+
+    def matvec(self, x, y, stream=None) -> None:
+        _check(load().qsf_hip_matvec_dev(self.handle, _addr(x), _addr(y), _stream(stream)),
+               "qsf_hip_matvec_dev")
+
+
+class Model:
+    """A QSF file loaded into the device arena (qsf_hip_model_load)."""
+
+    def __init__(self, path: str):
+        L = load()
+        self.handle = L.qsf_hip_model_load(path.encode())
+        if not self.handle:
+            code, detail = last_error()
+            raise QsfHipError(f"qsf_hip_model_load failed ({code}): {detail}")
+        self.info = ModelInfo()
+        _check(L.qsf_hip_model_get_info(self.handle, C.byref(self.info)), "qsf_hip_model_get_info")
+
+    def tensor(self, layer: int, tensor_type: int):
+        h = load().qsf_hip_model_tensor(self.handle, layer, tensor_type)
+        return _Ref(h) if h else None
+
+    def vector(self, layer: int, tensor_type: int):
+        n = C.c_int(0)
+        p = load().qsf_hip_model_vector(self.handle, layer, tensor_type, C.byref(n))
+        return (p, n.value) if p else (None, 0)
+
+    def embedding(self):
+        h = load().qsf_hip_model_embedding(self.handle)
+        return _Ref(h) if h else None
+
+    def output_head(self):
+        h = load().qsf_hip_model_output_head(self.handle)
+        return _Ref(h) if h else None
+
+    def final_norm(self):
+        b = _vp()
+        w = load().qsf_hip_model_final_norm(self.handle, C.byref(b))
+        return w, b.value
+
+    def free(self) -> None:
+        if self.handle:
+            load().qsf_hip_model_free(self.handle)
+            self.handle = None
 

@@ -31,3 +31,18 @@ def host(t) -> np.ndarray:
     torch = torch_cuda()
     torch.cuda.synchronize()
     return t.cpu().numpy()
+
+
+def device_floats(ptr: int, n: int) -> np.ndarray:
+    """Copy n fp32 values from a raw device address (memory a library
+    object owns) to the host with hipMemcpy of the HIP runtime this process
+    already loaded (torch's)."""
+    import ctypes as C
+    torch_cuda().cuda.synchronize()
+    path = next(line.split()[-1] for line in open("/proc/self/maps") if "libamdhip64" in line)
+    rt = C.CDLL(path)
+    rt.hipMemcpy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int]
+    out = np.empty(n, np.float32)
+    assert rt.hipMemcpy(out.ctypes.data, ptr, 4 * n, 2) == 0       # 2 = device to host
+    return out
+
