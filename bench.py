@@ -229,10 +229,13 @@ def run_profile(torch, hip, cfg, steps, warmup):
 
 def table_slot_step_us(hip, qt, bs, mats, x, calls=200):
     """PCIe-inclusive latency of the drop-in path: the qsf_matvec_fn table
-    slot (host x and y, synchronous; pinned H2D copy of x, the GEMV launch,
-    D2H copy of y) called through ctypes with precomputed pointers, weights
-    already resident in the device arena (one copy, so they may sit in the
-    MALL).  Microseconds per step (all matrices of the step)."""
+    slot (host x and y, synchronous; x prepared from host-mapped memory by
+    one small dispatch, the GEMV writing y into host-mapped memory, one
+    stream synchronisation) called through ctypes with precomputed pointers,
+    weights already resident in the device arena (one copy, so they may sit
+    in the MALL).  Every step has its own x, as a decode loop does (the
+    matrices of one step share it, as gate and up share a token's x), so
+    each step pays one x preparation.  Microseconds per step."""
     from qstream_amd import qsf_format as F
     L = hip.load()
     name = {F.Q2: "matvec_2bit", F.Q3: "matvec_3bit", F.Q4: "matvec_4bit",
@@ -240,16 +243,16 @@ def table_slot_step_us(hip, qt, bs, mats, x, calls=200):
             F.Q4_OUTLIER: "matvec_outlier_4bit"}[qt]
     fn = getattr(L, f"qsf_{name}_hip")
     ws = [np.frombuffer(p, np.uint8) for _, p, _, _ in mats]
-    xh = np.ascontiguousarray(x, np.float32)
+    xs = [np.ascontiguousarray(x * (1.0 + 2.0 ** -10 * i), np.float32) for i in range(4)]
     outs = [np.empty(r, np.float32) for _, _, r, _ in mats]
-    args = [(w.ctypes.data, xh.ctypes.data, o.ctypes.data, r, c, bs)
-            for w, o, (_, _, r, c) in zip(ws, outs, mats)]
-    for _ in range(10):
-        for a in args:
+    steps = [[(w.ctypes.data, xh.ctypes.data, o.ctypes.data, r, c, bs)
+              for w, o, (_, _, r, c) in zip(ws, outs, mats)] for xh in xs]
+    for i in range(10):
+        for a in steps[i % 4]:
             fn(*a)
     t0 = time.perf_counter()
-    for _ in range(calls):
-        for a in args:
+    for i in range(calls):
+        for a in steps[i % 4]:
             fn(*a)
     return (time.perf_counter() - t0) / calls * 1e6
 

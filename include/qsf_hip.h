@@ -42,6 +42,13 @@ int         qsf_hip_last_error(void);
 const char* qsf_hip_last_error_detail(void);
 
 /* ---- 1. drop-in table slots (qsf_matvec_fn) ------------------------------ */
+/* Synchronous: host x in, host y out, weights from the device arena.  The
+ * first call with a weight pointer uploads its payload; later calls run from
+ * HBM.  A pointer whose geometry, outlier count or sampled payload words
+ * differ from what was uploaded is uploaded again and marked volatile (every
+ * later call uploads it).  Rewriting a buffer that a slot has seen, without
+ * qsf_hip_arena_forget, is only safe once the pointer is volatile: the first
+ * rewrite is caught by the sampled words alone, not by a full comparison. */
 /* src/kernels_scalar.c:16-37 (2-bit; also QSF_QUANT_2BIT_SYM, src/engine.c:143) */
 void qsf_matvec_2bit_hip(const void* weights_q, const float* input, float* output,
                          int rows, int cols, int block_size);
@@ -87,7 +94,10 @@ qsf_hip_tensor* qsf_hip_tensor_upload(const void* host_payload, int quant_type,
 /* Tensor registered for this host pointer, or NULL. */
 qsf_hip_tensor* qsf_hip_tensor_lookup(const void* host_payload);
 void            qsf_hip_tensor_free(qsf_hip_tensor* t);
-/* Forget a host pointer (call when the caller reuses the buffer). */
+/* Forget a host pointer and its volatile mark.  Required before a slot call
+ * with a buffer the caller has rewritten since a slot last saw it, unless
+ * the pointer is already volatile.  Returns QSF_ERR_INVALID_INPUT when the pointer
+ * is not registered. */
 int             qsf_hip_arena_forget(const void* host_payload);
 /* Bytes of HBM held by the arena. */
 size_t          qsf_hip_arena_bytes(void);

@@ -394,16 +394,26 @@ __device__ __forceinline__ void prep_block(const float* __restrict__ x, int cols
 }
 
 // Stand-alone x preparation (prepared mode): 256 threads, 256/LPB blocks each.
+// With `xcopy` it also writes fp32 x there (nb*BS floats, zero past cols for
+// 2/4-bit), which lets x come from host-mapped memory in one read.
 template <int FMT, int BS>
 __global__ __launch_bounds__(256) void xprep_kernel(const float* __restrict__ x, int cols, int nb,
                                                     uint32_t* __restrict__ xq,
-                                                    float2* __restrict__ xmeta) {
+                                                    float2* __restrict__ xmeta,
+                                                    float* __restrict__ xcopy) {
     using F = Fmt<FMT, BS>;
     const int b = blockIdx.x * (256 / F::LPB) + threadIdx.x / F::LPB;
     const bool live = b < nb;
     const int bb = live ? b : 0;
     prep_block<FMT, BS>(x, cols, b, live, threadIdx.x & (F::LPB - 1), xq + (size_t)bb * F::DWS,
-                        xmeta + bb);
+                        xmeta + bb, xcopy);
+}
+
+// Prepared digits at ws, block meta after them at the next 256-byte boundary.
+template <int FMT, int BS>
+__host__ __device__ inline float2* xmeta_in(void* ws, int nb) {
+    const size_t dig = (size_t)nb * Fmt<FMT, BS>::DWS * 4;
+    return (float2*)((uint8_t*)ws + ((dig + 255) & ~(size_t)255));
 }
 
 // Group sum over `lpg` lanes (power of two) with DPP; the total is valid in
@@ -1061,6 +1071,20 @@ __global__ void fill_kernel(float* y, int n, float v) {
     if (i < n) y[i] = v;
 }
 
+// n floats from `src` (host memory mapped into the device address space) to
+// device memory: the table slots' x in one dispatch on their own queue, no
+// copy engine.  Whole float4s where the tail allows, then single floats.
+__global__ __launch_bounds__(256) void stage_kernel(float* __restrict__ dst,
+                                                     const float* __restrict__ src, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    const int n4 = n >> 2;
+    if (i < n4) {
+        reinterpret_cast<float4*>(dst)[i] = reinterpret_cast<const float4*>(src)[i];
+    } else if (4 * n4 + (i - n4) < n) {
+        dst[4 * n4 + (i - n4)] = src[4 * n4 + (i - n4)];
+    }
+}
+
 int num_cus() {
     static int n = 0;
     if (!n) {
@@ -1165,12 +1189,11 @@ int launch_rt(const qsf_hip_tensor* const* t, int n, int cols, const float* d_x,
     const int nb = (cols + BS - 1) / BS;
     // prepared digits and block meta (QK_RUN_XPREP / a prepared run only)
     uint32_t* xq = (uint32_t*)d_ws;
-    size_t dig = (size_t)nb * F::DWS * 4;
-    float2* xmeta = d_ws ? (float2*)((uint8_t*)d_ws + ((dig + 255) & ~(size_t)255)) : nullptr;
+    float2* xmeta = d_ws ? xmeta_in<FMT, BS>(d_ws, nb) : nullptr;
     if (!d_ws && (mode != QK_RUN_BOTH)) return -2;
     if ((mode & QK_RUN_XPREP) && (!(mode & QK_RUN_GEMV) || (mode & QK_RUN_STANDALONE_PREP)))
         hipLaunchKernelGGL((xprep_kernel<FMT, BS>), dim3((nb + 256 / F::LPB - 1) / (256 / F::LPB)),
-                           dim3(256), 0, s, d_x, cols, nb, xq, xmeta);
+                           dim3(256), 0, s, d_x, cols, nb, xq, xmeta, (float*)nullptr);
     if (!(mode & QK_RUN_GEMV)) return hipGetLastError() == hipSuccess ? 0 : -1;
 
     GemvArgs a = {};
@@ -1466,6 +1489,47 @@ extern "C" int qk_gemv_group(const qsf_hip_tensor* const* t, int n, const float*
         return hipGetLastError() == hipSuccess ? 0 : -1;
     }
     return launch_fmt(fmt, bs, t, n, cols, d_x, d_y, d_ws, mode, s);
+}
+
+template <int FMT, int BS>
+int xstage_t(int cols, const float* x, float* d_xcopy, void* d_ws, hipStream_t s) {
+    using F = Fmt<FMT, BS>;
+    const int nb = (cols + BS - 1) / BS;
+    hipLaunchKernelGGL((xprep_kernel<FMT, BS>), dim3((nb + 256 / F::LPB - 1) / (256 / F::LPB)),
+                       dim3(256), 0, s, x, cols, nb, (uint32_t*)d_ws, xmeta_in<FMT, BS>(d_ws, nb),
+                       d_xcopy);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+template <int FMT>
+int xstage_bs(int bs, int cols, const float* x, float* d_xcopy, void* d_ws, hipStream_t s) {
+    switch (bs) {
+    case 32: return xstage_t<FMT, 32>(cols, x, d_xcopy, d_ws, s);
+    case 64: return xstage_t<FMT, 64>(cols, x, d_xcopy, d_ws, s);
+    case 128: return xstage_t<FMT, 128>(cols, x, d_xcopy, d_ws, s);
+    case 256: return xstage_t<FMT, 256>(cols, x, d_xcopy, d_ws, s);
+    default: return -2;
+    }
+}
+
+extern "C" int qk_xprep_stage(int fmt, int bs, int cols, const float* x, float* d_xcopy,
+                              void* d_ws, hipStream_t s) {
+    if (cols <= 0) return 0;
+    switch (fmt) {
+    case QK_FMT_2: return xstage_bs<QK_FMT_2>(bs, cols, x, d_xcopy, d_ws, s);
+    case QK_FMT_3: return xstage_bs<QK_FMT_3>(bs, cols, x, d_xcopy, d_ws, s);
+    case QK_FMT_4: return xstage_bs<QK_FMT_4>(bs, cols, x, d_xcopy, d_ws, s);
+    case QK_FMT_4SYM: return xstage_bs<QK_FMT_4SYM>(bs, cols, x, d_xcopy, d_ws, s);
+    default: return -2;
+    }
+}
+
+extern "C" int qk_stage_f32(float* d_dst, const float* src, int n, hipStream_t s) {
+    if (n <= 0) return 0;
+    if (((uintptr_t)d_dst | (uintptr_t)src) & 15) return -2;
+    const int threads = (n >> 2) + 3;
+    hipLaunchKernelGGL(stage_kernel, dim3((threads + 255) / 256), dim3(256), 0, s, d_dst, src, n);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
 extern "C" int qk_unpack(int qt, const void* d_blocks, int nblocks, int bs, int8_t* d_codes,

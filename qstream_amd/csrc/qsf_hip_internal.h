@@ -52,6 +52,14 @@ typedef struct qsf_hip_tensor {
 /* Per-call prepared activation: block-fixed-point digits of x. */
 size_t qk_xprep_bytes(int fmt, int bs, int cols);
 
+/* n floats from host-mapped `src` to device `d_dst` (both 16-B aligned) */
+int qk_stage_f32(float* d_dst, const float* src, int n, hipStream_t s);
+
+/* qk_xprep from x in host-mapped memory, also writing fp32 x to d_xcopy
+ * (room for ceil(cols/bs)*bs floats): the table slots' one x dispatch */
+int qk_xprep_stage(int fmt, int bs, int cols, const float* x, float* d_xcopy, void* d_ws,
+                   hipStream_t s);
+
 /* x preparation into ws (qk_xprep_bytes(fmt, bs, cols) bytes, 256-B aligned) */
 int qk_xprep(int fmt, int bs, int cols, const float* d_x, void* d_ws, hipStream_t s);
 /* GEMV over n tensors sharing x.  mode: QK_RUN_BOTH prepares x inside the

@@ -60,10 +60,11 @@ typedef struct {
     hipStream_t stream;
     void* ws;          size_t ws_bytes;       /* prefill workspace */
     void* att_ws;      size_t att_ws_bytes;   /* attention partials */
-    float* d_x;        size_t d_x_n;          /* staging for host-pointer calls */
-    float* d_y;        size_t d_y_n;
-    float* h_x;        size_t h_x_n;          /* pinned host staging */
-    float* h_y;        size_t h_y_n;
+    float* d_x;        size_t d_x_n;          /* device copy of a table slot's x */
+    void* slot_xq;     size_t slot_xq_bytes;  /* a table slot's prepared x */
+    int xq_ok, xq_fmt, xq_bs, xq_cols;        /* slot_xq and d_x hold h_x prepared so */
+    float* h_x;        size_t h_x_n;          /* host-mapped, coherent: slot x ... */
+    float* h_y;        size_t h_y_n;          /* ... and y (the kernel writes it) */
     size_t arena_bytes;
 } dev_state;
 
@@ -137,13 +138,17 @@ static int ensure_dev(void** p, size_t* have, size_t need) {
     return E_OK;
 }
 
+/* grow-only pinned host buffer, mapped into the device address space and
+ * coherent (fine-grained): kernels read and write it directly and the host
+ * sees a kernel's stores once the stream has been synchronised.  Only the
+ * synchronous table slots use these, so the old buffer is idle when freed. */
 static int ensure_host(void** p, size_t* have, size_t need) {
     if (*have >= need) return E_OK;
     if (*p) hipHostFree(*p);
     *p = NULL;
     *have = 0;
     size_t sz = need < 4096 ? 4096 : need + need / 2;
-    HIPCHK(hipHostMalloc(p, sz, hipHostMallocDefault), E_OOM);
+    HIPCHK(hipHostMalloc(p, sz, hipHostMallocMapped | hipHostMallocCoherent), E_OOM);
     *have = sz;
     return E_OK;
 }
@@ -174,6 +179,7 @@ typedef struct {
     const void* key;
     qsf_hip_tensor* t;
     uint64_t fp;       /* fingerprint of sampled payload words */
+    int vol;           /* the bytes at key have changed once: upload on every call */
 } reg_slot;
 
 static reg_slot* g_reg;
@@ -206,7 +212,7 @@ static reg_slot* reg_find(const void* key) {
     }
 }
 
-static int reg_put(const void* key, qsf_hip_tensor* t, uint64_t fp) {
+static int reg_put(const void* key, qsf_hip_tensor* t, uint64_t fp, int vol) {
     if ((g_reg_n + 1) * 2 > g_reg_cap) {
         size_t cap = g_reg_cap ? g_reg_cap * 2 : 256;
         reg_slot* nr = calloc(cap, sizeof *nr);
@@ -227,6 +233,7 @@ static int reg_put(const void* key, qsf_hip_tensor* t, uint64_t fp) {
     g_reg[i].key = key;
     g_reg[i].t = t;
     g_reg[i].fp = fp;
+    g_reg[i].vol = vol;
     return E_OK;
 }
 
@@ -242,7 +249,7 @@ static void reg_del(const void* key) {
         reg_slot tmp = g_reg[j];
         g_reg[j].key = NULL;
         g_reg_n--;
-        reg_put(tmp.key, tmp.t, tmp.fp);
+        reg_put(tmp.key, tmp.t, tmp.fp, tmp.vol);
     }
 }
 
@@ -428,7 +435,7 @@ qsf_hip_tensor* qsf_hip_tensor_upload(const void* host, int qt, int rows, int co
     qsf_hip_tensor* t = upload_locked(host, qt, rows, cols, bs);
     if (t) {
         reg_drop(host);
-        if (reg_put(host, t, fingerprint(host, t->payload_bytes)) != E_OK) {
+        if (reg_put(host, t, fingerprint(host, t->payload_bytes), 0) != E_OK) {
             tensor_destroy(t);
             t = NULL;
         }
@@ -528,7 +535,7 @@ void qsf_hip_shutdown(void) {
         if (g_dev.ws) hipFree(g_dev.ws);
         if (g_dev.att_ws) hipFree(g_dev.att_ws);
         if (g_dev.d_x) hipFree(g_dev.d_x);
-        if (g_dev.d_y) hipFree(g_dev.d_y);
+        if (g_dev.slot_xq) hipFree(g_dev.slot_xq);
         if (g_dev.h_x) hipHostFree(g_dev.h_x);
         if (g_dev.h_y) hipHostFree(g_dev.h_y);
         for (size_t i = 0; i < g_retired_n; i++) hipFree(g_retired[i]);
@@ -924,8 +931,23 @@ static void nan_fill(float* out, int rows) {
     for (int i = 0; i < rows; i++) out[i] = NAN;
 }
 
-/* Synchronous host-pointer matvec: look up (or upload) the payload, stage x
- * through pinned memory, run, copy y back. */
+/* Synchronous host-pointer matvec.  The payload is looked up in the arena
+ * (uploaded on first sight).  x is written to host-mapped memory and one
+ * dispatch prepares it (block fixed point digits) straight from there,
+ * leaving an fp32 copy in HBM; the GEMV runs on the prepared x and writes y
+ * into host-mapped memory; one stream synchronisation ends the call.  When x
+ * is bit-identical to the previous slot call's (gate and up, or q, k and v,
+ * of one token share it) and of the same format, block size and length, the
+ * prepared x is still in HBM and the call is one dispatch.
+ *
+ * Stale weights: a pointer's entry is checked against the call's geometry,
+ * the outlier count and a fingerprint of nine sampled payload words.  Any
+ * mismatch uploads the payload again and marks the pointer volatile: from
+ * then on it is uploaded on every call (an engine that decompresses each
+ * layer into one reused buffer, src/engine.c:786-789, pays one upload per
+ * call and is never served another layer's weights).  A caller that rewrites
+ * a buffer whose first change could leave the sampled words equal must call
+ * qsf_hip_arena_forget on it first. */
 static void host_matvec(int qt, const void* w, const float* in, float* out,
                         int rows, int cols, int bs) {
     if (rows <= 0) return;
@@ -935,49 +957,81 @@ static void host_matvec(int qt, const void* w, const float* in, float* out,
     if (!rc) {
         reg_slot* s = reg_find(w);
         t = s ? s->t : NULL;
-        /* a reused host buffer must not be served stale: compare geometry,
-         * then the payload size this call implies, then sampled words */
-        if (t && (t->qt != qt || t->rows != rows || t->cols != cols ||
+        int vol = s ? s->vol : 0;
+        if (t && (vol || t->qt != qt || t->rows != rows || t->cols != cols ||
                   (t->fmt >= 0 && t->bs != bs) ||
                   (is_outlier(qt) && rd_u32((const uint8_t*)w) != t->n_outliers) ||
                   s->fp != fingerprint(w, t->payload_bytes))) {
+            vol = 1;
             reg_drop(w);
             t = NULL;
         }
         if (!t) {
             t = upload_locked(w, qt, rows, cols, bs);
             if (t) t->registry_owned = 1;
-            if (!t || reg_put(w, t, fingerprint(w, t->payload_bytes)) != E_OK) {
+            if (!t || reg_put(w, t, vol ? 0 : fingerprint(w, t->payload_bytes), vol) != E_OK) {
                 if (t) tensor_destroy(t);
                 t = NULL;
                 rc = g_err ? g_err : E_INTERNAL;
             }
         }
     }
-    if (!rc) rc = ensure_dev((void**)&g_dev.d_x, &g_dev.d_x_n, sizeof(float) * (size_t)(cols > 0 ? cols : 1));
-    if (!rc) rc = ensure_dev((void**)&g_dev.d_y, &g_dev.d_y_n, sizeof(float) * (size_t)rows);
-    if (!rc) rc = ensure_host((void**)&g_dev.h_x, &g_dev.h_x_n, sizeof(float) * (size_t)(cols > 0 ? cols : 1));
-    if (!rc) rc = ensure_host((void**)&g_dev.h_y, &g_dev.h_y_n, sizeof(float) * (size_t)rows);
-    hipStream_t s = g_dev.stream;
-    if (!rc && cols > 0) {
-        memcpy(g_dev.h_x, in, sizeof(float) * (size_t)cols);
-        if (hipMemcpyAsync(g_dev.d_x, g_dev.h_x, sizeof(float) * (size_t)cols,
-                           hipMemcpyHostToDevice, s) != hipSuccess)
-            rc = fail(E_INTERNAL, "qsf_hip: H2D copy");
+    const int fmt = t ? t->fmt : -1, tbs = t ? t->bs : 32;
+    const size_t xn = sizeof(float) * (size_t)(cols > 0 ? cols : 1), yn = sizeof(float) * (size_t)rows;
+    /* the prepared form writes x up to the last block's end */
+    const size_t xpad = sizeof(float) * ((size_t)(cols > 0 ? cols : 1) + 256);
+    if (!rc) {
+        void* old_x = g_dev.d_x;
+        rc = ensure_dev((void**)&g_dev.d_x, &g_dev.d_x_n, xpad);
+        if (g_dev.d_x != old_x) g_dev.xq_ok = 0;
+    }
+    if (!rc && fmt >= 0 && cols > 0) {
+        void* old_q = g_dev.slot_xq;
+        rc = ensure_dev(&g_dev.slot_xq, &g_dev.slot_xq_bytes, qk_xprep_bytes(fmt, tbs, cols));
+        if (g_dev.slot_xq != old_q) g_dev.xq_ok = 0;
     }
     if (!rc) {
-        if (t->fmt < 0) rc = mxfp4_locked(t, g_dev.d_x, g_dev.d_y, s);
-        else rc = group_locked((const qsf_hip_tensor* const*)&t, 1, g_dev.d_x, &g_dev.d_y, s);
+        void* old_h = g_dev.h_x;
+        rc = ensure_host((void**)&g_dev.h_x, &g_dev.h_x_n, xn);
+        if (g_dev.h_x != old_h) g_dev.xq_ok = 0;
     }
-    if (!rc && hipMemcpyAsync(g_dev.h_y, g_dev.d_y, sizeof(float) * (size_t)rows,
-                              hipMemcpyDeviceToHost, s) != hipSuccess)
-        rc = fail(E_INTERNAL, "qsf_hip: D2H copy");
+    if (!rc) rc = ensure_host((void**)&g_dev.h_y, &g_dev.h_y_n, yn);
+    float *hx_dev = NULL, *hy_dev = NULL;
+    if (!rc && (hipHostGetDevicePointer((void**)&hx_dev, g_dev.h_x, 0) != hipSuccess ||
+                hipHostGetDevicePointer((void**)&hy_dev, g_dev.h_y, 0) != hipSuccess))
+        rc = fail(E_INTERNAL, "qsf_hip: host-mapped staging");
+    hipStream_t s = g_dev.stream;
+    if (!rc && cols > 0) {
+        const int same = g_dev.xq_ok && fmt >= 0 && g_dev.xq_fmt == fmt && g_dev.xq_bs == tbs &&
+                         g_dev.xq_cols == cols && memcmp(g_dev.h_x, in, xn) == 0;
+        g_dev.xq_ok = 0;
+        if (!same) {
+            memcpy(g_dev.h_x, in, xn);
+            if (fmt < 0 ? qk_stage_f32(g_dev.d_x, hx_dev, cols, s)
+                        : qk_xprep_stage(fmt, tbs, cols, hx_dev, g_dev.d_x, g_dev.slot_xq, s))
+                rc = fail(E_INTERNAL, "qsf_hip: x staging");
+        }
+    }
+    if (!rc) {
+        if (fmt < 0) rc = mxfp4_locked(t, g_dev.d_x, hy_dev, s);
+        else if (qk_gemv_group((const qsf_hip_tensor* const*)&t, 1, g_dev.d_x, &hy_dev,
+                               g_dev.slot_xq, cols > 0 ? QK_RUN_GEMV : QK_RUN_BOTH, s))
+            rc = fail(E_INTERNAL, "qsf_hip: GEMV launch failed");
+    }
     if (!rc) {
         hipError_t e = hipStreamSynchronize(s);
         if (e != hipSuccess) rc = fail(E_INTERNAL, "qsf_hip: %s", hipGetErrorString(e));
     }
-    if (!rc) memcpy(out, g_dev.h_y, sizeof(float) * (size_t)rows);
-    else nan_fill(out, rows);
+    if (!rc) {
+        memcpy(out, g_dev.h_y, yn);
+        /* valid for the next call only after this one completed */
+        g_dev.xq_ok = fmt >= 0 && cols > 0;
+        g_dev.xq_fmt = fmt;
+        g_dev.xq_bs = tbs;
+        g_dev.xq_cols = cols;
+    } else {
+        nan_fill(out, rows);
+    }
     pthread_mutex_unlock(&g_lock);
 }
 

@@ -193,6 +193,13 @@ def init(device: int = 0) -> None:
     _check(load().qsf_hip_init(device), "qsf_hip_init")
 
 
+def arena_forget(payload) -> bool:
+    """Drop the arena entry (and volatile mark) of a host payload buffer;
+    False when the buffer was not registered."""
+    a = payload if isinstance(payload, np.ndarray) else np.frombuffer(payload, np.uint8)
+    return load().qsf_hip_arena_forget(a.ctypes.data) == 0
+
+
 class KernelTable:
     """The six matvec slots of QSFKernelTable backed by libqsf_hip.
 

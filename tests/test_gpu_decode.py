@@ -358,3 +358,101 @@ def test_nonfinite_input_gives_nan(hip, qt, bad):
             F.Q4SYM: "matvec_4bit_sym", F.Q2_OUTLIER: "matvec_outlier_2bit"}[qt]
     getattr(hip.KernelTable(), slot)(p, x, out, rows, cols, bs)
     assert np.all(np.isnan(out)), out
+
+
+def _unsampled_edit(payload: np.ndarray) -> np.ndarray:
+    """A copy of `payload` changed in one byte that none of the slot's nine
+    sampled 8-byte words covers (offset n/16, inside the first eighth)."""
+    n = payload.size
+    pos = n // 16
+    assert 8 <= pos and pos + 1 < n // 8
+    out = payload.copy()
+    out[pos] ^= 0x5A
+    return out
+
+
+@pytest.mark.parametrize("qt", [F.Q4, F.Q2_OUTLIER])
+def test_slot_reused_buffer_forget_and_volatile(hip, oracle, qt):
+    """A reused host buffer (src/engine.c:786-789 decompresses every layer
+    into one layer_buf) is never served stale weights when the caller keeps
+    the contract: qsf_hip_arena_forget after a rewrite whose first change
+    only an unsampled byte shows; and once the slot has seen the content
+    change, the pointer is volatile and every rewrite is picked up."""
+    rows, cols, bs = 300, 4096, 64
+    rng = np.random.default_rng(11 + qt)
+    mk = (lambda: F.heavy_tail_weights(rng, rows, cols)) if qt == F.Q2_OUTLIER else \
+        (lambda: F.gaussian(rng, (rows, cols), 0.02))
+    a = np.frombuffer(F.quantize_matrix(mk(), qt, bs), np.uint8).copy()
+    b = _unsampled_edit(a)
+    c = np.frombuffer(F.quantize_matrix(mk(), qt, bs), np.uint8).copy()
+    assert c.size == a.size
+    x = F.gaussian(rng, cols)
+    slot = _slot(hip, qt)
+    buf = a.copy()
+    out = np.full(rows, np.nan, np.float32)
+
+    def run_and_check(content):
+        out[:] = np.nan
+        slot(buf, x, out, rows, cols, bs)
+        assert rel_l2(out, oracle.matvec(qt, content.tobytes(), x, rows, cols, bs)) <= REL_L2
+
+    run_and_check(a)
+    buf[:] = b                                   # first rewrite: only an unsampled byte
+    assert hip.arena_forget(buf)                 # the contract
+    run_and_check(b)
+    assert not np.array_equal(oracle.matvec(qt, a.tobytes(), x, rows, cols, bs),
+                              oracle.matvec(qt, b.tobytes(), x, rows, cols, bs))
+    buf[:] = c                                   # sampled words change: volatile from now on
+    run_and_check(c)
+    buf[:] = _unsampled_edit(c)                  # caught without forget: the pointer is volatile
+    run_and_check(buf.copy())
+    buf[:] = c
+    run_and_check(c)
+    assert hip.arena_forget(buf) and not hip.arena_forget(buf)
+
+
+def test_slot_x_reuse_between_calls(hip, oracle):
+    """The slots keep the last call's prepared x in HBM and skip the
+    preparation when x is bit-identical and the format, block size and
+    length match.  Every change of any of these must be picked up: same x
+    across matrices (gate, up), one element changed, another format or block
+    size at the same length, a shorter x, and an MXFP4 call in between."""
+    rng = np.random.default_rng(21)
+    cols = 4096
+    cases = [(F.Q2_OUTLIER, 64, 700), (F.Q2_OUTLIER, 64, 500), (F.Q4, 64, 300),
+             (F.Q4, 128, 300), (F.Q3, 128, 260), (F.Q4SYM, 32, 130)]
+    mats = []
+    for qt, bs, rows in cases:
+        w = F.heavy_tail_weights(rng, rows, cols) if qt == F.Q2_OUTLIER else \
+            F.gaussian(rng, (rows, cols), 0.02)
+        mats.append((qt, bs, rows, F.quantize_matrix(w, qt, bs)))
+    x = F.gaussian(rng, cols)
+    x2 = x.copy()
+    x2[1234] += 0.5
+    mx = F.quantize_mxfp4(F.gaussian(rng, (64, cols), 0.02))
+    kt = hip.KernelTable()
+
+    def check(i, xv):
+        qt, bs, rows, p = mats[i]
+        out = np.full(rows, np.nan, np.float32)
+        _slot(hip, qt)(p, xv.copy(), out, rows, cols, bs)
+        assert rel_l2(out, oracle.matvec(qt, p, xv, rows, cols, bs)) <= REL_L2, (i, qt, bs)
+
+    for seq in ([0, 1, 1, 0], [2, 3, 2], [4, 5, 0]):
+        for i in seq:
+            check(i, x)
+    check(0, x2)
+    check(1, x2)
+    check(1, x)
+    out = np.full(64, np.nan, np.float32)
+    kt.matvec_mxfp4(mx, x, out, 64, cols, 32)
+    assert rel_l2(out, oracle.matvec(F.MXFP4, mx, x, 64, cols, 32)) <= REL_L2
+    check(1, x)
+    # a shorter x whose leading bytes equal the last one's
+    qt, bs, rows, _ = mats[2]
+    short = 2048
+    p = F.quantize_matrix(F.gaussian(rng, (rows, short), 0.02), qt, bs)
+    out = np.full(rows, np.nan, np.float32)
+    _slot(hip, qt)(p, x[:short].copy(), out, rows, short, bs)
+    assert rel_l2(out, oracle.matvec(qt, p, x[:short], rows, short, bs)) <= REL_L2
+    check(2, x)
