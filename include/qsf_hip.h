@@ -99,6 +99,10 @@ void            qsf_hip_tensor_free(qsf_hip_tensor* t);
  * the pointer is already volatile.  Returns QSF_ERR_INVALID_INPUT when the pointer
  * is not registered. */
 int             qsf_hip_arena_forget(const void* host_payload);
+/* Forget every registered pointer in [base, base + bytes), e.g. all tensors
+ * of an LZ4 layer buffer after it is decompressed again (src/engine.c:786-789).
+ * Returns the number forgotten, or -QSF_ERR_OUT_OF_MEMORY. */
+int             qsf_hip_arena_forget_range(const void* base, size_t bytes);
 /* Bytes of HBM held by the arena. */
 size_t          qsf_hip_arena_bytes(void);
 /* On-disk payload bytes of a registered tensor. */
@@ -148,11 +152,13 @@ typedef struct {
              intermediate_dim, head_dim, block_size;
     uint32_t quant_type, activation, norm_type, pos_enc_type, ffn_type, attn_type;
     uint32_t has_bias, weight_tied, num_experts, num_active_experts, expert_intermediate_dim;
+    uint32_t moe_norm_topk;
     float    rope_theta, norm_epsilon;
     uint32_t num_tensors;        /* tensor records in all layers */
     uint32_t has_embedding;
     uint32_t crc_mismatches;     /* header, layers, embedding, final section */
     uint32_t size_mismatch;      /* total_file_size differs from the file */
+    uint32_t moe_layers;         /* layers given a device MXFP4 expert table */
     size_t   device_bytes;       /* bytes uploaded to HBM */
 } qsf_hip_model_info;
 /* Load an uncompressed QSF file: validate the header (src/format.c:37-99),
@@ -178,6 +184,10 @@ const uint16_t* qsf_hip_model_embedding_fp16(const qsf_hip_model* m);
 const qsf_hip_tensor* qsf_hip_model_output_head(const qsf_hip_model* m);
 /* Final norm weight (and bias, NULL when absent) as device fp32. */
 const float* qsf_hip_model_final_norm(const qsf_hip_model* m, const float** bias);
+/* Device expert table of an MoE layer (ffn_type 3, num_experts > 1) whose
+ * gate/up/down experts are all MXFP4, built at load with their FP16 biases
+ * (src/engine.c:1024-1107); NULL otherwise.  Owned by the model. */
+struct qsf_hip_moe* qsf_hip_model_moe(const qsf_hip_model* m, int layer);
 
 /* ---- MoE FFN with MXFP4 experts (src/engine.c:951-1107) ------------------ */
 typedef struct qsf_hip_moe qsf_hip_moe;         /* opaque device expert table */

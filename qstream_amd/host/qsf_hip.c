@@ -521,6 +521,25 @@ int qsf_hip_arena_forget(const void* host) {
     return found ? E_OK : E_INVALID;
 }
 
+int qsf_hip_arena_forget_range(const void* base, size_t bytes) {
+    const uintptr_t lo = (uintptr_t)base, hi = lo + bytes;
+    int n = 0;
+    pthread_mutex_lock(&g_lock);
+    /* collect first: reg_drop moves entries of a probe run */
+    const void** keys = g_reg_n ? malloc(g_reg_n * sizeof *keys) : NULL;
+    if (g_reg_n && !keys) {
+        pthread_mutex_unlock(&g_lock);
+        return -fail(E_OOM, "qsf_hip_arena_forget_range");
+    }
+    for (size_t i = 0; i < g_reg_cap; i++)
+        if (g_reg[i].key && (uintptr_t)g_reg[i].key >= lo && (uintptr_t)g_reg[i].key < hi)
+            keys[n++] = g_reg[i].key;
+    for (int i = 0; i < n; i++) reg_drop(keys[i]);
+    free(keys);
+    pthread_mutex_unlock(&g_lock);
+    return n;
+}
+
 size_t qsf_hip_arena_bytes(void) { return g_dev.arena_bytes; }
 size_t qsf_hip_tensor_payload_bytes(const qsf_hip_tensor* t) { return t ? t->payload_bytes : 0; }
 

@@ -105,6 +105,7 @@ typedef struct {
 typedef struct {
     int n;
     rec_t* recs;
+    qsf_hip_moe* moe;    /* MXFP4 expert table of an MoE layer, or NULL */
 } layer_t;
 
 struct qsf_hip_model {
@@ -126,6 +127,7 @@ static void free_model(qsf_hip_model* m) {
                 qsf_host_device_free(m->layers[l].recs[i].d_vec);
             }
             free(m->layers[l].recs);
+            qsf_hip_moe_free(m->layers[l].moe);
         }
         free(m->layers);
     }
@@ -138,6 +140,13 @@ static void free_model(qsf_hip_model* m) {
 }
 
 void qsf_hip_model_free(qsf_hip_model* m) { free_model(m); }
+
+/* first record of a tensor type in a layer (find_tensor, src/engine.c:183-202) */
+static const rec_t* find_rec_in(const layer_t* L, int type) {
+    for (int i = 0; i < L->n; i++)
+        if (L->recs[i].type == (uint16_t)type) return &L->recs[i];
+    return NULL;
+}
 
 static int warn_crc(qsf_hip_model* m, const char* what, uint32_t got, uint32_t want) {
     fprintf(stderr, "[qsf_hip] %s CRC mismatch (got 0x%08X, expected 0x%08X)\n", what, got, want);
@@ -171,6 +180,7 @@ static int parse_header(const uint8_t* h, size_t fsize, qsf_hip_model_info* in) 
     in->weight_tied = h[143] == 1 || le32(h + 156) == 1;
     in->num_experts = h[173];
     in->num_active_experts = h[174];
+    in->moe_norm_topk = h[175];
     in->expert_intermediate_dim = le32(h + 177);
     if (in->num_layers == 0 || in->num_layers > 1000u)
         return qsf_host_fail(E_INVALID_MODEL, "qsf_hip_model_load: invalid num_layers %u", in->num_layers);
@@ -360,6 +370,52 @@ static int load_mapped(qsf_hip_model* m, const uint8_t* f, size_t fsize) {
             }
         }
     }
+    /* MoE layers whose experts are all MXFP4: one device expert table per
+     * layer (gate/up/down tensors and their FP16 biases, the
+     * QSF_MOE_*(e) records of include/qsf/types.h:145-162) */
+    if (in->ffn_type == 3 && in->num_experts > 1) {
+        const int ne = (int)in->num_experts;
+        const int eid = (int)(in->expert_intermediate_dim ? in->expert_intermediate_dim
+                                                          : in->intermediate_dim);
+        const qsf_hip_tensor** tt = calloc((size_t)ne * 3, sizeof *tt);
+        const uint16_t** bb = calloc((size_t)ne * 3, sizeof *bb);
+        if (!tt || !bb) {
+            free(tt);
+            free(bb);
+            return qsf_host_fail(E_OOM, "qsf_hip_model_load: expert tables");
+        }
+        for (uint32_t l = 0; l < in->num_layers && !rc; l++) {
+            int all = 1;
+            for (int e = 0; e < ne && all; e++) {
+                for (int j = 0; j < 3; j++) {
+                    const rec_t* w = find_rec_in(&m->layers[l], 23 + 6 * e + 2 * j);
+                    const rec_t* b = find_rec_in(&m->layers[l], 24 + 6 * e + 2 * j);
+                    if (!w || w->qt != QSF_HIP_QUANT_MXFP4) {
+                        all = 0;
+                        break;
+                    }
+                    const uint32_t blen = j < 2 ? (uint32_t)eid : in->hidden_dim;
+                    tt[3 * e + j] = w->t;
+                    bb[3 * e + j] = b && b->qt == 7 && b->data_size >= 2 * blen ? (const uint16_t*)b->data
+                                                                               : NULL;
+                }
+            }
+            if (!all) continue;
+            /* the bias vectors are copied from the mapping at creation */
+            const qsf_hip_tensor *g[256], *u[256], *d[256];
+            const uint16_t *gb[256], *ub[256], *db[256];
+            for (int e = 0; e < ne; e++) {
+                g[e] = tt[3 * e]; u[e] = tt[3 * e + 1]; d[e] = tt[3 * e + 2];
+                gb[e] = bb[3 * e]; ub[e] = bb[3 * e + 1]; db[e] = bb[3 * e + 2];
+            }
+            m->layers[l].moe = qsf_hip_moe_create(ne, hd, eid, g, u, d, gb, ub, db);
+            if (!m->layers[l].moe) rc = qsf_hip_last_error() ? qsf_hip_last_error() : E_INVALID_MODEL;
+            else in->moe_layers++;
+        }
+        free(tt);
+        free(bb);
+        if (rc) return rc;
+    }
     if (emb) {
         if (emb_qt == 7) {
             size_t nb = (size_t)in->vocab_size * hd * 2;
@@ -429,10 +485,12 @@ int qsf_hip_model_get_info(const qsf_hip_model* m, qsf_hip_model_info* out) {
 
 static const rec_t* find_rec(const qsf_hip_model* m, int layer, int type) {
     if (!m || layer < 0 || (uint32_t)layer >= m->info.num_layers) return NULL;
-    const layer_t* L = &m->layers[layer];
-    for (int i = 0; i < L->n; i++)
-        if (L->recs[i].type == (uint16_t)type) return &L->recs[i];
-    return NULL;
+    return find_rec_in(&m->layers[layer], type);
+}
+
+qsf_hip_moe* qsf_hip_model_moe(const qsf_hip_model* m, int layer) {
+    if (!m || layer < 0 || (uint32_t)layer >= m->info.num_layers) return NULL;
+    return m->layers[layer].moe;
 }
 
 const qsf_hip_tensor* qsf_hip_model_tensor(const qsf_hip_model* m, int layer, int tensor_type) {

@@ -301,7 +301,14 @@ QSF_MAGIC = 0x51534631
 T_ATTN_Q, T_ATTN_K, T_ATTN_V, T_ATTN_O = 0, 1, 2, 3
 T_FFN_GATE, T_FFN_UP, T_FFN_DOWN = 4, 5, 6
 T_ATTN_NORM_W, T_FFN_NORM_W = 7, 9
+T_MOE_ROUTER, T_MOE_ROUTER_BIAS = 21, 22
 FP16 = 7
+FFN_MOE = 3
+
+
+def t_moe(e: int, role: str, bias: bool = False) -> int:
+    """QSF_MOE_{GATE,UP,DOWN}[_BIAS](e) (include/qsf/types.h:145-162)."""
+    return 23 + 6 * e + {"gate": 0, "up": 2, "down": 4}[role] + (1 if bias else 0)
 
 
 def _crc32(b: bytes) -> int:
@@ -320,7 +327,8 @@ def write_qsf(path: str, *, hidden: int, heads: int, vocab: int, inter: int, lay
               embedding=None, final_norm=None, output_head=None, tied: bool = False,
               activation: int = 2, norm_type: int = 2, pos_enc: int = 1, ffn_type: int = 1,
               rope_theta: float = 10000.0, eps: float = 1e-5, layer_crc: bool = True,
-              header_crc: bool = True, compression=None) -> dict:
+              header_crc: bool = True, compression=None, num_experts: int = 0,
+              num_active_experts: int = 0, moe_norm_topk: int = 0, expert_dim: int = 0) -> dict:
     """Write a QSF file.  layers: per layer a list of (tensor_type, qt, rows,
     cols, payload); embedding: (qt, payload) of a [vocab][hidden] table;
     final_norm: fp16 array [hidden]; output_head: payload of a separate
@@ -371,8 +379,9 @@ def write_qsf(path: str, *, hidden: int, heads: int, vocab: int, inter: int, lay
     struct.pack_into("<BBBB", h, 140, 0, ffn_type, 0, 1 if tied else 0)
     struct.pack_into("<I", h, 156, 1 if tied else 0)
     struct.pack_into("<Q", h, 160, len(body))
-    struct.pack_into("<I", h, 168, _crc32(bytes(h[:168])) if header_crc else 0)
     h[172] = 1
+    struct.pack_into("<BBBBI", h, 173, num_experts, num_active_experts, moe_norm_topk, 0, expert_dim)
+    struct.pack_into("<I", h, 168, _crc32(bytes(h[:168])) if header_crc else 0)
     body[:256] = h
     with open(path, "wb") as f:
         f.write(body)

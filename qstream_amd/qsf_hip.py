@@ -29,7 +29,7 @@ EXPORTS = (
     "qsf_matvec_4bit_sym_hip", "qsf_matvec_outlier_2bit_hip", "qsf_matvec_outlier_4bit_hip",
     "qsf_matvec_mxfp4_hip", "qsf_kernels_init_hip",
     "qsf_hip_tensor_upload", "qsf_hip_tensor_lookup", "qsf_hip_tensor_free",
-    "qsf_hip_arena_forget", "qsf_hip_arena_bytes", "qsf_hip_tensor_payload_bytes",
+    "qsf_hip_arena_forget", "qsf_hip_arena_forget_range", "qsf_hip_arena_bytes", "qsf_hip_tensor_payload_bytes",
     "qsf_hip_matvec_dev", "qsf_hip_matvec_group_dev", "qsf_hip_xprep_bytes",
     "qsf_hip_xprep_dev", "qsf_hip_matvec_group_prepared_dev",
     "qsf_hip_moe_create", "qsf_hip_moe_free", "qsf_hip_moe_forward_dev",
@@ -40,7 +40,7 @@ EXPORTS = (
     "qsf_hip_residual_dev", "qsf_hip_embed_row_dev", "qsf_hip_embed_row_fp16_dev",
     "qsf_hip_crc32", "qsf_hip_model_load", "qsf_hip_model_free", "qsf_hip_model_get_info",
     "qsf_hip_model_tensor", "qsf_hip_model_vector", "qsf_hip_model_embedding",
-    "qsf_hip_model_embedding_fp16", "qsf_hip_model_output_head", "qsf_hip_model_final_norm",
+    "qsf_hip_model_embedding_fp16", "qsf_hip_model_output_head", "qsf_hip_model_final_norm", "qsf_hip_model_moe",
 )
 
 _lib = None
@@ -80,6 +80,7 @@ def load(path: str = LIB_PATH) -> C.CDLL:
     L.qsf_hip_tensor_lookup.restype = _vp
     L.qsf_hip_tensor_free.argtypes = [_vp]
     L.qsf_hip_arena_forget.argtypes = [_vp]
+    L.qsf_hip_arena_forget_range.argtypes = [_vp, C.c_size_t]
     L.qsf_hip_arena_bytes.restype = C.c_size_t
     L.qsf_hip_tensor_payload_bytes.argtypes = [_vp]
     L.qsf_hip_tensor_payload_bytes.restype = C.c_size_t
@@ -137,6 +138,8 @@ def load(path: str = LIB_PATH) -> C.CDLL:
         getattr(L, n).restype = _vp
     L.qsf_hip_model_final_norm.argtypes = [_vp, C.POINTER(_vp)]
     L.qsf_hip_model_final_norm.restype = _vp
+    L.qsf_hip_model_moe.argtypes = [_vp, _i]
+    L.qsf_hip_model_moe.restype = _vp
     L.qsf_hip_kernel_timing.argtypes = [_i]
     L.qsf_hip_kernel_timing.restype = _i
     L.qsf_hip_kernel_timing_read.argtypes = [C.POINTER(C.c_float), _i]
@@ -198,6 +201,12 @@ def arena_forget(payload) -> bool:
     False when the buffer was not registered."""
     a = payload if isinstance(payload, np.ndarray) else np.frombuffer(payload, np.uint8)
     return load().qsf_hip_arena_forget(a.ctypes.data) == 0
+
+
+def arena_forget_range(buf) -> int:
+    """Forget every registered pointer inside a host buffer; returns how many."""
+    a = buf if isinstance(buf, np.ndarray) else np.frombuffer(buf, np.uint8)
+    return load().qsf_hip_arena_forget_range(a.ctypes.data, a.nbytes)
 
 
 class KernelTable:
@@ -394,10 +403,10 @@ class ModelInfo(C.Structure):
         "num_layers", "hidden_dim", "num_heads", "num_kv_heads", "vocab_size", "max_seq_len",
         "intermediate_dim", "head_dim", "block_size", "quant_type", "activation", "norm_type",
         "pos_enc_type", "ffn_type", "attn_type", "has_bias", "weight_tied", "num_experts",
-        "num_active_experts", "expert_intermediate_dim")] + [
+        "num_active_experts", "expert_intermediate_dim", "moe_norm_topk")] + [
         ("rope_theta", C.c_float), ("norm_epsilon", C.c_float), ("num_tensors", C.c_uint32),
         ("has_embedding", C.c_uint32), ("crc_mismatches", C.c_uint32),
-        ("size_mismatch", C.c_uint32), ("device_bytes", C.c_size_t)]
+        ("size_mismatch", C.c_uint32), ("moe_layers", C.c_uint32), ("device_bytes", C.c_size_t)]
 
 
 def crc32(data: bytes) -> int:
@@ -444,6 +453,16 @@ class Model:
     def output_head(self):
         h = load().qsf_hip_model_output_head(self.handle)
         return _Ref(h) if h else None
+
+    def moe(self, layer: int):
+        """The layer's device MXFP4 expert table (forward like Moe), or None."""
+        h = load().qsf_hip_model_moe(self.handle, layer)
+        if not h:
+            return None
+        m = Moe.__new__(Moe)
+        m.handle, m._keep = h, [self]
+        m.free = lambda: None          # owned by the model
+        return m
 
     def final_norm(self):
         b = _vp()

@@ -409,6 +409,12 @@ def test_slot_reused_buffer_forget_and_volatile(hip, oracle, qt):
     buf[:] = c
     run_and_check(c)
     assert hip.arena_forget(buf) and not hip.arena_forget(buf)
+    # the range form, as after an LZ4 layer is decompressed again
+    run_and_check(c)
+    buf[:] = b
+    # >= 1: keys that earlier, freed arrays left inside this address range go too
+    assert hip.arena_forget_range(buf) >= 1 and hip.arena_forget_range(buf) == 0
+    run_and_check(b)
 
 
 def test_slot_x_reuse_between_calls(hip, oracle):
