@@ -215,12 +215,18 @@ int qsf_hip_moe_forward_dev(qsf_hip_moe* m, int top_k, int norm_topk, int activa
 /* Batched prefill through the 4-bit format (no reference kernel: the engine
  * runs one qsf_matvec_4bit call per token, src/engine.c:1289-1295):
  * d_y[m][rows] = W . float(d_x[m][cols]) for m tokens.  W is a 4-bit
- * asymmetric tensor (block 64, 128 or 256, no outliers); its weights are
- * dequantised in registers, s*q + z exactly in fp32, rounded to bf16
- * (round-to-nearest-even) and contracted on MFMA in fp32.  d_x is bf16
- * [m][cols] (16-byte aligned, cols >= 32, cols % 8 == 0); asynchronous on
- * `stream`.  Uses the library workspace (x repacked, about 2*m*cols bytes):
- * calls must not overlap with other workspace users on other streams. */
+ * asymmetric tensor (block 64, 128 or 256, no outliers).  Per block,
+ * s * (sum q x) + z * (sum x): the integer codes (exact in bf16) meet bf16 x
+ * on MFMA with fp32 accumulation, the scale is applied in fp32 every 64
+ * codes, and the zero-point term runs on exact bf16 splits of z and of the
+ * block sums; nothing is rounded below fp32 (about 1e-6 rel-L2 against the
+ * scalar matvec on float(x)).  d_x is bf16 [m][cols] (16-byte aligned,
+ * cols >= 32, cols % 8 == 0); asynchronous on `stream`.  Uses the library
+ * workspace (x repacked into fragment order with the block-sum splits,
+ * about 2*m*cols bytes plus 16 per block and token): calls must not overlap
+ * with other workspace users on other streams.  The workspace grows as
+ * needed; an outgrown one is kept until qsf_hip_shutdown, so graphs
+ * captured with it stay valid. */
 int qsf_hip_prefill_4bit_dev(const qsf_hip_tensor* t, const uint16_t* d_x_bf16, int m,
                              float* d_y, void* stream);
 
