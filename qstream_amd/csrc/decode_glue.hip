@@ -194,6 +194,93 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_part_kernel(
     }
 }
 
+// The same chunk result for head_dim = 16 HC in {64, 128, 256}, with every
+// K and V byte of the chunk (and its scales) requested before any is used:
+// the chunk arrives in one memory round trip instead of one a 16-byte K load
+// and one a V position.  Two threads a position for the scores (half a row
+// each); for the weighted V each thread keeps 16 output dims of the 16-byte
+// pieces it loaded (ATT_THREADS % HC == 0, so always the same 16), summed
+// over threads through LDS.  Positions past the chunk end load the last
+// valid row and are masked.
+template <int HC>
+__global__ __launch_bounds__(ATT_THREADS) void attention_part_fast_kernel(
+    const float* __restrict__ q, const int8_t* __restrict__ kc, const int8_t* __restrict__ vc,
+    const float* __restrict__ ks, const float* __restrict__ vs, int max_seq, int groups, int seq,
+    int nsplit, float* __restrict__ ws) {
+    constexpr int HD = 16 * HC, KH = HC / 2, VJ = ATT_CHUNK * HC / ATT_THREADS;
+    static_assert(HD <= ATT_THREADS && ATT_THREADS % HC == 0, "one q element a thread");
+    __shared__ float qs[HD];
+    __shared__ float ew[ATT_CHUNK];                      // exp(score - m) * v_scale per position
+    __shared__ float red[ATT_THREADS / 64];
+    __shared__ float part[ATT_THREADS][17];
+    const int h = blockIdx.x, chunk = blockIdx.y, kvh = h / groups, t = threadIdx.x;
+    const int p0 = chunk * ATT_CHUNK, np = min(ATT_CHUNK, seq - p0);
+    const size_t row0 = (size_t)kvh * max_seq + p0;
+    // 1. all loads
+    const int kp = t >> 1, kh = t & 1;
+    const int kpc = min(kp, np - 1);
+    const att_u32x4* kr = reinterpret_cast<const att_u32x4*>(kc + (row0 + kpc) * HD) + kh * KH;
+    att_u32x4 kv[KH];
+#pragma unroll
+    for (int j = 0; j < KH; j++) kv[j] = kr[j];
+    const float kscale = ks[row0 + kpc];
+    const float vscale = vs[row0 + kpc];
+    const att_u32x4* vr = reinterpret_cast<const att_u32x4*>(vc + row0 * HD);
+    att_u32x4 vv[VJ];
+#pragma unroll
+    for (int j = 0; j < VJ; j++) {
+        const int i = t + ATT_THREADS * j;
+        vv[j] = vr[min(i / HC, np - 1) * HC + i % HC];
+    }
+    if (t < HD) qs[t] = q[(size_t)h * HD + t];
+    __syncthreads();
+    // 2. scores and the chunk's softmax terms
+    const float inv_sqrt_d = __fdiv_rn(1.0f, __fsqrt_rn((float)HD));
+    float dot = 0.f;
+#pragma unroll
+    for (int j = 0; j < KH; j++)
+#pragma unroll
+        for (int b = 0; b < 16; b++)
+            dot = fmaf(qs[16 * (kh * KH + j) + b], __fmul_rn(sbyte(kv[j][b >> 2], b & 3), kscale), dot);
+    dot += __shfl_xor(dot, 1, 64);
+    const bool mine = kh == 0 && kp < np;
+    const float sc = kp < np ? __fmul_rn(dot, inv_sqrt_d) : -INFINITY;
+    float m = sc;
+    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+    if ((t & 63) == 0) red[t >> 6] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    const float e = mine ? expf(sc - m) : 0.f;
+    if (mine) ew[kp] = __fmul_rn(e, vscale);
+    const float l = block_sum(e, red);                   // also orders the ew writes
+    // 3. weighted V: dims 16 (t % HC) .. +15 of the thread's pieces
+    float acc[16];
+#pragma unroll
+    for (int b = 0; b < 16; b++) acc[b] = 0.f;
+#pragma unroll
+    for (int j = 0; j < VJ; j++) {
+        const int p = (t + ATT_THREADS * j) / HC;
+        const float w = p < np ? ew[p] : 0.f;
+#pragma unroll
+        for (int b = 0; b < 16; b++) acc[b] = fmaf(w, sbyte(vv[j][b >> 2], b & 3), acc[b]);
+    }
+#pragma unroll
+    for (int b = 0; b < 16; b++) part[t][b] = acc[b];
+    __syncthreads();
+    float* rec = ws + ((size_t)h * nsplit + chunk) * (HD + 2);
+    if (t < HD) {
+        const int c = t >> 4, b = t & 15;
+        float o = 0.f;
+#pragma unroll
+        for (int r = 0; r < ATT_THREADS / HC; r++) o += part[c + HC * r][b];
+        rec[2 + t] = o;
+    }
+    if (t == 0) {
+        rec[0] = m;
+        rec[1] = l;
+    }
+}
+
 __global__ __launch_bounds__(256) void attention_combine_kernel(const float* __restrict__ ws,
                                                                 int head_dim, int nsplit,
                                                                 float* __restrict__ out) {
@@ -331,8 +418,26 @@ extern "C" int qk_attention(const float* q, const int8_t* kc, const int8_t* vc, 
         n_heads % n_kv)
         return -2;
     const int nsplit = (seq + ATT_CHUNK - 1) / ATT_CHUNK;
-    hipLaunchKernelGGL(attention_part_kernel, dim3(n_heads, nsplit), dim3(ATT_THREADS), 0, s, q, kc, vc,
-                       ks, vs, max_seq, n_heads / n_kv, head_dim, seq, nsplit, (float*)ws);
+    const dim3 grid(n_heads, nsplit), block(ATT_THREADS);
+    const int groups = n_heads / n_kv;
+    float* part = (float*)ws;
+    switch (head_dim) {
+    case 64:
+        hipLaunchKernelGGL(attention_part_fast_kernel<4>, grid, block, 0, s, q, kc, vc, ks, vs, max_seq,
+                           groups, seq, nsplit, part);
+        break;
+    case 128:
+        hipLaunchKernelGGL(attention_part_fast_kernel<8>, grid, block, 0, s, q, kc, vc, ks, vs, max_seq,
+                           groups, seq, nsplit, part);
+        break;
+    case 256:
+        hipLaunchKernelGGL(attention_part_fast_kernel<16>, grid, block, 0, s, q, kc, vc, ks, vs, max_seq,
+                           groups, seq, nsplit, part);
+        break;
+    default:
+        hipLaunchKernelGGL(attention_part_kernel, grid, block, 0, s, q, kc, vc, ks, vs, max_seq, groups,
+                           head_dim, seq, nsplit, part);
+    }
     hipLaunchKernelGGL(attention_combine_kernel, dim3(n_heads), dim3(256), 0, s, (const float*)ws,
                        head_dim, nsplit, out);
     return hipGetLastError() == hipSuccess ? 0 : -1;

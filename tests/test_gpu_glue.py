@@ -85,8 +85,12 @@ def test_kv_store_bit_exact(hip, oracle):
     assert np.array_equal(host(dvs).view(np.uint32), vs.view(np.uint32))
 
 
+# head_dim 64, 128 and 256 take the load-everything-first kernel, others the
+# general one; positions 129 and 300 leave a partial last chunk of 128
 @pytest.mark.parametrize("nh,nkv,hd,position", [(32, 32, 128, 0), (32, 32, 128, 1023),
-                                                (32, 8, 128, 300), (8, 2, 64, 4095)])
+                                                (32, 8, 128, 300), (8, 2, 64, 4095),
+                                                (32, 8, 128, 129), (4, 4, 256, 700),
+                                                (6, 2, 80, 200), (2, 1, 64, 0)])
 def test_attention(hip, oracle, nh, nkv, hd, position):
     torch = torch_cuda()
     rng = np.random.default_rng(nh + position)
