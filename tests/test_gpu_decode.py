@@ -462,3 +462,40 @@ def test_slot_x_reuse_between_calls(hip, oracle):
     _slot(hip, qt)(p, x[:short].copy(), out, rows, short, bs)
     assert rel_l2(out, oracle.matvec(qt, p, x[:short], rows, short, bs)) <= REL_L2
     check(2, x)
+
+
+@pytest.mark.parametrize("qt,bs", [(F.Q2_OUTLIER, 64), (F.Q4_OUTLIER, 64)])
+def test_outlier_rows_across_pass_boundaries(hip, oracle, qt, bs):
+    """A 64-lane row group takes a row's first 64 outlier entries in one pass
+    (one entry a lane) and the rest in further passes.  Rows with 0, 1, 63,
+    64, 65, 100, 128 and 129 entries straddle those boundaries, among rows of
+    2 or 0; duplicates and an out-of-range entry as usual.  Both the device
+    path and the table slot, and every row on its own."""
+    torch = torch_cuda()
+    rows, cols = 300, 4096
+    rng = np.random.default_rng(61 + qt)
+    base = F.Q2 if qt == F.Q2_OUTLIER else F.Q4
+    counts = {3: 1, 10: 63, 11: 64, 12: 65, 13: 100, 14: 128, 15: 129, 299: 100, 150: 7}
+    idx, vals = [], []
+    for r in range(rows):
+        c = counts.get(r, 2 if r % 5 else 0)
+        cs = rng.choice(cols, size=c, replace=False)
+        idx += [r * cols + int(k) for k in cs]
+        vals += list(rng.standard_normal(c) * 0.5)
+    idx += [15 * cols + 7, 15 * cols + 7, rows * cols + 5]      # duplicate pair, out of range
+    vals += [1.0, 2.0, 9.0]
+    w = F.gaussian(rng, (rows, cols), 0.02)
+    blocks = F.quantize_blocks(F._row_blocks(w, bs), base).tobytes()
+    payload = F.outlier_payload(np.array(idx, np.uint32),
+                                np.array(vals, np.float16).view(np.uint16), blocks)
+    x = F.gaussian(rng, cols)
+    ref = oracle.matvec(qt, payload, x, rows, cols, bs)
+    t = hip.Tensor(payload, qt, rows, cols, bs)
+    y = torch.full((rows,), float("nan"), device="cuda:0")
+    t.matvec(dev(x), y, stream=_stream())
+    assert rel_l2(host(y), ref) <= REL_L2, "device"
+    t.free()
+    out = np.full(rows, np.nan, np.float32)
+    _slot(hip, qt)(payload, x, out, rows, cols, bs)
+    assert rel_l2(out, ref) <= REL_L2, "slot"
+    np.testing.assert_allclose(out, ref, rtol=1e-4, atol=1e-4 * np.abs(ref).max())
