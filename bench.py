@@ -445,10 +445,11 @@ def bench_layers(torch, hip, steps, warmup, with_cpu=True, cpu_budget=10.0):
 def bench_decode_layer(torch, hip, steps, warmup, position=1023):
     """One device-resident 7B decoder layer step per step (LLaMA-7B shapes:
     hidden 4096, 32 heads of 128, intermediate 11008, 3-bit block 128
-    weights): RMSNorm, q/k/v (one grouped launch), RoPE, int8 KV store,
-    attention over `position` + 1 cached positions, o, residual, RMSNorm,
-    gate/up (grouped), SiLU x up, down, residual + NaN check -- 12 launches,
-    no host round trip.  Steps cycle over 32 layers' distinct weights and
+    weights): q/k/v (one grouped launch) on the normed input, RoPE + int8 KV
+    store (one launch), attention over `position` + 1 cached positions (two
+    launches), o, residual + NaN check + FFN RMSNorm (one launch), gate/up
+    (grouped), SiLU x up, down, residual + NaN check + the next layer's
+    attention RMSNorm (one launch) -- 10 launches, no host round trip.  Steps cycle over 32 layers' distinct weights and
     KV caches (2.9 GB), so neither stays in the MALL.  Bytes per step: the
     layer's weight payloads, the KV rows attention reads, activations."""
     qt, bs, mats = cfg2_layer()
@@ -474,20 +475,19 @@ def bench_decode_layer(torch, hip, steps, warmup, position=1023):
     def step(i, stream):
         li = i % n_layers
         ts = layers[li]
-        hip.rms_norm(res, x, an_w, 1e-5, stream=stream)
         hip.matvec_group(ts[0:3], x, [ys["q"], ys["k"], ys["v"]], stream=stream)
-        rope.apply(ys["q"], ys["k"], nh, nh, position, stream=stream)
-        hip.kv_store(kcs[li], vcs[li], kss[li], vss[li], max_seq, nh, hd, position, ys["k"], ys["v"],
-                     stream=stream)
+        rope.apply_and_store(ys["q"], ys["k"], ys["v"], nh, nh, position, kcs[li], vcs[li], kss[li],
+                             vss[li], max_seq, stream=stream)
         hip.attention(ys["q"], kcs[li], vcs[li], kss[li], vss[li], max_seq, nh, nh, hd, position, attn,
                       stream=stream)
         hip.matvec_group(ts[3:4], attn, [ys["o"]], stream=stream)
-        hip.residual(res, ys["o"], None, stream=stream)
-        hip.rms_norm(res, x, fn_w, 1e-5, stream=stream)
+        hip.residual_norm(res, ys["o"], fn_w, 1e-5, x, stream=stream)
         hip.matvec_group(ts[4:6], x, [ys["gate"], ys["up"]], stream=stream)
         hip.act_mul(ys["gate"], ys["up"], 2, stream=stream)
         hip.matvec_group(ts[6:7], ys["gate"], [ys["down"]], stream=stream)
-        hip.residual(res, ys["down"], bad, stream=stream)
+        hip.residual_norm(res, ys["down"], an_w, 1e-5, x, bad=bad, stream=stream)
+
+    hip.rms_norm(res, x, an_w, 1e-5, stream=torch.cuda.current_stream())   # the first layer's input
 
     for i in range(warmup):
         step(i, torch.cuda.current_stream())
@@ -723,7 +723,7 @@ def run_config(torch, hip, key: str, args, cpu_budget: float, cache: dict) -> di
                          "int8 KV cache)",
                     config={"workload": f"device-resident 7B decoder layer step (3-bit block 128), "
                                         f"attention over {r['position'] + 1} cached positions, "
-                                        f"12 launches",
+                                        f"10 launches (residual + norm and RoPE + KV store fused)",
                             "us_per_layer": round(r["ms_per_step"] * 1e3, 3),
                             "bytes_per_step": r["bytes_per_step"], "weight_bytes": r["weight_bytes"],
                             "kv_bytes": r["kv_bytes"],

@@ -287,6 +287,19 @@ int qsf_hip_act_mul_dev(float* d_gate, const float* d_up, int n, int activation,
  * src/engine.c:1176-1187: *d_bad = first index holding NaN or |v| > 1e30,
  * or -1 (written on every call; nothing to clear beforehand). */
 int qsf_hip_residual_dev(float* d_res, const float* d_x, int n, int* d_bad, void* stream);
+/* Fused forms of the sequences a layer step runs back to back; each equals
+ * its separate calls bit for bit, in one launch instead of two.
+ * Residual + NaN check + the next norm: res += x (src/engine.c:937, 1174),
+ * the check of 1176-1187 into d_bad (may be NULL), then d_out = norm(res)
+ * (RMS, or layer norm with d_b when layer_norm != 0; 940-948, 805-815). */
+int qsf_hip_residual_norm_dev(float* d_res, const float* d_x, int n, int* d_bad, const float* d_w,
+                              const float* d_b, float eps, int layer_norm, float* d_out, void* stream);
+/* RoPE of q and k (apply_rope, src/engine.c:204-235) and the int8 KV store
+ * of the rotated k and of v at `position` (kv_cache_store, 240-300);
+ * head_dim <= 256. */
+int qsf_hip_rope_kv_store_dev(const qsf_hip_rope* r, float* d_q, float* d_k, const float* d_v,
+                              int n_heads, int n_kv_heads, int position, int8_t* d_kc, int8_t* d_vc,
+                              float* d_ks, float* d_vs, int max_seq, void* stream);
 /* Embedding lookup, src/engine.c:709-765: row `token` of a blockwise table
  * uploaded with qsf_hip_tensor_upload (rows = vocab, cols = hidden),
  * dequantised bit-exactly; or of an FP16 table [vocab][hd] in device memory. */

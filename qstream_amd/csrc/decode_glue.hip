@@ -340,6 +340,133 @@ __global__ __launch_bounds__(1024) void residual_kernel(float* res, const float*
     }
 }
 
+// Residual add + NaN check, then the next norm of the updated residual, in
+// one workgroup: the engine's sequence res += x (src/engine.c:937 / 1174),
+// check (1176-1187), norm (940-948 / 805-815).  Each thread walks the same
+// elements as residual_kernel and norm_kernel, so the results equal those
+// two launches bit for bit.
+template <bool LAYER>
+__global__ __launch_bounds__(NORM_THREADS) void residual_norm_kernel(
+    float* res, const float* __restrict__ x, int n, int* bad, const float* __restrict__ w,
+    const float* __restrict__ b, float eps, float* out) {
+    __shared__ int ired[NORM_THREADS / 64];
+    __shared__ float red[NORM_THREADS / 64];
+    int first = n;
+    float acc = 0.f;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        const float r = __fadd_rn(res[i], x[i]);
+        res[i] = r;
+        if ((r != r || r > 1e30f || r < -1e30f) && i < first) first = i;
+        acc = LAYER ? acc + r : fmaf(r, r, acc);
+    }
+    if (bad) {
+        for (int off = 32; off > 0; off >>= 1) first = min(first, __shfl_xor(first, off, 64));
+        if ((threadIdx.x & 63) == 0) ired[threadIdx.x >> 6] = first;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            int f = n;
+            for (int wv = 0; wv < (int)(blockDim.x >> 6); wv++) f = min(f, ired[wv]);
+            *bad = f < n ? f : -1;
+        }
+    }
+    if (!LAYER) {
+        const float ss = block_sum(acc, red);
+        const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)n), eps)));
+        for (int i = threadIdx.x; i < n; i += blockDim.x) out[i] = __fmul_rn(__fmul_rn(res[i], inv), w[i]);
+    } else {
+        const float mean = __fdiv_rn(block_sum(acc, red), (float)n);
+        float v = 0.f;
+        for (int i = threadIdx.x; i < n; i += blockDim.x) {
+            const float d = res[i] - mean;
+            v = fmaf(d, d, v);
+        }
+        const float var = __fdiv_rn(block_sum(v, red), (float)n);
+        const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(var, eps)));
+        for (int i = threadIdx.x; i < n; i += blockDim.x) {
+            float o = __fmul_rn(__fmul_rn(__fsub_rn(res[i], mean), inv), w[i]);
+            if (b) o = __fadd_rn(o, b[i]);
+            out[i] = o;
+        }
+    }
+}
+
+// RoPE of q and k and the int8 KV store of k (rotated) and v in one launch:
+// one wave per q head (rotate), per kv head's k (rotate, then store) and
+// per kv head's v (store).  The rotation is rope_kernel's arithmetic and the
+// store kv_store_kernel's, so q, k and the cache rows equal the two
+// launches bit for bit (absmax and the per-element codes do not depend on
+// the order elements are visited).  head_dim <= 256: two pairs a lane.
+__device__ __forceinline__ void rope_pair(float& a0, float& a1, const float* __restrict__ freq, int j,
+                                          int position) {
+    double ang = (double)position * (double)freq[j];
+    ang = fmod(ang, 2.0 * 3.14159265358979323846);
+    const float c = cosf((float)ang), sn = sinf((float)ang);
+    const float x0 = a0, x1 = a1;
+    a0 = __fsub_rn(__fmul_rn(x0, c), __fmul_rn(x1, sn));
+    a1 = __fadd_rn(__fmul_rn(x0, sn), __fmul_rn(x1, c));
+}
+
+__device__ __forceinline__ int8_t kv_code(float x, float inv) {
+    x = __fmul_rn(x, inv);
+    if (x > 127.0f) x = 127.0f;
+    if (x < -127.0f) x = -127.0f;
+    return (int8_t)(int)__fadd_rn(x, x >= 0 ? 0.5f : -0.5f);
+}
+
+__global__ __launch_bounds__(64) void rope_kv_kernel(float* q, float* k, const float* __restrict__ v,
+                                                     const float* __restrict__ freq, int head_dim,
+                                                     int n_heads, int position, int8_t* kc, int8_t* vc,
+                                                     float* ks, float* vs, int max_seq) {
+    const int lane = threadIdx.x, hp = head_dim / 2;
+    if ((int)blockIdx.x < n_heads) {
+        float* qh = q + (size_t)blockIdx.x * head_dim;
+        for (int j = lane; j < hp; j += 64) rope_pair(qh[2 * j], qh[2 * j + 1], freq, j, position);
+        return;
+    }
+    const int idx = (int)blockIdx.x - n_heads, h = idx >> 1, isv = idx & 1;
+    const size_t row = (size_t)h * max_seq + position;
+    float val[2][2] = {{0.f, 0.f}, {0.f, 0.f}};
+    const float* src = (isv ? v : k) + (size_t)h * head_dim;
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+        const int j = lane + 64 * u;
+        if (j < hp) {
+            val[u][0] = src[2 * j];
+            val[u][1] = src[2 * j + 1];
+            if (!isv) {
+                rope_pair(val[u][0], val[u][1], freq, j, position);
+                float* kh = k + (size_t)h * head_dim;
+                kh[2 * j] = val[u][0];
+                kh[2 * j + 1] = val[u][1];
+            }
+        }
+    }
+    float amax = 0.f;
+#pragma unroll
+    for (int u = 0; u < 2; u++)
+#pragma unroll
+        for (int e = 0; e < 2; e++) {
+            const float a = val[u][e] < 0 ? -val[u][e] : val[u][e];
+            amax = a > amax ? a : amax;
+        }
+    for (int off = 32; off > 0; off >>= 1) {
+        const float o = __shfl_xor(amax, off, 64);
+        amax = o > amax ? o : amax;
+    }
+    if (lane == 0) (isv ? vs : ks)[row] = __fdiv_rn(amax, 127.0f);
+    int8_t* dst = (isv ? vc : kc) + row * head_dim;
+    const bool live = amax > 1e-30f;
+    const float inv = live ? __fdiv_rn(127.0f, amax) : 0.f;
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+        const int j = lane + 64 * u;
+        if (j < hp) {
+            dst[2 * j] = live ? kv_code(val[u][0], inv) : (int8_t)0;
+            dst[2 * j + 1] = live ? kv_code(val[u][1], inv) : (int8_t)0;
+        }
+    }
+}
+
 // One row of a blockwise table: value i = scale * q + zero (4-bit sym:
 // scale * q), each product and sum rounded as in src/quant.c:95-177.
 __device__ __forceinline__ unsigned code_of(int fmt, const uint8_t* packed, int i) {
@@ -452,6 +579,29 @@ extern "C" int qk_act_mul(float* gate, const float* up, int n, int act, hipStrea
 extern "C" int qk_residual(float* res, const float* x, int n, int* bad, hipStream_t s) {
     if (n <= 0) return 0;
     hipLaunchKernelGGL(residual_kernel, dim3(1), dim3(1024), 0, s, res, x, n, bad);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+extern "C" int qk_residual_norm(float* res, const float* x, int n, int* bad, const float* w,
+                                const float* b, float eps, int layer, float* out, hipStream_t s) {
+    if (n <= 0) return 0;
+    if (layer)
+        hipLaunchKernelGGL(residual_norm_kernel<true>, dim3(1), dim3(NORM_THREADS), 0, s, res, x, n, bad, w,
+                           b, eps, out);
+    else
+        hipLaunchKernelGGL(residual_norm_kernel<false>, dim3(1), dim3(NORM_THREADS), 0, s, res, x, n, bad,
+                           w, b, eps, out);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+extern "C" int qk_rope_kv_store(float* q, float* k, const float* v, const float* freq, int head_dim,
+                                int n_heads, int n_kv, int position, int8_t* kc, int8_t* vc, float* ks,
+                                float* vs, int max_seq, hipStream_t s) {
+    if (head_dim <= 0 || head_dim > 256 || (head_dim & 1) || n_kv <= 0 || position < 0 ||
+        position >= max_seq)
+        return -2;
+    hipLaunchKernelGGL(rope_kv_kernel, dim3(n_heads + 2 * n_kv), dim3(64), 0, s, q, k, v, freq, head_dim,
+                       n_heads, position, kc, vc, ks, vs, max_seq);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

@@ -137,6 +137,11 @@ int qk_attention(const float* q, const int8_t* kc, const int8_t* vc, const float
                  int position, float* out, void* ws, hipStream_t s);
 int qk_act_mul(float* gate, const float* up, int n, int act, hipStream_t s);
 int qk_residual(float* res, const float* x, int n, int* bad, hipStream_t s);
+int qk_residual_norm(float* res, const float* x, int n, int* bad, const float* w, const float* b,
+                     float eps, int layer, float* out, hipStream_t s);
+int qk_rope_kv_store(float* q, float* k, const float* v, const float* freq, int head_dim, int n_heads,
+                     int n_kv, int position, int8_t* kc, int8_t* vc, float* ks, float* vs, int max_seq,
+                     hipStream_t s);
 int qk_embed_row(const qsf_hip_tensor* t, int token, float* out, hipStream_t s);
 int qk_embed_row_fp16(const uint16_t* table, int hd, int token, float* out, hipStream_t s);
 

@@ -835,6 +835,27 @@ int qsf_hip_residual_dev(float* d_res, const float* d_x, int n, int* d_bad, void
     return glue_rc("qsf_hip_residual_dev", qk_residual(d_res, d_x, n, d_bad, pick_stream(stream)));
 }
 
+int qsf_hip_residual_norm_dev(float* d_res, const float* d_x, int n, int* d_bad, const float* d_w,
+                              const float* d_b, float eps, int layer_norm, float* d_out, void* stream) {
+    if (n < 0 || (n > 0 && (!d_res || !d_x || !d_w || !d_out)))
+        return fail(E_INVALID, "qsf_hip_residual_norm_dev: bad arguments");
+    return glue_rc("qsf_hip_residual_norm_dev",
+                   qk_residual_norm(d_res, d_x, n, d_bad, d_w, layer_norm ? d_b : NULL, eps, layer_norm != 0,
+                                    d_out, pick_stream(stream)));
+}
+
+int qsf_hip_rope_kv_store_dev(const qsf_hip_rope* r, float* d_q, float* d_k, const float* d_v,
+                              int n_heads, int n_kv_heads, int position, int8_t* d_kc, int8_t* d_vc,
+                              float* d_ks, float* d_vs, int max_seq, void* stream) {
+    if (!r || n_heads < 0 || n_kv_heads <= 0 || (n_heads > 0 && !d_q) || !d_k || !d_v || !d_kc ||
+        !d_vc || !d_ks || !d_vs || position < 0 || position >= max_seq || r->head_dim > 256)
+        return fail(E_INVALID, "qsf_hip_rope_kv_store_dev: bad arguments (position %d of %d)", position,
+                    max_seq);
+    return glue_rc("qsf_hip_rope_kv_store_dev",
+                   qk_rope_kv_store(d_q, d_k, d_v, r->d_freq, r->head_dim, n_heads, n_kv_heads, position,
+                                    d_kc, d_vc, d_ks, d_vs, max_seq, pick_stream(stream)));
+}
+
 int qsf_hip_embed_row_dev(const qsf_hip_tensor* t, int token, float* d_out, void* stream) {
     if (!t || !d_out || t->fmt < 0 || token < 0 || token >= t->rows)
         return fail(E_INVALID, "qsf_hip_embed_row_dev: bad arguments (token %d)", token);

@@ -38,6 +38,7 @@ EXPORTS = (
     "qsf_hip_rms_norm_dev", "qsf_hip_layer_norm_dev", "qsf_hip_rope_create", "qsf_hip_rope_free",
     "qsf_hip_rope_dev", "qsf_hip_kv_store_dev", "qsf_hip_attention_dev", "qsf_hip_act_mul_dev",
     "qsf_hip_residual_dev", "qsf_hip_embed_row_dev", "qsf_hip_embed_row_fp16_dev",
+    "qsf_hip_residual_norm_dev", "qsf_hip_rope_kv_store_dev",
     "qsf_hip_crc32", "qsf_hip_model_load", "qsf_hip_model_free", "qsf_hip_model_get_info",
     "qsf_hip_model_tensor", "qsf_hip_model_vector", "qsf_hip_model_embedding",
     "qsf_hip_model_embedding_fp16", "qsf_hip_model_output_head", "qsf_hip_model_final_norm", "qsf_hip_model_moe",
@@ -118,9 +119,12 @@ def load(path: str = LIB_PATH) -> C.CDLL:
     L.qsf_hip_residual_dev.argtypes = [_vp, _vp, _i, _vp, _vp]
     L.qsf_hip_embed_row_dev.argtypes = [_vp, _i, _vp, _vp]
     L.qsf_hip_embed_row_fp16_dev.argtypes = [_vp, _i, _i, _vp, _vp]
+    L.qsf_hip_residual_norm_dev.argtypes = [_vp, _vp, _i, _vp, _vp, _vp, _f, _i, _vp, _vp]
+    L.qsf_hip_rope_kv_store_dev.argtypes = [_vp, _vp, _vp, _vp, _i, _i, _i, _vp, _vp, _vp, _vp, _i, _vp]
     for n in ("qsf_hip_rms_norm_dev", "qsf_hip_layer_norm_dev", "qsf_hip_rope_dev",
               "qsf_hip_kv_store_dev", "qsf_hip_attention_dev", "qsf_hip_act_mul_dev",
-              "qsf_hip_residual_dev", "qsf_hip_embed_row_dev", "qsf_hip_embed_row_fp16_dev"):
+              "qsf_hip_residual_dev", "qsf_hip_embed_row_dev", "qsf_hip_embed_row_fp16_dev",
+              "qsf_hip_residual_norm_dev", "qsf_hip_rope_kv_store_dev"):
         getattr(L, n).restype = _i
     L.qsf_hip_crc32.argtypes = [_vp, C.c_size_t]
     L.qsf_hip_crc32.restype = C.c_uint32
@@ -357,6 +361,14 @@ class Rope:
         _check(load().qsf_hip_rope_dev(self.handle, _addr(q), _addr(k), n_heads, n_kv, position,
                                        _stream(stream)), "qsf_hip_rope_dev")
 
+    def apply_and_store(self, q, k, v, n_heads, n_kv, position, kc, vc, ks, vs, max_seq,
+                        stream=None) -> None:
+        """RoPE of q and k, then the int8 KV store of k and v, in one launch."""
+        _check(load().qsf_hip_rope_kv_store_dev(self.handle, _addr(q), _addr(k), _addr(v), n_heads,
+                                                n_kv, position, _addr(kc), _addr(vc), _addr(ks),
+                                                _addr(vs), max_seq, _stream(stream)),
+               "qsf_hip_rope_kv_store_dev")
+
     def free(self) -> None:
         if self.handle:
             load().qsf_hip_rope_free(self.handle)
@@ -384,6 +396,13 @@ def act_mul(gate, up, activation, stream=None) -> None:
 def residual(res, x, bad=None, stream=None) -> None:
     _check(load().qsf_hip_residual_dev(_addr(res), _addr(x), res.numel(), _addr(bad),
                                        _stream(stream)), "qsf_hip_residual_dev")
+
+
+def residual_norm(res, x, w, eps, out, bad=None, b=None, layer_norm=False, stream=None) -> None:
+    """res += x (with the NaN check into `bad`), then out = norm(res), in one launch."""
+    _check(load().qsf_hip_residual_norm_dev(_addr(res), _addr(x), res.numel(), _addr(bad), _addr(w),
+                                            _addr(b), eps, int(layer_norm), _addr(out),
+                                            _stream(stream)), "qsf_hip_residual_norm_dev")
 
 
 def embed_row(table: "Tensor", token: int, out, stream=None) -> None:

@@ -274,3 +274,63 @@ def test_device_resident_layer_chain(hip, oracle):
     rope.free()
     for t in T.values():
         t.free()
+
+
+# ---- fused launches: bit-identical to the separate calls ------------------------
+@pytest.mark.parametrize("layer_norm,with_bias", [(False, False), (True, False), (True, True)])
+@pytest.mark.parametrize("poison", [None, "nan", "big"])
+def test_residual_norm_equals_separate_calls(hip, layer_norm, with_bias, poison):
+    torch = torch_cuda()
+    rng = np.random.default_rng(7 + 2 * layer_norm + with_bias)
+    n = 4096
+    res = rng.standard_normal(n).astype(np.float32)
+    x = rng.standard_normal(n).astype(np.float32)
+    if poison == "nan":
+        x[1234] = np.nan
+    elif poison == "big":
+        x[77] = 3e30
+    w = (1 + 0.1 * rng.standard_normal(n)).astype(np.float32)
+    b = (0.1 * rng.standard_normal(n)).astype(np.float32) if with_bias else None
+    eps = 1e-5
+    r1, r2 = dev(res), dev(res)
+    o1, o2 = torch.empty(n, device="cuda:0"), torch.empty(n, device="cuda:0")
+    bad1 = torch.full((1,), 7, dtype=torch.int32, device="cuda:0")
+    bad2 = bad1.clone()
+    hip.residual(r1, dev(x), bad1, stream=_s())
+    if layer_norm:
+        hip.layer_norm(r1, o1, dev(w), None if b is None else dev(b), eps, stream=_s())
+    else:
+        hip.rms_norm(r1, o1, dev(w), eps, stream=_s())
+    hip.residual_norm(r2, dev(x), dev(w), eps, o2, bad=bad2, b=None if b is None else dev(b),
+                      layer_norm=layer_norm, stream=_s())
+    assert np.array_equal(host(r1).view(np.uint32), host(r2).view(np.uint32))
+    assert np.array_equal(host(o1).view(np.uint32), host(o2).view(np.uint32))
+    assert int(host(bad1)[0]) == int(host(bad2)[0]) == {None: -1, "nan": 1234, "big": 77}[poison]
+
+
+@pytest.mark.parametrize("nh,nkv,hd,position", [(32, 32, 128, 1023), (32, 8, 128, 5), (8, 2, 64, 300),
+                                                (4, 4, 256, 77), (6, 2, 80, 0)])
+def test_rope_kv_store_equals_separate_calls(hip, nh, nkv, hd, position):
+    torch = torch_cuda()
+    rng = np.random.default_rng(nh + hd + position)
+    max_seq = position + 4
+    q = rng.standard_normal(nh * hd).astype(np.float32)
+    k = rng.standard_normal(nkv * hd).astype(np.float32)
+    v = rng.standard_normal(nkv * hd).astype(np.float32)
+    k[:hd] = 0.0                               # a zero head: scale 0, codes 0
+    rope = hip.Rope(hd, 10000.0)
+    outs = []
+    for fused in (False, True):
+        dq, dk, dv = dev(q), dev(k), dev(v)
+        kc = torch.full((nkv, max_seq, hd), 5, dtype=torch.int8, device="cuda:0")
+        vc = kc.clone()
+        ks = torch.full((nkv, max_seq), 0.5, device="cuda:0")
+        vs = ks.clone()
+        if fused:
+            rope.apply_and_store(dq, dk, dv, nh, nkv, position, kc, vc, ks, vs, max_seq, stream=_s())
+        else:
+            rope.apply(dq, dk, nh, nkv, position, stream=_s())
+            hip.kv_store(kc, vc, ks, vs, max_seq, nkv, hd, position, dk, dv, stream=_s())
+        outs.append([host(a).view(np.uint8) for a in (dq, dk, kc, vc, ks, vs)])
+    for name, a, c in zip(("q", "k", "kc", "vc", "ks", "vs"), *outs):
+        assert np.array_equal(a, c), name
