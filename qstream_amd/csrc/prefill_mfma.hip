@@ -137,24 +137,45 @@ __global__ __launch_bounds__(256) void xpack_kernel(const uint16_t* __restrict__
     __shared__ __align__(16) uint16_t tile[16 * XP_PITCH];
     const int g = blockIdx.y, t = threadIdx.x;
     if ((int)blockIdx.x < kz / 8) {
-        // 32 blocks of each of the 16 rows; a lane sums one block in order
+        // 32 blocks of each of the 16 rows; a lane sums one block in order,
+        // for two rows.  Each 64-value piece of both rows' blocks is
+        // requested before any of it is summed (one memory round trip a
+        // piece instead of one a 16-byte load).
+        const int b = (int)blockIdx.x * 32 + (t & 31);
+        float Xs[2] = {0.f, 0.f};
+        const uint16_t* xr[2];
+        int cnt[2];
 #pragma unroll
         for (int h = 0; h < 2; h++) {
-            const int r = (t >> 5) + 8 * h, row = g * 16 + r;
-            const int b = (int)blockIdx.x * 32 + (t & 31);
-            float X = 0.f;
-            if (row < m && b < nb) {
-                const uint16_t* xr = x + (size_t)row * k + (size_t)b * bs;
-                const int cnt = min(bs, k - b * bs);       // a multiple of 8
-                for (int e = 0; e < cnt; e += 8) {
-                    const u32x4 v = *reinterpret_cast<const u32x4*>(xr + e);
+            const int row = g * 16 + (t >> 5) + 8 * h;
+            const bool live = row < m && b < nb;
+            xr[h] = x + (size_t)(live ? row : 0) * k + (size_t)(live ? b : 0) * bs;
+            cnt[h] = live ? min(bs, k - b * bs) : 0;   // a multiple of 8
+        }
+        for (int e0 = 0; e0 < max(cnt[0], cnt[1]); e0 += 64) {
+            u32x4 v[2][8];
+#pragma unroll
+            for (int h = 0; h < 2; h++)
+#pragma unroll
+                for (int q = 0; q < 8; q++)
+                    v[h][q] = e0 + 8 * q < cnt[h] ? *reinterpret_cast<const u32x4*>(xr[h] + e0 + 8 * q)
+                                                  : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+            for (int h = 0; h < 2; h++)
+#pragma unroll
+                for (int q = 0; q < 8; q++) {
+                    if (e0 + 8 * q >= cnt[h]) continue;
 #pragma unroll
                     for (int j = 0; j < 4; j++) {
-                        X += __builtin_bit_cast(float, v[j] << 16);
-                        X += __builtin_bit_cast(float, v[j] & 0xFFFF0000u);
+                        Xs[h] += __builtin_bit_cast(float, v[h][q][j] << 16);
+                        Xs[h] += __builtin_bit_cast(float, v[h][q][j] & 0xFFFF0000u);
                     }
                 }
-            }
+        }
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const int r = (t >> 5) + 8 * h;
+            const float X = Xs[h];
             const bf16x2 p1 = to_bf16x2(X, 0.f);
             const float r1 = X - bf16_f32(p1[0]);
             const bf16x2 p2 = to_bf16x2(r1, 0.f);
