@@ -203,7 +203,8 @@ qsf_hip_moe* qsf_hip_moe_create(int n_experts, int hidden, int expert_dim,
                                 const uint16_t* const* up_bias,
                                 const uint16_t* const* down_bias);
 void qsf_hip_moe_free(qsf_hip_moe* m);
-/* For each of ntok (<= 8) tokens: softmax(router logits), top_k by strict
+/* For each of ntok tokens (any count: they run in launches of up to 8, in
+ * order on `stream`; top_k <= 8): softmax(router logits), top_k by strict
  * '>' insertion, optional renormalisation, then per selected expert
  * gate/up + bias, activation (QSFActivation: 2 SiLU, 0/1 GELU, else ReLU)
  * times up, down + bias, weighted sum in rank order.  d_x [ntok][hidden],

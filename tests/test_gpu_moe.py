@@ -144,7 +144,8 @@ def test_moe_tie_keeps_lower_expert(hip, oracle):
 def test_moe_repeated_calls_reuse_workspace(hip, oracle):
     """One expert table, calls with different token counts and K in a row:
     the workspace (routing list, gate/up and down outputs) is reused and
-    every call must still match the oracle."""
+    every call must still match the oracle.  Calls of more than 8 tokens run
+    as consecutive launches of up to 8."""
     torch = torch_cuda()
     rng = np.random.default_rng(7)
     n_exp, hidden, eid = 8, 256, 512
@@ -153,7 +154,8 @@ def test_moe_repeated_calls_reuse_workspace(hip, oracle):
                 for e in ex] for n in ("gate", "up", "down")}
     biases = {n: [e[n] for e in ex] for n in ("gate_bias", "up_bias", "down_bias")}
     moe = hip.Moe(tens["gate"], tens["up"], tens["down"], hidden, eid, **biases)
-    for ntok, k in ((8, 4), (1, 2), (5, 3), (8, 8), (2, 1)):
+    # 20 and 9 tokens: launches of 8, 8, 4 and 8, 1 on one stream and workspace
+    for ntok, k in ((8, 4), (1, 2), (5, 3), (8, 8), (2, 1), (20, 4), (9, 2)):
         x = F.gaussian(rng, (ntok, hidden))
         logits = F.gaussian(rng, (ntok, n_exp))
         out = torch.full((ntok, hidden), float("nan"), device="cuda:0")
