@@ -14,7 +14,9 @@ cannot serve them; inputs are resident in HBM before the timed region.
 Prints one JSON line.  `value` is algorithmic bytes per step (on-disk QSF
 payload + x read once + y written, per matrix) / wall time per step, over K
 steps captured once into a HIP graph and replayed between two HIP events on
-the replay stream.  For the one-launch decode steps (configs 0 and 1) that
+the replay stream, after W untimed eager steps and at least 0.2 s of untimed
+replays (the clocks settle after about 40 ms of sustained work).  For the
+one-launch decode steps (configs 0 and 1) that
 timed region is also the kernel's time: `roofline.kernel_us` is the region
 time per launch, so it never exceeds the step.  Configs 2-4 time their
 dominant kernel separately (see each function).  `roofline.traffic` is the
@@ -92,10 +94,15 @@ def algo_bytes(mats) -> int:
     return sum(len(p) + 4 * c + 4 * r for _, p, r, c in mats)
 
 
+WARM_S = 0.2     # untimed replays before the timed one (clocks settle after ~40 ms of work)
+
+
 def graph_ms(torch, fn, steps):
     """Mean ms per step of `fn(i, stream)` for i < steps, captured once into a
-    HIP graph and replayed between two HIP events on the replay stream (two
-    untimed replays first)."""
+    HIP graph and replayed between two HIP events on the replay stream.
+    Untimed replays run first for at least WARM_S seconds (and at least two):
+    a config-1 step measures about 10.7 us in the first 10 ms of sustained
+    work and settles at 9.9-10.0 us from about 40 ms on."""
     graph = torch.cuda.CUDAGraph()
     cap = torch.cuda.Stream()
     cap.wait_stream(torch.cuda.current_stream())
@@ -104,9 +111,11 @@ def graph_ms(torch, fn, steps):
             for i in range(steps):
                 fn(i, cap)
     stream = torch.cuda.current_stream()
-    for _ in range(2):
+    t_warm, n_warm = time.perf_counter(), 0
+    while n_warm < 2 or time.perf_counter() - t_warm < WARM_S:
         graph.replay()
-    torch.cuda.synchronize()
+        torch.cuda.synchronize()
+        n_warm += 1
     t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0.record(stream)
     graph.replay()
