@@ -21,6 +21,7 @@
 #include "qsf_host.h"
 
 #include <fcntl.h>
+#include <pthread.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
@@ -35,6 +36,7 @@ enum {
 
 /* ---- CRC-32 (ISO 3309, reflected 0xEDB88320), src/format.c:11-34 ------- */
 static uint32_t g_crc_table[256];
+static pthread_once_t g_crc_once = PTHREAD_ONCE_INIT;
 
 static void crc_table_init(void) {
     for (uint32_t i = 0; i < 256; i++) {
@@ -45,7 +47,7 @@ static void crc_table_init(void) {
 }
 
 uint32_t qsf_hip_crc32(const void* data, size_t len) {
-    if (!g_crc_table[1]) crc_table_init();
+    pthread_once(&g_crc_once, crc_table_init);
     const uint8_t* p = (const uint8_t*)data;
     uint32_t c = 0xFFFFFFFFu;
     for (size_t i = 0; i < len; i++) c = g_crc_table[(c ^ p[i]) & 0xFFu] ^ (c >> 8);
@@ -245,6 +247,13 @@ static int parse_layer(const uint8_t* data, size_t size, int num_tensors, uint8_
     return E_OK;
 }
 
+/* Error code of a failed upload: the recorded one, never 0 (a load that
+ * reports success must hold every tensor). */
+static int upload_failed(void) {
+    const int e = qsf_hip_last_error();
+    return e ? e : qsf_host_fail(E_INTERNAL, "qsf_hip_model_load: upload failed");
+}
+
 static float* fp16_to_device(const uint8_t* p, size_t n) {
     float* h = malloc(sizeof(float) * (n ? n : 1));
     if (!h) {
@@ -354,18 +363,18 @@ static int load_mapped(qsf_hip_model* m, const uint8_t* f, size_t fsize) {
     }
 
     /* everything checked: upload */
-    if (qsf_hip_init(0) != E_OK) return qsf_hip_last_error();
+    if (qsf_hip_init(0) != E_OK) return upload_failed();
     for (uint32_t l = 0; l < in->num_layers; l++) {
         for (int i = 0; i < m->layers[l].n; i++) {
             rec_t* r = &m->layers[l].recs[i];
             if (r->qt == 7) {
                 r->n_vec = r->data_size / 2;
                 r->d_vec = fp16_to_device(r->data, r->n_vec);
-                if (!r->d_vec) return qsf_hip_last_error();
+                if (!r->d_vec) return upload_failed();
                 in->device_bytes += r->n_vec * 4;
             } else {
                 r->t = qsf_host_upload_owned(r->data, r->qt, (int)r->rows, (int)r->cols, bs);
-                if (!r->t) return qsf_hip_last_error();
+                if (!r->t) return upload_failed();
                 in->device_bytes += qsf_hip_tensor_payload_bytes(r->t);
             }
         }
@@ -409,8 +418,16 @@ static int load_mapped(qsf_hip_model* m, const uint8_t* f, size_t fsize) {
                 gb[e] = bb[3 * e]; ub[e] = bb[3 * e + 1]; db[e] = bb[3 * e + 2];
             }
             m->layers[l].moe = qsf_hip_moe_create(ne, hd, eid, g, u, d, gb, ub, db);
-            if (!m->layers[l].moe) rc = qsf_hip_last_error() ? qsf_hip_last_error() : E_INVALID_MODEL;
-            else in->moe_layers++;
+            if (m->layers[l].moe) {
+                in->moe_layers++;
+            } else if (qsf_hip_last_error() == 11) {
+                /* a shape the expert table does not take (hidden or expert
+                 * dim not a multiple of 4): the experts stay ordinary tensors */
+                fprintf(stderr, "[qsf_hip] layer %u: no MXFP4 expert table (%s); experts load as tensors\n",
+                        l, qsf_hip_last_error_detail());
+            } else {
+                rc = upload_failed();
+            }
         }
         free(tt);
         free(bb);
@@ -420,24 +437,24 @@ static int load_mapped(qsf_hip_model* m, const uint8_t* f, size_t fsize) {
         if (emb_qt == 7) {
             size_t nb = (size_t)in->vocab_size * hd * 2;
             m->d_embedding_fp16 = (uint16_t*)qsf_host_device_bytes(emb, nb);
-            if (!m->d_embedding_fp16) return qsf_hip_last_error();
+            if (!m->d_embedding_fp16) return upload_failed();
             in->device_bytes += nb;
         } else {
             m->embedding = qsf_host_upload_owned(emb, (int)emb_qt, (int)in->vocab_size, hd, bs);
-            if (!m->embedding) return qsf_hip_last_error();
+            if (!m->embedding) return upload_failed();
             in->device_bytes += qsf_hip_tensor_payload_bytes(m->embedding);
         }
     }
     if (norm) {
         m->d_final_norm_w = fp16_to_device(norm, (size_t)hd);
-        if (!m->d_final_norm_w) return qsf_hip_last_error();
+        if (!m->d_final_norm_w) return upload_failed();
         if ((in->has_bias & 0x08) && norm_size >= (uint32_t)hd * 4) {
             m->d_final_norm_b = fp16_to_device(norm + 2 * (size_t)hd, (size_t)hd);
-            if (!m->d_final_norm_b) return qsf_hip_last_error();
+            if (!m->d_final_norm_b) return upload_failed();
         }
         if (head) {
             m->output_head = qsf_host_upload_owned(head, in->quant_type, (int)in->vocab_size, hd, bs);
-            if (!m->output_head) return qsf_hip_last_error();
+            if (!m->output_head) return upload_failed();
             in->device_bytes += qsf_hip_tensor_payload_bytes(m->output_head);
         }
     }
