@@ -443,6 +443,9 @@ struct GemvArgs {
     int n, cols, nb, lpg, lpg_log2, chunk, tpw;
     int xs_off;                    // LDS dword offset of fp32 x (main kernel)
     int st_off, st_wave;           // LDS dword offset / floats per wave of the result stash
+    uint32_t row_bytes;            // SPLIT kernels: bytes a stored row
+    uint32_t pbb;                  // SPLIT: bytes of a stored block
+    int lsplit;                    // SPLIT: log2(stored block size / BS)
     const uint32_t* xq;            // prepared digits (stride DWS), or null: prepare here
     const float2* xmeta;
     const float* x;
@@ -469,11 +472,35 @@ __device__ __forceinline__ void entry_at(const GemvArgs& a, int m, uint32_t e, u
 }
 
 // Weights of one block for the R rows of a tile (row offsets in roff).
-template <int FMT, int BS, int R>
+template <int FMT, int BS, int R, bool SPLIT = false>
 __device__ __forceinline__ void load_block(const uint8_t* __restrict__ w, const uint32_t (&roff)[R],
-                                           int b, uint32_t (&wv)[R][1 + Fmt<FMT, BS>::CW]) {
+                                           int b, uint32_t (&wv)[R][1 + Fmt<FMT, BS>::CW],
+                                           uint32_t pbb = 0, int lsplit = 0) {
     using F = Fmt<FMT, BS>;
     constexpr int NW = 1 + F::CW;
+    if constexpr (SPLIT) {
+        // block b is part b % 2^lsplit of stored block b >> lsplit (pbb bytes):
+        // that block's meta dword, then the part's BS codes, which start on a
+        // byte (BS codes of any width are whole bytes) and on a dword
+        const uint32_t moff = (uint32_t)(b >> lsplit) * pbb;
+        const uint32_t coff = moff + 4u + (uint32_t)(b & ((1 << lsplit) - 1)) * (4u * F::CW);
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            wv[r][0] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(w + roff[r] + moff));
+            const uint32_t* c = reinterpret_cast<const uint32_t*>(w + roff[r] + coff);
+#pragma unroll
+            for (int i = 0; i + 4 <= F::CW; i += 4) {
+                const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_a4*>(c + i));
+                wv[r][1 + i] = v.x;
+                wv[r][2 + i] = v.y;
+                wv[r][3 + i] = v.z;
+                wv[r][4 + i] = v.w;
+            }
+#pragma unroll
+            for (int i = F::CW & ~3; i < F::CW; i++) wv[r][1 + i] = __builtin_nontemporal_load(c + i);
+        }
+        return;
+    }
     // dwordx4 pieces, then single dwords: the address unit takes 4 lanes a
     // clock whatever the width, so a 20-byte 2-bit block costs 2 load
     // instructions instead of 5 (the compiler does not merge dword loads of
@@ -639,7 +666,7 @@ __device__ __forceinline__ void flush_tile(const GemvArgs& a, int m, int row0, i
 // tile; the barrier; the rest of the first D weight items; then the item loop
 // (the first entries join the row sums before the one reduction a row), the
 // remaining outlier entries and the stores.
-template <int FMT, int BS, int R, int D, bool OUT, bool PREP, bool DREG>
+template <int FMT, int BS, int R, int D, bool OUT, bool PREP, bool DREG, bool SPLIT = false>
 __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
     constexpr int XV = kXvMax;
     constexpr int MT = tiles_per_wave(DREG);
@@ -674,7 +701,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
     const int ni = nt * ipt;
     const int tl = nt > 0 ? tw : 0;                           // tile the loads are anchored on
     const int ntl = nt > 0 ? nt : 1;
-    const uint32_t row_bytes = (uint32_t)a.nb * F::BB;
+    const uint32_t row_bytes = SPLIT ? a.row_bytes : (uint32_t)a.nb * F::BB;
 
     // first row of the lane's group in tile j (clamped to the wave's last)
     auto row_of = [&](int j) __attribute__((always_inline)) {
@@ -703,7 +730,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
     // next item's weights; past the last item, the last tile's row starts
     auto issue = [&](WV& wv) __attribute__((always_inline)) {
         const int b = ij < nt ? min(lig + (iq << lgl), a.nb - 1) : 0;
-        load_block<FMT, BS, R>(W, ioff, b, wv);
+        load_block<FMT, BS, R, SPLIT>(W, ioff, b, wv, a.pbb, a.lsplit);
         if (++iq == ipt) {
             iq = 0;
             ++ij;
@@ -1012,7 +1039,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
 
 // Fallback when the digits of a row do not fit in LDS: K in chunks, at most
 // MAXT tiles a wave kept in registers across chunks, no prefetch.
-template <int FMT, int BS, int R>
+template <int FMT, int BS, int R, bool SPLIT = false>
 __global__ __launch_bounds__(WAVES * 64) void gemv_chunked_kernel(GemvArgs a) {
     using F = Fmt<FMT, BS>;
     extern __shared__ __align__(16) uint32_t lds[];
@@ -1026,7 +1053,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_chunked_kernel(GemvArgs a) {
     const int rows_per_tile = R * (64 / lpg);
     const int t_begin = blockIdx.x * a.tpw;
     const int t_end = min(a.tile0[a.n], t_begin + a.tpw);
-    const uint32_t row_bytes = (uint32_t)a.nb * F::BB;
+    const uint32_t row_bytes = SPLIT ? a.row_bytes : (uint32_t)a.nb * F::BB;
 
     float rs[MAXT][R];
 #pragma unroll
@@ -1051,7 +1078,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_chunked_kernel(GemvArgs a) {
             for (int r = 0; r < R; r++) roff[r] = (uint32_t)min(row0 + r, a.rows[m] - 1) * row_bytes;
             for (int b = c0 + lig; b < c1; b += lpg) {
                 uint32_t wv[R][1 + F::CW];
-                load_block<FMT, BS, R>(a.w[m], roff, b, wv);
+                load_block<FMT, BS, R, SPLIT>(a.w[m], roff, b, wv, a.pbb, a.lsplit);
                 compute_block<FMT, BS, R>(wv, dig + (b - c0) * F::DWS, meta[b - c0], rs[j]);
             }
         }
@@ -1181,9 +1208,11 @@ constexpr int prefetch_depth() {
     return budget / per < 2 ? 2 : (budget / per > 4 ? 4 : budget / per);
 }
 
-template <int FMT, int BS, int R, bool DREG = false>
+template <int FMT, int BS, int R, bool DREG = false, bool SPLIT = false>
 int launch_rt(const qsf_hip_tensor* const* t, int n, int cols, const float* d_x,
               float* const* d_y, void* d_ws, int mode, hipStream_t s) {
+    // SPLIT: the stored blocks are t[0]->bs codes, read as parts of BS
+    if (SPLIT && (mode != QK_RUN_BOTH || t[0]->bs <= BS)) return -2;
     constexpr int MT = tiles_per_wave(DREG);
     using F = Fmt<FMT, BS>;
     const int nb = (cols + BS - 1) / BS;
@@ -1198,6 +1227,10 @@ int launch_rt(const qsf_hip_tensor* const* t, int n, int cols, const float* d_x,
 
     GemvArgs a = {};
     a.n = n;
+    a.row_bytes = (uint32_t)((size_t)t[0]->nb * t[0]->block_bytes);
+    a.pbb = (uint32_t)t[0]->block_bytes;
+    a.lsplit = 0;
+    while ((BS << a.lsplit) < t[0]->bs) a.lsplit++;
     a.cols = cols;
     a.nb = nb;
     int lpg = 1, lgl = 0;
@@ -1311,6 +1344,20 @@ int launch_rt(const qsf_hip_tensor* const* t, int n, int cols, const float* d_x,
     constexpr int DO = DREG ? 2 : prefetch_depth<FMT, BS, R, kHasOut>();
     if (any_out && !kHasOut) return -2;
     const dim3 g(grid, whole ? n : 1), b(WAVES * 64);
+    if constexpr (SPLIT) {
+        // one-launch decode only (the split view prepares x in its own parts)
+        if (!whole)
+            hipLaunchKernelGGL((gemv_chunked_kernel<FMT, BS, R, true>), g, b, lds, s, a);
+        else if (any_out)
+            launch_main<gemv_kernel<FMT, BS, R, DO, kHasOut, false, DREG, true>>(g, b, lds, s, a);
+        else if (most <= 1)
+            launch_main<gemv_kernel<FMT, BS, R, 1, false, false, DREG, true>>(g, b, lds, s, a);
+        else if (D > 2 && most <= 2)
+            launch_main<gemv_kernel<FMT, BS, R, (D > 2 ? 2 : D), false, false, DREG, true>>(g, b, lds, s, a);
+        else
+            launch_main<gemv_kernel<FMT, BS, R, D, false, false, DREG, true>>(g, b, lds, s, a);
+        return hipGetLastError() == hipSuccess ? 0 : -1;
+    }
     if (!whole)
         hipLaunchKernelGGL((gemv_chunked_kernel<FMT, BS, R>), g, b, lds, s, a);
     else if (prepared && any_out)
@@ -1331,7 +1378,7 @@ int launch_rt(const qsf_hip_tensor* const* t, int n, int cols, const float* d_x,
 // Two-row tiles halve the digit reads a row, one-row tiles double the
 // parallelism: one row when two-row tiles would leave waves of the chip
 // without a tile (a 4096-row matrix fills half of it).
-template <int FMT, int BS>
+template <int FMT, int BS, bool SPLIT = false>
 int launch_t(const qsf_hip_tensor* const* t, int n, int cols, const float* d_x,
              float* const* d_y, void* d_ws, int mode, hipStream_t s) {
     // digits in registers when a row is one block a lane and the lane's
@@ -1342,10 +1389,10 @@ int launch_t(const qsf_hip_tensor* const* t, int n, int cols, const float* d_x,
         bool out = false;
         for (int i = 0; i < n; i++) out |= t[i]->d_row_ptr != nullptr;
         if ((cols + BS - 1) / BS <= 64 && !(out && FMT == QK_FMT_4 && BS == 64))
-            return launch_rt<FMT, BS, 1, true>(t, n, cols, d_x, d_y, d_ws, mode, s);
+            return launch_rt<FMT, BS, 1, true, SPLIT>(t, n, cols, d_x, d_y, d_ws, mode, s);
     }
     if constexpr (tile_rows<FMT, BS>() == 1) {
-        return launch_rt<FMT, BS, 1>(t, n, cols, d_x, d_y, d_ws, mode, s);
+        return launch_rt<FMT, BS, 1, false, SPLIT>(t, n, cols, d_x, d_y, d_ws, mode, s);
     } else {
         const int nb = (cols + BS - 1) / BS;
         int lpg = 1;
@@ -1354,8 +1401,8 @@ int launch_t(const qsf_hip_tensor* const* t, int n, int cols, const float* d_x,
         long tiles2 = 0;
         for (int i = 0; i < n; i++) tiles2 += (t[i]->rows + rpt2 - 1) / rpt2;
         if (tiles2 < (long)num_cus() * WAVES)
-            return launch_rt<FMT, BS, 1>(t, n, cols, d_x, d_y, d_ws, mode, s);
-        return launch_rt<FMT, BS, 2>(t, n, cols, d_x, d_y, d_ws, mode, s);
+            return launch_rt<FMT, BS, 1, false, SPLIT>(t, n, cols, d_x, d_y, d_ws, mode, s);
+        return launch_rt<FMT, BS, 2, false, SPLIT>(t, n, cols, d_x, d_y, d_ws, mode, s);
     }
 }
 
@@ -1474,6 +1521,21 @@ extern "C" int qk_xprep(int fmt, int bs, int cols, const float* d_x, void* d_ws,
     return launch_fmt(fmt, bs, nullptr, 0, cols, d_x, nullptr, d_ws, QK_RUN_XPREP, s);
 }
 
+// Blocks of 128 or 256 codes are read as parts of 64, each part a block
+// with the stored block's meta.  A 4096-row matrix of 32 blocks a row then
+// uses every lane of its 64-lane row groups instead of half, and 86 blocks
+// (11008 columns) 172 of 192 lanes instead of 86 of 128; on config 2's
+// 3-bit block-128 layer every launch got faster (q/k/v 9.91 -> 9.53 us, o
+// 6.48 -> 5.32, gate/up 14.26 -> 13.69, down 12.69 -> 11.92), so the view
+// is taken whatever the row count, which also keeps a grouped launch's
+// results equal to its single launches'.  One-launch mode only: prepared x
+// is laid out for the stored block size.
+template <int FMT>
+int launch_split(const qsf_hip_tensor* const* t, int n, int cols, const float* x, float* const* y,
+                 void* ws, int mode, hipStream_t s) {
+    return launch_t<FMT, 64, true>(t, n, cols, x, y, ws, mode, s);
+}
+
 extern "C" int qk_gemv_group(const qsf_hip_tensor* const* t, int n, const float* d_x,
                              float* const* d_y, void* d_ws, int mode, hipStream_t s) {
     if (n <= 0 || n > QK_MAX_GROUP) return -2;
@@ -1487,6 +1549,15 @@ extern "C" int qk_gemv_group(const qsf_hip_tensor* const* t, int n, const float*
                 hipLaunchKernelGGL(fill_kernel, dim3((t[i]->rows + 255) / 256), dim3(256), 0, s,
                                    d_y[i], t[i]->rows, 0.0f);
         return hipGetLastError() == hipSuccess ? 0 : -1;
+    }
+    if (mode == QK_RUN_BOTH && (bs == 128 || bs == 256)) {
+        switch (fmt) {
+        case QK_FMT_2: return launch_split<QK_FMT_2>(t, n, cols, d_x, d_y, d_ws, mode, s);
+        case QK_FMT_3: return launch_split<QK_FMT_3>(t, n, cols, d_x, d_y, d_ws, mode, s);
+        case QK_FMT_4: return launch_split<QK_FMT_4>(t, n, cols, d_x, d_y, d_ws, mode, s);
+        case QK_FMT_4SYM: return launch_split<QK_FMT_4SYM>(t, n, cols, d_x, d_y, d_ws, mode, s);
+        default: return -2;
+        }
     }
     return launch_fmt(fmt, bs, t, n, cols, d_x, d_y, d_ws, mode, s);
 }

@@ -499,3 +499,29 @@ def test_outlier_rows_across_pass_boundaries(hip, oracle, qt, bs):
     _slot(hip, qt)(payload, x, out, rows, cols, bs)
     assert rel_l2(out, ref) <= REL_L2, "slot"
     np.testing.assert_allclose(out, ref, rtol=1e-4, atol=1e-4 * np.abs(ref).max())
+
+
+@pytest.mark.parametrize("qt", [F.Q2, F.Q3, F.Q4, F.Q4SYM, F.Q2_OUTLIER])
+@pytest.mark.parametrize("bs", [128, 256])
+@pytest.mark.parametrize("rows,cols", [(300, 4096), (4096, 4096), (512, 11008), (200, 1000), (33, 800)])
+def test_split_block_view(hip, oracle, qt, bs, rows, cols):
+    """One-launch device calls read 128- and 256-code blocks as 64-code
+    parts sharing the stored block's meta when that keeps more lanes of a
+    row group busy (few rows, 86 blocks a row); partial last blocks
+    included.  Against the oracle, and against the table slot, which runs
+    on prepared x at the stored block size."""
+    torch = torch_cuda()
+    rng = np.random.default_rng(rows + cols + bs + qt)
+    w = F.heavy_tail_weights(rng, rows, cols) if qt == F.Q2_OUTLIER else F.gaussian(rng, (rows, cols), 0.02)
+    x = F.gaussian(rng, cols)
+    payload = F.quantize_matrix(w, qt, bs)
+    ref = oracle.matvec(qt, payload, x, rows, cols, bs)
+    t = hip.Tensor(payload, qt, rows, cols, bs)
+    y = torch.full((rows,), float("nan"), device="cuda:0")
+    t.matvec(dev(x), y, stream=_stream())
+    got = host(y)
+    t.free()
+    assert rel_l2(got, ref) <= REL_L2, "device"
+    out = np.full(rows, np.nan, np.float32)
+    _slot(hip, qt)(payload, x, out, rows, cols, bs)
+    assert rel_l2(out, ref) <= REL_L2, "slot"
