@@ -317,10 +317,11 @@ constexpr int XBP = 36;
 // the lane partial sums acc[m][r] go to done(i, acc).
 // Rows per 32-lane group (rows per workgroup waves * 2 * MR): 1 for gate/up
 // and down (about 64 registers, so many workgroups stay resident; two rows
-// took 158-206), 3 for the batch-1 fused down (a workgroup there carries
-// four experts' rows; 12-row workgroups make 240 of them at hidden 2880, on
-// 256 CUs: 16 rows left 76 CUs idle, 8 rows needed two rounds).
-constexpr int GU_MR = 1, DN_MR = 1, FD_MR = 3;
+// took 158-206), and 1 for the batch-1 fused down too, where a workgroup
+// carries four experts' rows: 4-row workgroups make 720 of them at hidden
+// 2880, three a CU, with more loads in flight than 240 of 12 rows (batch-1
+// step 20.7 -> 20.0 us; 8-row workgroups 22.7 us).
+constexpr int GU_MR = 1, DN_MR = 1, FD_MR = 1;
 // Waves an expert workgroup: 8, so the 16 rows of a workgroup share one
 // staging of its inputs (4-wave workgroups staged them for 8 rows).
 constexpr int GU_WAVES = 8, DN_WAVES = 8;
@@ -598,7 +599,7 @@ __global__ __launch_bounds__(DN_WAVES * 64) void moe_down_kernel(MoeArgs a) {
 constexpr int FG = 4;                      // wave groups: experts of the token
 constexpr int FGW = 2;                     // waves a group (512 threads: 256 VGPRs a lane)
 constexpr int FMR = FD_MR;                 // rows per 32-lane group
-constexpr int FROWS = FGW * 2 * FMR;       // rows of a workgroup (12)
+constexpr int FROWS = FGW * 2 * FMR;       // rows of a workgroup (4)
 template <int NI>
 __global__ __launch_bounds__(FG * FGW * 64) void moe_down_fused_kernel(MoeArgs a) {
     extern __shared__ __align__(16) float xs[];  // [FG][eid, padded], then [FG][FROWS] row sums
