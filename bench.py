@@ -236,7 +236,7 @@ def run_profile(torch, hip, cfg, steps, warmup):
     log(f"profile run: config {cfg}, {warmup} + {steps} launches done")
 
 
-def table_slot_step_us(hip, qt, bs, mats, x, calls=200):
+def table_slot_step_us(hip, qt, bs, mats, x, calls=200, lookahead=None):
     """PCIe-inclusive latency of the drop-in path: the qsf_matvec_fn table
     slot (host x and y, synchronous; x prepared from host-mapped memory by
     one small dispatch, the GEMV writing y into host-mapped memory, one
@@ -244,9 +244,13 @@ def table_slot_step_us(hip, qt, bs, mats, x, calls=200):
     weights already resident in the device arena (one copy, so they may sit
     in the MALL).  Every step has its own x, as a decode loop does (the
     matrices of one step share it, as gate and up share a token's x), so
-    each step pays one x preparation.  Microseconds per step."""
+    each step pays one x preparation.  With the slots' look-ahead (the
+    library default) the first call of a step, once learnt, runs the second
+    matrix in its own launch and the second call is served its result;
+    lookahead=0 times every call alone.  Microseconds per step."""
     from qstream_amd import qsf_format as F
     L = hip.load()
+    old = L.qsf_hip_slot_lookahead(-1 if lookahead is None else lookahead)
     name = {F.Q2: "matvec_2bit", F.Q3: "matvec_3bit", F.Q4: "matvec_4bit",
             F.Q4SYM: "matvec_4bit_sym", F.Q2_OUTLIER: "matvec_outlier_2bit",
             F.Q4_OUTLIER: "matvec_outlier_4bit"}[qt]
@@ -263,7 +267,11 @@ def table_slot_step_us(hip, qt, bs, mats, x, calls=200):
     for i in range(calls):
         for a in steps[i % 4]:
             fn(*a)
-    return (time.perf_counter() - t0) / calls * 1e6
+    dt = time.perf_counter() - t0
+    L.qsf_hip_slot_lookahead(old)
+    for w in ws:
+        hip.arena_forget(w)
+    return dt / calls * 1e6
 
 
 def bench_dense(torch, hip, cfg, steps, warmup, with_cpu=True, split=False, slot=True,
@@ -292,6 +300,7 @@ def bench_dense(torch, hip, cfg, steps, warmup, with_cpu=True, split=False, slot
                            "bytes_per_launch": bytes_step}
     if slot:
         out["table_slot_us_per_step"] = table_slot_step_us(hip, qt, bs, mats, x)
+        out["table_slot_alone_us_per_step"] = table_slot_step_us(hip, qt, bs, mats, x, lookahead=0)
     if with_cpu:
         out["cpu_baseline"] = cpu_baseline_dense(qt, bs, mats, x, cpu_budget)
     return out
@@ -693,6 +702,8 @@ def run_config(torch, hip, key: str, args, cpu_budget: float, cache: dict) -> di
                 "rotation_mib": round(r["rotation_mib"], 1)}
         if "table_slot_us_per_step" in r:
             conf["table_slot_us_per_step_pcie"] = round(r["table_slot_us_per_step"], 3)
+            conf["table_slot_lookahead_off_us_per_step_pcie"] = round(
+                r["table_slot_alone_us_per_step"], 3)
             conf["table_slot_gbs_pcie"] = round(
                 r["bytes_per_step"] / (r["table_slot_us_per_step"] * 1e-6) / 1e9, 2)
         line = dict(base, value=round(r["value"], 2), ms_per_step=round(r["ms_per_step"], 5),

@@ -83,6 +83,20 @@ void qsf_matvec_mxfp4_hip(const void* weights_q, const float* input, float* outp
  * engine appends to the table for quant type 11). */
 void qsf_kernels_init_hip(void* kernel_table, const void* platform, void** mxfp4_slot);
 
+/* No counterpart in the reference: a tuning knob of the slots above.  A
+ * slot call learns which weight pointer the engine calls next with the same
+ * x (k after q, up after gate: src/engine.c:848-866, 1118-1125); once the
+ * same one has followed twice running, the call also runs up to n such
+ * successors in its own launch and holds their results until they are
+ * called.  A held result is served only when that later call passes every
+ * check a call makes and finds x, the tensor and the arena unchanged, and
+ * only for groups whose launch gives each matrix the arithmetic it gets
+ * alone: every result is bit-identical to the call made by itself.  A held
+ * result not called for costs one GEMV and its predecessor the successor.
+ * n = 0 turns it off; default 2 (q, k, v); at most 7.  n < 0 only queries.
+ * Returns the previous setting. */
+int qsf_hip_slot_lookahead(int n);
+
 /* ---- device weight arena (replaces mmap streaming, src/file_access.c:80-88) */
 typedef struct qsf_hip_tensor qsf_hip_tensor;   /* opaque */
 

@@ -1208,24 +1208,24 @@ constexpr int prefetch_depth() {
     return budget / per < 2 ? 2 : (budget / per > 4 ? 4 : budget / per);
 }
 
+// The launch plan of a GEMV over n tensors sharing x: kernel arguments, grid,
+// LDS and the kernel instantiation (kid).  A row's arithmetic (the order of
+// its fp32 adds) follows from R, DREG, the row-group width lpg, the chunk
+// and kid alone; qk_gemv_signature packs those.  Returns 1 when there is
+// nothing to launch, a negative code when the group is not supported.
+struct Plan {
+    int kid;        // 0 chunked; 1-4 split view; 5-10 whole-row (launch_rt)
+    int grid, ny;
+    size_t lds;
+};
+
 template <int FMT, int BS, int R, bool DREG = false, bool SPLIT = false>
-int launch_rt(const qsf_hip_tensor* const* t, int n, int cols, const float* d_x,
-              float* const* d_y, void* d_ws, int mode, hipStream_t s) {
-    // SPLIT: the stored blocks are t[0]->bs codes, read as parts of BS
-    if (SPLIT && (mode != QK_RUN_BOTH || t[0]->bs <= BS)) return -2;
+int plan_rt(const qsf_hip_tensor* const* t, int n, int cols, int mode, float* const* d_y,
+            GemvArgs& a, Plan& p) {
     constexpr int MT = tiles_per_wave(DREG);
     using F = Fmt<FMT, BS>;
     const int nb = (cols + BS - 1) / BS;
-    // prepared digits and block meta (QK_RUN_XPREP / a prepared run only)
-    uint32_t* xq = (uint32_t*)d_ws;
-    float2* xmeta = d_ws ? xmeta_in<FMT, BS>(d_ws, nb) : nullptr;
-    if (!d_ws && (mode != QK_RUN_BOTH)) return -2;
-    if ((mode & QK_RUN_XPREP) && (!(mode & QK_RUN_GEMV) || (mode & QK_RUN_STANDALONE_PREP)))
-        hipLaunchKernelGGL((xprep_kernel<FMT, BS>), dim3((nb + 256 / F::LPB - 1) / (256 / F::LPB)),
-                           dim3(256), 0, s, d_x, cols, nb, xq, xmeta, (float*)nullptr);
-    if (!(mode & QK_RUN_GEMV)) return hipGetLastError() == hipSuccess ? 0 : -1;
-
-    GemvArgs a = {};
+    a = GemvArgs{};
     a.n = n;
     a.row_bytes = (uint32_t)((size_t)t[0]->nb * t[0]->block_bytes);
     a.pbb = (uint32_t)t[0]->block_bytes;
@@ -1258,33 +1258,31 @@ int launch_rt(const qsf_hip_tensor* const* t, int n, int cols, const float* d_x,
     a.tile0[0] = 0;
     for (int i = 0; i < n; i++) {
         if ((size_t)t[i]->rows * nb * F::BB > 0xFFFFFFF0ull) return -2;   // 32-bit offsets
+        float* y = d_y ? d_y[i] : nullptr;
         a.w[i] = t[i]->d_blocks;
-        a.y[i] = d_y[i];
+        a.y[i] = y;
         a.rp[i] = t[i]->d_row_ptr;
         a.oe[i] = t[i]->d_oent;
         a.oc[i] = t[i]->d_ocol;
         a.ov[i] = t[i]->d_oval;
         a.nent[i] = (int)t[i]->n_csr;
         a.rows[i] = t[i]->rows;
-        a.mat[i] = {t[i]->d_blocks, d_y[i], t[i]->d_row_ptr, t[i]->d_oent, t[i]->rows,
+        a.mat[i] = {t[i]->d_blocks, y, t[i]->d_row_ptr, t[i]->d_oent, t[i]->rows,
                     (int)t[i]->n_csr, (t[i]->rows + rows_per_tile - 1) / rows_per_tile, 0};
         a.tile0[i + 1] = a.tile0[i] + a.mat[i].tiles;
         any_out |= t[i]->d_row_ptr != nullptr;
         split |= t[i]->d_row_ptr != nullptr && t[i]->d_oent == nullptr;
     }
     const int tiles = a.tile0[n];
-    if (tiles == 0) return 0;
     // one workgroup per CU (fewer for small problems); at most MAXT tiles a
     // wave here (the chunked kernel's bound; the main kernel may take up to
     // MT below, to fit its grid in one round)
     int grid = (tiles + WAVES - 1) / WAVES;
     grid = grid < num_cus() ? grid : num_cus();
-    if ((tiles + grid - 1) / grid > WAVES * MAXT) grid = (tiles + WAVES * MAXT - 1) / (WAVES * MAXT);
-    a.tpw = (tiles + grid - 1) / grid;
+    if (grid > 0 && (tiles + grid - 1) / grid > WAVES * MAXT)
+        grid = (tiles + WAVES * MAXT - 1) / (WAVES * MAXT);
+    a.tpw = grid > 0 ? (tiles + grid - 1) / grid : 0;
     const bool prepared = !(mode & QK_RUN_XPREP) || (mode & QK_RUN_STANDALONE_PREP);
-    a.xq = prepared ? xq : nullptr;
-    a.xmeta = xmeta;
-    a.x = d_x;
 
     // Main kernel LDS: [meta: nb x 16 B][digits: nb x DWS dwords, padded to
     // 4][x: nb*BS floats][fp32 stash: a wave's tiles x rows_per_tile].  When
@@ -1304,6 +1302,10 @@ int launch_rt(const qsf_hip_tensor* const* t, int n, int cols, const float* d_x,
     a.xs_off = 0;
     a.st_off = 0;
     a.st_wave = 0;
+    if (tiles == 0) {
+        p = {0, 0, 0, 0};
+        return 1;
+    }
     if (whole) {
         const size_t room = (lds_limit() - main_fixed) / per_tile;
         if ((size_t)a.tpw > WAVES * room) a.tpw = (int)(WAVES * room);
@@ -1333,6 +1335,47 @@ int launch_rt(const qsf_hip_tensor* const* t, int n, int cols, const float* d_x,
     }
     // only the 2-bit and 4-bit asymmetric formats have outlier variants
     constexpr bool kHasOut = FMT == QK_FMT_2 || FMT == QK_FMT_4;
+    constexpr int D = DREG ? 2 : prefetch_depth<FMT, BS, R, false>();
+    if (any_out && !kHasOut) return -2;
+    int kid;
+    if (!whole) kid = 0;
+    else if (SPLIT) kid = any_out ? 1 : most <= 1 ? 2 : (D > 2 && most <= 2) ? 3 : 4;
+    else if (prepared && any_out) kid = 5;
+    else if (prepared) kid = 6;
+    else if (any_out) kid = 7;
+    else if (most <= 1) kid = 8;
+    else if (D > 2 && most <= 2) kid = 9;
+    else kid = 10;
+    p = {kid, grid, whole ? n : 1, lds};
+    return 0;
+}
+
+template <int FMT, int BS, int R, bool DREG = false, bool SPLIT = false>
+int launch_rt(const qsf_hip_tensor* const* t, int n, int cols, const float* d_x,
+              float* const* d_y, void* d_ws, int mode, hipStream_t s) {
+    // SPLIT: the stored blocks are t[0]->bs codes, read as parts of BS
+    if (SPLIT && (mode != QK_RUN_BOTH || t[0]->bs <= BS)) return -2;
+    using F = Fmt<FMT, BS>;
+    const int nb = (cols + BS - 1) / BS;
+    // prepared digits and block meta (QK_RUN_XPREP / a prepared run only)
+    uint32_t* xq = (uint32_t*)d_ws;
+    float2* xmeta = d_ws ? xmeta_in<FMT, BS>(d_ws, nb) : nullptr;
+    if (!d_ws && (mode != QK_RUN_BOTH)) return -2;
+    if ((mode & QK_RUN_XPREP) && (!(mode & QK_RUN_GEMV) || (mode & QK_RUN_STANDALONE_PREP)))
+        hipLaunchKernelGGL((xprep_kernel<FMT, BS>), dim3((nb + 256 / F::LPB - 1) / (256 / F::LPB)),
+                           dim3(256), 0, s, d_x, cols, nb, xq, xmeta, (float*)nullptr);
+    if (!(mode & QK_RUN_GEMV)) return hipGetLastError() == hipSuccess ? 0 : -1;
+
+    GemvArgs a;
+    Plan p;
+    const int rc = plan_rt<FMT, BS, R, DREG, SPLIT>(t, n, cols, mode, d_y, a, p);
+    if (rc) return rc < 0 ? rc : 0;
+    const bool prepared = !(mode & QK_RUN_XPREP) || (mode & QK_RUN_STANDALONE_PREP);
+    a.xq = prepared ? xq : nullptr;
+    a.xmeta = xmeta;
+    a.x = d_x;
+
+    constexpr bool kHasOut = FMT == QK_FMT_2 || FMT == QK_FMT_4;
     // one item a wave at most (a 4096-row matrix of up to 64 blocks): one
     // item in flight.  A second would only re-read a row for nothing, and
     // its wave could not retire before that load returned (4096x4096 4-bit
@@ -1342,57 +1385,58 @@ int launch_rt(const qsf_hip_tensor* const* t, int n, int cols, const float* d_x,
     // alternates issue and compute
     constexpr int D = DREG ? 2 : prefetch_depth<FMT, BS, R, false>();
     constexpr int DO = DREG ? 2 : prefetch_depth<FMT, BS, R, kHasOut>();
-    if (any_out && !kHasOut) return -2;
-    const dim3 g(grid, whole ? n : 1), b(WAVES * 64);
+    const dim3 g(p.grid, p.ny), b(WAVES * 64);
     if constexpr (SPLIT) {
         // one-launch decode only (the split view prepares x in its own parts)
-        if (!whole)
-            hipLaunchKernelGGL((gemv_chunked_kernel<FMT, BS, R, true>), g, b, lds, s, a);
-        else if (any_out)
-            launch_main<gemv_kernel<FMT, BS, R, DO, kHasOut, false, DREG, true>>(g, b, lds, s, a);
-        else if (most <= 1)
-            launch_main<gemv_kernel<FMT, BS, R, 1, false, false, DREG, true>>(g, b, lds, s, a);
-        else if (D > 2 && most <= 2)
-            launch_main<gemv_kernel<FMT, BS, R, (D > 2 ? 2 : D), false, false, DREG, true>>(g, b, lds, s, a);
-        else
-            launch_main<gemv_kernel<FMT, BS, R, D, false, false, DREG, true>>(g, b, lds, s, a);
+        switch (p.kid) {
+        case 0: hipLaunchKernelGGL((gemv_chunked_kernel<FMT, BS, R, true>), g, b, p.lds, s, a); break;
+        case 1: launch_main<gemv_kernel<FMT, BS, R, DO, kHasOut, false, DREG, true>>(g, b, p.lds, s, a); break;
+        case 2: launch_main<gemv_kernel<FMT, BS, R, 1, false, false, DREG, true>>(g, b, p.lds, s, a); break;
+        case 3: launch_main<gemv_kernel<FMT, BS, R, (D > 2 ? 2 : D), false, false, DREG, true>>(g, b, p.lds, s, a); break;
+        default: launch_main<gemv_kernel<FMT, BS, R, D, false, false, DREG, true>>(g, b, p.lds, s, a); break;
+        }
         return hipGetLastError() == hipSuccess ? 0 : -1;
     }
-    if (!whole)
-        hipLaunchKernelGGL((gemv_chunked_kernel<FMT, BS, R>), g, b, lds, s, a);
-    else if (prepared && any_out)
-        launch_main<gemv_kernel<FMT, BS, R, DO, kHasOut, true, DREG>>(g, b, lds, s, a);
-    else if (prepared)
-        launch_main<gemv_kernel<FMT, BS, R, D, false, true, DREG>>(g, b, lds, s, a);
-    else if (any_out)
-        launch_main<gemv_kernel<FMT, BS, R, DO, kHasOut, false, DREG>>(g, b, lds, s, a);
-    else if (most <= 1)
-        launch_main<gemv_kernel<FMT, BS, R, 1, false, false, DREG>>(g, b, lds, s, a);
-    else if (D > 2 && most <= 2)
-        launch_main<gemv_kernel<FMT, BS, R, (D > 2 ? 2 : D), false, false, DREG>>(g, b, lds, s, a);
-    else
-        launch_main<gemv_kernel<FMT, BS, R, D, false, false, DREG>>(g, b, lds, s, a);
+    switch (p.kid) {
+    case 0: hipLaunchKernelGGL((gemv_chunked_kernel<FMT, BS, R>), g, b, p.lds, s, a); break;
+    case 5: launch_main<gemv_kernel<FMT, BS, R, DO, kHasOut, true, DREG>>(g, b, p.lds, s, a); break;
+    case 6: launch_main<gemv_kernel<FMT, BS, R, D, false, true, DREG>>(g, b, p.lds, s, a); break;
+    case 7: launch_main<gemv_kernel<FMT, BS, R, DO, kHasOut, false, DREG>>(g, b, p.lds, s, a); break;
+    case 8: launch_main<gemv_kernel<FMT, BS, R, 1, false, false, DREG>>(g, b, p.lds, s, a); break;
+    case 9: launch_main<gemv_kernel<FMT, BS, R, (D > 2 ? 2 : D), false, false, DREG>>(g, b, p.lds, s, a); break;
+    default: launch_main<gemv_kernel<FMT, BS, R, D, false, false, DREG>>(g, b, p.lds, s, a); break;
+    }
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
-// Two-row tiles halve the digit reads a row, one-row tiles double the
-// parallelism: one row when two-row tiles would leave waves of the chip
-// without a tile (a 4096-row matrix fills half of it).
-template <int FMT, int BS, bool SPLIT = false>
-int launch_t(const qsf_hip_tensor* const* t, int n, int cols, const float* d_x,
-             float* const* d_y, void* d_ws, int mode, hipStream_t s) {
-    // digits in registers when a row is one block a lane and the lane's
-    // digit words fit in 48 registers (2- and 4-bit blocks of <= 64 codes)
-    // (not the 4-bit 64-code outlier kernel: its CSR state on top spills)
+template <int FMT, int BS, int R, bool DREG, bool SPLIT>
+uint64_t sig_rt(const qsf_hip_tensor* const* t, int n, int cols, int mode) {
+    GemvArgs a;
+    Plan p;
+    if (SPLIT && (mode != QK_RUN_BOTH || t[0]->bs <= BS)) return 0;
+    if (plan_rt<FMT, BS, R, DREG, SPLIT>(t, n, cols, mode, nullptr, a, p) < 0) return 0;
+    return 1ull | (uint64_t)R << 1 | (uint64_t)DREG << 3 | (uint64_t)SPLIT << 4 |
+           (uint64_t)(mode & 7) << 5 | (uint64_t)a.lpg << 8 | (uint64_t)p.kid << 16 |
+           (uint64_t)a.chunk << 24 | (uint64_t)BS << 48;
+}
+
+// Tiles: 0 = one-row tiles with the digits in registers (a row is one block
+// a lane and the lane's digit words fit in 48 registers: 2- and 4-bit blocks
+// of <= 64 codes; not the 4-bit 64-code outlier kernel, whose CSR state on
+// top spills), 1 = one-row tiles, 2 = two-row tiles.  Two-row tiles halve
+// the digit reads a row, one-row tiles double the parallelism: one row when
+// two-row tiles would leave waves of the chip without a tile (a 4096-row
+// matrix fills half of it).
+template <int FMT, int BS>
+int pick_tiles(const qsf_hip_tensor* const* t, int n, int cols) {
     constexpr bool kDreg = FMT != QK_FMT_3 && Fmt<FMT, BS>::CW * Fmt<FMT, BS>::NC * ND <= 48;
     if constexpr (kDreg) {
         bool out = false;
         for (int i = 0; i < n; i++) out |= t[i]->d_row_ptr != nullptr;
-        if ((cols + BS - 1) / BS <= 64 && !(out && FMT == QK_FMT_4 && BS == 64))
-            return launch_rt<FMT, BS, 1, true, SPLIT>(t, n, cols, d_x, d_y, d_ws, mode, s);
+        if ((cols + BS - 1) / BS <= 64 && !(out && FMT == QK_FMT_4 && BS == 64)) return 0;
     }
     if constexpr (tile_rows<FMT, BS>() == 1) {
-        return launch_rt<FMT, BS, 1, false, SPLIT>(t, n, cols, d_x, d_y, d_ws, mode, s);
+        return 1;
     } else {
         const int nb = (cols + BS - 1) / BS;
         int lpg = 1;
@@ -1400,10 +1444,31 @@ int launch_t(const qsf_hip_tensor* const* t, int n, int cols, const float* d_x,
         const long rpt2 = 2L * (64 / lpg);
         long tiles2 = 0;
         for (int i = 0; i < n; i++) tiles2 += (t[i]->rows + rpt2 - 1) / rpt2;
-        if (tiles2 < (long)num_cus() * WAVES)
-            return launch_rt<FMT, BS, 1, false, SPLIT>(t, n, cols, d_x, d_y, d_ws, mode, s);
-        return launch_rt<FMT, BS, 2, false, SPLIT>(t, n, cols, d_x, d_y, d_ws, mode, s);
+        return tiles2 < (long)num_cus() * WAVES ? 1 : 2;
     }
+}
+
+template <int FMT, int BS, bool SPLIT = false>
+int launch_t(const qsf_hip_tensor* const* t, int n, int cols, const float* d_x,
+             float* const* d_y, void* d_ws, int mode, hipStream_t s) {
+    constexpr bool kDreg = FMT != QK_FMT_3 && Fmt<FMT, BS>::CW * Fmt<FMT, BS>::NC * ND <= 48;
+    const int k = pick_tiles<FMT, BS>(t, n, cols);
+    if constexpr (kDreg)
+        if (k == 0) return launch_rt<FMT, BS, 1, true, SPLIT>(t, n, cols, d_x, d_y, d_ws, mode, s);
+    if constexpr (tile_rows<FMT, BS>() == 2)
+        if (k == 2) return launch_rt<FMT, BS, 2, false, SPLIT>(t, n, cols, d_x, d_y, d_ws, mode, s);
+    return launch_rt<FMT, BS, 1, false, SPLIT>(t, n, cols, d_x, d_y, d_ws, mode, s);
+}
+
+template <int FMT, int BS, bool SPLIT = false>
+uint64_t sig_t(const qsf_hip_tensor* const* t, int n, int cols, int mode) {
+    constexpr bool kDreg = FMT != QK_FMT_3 && Fmt<FMT, BS>::CW * Fmt<FMT, BS>::NC * ND <= 48;
+    const int k = pick_tiles<FMT, BS>(t, n, cols);
+    if constexpr (kDreg)
+        if (k == 0) return sig_rt<FMT, BS, 1, true, SPLIT>(t, n, cols, mode);
+    if constexpr (tile_rows<FMT, BS>() == 2)
+        if (k == 2) return sig_rt<FMT, BS, 2, false, SPLIT>(t, n, cols, mode);
+    return sig_rt<FMT, BS, 1, false, SPLIT>(t, n, cols, mode);
 }
 
 template <int FMT>
@@ -1504,6 +1569,17 @@ int unpack_bs(int bs, const uint8_t* blk, int n, int8_t* c, uint32_t* m, float* 
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
+template <int FMT>
+uint64_t sig_bs(int bs, const qsf_hip_tensor* const* t, int n, int cols, int mode) {
+    switch (bs) {
+    case 32: return sig_t<FMT, 32>(t, n, cols, mode);
+    case 64: return sig_t<FMT, 64>(t, n, cols, mode);
+    case 128: return sig_t<FMT, 128>(t, n, cols, mode);
+    case 256: return sig_t<FMT, 256>(t, n, cols, mode);
+    default: return 0;
+    }
+}
+
 }  // namespace
 
 extern "C" size_t qk_xprep_bytes(int fmt, int bs, int cols) {
@@ -1560,6 +1636,30 @@ extern "C" int qk_gemv_group(const qsf_hip_tensor* const* t, int n, const float*
         }
     }
     return launch_fmt(fmt, bs, t, n, cols, d_x, d_y, d_ws, mode, s);
+}
+
+extern "C" uint64_t qk_gemv_signature(const qsf_hip_tensor* const* t, int n, int mode) {
+    if (n <= 0 || n > QK_MAX_GROUP) return 0;
+    const int fmt = t[0]->fmt, bs = t[0]->bs, cols = t[0]->cols;
+    for (int i = 1; i < n; i++)
+        if (t[i]->fmt != fmt || t[i]->bs != bs || t[i]->cols != cols) return 0;
+    if (cols <= 0) return 2;
+    if (mode == QK_RUN_BOTH && (bs == 128 || bs == 256)) {
+        switch (fmt) {
+        case QK_FMT_2: return sig_t<QK_FMT_2, 64, true>(t, n, cols, mode);
+        case QK_FMT_3: return sig_t<QK_FMT_3, 64, true>(t, n, cols, mode);
+        case QK_FMT_4: return sig_t<QK_FMT_4, 64, true>(t, n, cols, mode);
+        case QK_FMT_4SYM: return sig_t<QK_FMT_4SYM, 64, true>(t, n, cols, mode);
+        default: return 0;
+        }
+    }
+    switch (fmt) {
+    case QK_FMT_2: return sig_bs<QK_FMT_2>(bs, t, n, cols, mode);
+    case QK_FMT_3: return sig_bs<QK_FMT_3>(bs, t, n, cols, mode);
+    case QK_FMT_4: return sig_bs<QK_FMT_4>(bs, t, n, cols, mode);
+    case QK_FMT_4SYM: return sig_bs<QK_FMT_4SYM>(bs, t, n, cols, mode);
+    default: return 0;
+    }
 }
 
 template <int FMT, int BS>

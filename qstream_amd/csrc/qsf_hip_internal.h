@@ -43,6 +43,8 @@ typedef struct qsf_hip_tensor {
     uint16_t* d_oval;           /* ... and n_csr fp16 values */
     void*    d_alloc;           /* base of the single device allocation */
     int      registry_owned;    /* uploaded implicitly by a table-slot call */
+    const void* succ;           /* table slots: the key called next with the same x ... */
+    int      succ_hits;         /* ... this many times since it last differed */
     struct qsf_hip_tensor* prev; /* list of live tensors (freed at shutdown) */
     struct qsf_hip_tensor* next;
 } qsf_hip_tensor;
@@ -68,6 +70,11 @@ int qk_xprep(int fmt, int bs, int cols, const float* d_x, void* d_ws, hipStream_
 enum { QK_RUN_XPREP = 1, QK_RUN_GEMV = 2, QK_RUN_BOTH = 3, QK_RUN_STANDALONE_PREP = 4 };
 int qk_gemv_group(const qsf_hip_tensor* const* t, int n, const float* d_x,
                   float* const* d_y, void* d_ws, int mode, hipStream_t s);
+/* What fixes a row's arithmetic in qk_gemv_group(t, n, ..., mode): the
+ * kernel instantiation, row-group width, tile rows and chunk.  A tensor's
+ * rows come out bit-identical in two launches whose signatures are equal
+ * (0: the group is not supported). */
+uint64_t qk_gemv_signature(const qsf_hip_tensor* const* t, int n, int mode);
 
 /* Kernel timing of main-path GEMV and prefill launches (event pair at the
  * kernel's own start and end): on/off (on resets the record), then read

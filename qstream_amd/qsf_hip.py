@@ -27,7 +27,7 @@ EXPORTS = (
     "qsf_hip_init", "qsf_hip_shutdown", "qsf_hip_last_error", "qsf_hip_last_error_detail",
     "qsf_matvec_2bit_hip", "qsf_matvec_3bit_hip", "qsf_matvec_4bit_hip",
     "qsf_matvec_4bit_sym_hip", "qsf_matvec_outlier_2bit_hip", "qsf_matvec_outlier_4bit_hip",
-    "qsf_matvec_mxfp4_hip", "qsf_kernels_init_hip",
+    "qsf_matvec_mxfp4_hip", "qsf_kernels_init_hip", "qsf_hip_slot_lookahead",
     "qsf_hip_tensor_upload", "qsf_hip_tensor_lookup", "qsf_hip_tensor_free",
     "qsf_hip_arena_forget", "qsf_hip_arena_forget_range", "qsf_hip_arena_bytes", "qsf_hip_tensor_payload_bytes",
     "qsf_hip_matvec_dev", "qsf_hip_matvec_group_dev", "qsf_hip_xprep_bytes",
@@ -82,6 +82,8 @@ def load(path: str = LIB_PATH) -> C.CDLL:
     L.qsf_hip_tensor_free.argtypes = [_vp]
     L.qsf_hip_arena_forget.argtypes = [_vp]
     L.qsf_hip_arena_forget_range.argtypes = [_vp, C.c_size_t]
+    L.qsf_hip_slot_lookahead.argtypes = [_i]
+    L.qsf_hip_slot_lookahead.restype = _i
     L.qsf_hip_arena_bytes.restype = C.c_size_t
     L.qsf_hip_tensor_payload_bytes.argtypes = [_vp]
     L.qsf_hip_tensor_payload_bytes.restype = C.c_size_t
@@ -211,6 +213,12 @@ def arena_forget_range(buf) -> int:
     """Forget every registered pointer inside a host buffer; returns how many."""
     a = buf if isinstance(buf, np.ndarray) else np.frombuffer(buf, np.uint8)
     return load().qsf_hip_arena_forget_range(a.ctypes.data, a.nbytes)
+
+
+def slot_lookahead(n: int = -1) -> int:
+    """Successors a table-slot call may run in its own launch (0 = off);
+    n < 0 only queries.  Returns the previous setting."""
+    return load().qsf_hip_slot_lookahead(int(n))
 
 
 class KernelTable:
