@@ -80,7 +80,11 @@ struct Fmt {
     static constexpr int BB = 4 + 4 * CW;                           // block bytes
     static constexpr int DW = CW * NC * ND;                         // digit dwords / block
     static constexpr int DWS = DW | 1;                              // odd LDS stride
-    static constexpr int LPB = pow2ceil(CW);                        // x-prep lanes / block
+    // x-prep lanes per block and x values per lane: 2/4-bit, one code dword
+    // a lane (its 16 or 8 codes); 3-bit, three code dwords (32 codes, whose
+    // slots then map to fixed columns and shifts)
+    static constexpr int LPB = FMT == QK_FMT_3 ? CW / 3 : pow2ceil(CW);
+    static constexpr int NX = FMT == QK_FMT_3 ? 32 : NC * 8;
     // |X| <= 2^XB.  Digit multipliers M = X * 2^shift (shift <= 2 for 3-bit)
     // must lie in the 6-digit balanced range [-0x888888, 0x777777].  A
     // digit sum over a block is at most 8 * 8 * BS <= 2^14 in magnitude, so
@@ -158,68 +162,51 @@ __device__ __forceinline__ void digit_words(const uint32_t (&U)[8], uint32_t (&o
 // before other vector-memory traffic (loads return in issue order).
 template <int FMT, int BS, bool V4 = false>
 __device__ __forceinline__ void prep_load(const float* __restrict__ x, int cols, int b, bool live,
-                                          int w, float (&xv)[Fmt<FMT, BS>::NC * 8]) {
+                                          int w, float (&xv)[Fmt<FMT, BS>::NX]) {
     using F = Fmt<FMT, BS>;
-    constexpr int NS = F::NC * 8;
-    const bool lane_live = live && w < F::CW;
-    if constexpr (FMT != QK_FMT_3 && !V4) {
-        // 2/4-bit, any cols: the lane's slots are NS consecutive x values
-        // (16-B vector loads when in range and aligned), re-ordered to slot order
-        constexpr int CPD = NS;                        // codes per code dword
-        float xr[CPD];
-        const int col0 = b * BS + w * CPD;
-        const bool full = lane_live && col0 + CPD <= cols &&
+    constexpr int NX = F::NX;
+    const bool lane_live = live && w < (FMT == QK_FMT_3 ? F::LPB : F::CW);
+    const int col0 = b * BS + w * NX;
+    if constexpr (!V4) {
+        // any cols: the lane's NX consecutive x values (16-B vector loads
+        // when in range and aligned), 2/4-bit re-ordered to slot order
+        float xr[NX];
+        const bool full = lane_live && col0 + NX <= cols &&
                           ((reinterpret_cast<uintptr_t>(x) & 15) == 0);
         if (full) {
             const float4* x4 = reinterpret_cast<const float4*>(x + col0);
 #pragma unroll
-            for (int k = 0; k < CPD / 4; k++) {
+            for (int k = 0; k < NX / 4; k++) {
                 const float4 v = x4[k];
                 xr[4 * k] = v.x; xr[4 * k + 1] = v.y; xr[4 * k + 2] = v.z; xr[4 * k + 3] = v.w;
             }
         } else {
 #pragma unroll
-            for (int k = 0; k < CPD; k++) {
+            for (int k = 0; k < NX; k++) {
                 const int col = col0 + k;
                 const float v = x[min(max(col, 0), cols - 1)];
                 xr[k] = (lane_live && col < cols) ? v : 0.0f;
             }
         }
 #pragma unroll
-        for (int s = 0; s < NS; s++) {
-            int code, shift;
-            slot_code<FMT>(0, s / 8, s % 8, code, shift);
-            xv[s] = xr[code];
-        }
-    } else if constexpr (FMT != QK_FMT_3) {
-        // 2/4-bit, cols >= 4 (V4): only the loads -- the lane's NS
-        // consecutive x values as dwordx4 (4-byte alignment suffices) at
-        // clamped addresses, raw into xv; prep_settle() fixes them up once
-        // they are needed, so nothing here waits for them
-        const int col0 = b * BS + w * NS;
-#pragma unroll
-        for (int k = 0; k < NS / 4; k++) {
-            const f32x4 v = *reinterpret_cast<const f32x4_a4*>(x + min(col0 + 4 * k, cols - 4));
-            xv[4 * k] = v.x; xv[4 * k + 1] = v.y; xv[4 * k + 2] = v.z; xv[4 * k + 3] = v.w;
-        }
-    } else if constexpr (V4) {
-        // 3-bit, cols >= 4: the lane's slots lie in the 12 columns from
-        // floor(32 w / 3); three dwordx4 loads at clamped addresses, raw into
-        // xv[0..11], re-indexed by prep_settle()
-        const int col0 = b * BS + (32 * w) / 3;
-#pragma unroll
-        for (int k = 0; k < 3; k++) {
-            const f32x4 v = *reinterpret_cast<const f32x4_a4*>(x + min(col0 + 4 * k, cols - 4));
-            xv[4 * k] = v.x; xv[4 * k + 1] = v.y; xv[4 * k + 2] = v.z; xv[4 * k + 3] = v.w;
+        for (int s = 0; s < NX; s++) {
+            if constexpr (FMT == QK_FMT_3) {
+                xv[s] = xr[s];
+            } else {
+                int code, shift;
+                slot_code<FMT>(0, s / 8, s % 8, code, shift);
+                xv[s] = xr[code];
+            }
         }
     } else {
+        // cols >= 4: only the loads -- the lane's NX consecutive x values as
+        // dwordx4 (4-byte alignment suffices) at clamped addresses, raw into
+        // xv; prep_settle() fixes them up once they are needed, so nothing
+        // here waits for them
 #pragma unroll
-        for (int s = 0; s < NS; s++) {
-            int code, shift;
-            slot_code<FMT>(w, s / 8, s % 8, code, shift);
-            const int col = b * BS + code;
-            const float v = x[min(max(col, 0), cols - 1)];
-            xv[s] = (lane_live && col < cols) ? v : 0.0f;
+        for (int k = 0; k < NX / 4; k++) {
+            const f32x4 v = *reinterpret_cast<const f32x4_a4*>(x + min(col0 + 4 * k, cols - 4));
+            xv[4 * k] = v.x; xv[4 * k + 1] = v.y; xv[4 * k + 2] = v.z; xv[4 * k + 3] = v.w;
         }
     }
 }
@@ -248,38 +235,21 @@ __device__ __forceinline__ void settle_chunks(float (&xv)[N], int col0, int cols
 // and put 2/4-bit values in slot order.
 template <int FMT, int BS>
 __device__ __forceinline__ void prep_settle(int b, bool live, int w, int cols,
-                                            float (&xv)[Fmt<FMT, BS>::NC * 8]) {
+                                            float (&xv)[Fmt<FMT, BS>::NX]) {
     using F = Fmt<FMT, BS>;
-    constexpr int NS = F::NC * 8;
-    const bool lane_live = live && w < F::CW;
+    constexpr int NX = F::NX;
+    const bool lane_live = live && w < (FMT == QK_FMT_3 ? F::LPB : F::CW);
+    const int col0 = b * BS + w * NX;
+    if (!lane_live || col0 + NX > cols) settle_chunks<NX / 4>(xv, col0, cols, lane_live);
     if constexpr (FMT != QK_FMT_3) {
-        const int col0 = b * BS + w * NS;
-        if (!lane_live || col0 + NS > cols) settle_chunks<NS / 4>(xv, col0, cols, lane_live);
-        float xr[NS];
+        float xr[NX];
 #pragma unroll
-        for (int s = 0; s < NS; s++) xr[s] = xv[s];
+        for (int s = 0; s < NX; s++) xr[s] = xv[s];
 #pragma unroll
-        for (int s = 0; s < NS; s++) {
+        for (int s = 0; s < NX; s++) {
             int code, shift;
             slot_code<FMT>(0, s / 8, s % 8, code, shift);
             xv[s] = xr[code];
-        }
-    } else {
-        // slot (c, m) of dword w = 3u + v pairs with column c0 + idx_v(m) + c,
-        // idx_v(m) = floor(4 (8v + m) / 3) - floor(32 v / 3)
-        const int col0 = b * BS + (32 * w) / 3;
-        if (!lane_live || col0 + 12 > cols) settle_chunks<3>(xv, col0, cols, lane_live);
-        float xr[12];
-#pragma unroll
-        for (int i = 0; i < 12; i++) xr[i] = xv[i];
-        const int v = w % 3;
-#pragma unroll
-        for (int s = 0; s < NS; s++) {
-            const int c = s / 8, m = s % 8;
-            const float a0 = xr[(4 * m) / 3 + c];
-            const float a1 = xr[(4 * (8 + m)) / 3 - 10 + c];
-            const float a2 = xr[(4 * (16 + m)) / 3 - 21 + c];
-            xv[s] = v == 0 ? a0 : (v == 1 ? a1 : a2);
         }
     }
 }
@@ -305,38 +275,29 @@ __device__ __forceinline__ int group_allreduce(int v, OP op) {
 }
 
 template <int FMT, int BS>
-__device__ __forceinline__ void prep_finish(const float (&xv)[Fmt<FMT, BS>::NC * 8], int b,
+__device__ __forceinline__ void prep_finish(const float (&xv)[Fmt<FMT, BS>::NX], int b,
                                             bool live, int w, uint32_t* dst, float2* meta,
                                             float* xs = nullptr, int cols = 0) {
     using F = Fmt<FMT, BS>;
-    constexpr int NS = F::NC * 8;
-    const bool lane_live = live && w < F::CW;
+    constexpr int NX = F::NX;
+    const bool lane_live = live && w < (FMT == QK_FMT_3 ? F::LPB : F::CW);
     if (xs && lane_live) {
-        if constexpr (FMT == QK_FMT_3) {
+        // the lane's NX consecutive columns from b*BS + NX*w (zero past cols,
+        // as the copy must hold there), in column order as 16-byte LDS stores
+        constexpr auto slot_of = [](int k) {
+            return FMT == QK_FMT_2 ? (k & 1) * 8 + (k >> 1) : k;   // 3-bit: column order
+        };
+        f32x4* d4 = reinterpret_cast<f32x4*>(xs + b * BS + NX * w);
 #pragma unroll
-            for (int s = 0; s < NS; s++) {
-                int code, shift;
-                slot_code<FMT>(w, s / 8, s % 8, code, shift);
-                const int col = b * BS + code;
-                if (col < cols && (3 * code) / 4 == 8 * w + s % 8) xs[col] = xv[s];
-            }
-        } else {
-            // 2/4-bit: the lane's slots are the NS consecutive columns from
-            // b*BS + NS*w (zero past cols, as the copy must hold there),
-            // written back in column order as 16-byte LDS stores
-            constexpr auto slot_of = [](int k) { return FMT == QK_FMT_2 ? (k & 1) * 8 + (k >> 1) : k; };
-            f32x4* d4 = reinterpret_cast<f32x4*>(xs + b * BS + NS * w);
-#pragma unroll
-            for (int q = 0; q < NS / 4; q++)
-                d4[q] = f32x4{xv[slot_of(4 * q)], xv[slot_of(4 * q + 1)], xv[slot_of(4 * q + 2)],
-                              xv[slot_of(4 * q + 3)]};
-        }
+        for (int q = 0; q < NX / 4; q++)
+            d4[q] = f32x4{xv[slot_of(4 * q)], xv[slot_of(4 * q + 1)], xv[slot_of(4 * q + 2)],
+                          xv[slot_of(4 * q + 3)]};
     }
     // block max of |x| as fp32 bits (non-negative floats order like their
     // bits), Inf or NaN counted as +Inf: one integer max over the group
     int amax_b = 0;
 #pragma unroll
-    for (int s = 0; s < NS; s++) {
+    for (int s = 0; s < NX; s++) {
         const float ax = fabsf(xv[s]);
         amax_b = max(amax_b, ax <= 3.402823466e38f ? __builtin_bit_cast(int, ax) : 0x7F800000);
     }
@@ -348,33 +309,38 @@ __device__ __forceinline__ void prep_finish(const float (&xv)[Fmt<FMT, BS>::NC *
         sh = F::XB - 1 - ilogbf(amax);                 // amax * 2^sh < 2^XB
         sh = sh > 126 ? 126 : sh;                      // f = 2^-sh stays a normal fp32
     }
-    uint32_t U[NS];
+    // X once per x value; every code counted once in the sum
+    int X[NX];
     int sum = 0;
 #pragma unroll
-    for (int s = 0; s < NS; s++) {
-        int code, shift;
-        slot_code<FMT>(w, s / 8, s % 8, code, shift);
-        const int X = bad ? 0 : (int)rintf(ldexpf(xv[s], sh));
-        U[s] = (uint32_t)(X * (1 << shift) + (int)DIGIT_BIAS);
-        // count every code once: 3-bit codes at the nibble holding their bit 0
-        if constexpr (FMT == QK_FMT_3) {
-            if ((3 * code) / 4 == 8 * w + s % 8) sum += X;
-        } else {
-            sum += X;
-        }
+    for (int s = 0; s < NX; s++) {
+        X[s] = bad ? 0 : (int)rintf(ldexpf(xv[s], sh));
+        sum += X[s];
     }
     // |block total| <= BS * 2^XB <= 2^29: exact in int32
     sum = group_allreduce<F::LPB>(sum, [](int u, int v) { return u + v; });
     const double dsum = (double)sum;
     if (lane_live) {
+        // code dwords of the lane: w (2/4-bit), 3w .. 3w+2 (3-bit); the
+        // multiplier of slot (c, m) of dword v is X[code] * 2^shift
+        constexpr int DPL = FMT == QK_FMT_3 ? 3 : 1;
 #pragma unroll
-        for (int c = 0; c < F::NC; c++) {
-            uint32_t u8[8], dw[ND];
+        for (int v = 0; v < DPL; v++) {
 #pragma unroll
-            for (int m = 0; m < 8; m++) u8[m] = U[c * 8 + m];
-            digit_words(u8, dw);
+            for (int c = 0; c < F::NC; c++) {
+                uint32_t u8[8], dw[ND];
 #pragma unroll
-            for (int d = 0; d < ND; d++) dst[(w * F::NC + c) * ND + d] = dw[d];
+                for (int m = 0; m < 8; m++) {
+                    int code, shift;
+                    slot_code<FMT>(v, c, m, code, shift);
+                    const int xi = FMT == QK_FMT_3 ? code : c * 8 + m;
+                    u8[m] = (uint32_t)(X[xi] * (1 << shift) + (int)DIGIT_BIAS);
+                }
+                digit_words(u8, dw);
+                const int wd = DPL * w + v;
+#pragma unroll
+                for (int d = 0; d < ND; d++) dst[(wd * F::NC + c) * ND + d] = dw[d];
+            }
         }
     }
     if (live && w == 0) {
@@ -388,7 +354,7 @@ template <int FMT, int BS>
 __device__ __forceinline__ void prep_block(const float* __restrict__ x, int cols, int b, bool live,
                                            int w, uint32_t* dst, float2* meta,
                                            float* xs = nullptr) {
-    float xv[Fmt<FMT, BS>::NC * 8];
+    float xv[Fmt<FMT, BS>::NX];
     prep_load<FMT, BS>(x, cols, b, live, w, xv);
     prep_finish<FMT, BS>(xv, b, live, w, dst, meta, xs, cols);
 }
@@ -769,27 +735,33 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
     float* xcopy = OUT ? xs : nullptr;
     uint32_t wv[D][R][1 + F::CW];
     if constexpr (!PREP) {
-        // the first two passes load their x together (the second pass is the
-        // 7B down projection's: 172 4-bit or 86 3-bit blocks); passes past
-        // the second, for still wider rows, run one after another
-        constexpr int NS = F::NC * 8;
+        // 2/4-bit: the first two passes load their x together (the second
+        // pass is the 7B down projection's: 172 4-bit blocks); 3-bit: one
+        // pass covers 512 or more blocks, loaded ahead.  Passes past those,
+        // for still wider rows, run one after another.
+        constexpr int NX = F::NX;
+        constexpr int AHEAD = FMT == QK_FMT_3 ? 1 : 2;
         const int pb1 = pb + PASS;
-        const bool two = prep_wave && PASS + wave * (64 / F::LPB) < a.nb;
-        float xv0[NS], xv1[NS];
+        const bool two = AHEAD == 2 && prep_wave && PASS + wave * (64 / F::LPB) < a.nb;
+        float xv0[NX], xv1[AHEAD == 2 ? NX : 1];
         if (prep_wave) prep_load<FMT, BS, true>(a.x, a.cols, pb, pb < a.nb, pw, xv0);
-        if (two) prep_load<FMT, BS, true>(a.x, a.cols, pb1, pb1 < a.nb, pw, xv1);
+        if constexpr (AHEAD == 2)
+            if (two) prep_load<FMT, BS, true>(a.x, a.cols, pb1, pb1 < a.nb, pw, xv1);
         issue(wv[0]);                                        // 3. the first weight item
         if (prep_wave) {
             const int b0 = pb < a.nb ? pb : 0;
             prep_settle<FMT, BS>(pb, pb < a.nb, pw, a.cols, xv0);
             prep_finish<FMT, BS>(xv0, pb, pb < a.nb, pw, dig + b0 * F::DWS, meta + b0, xcopy, a.cols);
         }
-        if (two) {
-            const int b1 = pb1 < a.nb ? pb1 : 0;
-            prep_settle<FMT, BS>(pb1, pb1 < a.nb, pw, a.cols, xv1);
-            prep_finish<FMT, BS>(xv1, pb1, pb1 < a.nb, pw, dig + b1 * F::DWS, meta + b1, xcopy, a.cols);
+        if constexpr (AHEAD == 2) {
+            if (two) {
+                const int b1 = pb1 < a.nb ? pb1 : 0;
+                prep_settle<FMT, BS>(pb1, pb1 < a.nb, pw, a.cols, xv1);
+                prep_finish<FMT, BS>(xv1, pb1, pb1 < a.nb, pw, dig + b1 * F::DWS, meta + b1, xcopy,
+                                     a.cols);
+            }
         }
-        for (int base = 2 * PASS; base < a.nb; base += PASS) {
+        for (int base = AHEAD * PASS; base < a.nb; base += PASS) {
             if (base + wave * (64 / F::LPB) >= a.nb) break;     // whole wave past the end
             const int b = base + pb;
             const bool live = b < a.nb;
