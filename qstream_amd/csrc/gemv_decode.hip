@@ -294,30 +294,34 @@ __device__ __forceinline__ void prep_finish(const float (&xv)[Fmt<FMT, BS>::NX],
                           xv[slot_of(4 * q + 3)]};
     }
     // block max of |x| as fp32 bits (non-negative floats order like their
-    // bits), Inf or NaN counted as +Inf: one integer max over the group
-    int amax_b = 0;
+    // bits; Inf and NaN give bits >= 0x7F800000): one integer max over the group
+    uint32_t amax_u = 0;
 #pragma unroll
-    for (int s = 0; s < NX; s++) {
-        const float ax = fabsf(xv[s]);
-        amax_b = max(amax_b, ax <= 3.402823466e38f ? __builtin_bit_cast(int, ax) : 0x7F800000);
-    }
-    amax_b = group_allreduce<F::LPB>(amax_b, [](int u, int v) { return max(u, v); });
-    const bool bad = amax_b == 0x7F800000;
+    for (int s = 0; s < NX; s++) amax_u = max(amax_u, __builtin_bit_cast(uint32_t, xv[s]) & 0x7FFFFFFFu);
+    const int amax_b = group_allreduce<F::LPB>((int)amax_u, [](int u, int v) { return max(u, v); });
+    const bool bad = amax_b >= 0x7F800000;
     const float amax = __builtin_bit_cast(float, amax_b);
     int sh = 0;
     if (!bad && amax > 0.0f) {
         sh = F::XB - 1 - ilogbf(amax);                 // amax * 2^sh < 2^XB
         sh = sh > 126 ? 126 : sh;                      // f = 2^-sh stays a normal fp32
     }
-    // X once per x value; every code counted once in the sum
-    int X[NX];
-    int sum = 0;
+    // X = rint(x * 2^sh) once per x value, biased: |x * 2^sh| < 2^XB <= 2^22,
+    // so x * 2^sh + 1.5 * 2^23 (one rounding, to nearest even, as rintf)
+    // is the integer 1.5 * 2^23 + X, whose bits are 0x4B400000 + X.  A block
+    // with Inf or NaN gets NaN meta, which makes its digits irrelevant.
+    const float scale = ldexpf(1.0f, sh);
+    uint32_t U0[NX];
+    uint32_t bsum = 0;
 #pragma unroll
     for (int s = 0; s < NX; s++) {
-        X[s] = bad ? 0 : (int)rintf(ldexpf(xv[s], sh));
-        sum += X[s];
+        const uint32_t bits = __builtin_bit_cast(uint32_t, fmaf(xv[s], scale, 12582912.0f));
+        U0[s] = bits - (0x4B400000u - DIGIT_BIAS);     // X + DIGIT_BIAS
+        bsum += bits;
     }
-    // |block total| <= BS * 2^XB <= 2^29: exact in int32
+    // every code counted once; |block total| <= BS * 2^XB <= 2^29: exact in
+    // int32 (the sum of biased bits wraps back to it)
+    int sum = bad ? 0 : (int)(bsum - (uint32_t)NX * 0x4B400000u);
     sum = group_allreduce<F::LPB>(sum, [](int u, int v) { return u + v; });
     const double dsum = (double)sum;
     if (lane_live) {
@@ -334,7 +338,8 @@ __device__ __forceinline__ void prep_finish(const float (&xv)[Fmt<FMT, BS>::NX],
                     int code, shift;
                     slot_code<FMT>(v, c, m, code, shift);
                     const int xi = FMT == QK_FMT_3 ? code : c * 8 + m;
-                    u8[m] = (uint32_t)(X[xi] * (1 << shift) + (int)DIGIT_BIAS);
+                    // X * 2^shift + DIGIT_BIAS
+                    u8[m] = (U0[xi] << shift) + (DIGIT_BIAS - (DIGIT_BIAS << shift));
                 }
                 digit_words(u8, dw);
                 const int wd = DPL * w + v;
