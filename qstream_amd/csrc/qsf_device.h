@@ -24,6 +24,14 @@ __device__ __forceinline__ float f16_bits(uint16_t v) {
 __device__ __forceinline__ int sdot8(uint32_t a, uint32_t b, int c) {
     return __builtin_amdgcn_sdot8((int)a, (int)b, c, false);
 }
+// The same with a zero accumulator, as the three-operand v_dot8_i32_i4 with
+// an inline-constant 0: for sdot8(a, b, 0) the compiler materialises the
+// zero with a v_mov and uses the two-address v_dot8c form.
+__device__ __forceinline__ int sdot8_z(uint32_t a, uint32_t b) {
+    int r;
+    asm("v_dot8_i32_i4 %0, %1, %2, 0" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
 
 // Butterfly sum over groups of `width` consecutive lanes (power of two).
 __device__ __forceinline__ float group_sum(float v, int width) {

@@ -102,7 +102,8 @@ def test_xprep_digits_exact(hip, qt, bs):
     nb = (cols + bs - 1) // bs
     cw, nc, slots = _slots(qt, bs)
     nd = 6
-    dws = (cw * nc * nd) | 1
+    dw = cw * nc * nd                            # digit words a block, a multiple of 4
+    dws = dw if (dw // 4) % 2 else dw + 4        # stride: an odd number of 16-byte quads
     xb = 20 if qt == F.Q3 else 22
     nbytes = hip.xprep_bytes(qt, bs, cols)
     buf = torch.zeros(nbytes + 256, dtype=torch.uint8, device="cuda:0")
