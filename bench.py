@@ -82,12 +82,13 @@ def cfg2_layer(seed=2):
     return F.config2_layer(seed)
 
 
-def cfg3_experts(seed=3, n_exp=32, dim=2880):
+def cfg3_experts(seed=3, n_exp=32, dim=2880, workers=None):
     """32 MXFP4 experts (gate, up [2880][2880], down [2880][2880]) quantised
     from N(0, 0.02) weights, one seed per matrix (qsf_format.moe_experts;
-    the config-3 parity tests build the same experts)."""
+    the config-3 parity tests build the same experts).  The bytes do not
+    depend on `workers`."""
     from qstream_amd import qsf_format as F
-    return F.moe_experts(seed, n_exp, dim, dim)
+    return F.moe_experts(seed, n_exp, dim, dim, workers=workers)
 
 
 def algo_bytes(mats) -> int:
@@ -552,7 +553,9 @@ def profile_moe(torch, hip, steps, warmup, ntok):
     rocprofv3 counter passes."""
     from qstream_amd import qsf_format as F
     n_exp, dim, k = 32, 2880, 4
-    ex = cfg3_experts()
+    # built in this process: worker processes started under a counter pass
+    # each carry the profiler, and one of them has failed to exit
+    ex = cfg3_experts(workers=1)
     tens = {n: [hip.Tensor(e[n], F.MXFP4, dim, dim, 32) for e in ex] for n in ("gate", "up", "down")}
     moe = hip.Moe(tens["gate"], tens["up"], tens["down"], dim, dim)
     rng = np.random.default_rng(30 + ntok)
