@@ -85,9 +85,10 @@ struct Fmt {
     static constexpr int DWS = (DW / 4) % 2 ? DW : DW + 4;
     static_assert(DW % 4 == 0, "digit words come in quads");
     // x-prep lanes per block and x values per lane: 2/4-bit, one code dword
-    // a lane (its 16 or 8 codes); 3-bit, three code dwords (32 codes, whose
-    // slots then map to fixed columns and shifts)
-    static constexpr int LPB = FMT == QK_FMT_3 ? CW / 3 : pow2ceil(CW);
+    // a lane (its 16 or 8 codes); 3-bit, two lanes for each three code
+    // dwords (32 codes, whose slots then map to fixed columns and shifts),
+    // one masked copy each
+    static constexpr int LPB = FMT == QK_FMT_3 ? 2 * CW / 3 : pow2ceil(CW);
     static constexpr int NX = FMT == QK_FMT_3 ? 32 : NC * 8;
     // |X| <= 2^XB.  Digit multipliers M = X * 2^shift (shift <= 2 for 3-bit)
     // must lie in the 6-digit balanced range [-0x888888, 0x777777].  A
@@ -170,7 +171,7 @@ __device__ __forceinline__ void prep_load(const float* __restrict__ x, int cols,
     using F = Fmt<FMT, BS>;
     constexpr int NX = F::NX;
     const bool lane_live = live && w < (FMT == QK_FMT_3 ? F::LPB : F::CW);
-    const int col0 = b * BS + w * NX;
+    const int col0 = b * BS + (FMT == QK_FMT_3 ? w >> 1 : w) * NX;
     if constexpr (!V4) {
         // any cols: the lane's NX consecutive x values (16-B vector loads
         // when in range and aligned), 2/4-bit re-ordered to slot order
@@ -243,7 +244,7 @@ __device__ __forceinline__ void prep_settle(int b, bool live, int w, int cols,
     using F = Fmt<FMT, BS>;
     constexpr int NX = F::NX;
     const bool lane_live = live && w < (FMT == QK_FMT_3 ? F::LPB : F::CW);
-    const int col0 = b * BS + w * NX;
+    const int col0 = b * BS + (FMT == QK_FMT_3 ? w >> 1 : w) * NX;
     if (!lane_live || col0 + NX > cols) settle_chunks<NX / 4>(xv, col0, cols, lane_live);
     if constexpr (FMT != QK_FMT_3) {
         float xr[NX];
@@ -285,13 +286,15 @@ __device__ __forceinline__ void prep_finish(const float (&xv)[Fmt<FMT, BS>::NX],
     using F = Fmt<FMT, BS>;
     constexpr int NX = F::NX;
     const bool lane_live = live && w < (FMT == QK_FMT_3 ? F::LPB : F::CW);
-    if (xs && lane_live) {
-        // the lane's NX consecutive columns from b*BS + NX*w (zero past cols,
-        // as the copy must hold there), in column order as 16-byte LDS stores
+    const int xg = FMT == QK_FMT_3 ? w >> 1 : w;         // the lane's group of NX x values
+    if (xs && lane_live && (FMT != QK_FMT_3 || (w & 1) == 0)) {
+        // the lane's NX consecutive columns from b*BS + NX*xg (zero past
+        // cols, as the copy must hold there), in column order as 16-byte
+        // LDS stores
         constexpr auto slot_of = [](int k) {
             return FMT == QK_FMT_2 ? (k & 1) * 8 + (k >> 1) : k;   // 3-bit: column order
         };
-        f32x4* d4 = reinterpret_cast<f32x4*>(xs + b * BS + NX * w);
+        f32x4* d4 = reinterpret_cast<f32x4*>(xs + b * BS + NX * xg);
 #pragma unroll
         for (int q = 0; q < NX / 4; q++)
             d4[q] = f32x4{xv[slot_of(4 * q)], xv[slot_of(4 * q + 1)], xv[slot_of(4 * q + 2)],
@@ -325,30 +328,41 @@ __device__ __forceinline__ void prep_finish(const float (&xv)[Fmt<FMT, BS>::NX],
     }
     // every code counted once; |block total| <= BS * 2^XB <= 2^29: exact in
     // int32 (the sum of biased bits wraps back to it)
-    int sum = bad ? 0 : (int)(bsum - (uint32_t)NX * 0x4B400000u);
+    // (3-bit: the two lanes of a group hold the same values; one counts them)
+    int sum = bad || (FMT == QK_FMT_3 && (w & 1)) ? 0 : (int)(bsum - (uint32_t)NX * 0x4B400000u);
     sum = group_allreduce<F::LPB>(sum, [](int u, int v) { return u + v; });
     const double dsum = (double)sum;
     if (lane_live) {
-        // code dwords of the lane: w (2/4-bit), 3w .. 3w+2 (3-bit); the
-        // multiplier of slot (c, m) of dword v is X[code] * 2^shift
-        constexpr int DPL = FMT == QK_FMT_3 ? 3 : 1;
+        if constexpr (FMT == QK_FMT_3) {
+            // code dwords 3*xg .. 3*xg+2, masked copy c = w % 2 of each: the
+            // multiplier of slot (c, m) of dword v is X[code] * 2^shift,
+            // where copy 1 pairs with the code after copy 0's
+            const int c = w & 1;
 #pragma unroll
-        for (int v = 0; v < DPL; v++) {
-#pragma unroll
-            for (int c = 0; c < F::NC; c++) {
+            for (int v = 0; v < 3; v++) {
                 uint32_t u8[8], dw[ND];
 #pragma unroll
                 for (int m = 0; m < 8; m++) {
                     int code, shift;
-                    slot_code<FMT>(v, c, m, code, shift);
-                    const int xi = FMT == QK_FMT_3 ? code : c * 8 + m;
+                    slot_code<FMT>(v, 0, m, code, shift);
+                    const uint32_t xu = c ? U0[code + 1] : U0[code];
                     // X * 2^shift + DIGIT_BIAS
-                    u8[m] = (U0[xi] << shift) + (DIGIT_BIAS - (DIGIT_BIAS << shift));
+                    u8[m] = (xu << shift) + (DIGIT_BIAS - (DIGIT_BIAS << shift));
                 }
                 digit_words(u8, dw);
-                const int wd = DPL * w + v;
 #pragma unroll
-                for (int d = 0; d < ND; d++) dst[(wd * F::NC + c) * ND + d] = dw[d];
+                for (int d = 0; d < ND; d++) dst[((3 * xg + v) * F::NC + c) * ND + d] = dw[d];
+            }
+        } else {
+            // code dword w, both masked copies (one for 4-bit)
+#pragma unroll
+            for (int c = 0; c < F::NC; c++) {
+                uint32_t u8[8], dw[ND];
+#pragma unroll
+                for (int m = 0; m < 8; m++) u8[m] = U0[c * 8 + m];   // X + DIGIT_BIAS
+                digit_words(u8, dw);
+#pragma unroll
+                for (int d = 0; d < ND; d++) dst[(w * F::NC + c) * ND + d] = dw[d];
             }
         }
     }
@@ -747,7 +761,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
     if constexpr (!PREP) {
         // 2/4-bit: the first two passes load their x together (the second
         // pass is the 7B down projection's: 172 4-bit blocks); 3-bit: one
-        // pass covers 512 or more blocks, loaded ahead.  Passes past those,
+        // pass covers 256 or more blocks, loaded ahead.  Passes past those,
         // for still wider rows, run one after another.
         constexpr int NX = F::NX;
         constexpr int AHEAD = FMT == QK_FMT_3 ? 1 : 2;
