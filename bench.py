@@ -726,7 +726,7 @@ def run_config(torch, hip, key: str, args, cpu_budget: float, cache: dict) -> di
     elif key in ("3", "3b1", "3b8"):
         ntok = args.moe_batch if key == "3" else int(key[2:])
         if "experts" not in cache:
-            cache["experts"] = cfg3_experts()
+            cache["experts"] = cfg3_experts(workers=args.data_workers)
         r = bench_moe(torch, hip, args.steps, args.warmup, ntok, with_cpu=with_cpu,
                       cpu_budget=cpu_budget, ex=cache["experts"])
         line = dict(base, value=round(r["value"], 2), ms_per_step=round(r["ms_per_step"], 5),
@@ -789,6 +789,9 @@ def main():
     ap.add_argument("--config", default="1", help="1 (default), 0, 2, 3, 4, layer, all, or copy")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-slot", action="store_true", help="skip the table-slot (PCIe) timing")
+    ap.add_argument("--data-workers", type=int, default=None,
+                    help="processes that build config 3's experts (default: up to 16; 1 under a "
+                         "profiler, whose worker processes have failed to exit)")
     ap.add_argument("--moe-batch", type=int, default=1, help="tokens per step for --config 3")
     ap.add_argument("--split", action="store_true",
                     help="stand-alone x-prep launch + GEMV on prepared digits")
