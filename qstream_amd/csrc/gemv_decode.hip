@@ -407,7 +407,10 @@ __host__ __device__ inline float2* xmeta_in(void* ws, int nb) {
 
 // Group sum over `lpg` lanes (power of two) with DPP; the total is valid in
 // the group's last lane (all lanes for lpg <= 16).
-__device__ __forceinline__ float group_reduce(float v, int lpg) { return qsf::group_sum_last(v, lpg); }
+__device__ __forceinline__ float group_reduce(float v, int lpg) {
+    if (lpg == 64) return qsf::group_sum_last(v, 64);
+    return qsf::group_sum_last(v, lpg);
+}
 #undef QSF_DPP
 
 struct GemvArgs {
