@@ -459,6 +459,40 @@ __device__ __forceinline__ void put_inputs(float* xs, const float4 (&xr)[T][XR],
         }
 }
 
+// Pointer fields [F0, F0 + NF) of every expert's table entry into LDS,
+// tab[e * NF + f], by the threads from t0 up of a TB-thread workgroup: the
+// loads into registers (table_load), then the LDS stores (table_store).
+// Loaded at a kernel's start, beside the routing or the route record's
+// reads (issued between the two calls, so that neither waits for the
+// other), the entries a work item needs are an LDS read away once its
+// expert is known, instead of one more memory round trip in front of the
+// first weight load.  The caller synchronises the workgroup before reading.
+static_assert(sizeof(MxExpert) == 9 * sizeof(void*), "expert table entry: nine pointers");
+template <int NF, int TB, int T0>
+constexpr int kTabPer = (MAX_EXP * NF + TB - T0 - 1) / (TB - T0);   // entries a thread
+template <int F0, int NF, int TB, int T0>
+__device__ __forceinline__ void table_load(const MxExpert* ex, int n_exp, uint64_t (&tv)[kTabPer<NF, TB, T0>]) {
+    const uint64_t* src = reinterpret_cast<const uint64_t*>(ex);
+#pragma unroll
+    for (int j = 0; j < kTabPer<NF, TB, T0>; j++) {
+        const int i = (int)threadIdx.x - T0 + j * (TB - T0);
+        const int e = i / NF, f = i - e * NF;
+        tv[j] = i >= 0 && i < n_exp * NF ? src[e * 9 + F0 + f] : 0ull;
+    }
+}
+template <int NF, int TB, int T0>
+__device__ __forceinline__ void table_store(int n_exp, const uint64_t (&tv)[kTabPer<NF, TB, T0>], uint64_t* tab) {
+#pragma unroll
+    for (int j = 0; j < kTabPer<NF, TB, T0>; j++) {
+        const int i = (int)threadIdx.x - T0 + j * (TB - T0);
+        if (i >= 0 && i < n_exp * NF) tab[i] = tv[j];
+    }
+}
+template <typename T>
+__device__ __forceinline__ T tab_ptr(const uint64_t* tab, int i) {
+    return reinterpret_cast<T>(tab[i]);
+}
+
 // Routing once per step: one wave per token, then the distinct-expert list
 // (one launch of MAX_TOK waves; the expert kernels read the result).
 __global__ __launch_bounds__(MAX_TOK * 64) void moe_route_kernel(MoeArgs a) {
@@ -493,12 +527,19 @@ __global__ __launch_bounds__(MAX_TOK * 64) void moe_route_kernel(MoeArgs a) {
 template <int NI, bool RT>
 __global__ __launch_bounds__(GU_WAVES * 64) void moe_gate_up_kernel(MoeArgs a) {
     constexpr int MR = GU_MR;
-    extern __shared__ __align__(16) float xs[];           // [n][hidden, padded]
+    extern __shared__ __align__(16) float xs[];           // [n][hidden, padded], expert table
     float4 xr[TCH][XR];
     const Route* rtp = a.route;
+    const int nb = (a.hidden + 31) / 32;
+    // in-kernel routing: the expert table after the input (wave 0 routes,
+    // the others load the table)
+    uint64_t* tab = reinterpret_cast<uint64_t*>(xs + (size_t)nb * XBP);
+    constexpr int T0 = 64;
     if constexpr (RT) {
+        uint64_t tv[kTabPer<6, GU_WAVES * 64, T0>];
         // the one token's input does not depend on the routing: loaded first
         load_inputs<TCH>(xr, 1, a.hidden, [&](int) { return a.x; });
+        table_load<0, 6, GU_WAVES * 64, T0>(a.experts, a.n_exp, tv);
         __shared__ int s_idx[MAX_K];
         __shared__ float s_w[MAX_K];
         __shared__ float s_p[MAX_EXP];
@@ -515,6 +556,7 @@ __global__ __launch_bounds__(GU_WAVES * 64) void moe_gate_up_kernel(MoeArgs a) {
             }
             build_work(s_idx, a.k, a.k, s_tok, s_item, s_rt);
         }
+        table_store<6, GU_WAVES * 64, T0>(a.n_exp, tv, tab);
         __syncthreads();
         if (blockIdx.x == 0 && blockIdx.y == 0) {
             const uint32_t* src = reinterpret_cast<const uint32_t*>(&s_rt);
@@ -525,8 +567,17 @@ __global__ __launch_bounds__(GU_WAVES * 64) void moe_gate_up_kernel(MoeArgs a) {
     }
     if ((int)blockIdx.y >= rtp->nwork) return;
     const Work& wk = rtp->work[blockIdx.y];
-    const MxExpert ex = a.experts[wk.expert];
-    const int nb = (a.hidden + 31) / 32;
+    struct { const uint8_t *gc, *gs; const uint16_t* gb; const uint8_t *uc, *us; const uint16_t* ub; } ex;
+    if constexpr (RT) {
+        const uint64_t* te = tab + wk.expert * 6;
+        ex = {tab_ptr<const uint8_t*>(te, 0), tab_ptr<const uint8_t*>(te, 1), tab_ptr<const uint16_t*>(te, 2),
+              tab_ptr<const uint8_t*>(te, 3), tab_ptr<const uint8_t*>(te, 4), tab_ptr<const uint16_t*>(te, 5)};
+    } else {
+        // (many workgroup rounds: a table copy in each cost more than the
+        // one dependent read it saves)
+        const MxExpert& e = a.experts[wk.expert];
+        ex = {e.gc, e.gs, e.gb, e.uc, e.us, e.ub};
+    }
     const MxMat mat[2] = {{ex.gc, ex.gs, a.eid, a.hidden, nb}, {ex.uc, ex.us, a.eid, a.hidden, nb}};
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int lig = lane & 31;
@@ -602,9 +653,35 @@ constexpr int FMR = FD_MR;                 // rows per 32-lane group
 constexpr int FROWS = FGW * 2 * FMR;       // rows of a workgroup (4)
 template <int NI>
 __global__ __launch_bounds__(FG * FGW * 64) void moe_down_fused_kernel(MoeArgs a) {
-    extern __shared__ __align__(16) float xs[];  // [FG][eid, padded], then [FG][FROWS] row sums
+    // [FG][eid, padded], then [FG][FROWS] row sums, then the expert table
+    extern __shared__ __align__(16) float xs[];
     const Route& rt = *a.route;
+    const int nb = (a.eid + 31) / 32;
+    float* part = xs + (size_t)FG * nb * XBP;
+    uint64_t* tab = reinterpret_cast<uint64_t*>(part + FG * FROWS);
+    // The route record first, every read at a fixed address so that they
+    // issue together: the count, each work item's expert and (one token)
+    // slot, and the combine's ranks and weights (k <= FG here; loaded one
+    // rank at a time at the end, each was a memory round trip in every
+    // workgroup's tail).  Ranks past k and empty ranks are left out of the
+    // sum below; items past the count are not used.  The table's loads are
+    // issued first and its LDS stores follow these reads.
+    uint64_t tv[kTabPer<3, FG * FGW * 64, 0>];
+    table_load<6, 3, FG * FGW * 64, 0>(a.experts, a.n_exp, tv);
     const int nwork = rt.nwork;
+    int w_e[FG], w_s[FG];
+    bool on[FG];
+    float wq[FG];
+#pragma unroll
+    for (int q = 0; q < FG; q++) {
+        w_e[q] = rt.work[q].expert;
+        w_s[q] = rt.work[q].slot[0];
+        on[q] = (q < a.k) & (rt.idx[q] >= 0);    // '&': the load is not skipped
+        wq[q] = rt.w[q];
+    }
+    asm volatile("" ::"s"(nwork), "s"(w_e[0]), "s"(w_e[1]), "s"(w_e[2]), "s"(w_e[3]), "s"(w_s[0]),
+                 "s"(w_s[1]), "s"(w_s[2]), "s"(w_s[3]));   // (as gate/up)
+    table_store<3, FG * FGW * 64, 0>(a.n_exp, tv, tab);
     if (nwork == 0) {                            // no expert picked: out = 0, as the combine
         const int row = blockIdx.x * FROWS + threadIdx.x;
         if ((int)threadIdx.x < FROWS && row < a.hidden) a.out[row] = 0.0f;
@@ -614,19 +691,22 @@ __global__ __launch_bounds__(FG * FGW * 64) void moe_down_fused_kernel(MoeArgs a
     const int wl = (threadIdx.x >> 6) & (FGW - 1);
     const int lane = threadIdx.x & 63, lig = lane & 31;
     const int gi = g < nwork ? g : 0;            // groups past the experts recompute item 0, store nothing
-    const Work& wk = rt.work[gi];
-    const MxExpert ex = a.experts[wk.expert];
-    const int nb = (a.eid + 31) / 32;
+    const int nst = nwork < FG ? nwork : FG;
+    __syncthreads();
+    int e_g = w_e[0];
+#pragma unroll
+    for (int i = 1; i < FG; i++) e_g = gi == i ? w_e[i] : e_g;
+    const uint64_t* te = tab + e_g * 3;
+    const struct { const uint8_t *dc, *ds; const uint16_t* db; } ex = {
+        tab_ptr<const uint8_t*>(te, 0), tab_ptr<const uint8_t*>(te, 1), tab_ptr<const uint16_t*>(te, 2)};
     const MxMat mat[1] = {{ex.dc, ex.ds, a.hidden, a.eid, nb}};
     const int tile0 = blockIdx.x * FROWS;
     const int row0 = tile0 + wl * 2 * FMR + (lane >> 5) * FMR;
-    float* part = xs + (size_t)FG * nb * XBP;
-    const int nst = nwork < FG ? nwork : FG;
     // one input a group, all groups' at once, loaded ahead of the codes
     static_assert(FG * FGW * 64 * XR * 4 >= 4096, "one register chunk holds a 4096-float input");
     float4 xr[FG][XR];
     auto pre = [&]() {
-        load_inputs<FG>(xr, nst, a.eid, [&](int i) { return (const float*)(a.h + (size_t)rt.work[i].slot[0] * a.eid); });
+        load_inputs<FG>(xr, nst, a.eid, [&](int i) { return (const float*)(a.h + (size_t)w_s[i] * a.eid); });
     };
     auto stage = [&](int, int) {
         put_inputs<FG>(xs, xr, nst, nb);
@@ -647,10 +727,9 @@ __global__ __launch_bounds__(FG * FGW * 64) void moe_down_fused_kernel(MoeArgs a
         const int row = tile0 + threadIdx.x;
         if (row < a.hidden) {
             float acc = 0.0f;
-            for (int q = 0; q < a.k; q++) {
-                if (rt.idx[q] < 0) continue;
-                acc += rt.w[q] * part[q * FROWS + threadIdx.x];
-            }
+#pragma unroll
+            for (int q = 0; q < FG; q++)
+                if (on[q]) acc += wq[q] * part[q * FROWS + threadIdx.x];
             a.out[row] = acc;
         }
     }
@@ -760,7 +839,8 @@ extern "C" int qk_moe_launch(const qk_mx_expert* d_experts, int n_exp, int k, in
     const bool one = ntok == 1 && k <= FG;
     if (!one) hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(MAX_TOK * 64), 0, s, a);
     const int tch = ntok < TCH ? ntok : TCH;
-    const size_t lds_gu = (size_t)tch * ((hidden + 31) / 32) * XBP * 4,
+    // inputs (one token: then the expert table's gate/up pointers)
+    const size_t lds_gu = (size_t)tch * ((hidden + 31) / 32) * XBP * 4 + (one ? (size_t)n_exp * 6 * 8 : 0),
                  lds_dn = (size_t)tch * ((eid + 31) / 32) * XBP * 4;
     const int ni_gu = (hidden + 1023) / 1024, ni_dn = (eid + 1023) / 1024;
 #define QK_GU(NI)                                                                        \
@@ -776,7 +856,8 @@ extern "C" int qk_moe_launch(const qk_mx_expert* d_experts, int n_exp, int k, in
     if (one) {
         // one token: down and combine in one launch
         const dim3 g_f((hidden + FROWS - 1) / FROWS), b_f(FG * FGW * 64);
-        const size_t lds_f = (size_t)FG * ((eid + 31) / 32) * XBP * 4 + (size_t)FG * FROWS * 4;
+        const size_t lds_f = (size_t)FG * ((eid + 31) / 32) * XBP * 4 + (size_t)FG * FROWS * 4 +
+                             (size_t)n_exp * 3 * 8;
         switch (ni_dn) {
         case 1: launch_lds<moe_down_fused_kernel<1>>(g_f, b_f, lds_f, s, a); break;
         case 2: launch_lds<moe_down_fused_kernel<2>>(g_f, b_f, lds_f, s, a); break;
