@@ -420,6 +420,14 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
                         __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // VALU
                     }
                     __builtin_amdgcn_sched_barrier(0);
+                } else {
+                    // zero-point stages: the next n-tile's B reads ahead of
+                    // this one's MFMAs too (left to the scheduler, they sank
+                    // behind them, into one register set, and every n-tile
+                    // waited for its reads)
+                    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);      // DS reads
+                    __builtin_amdgcn_sched_group_barrier(0x008, 2 * MT, 0); // MFMA
+                    __builtin_amdgcn_sched_barrier(0);
                 }
             }
             // this sub-block's A fragments are refilled with stage s+1's
