@@ -467,14 +467,19 @@ def bench_decode_layer(torch, hip, steps, warmup, position=1023):
     weights): q/k/v (one grouped launch) on the normed input, RoPE + int8 KV
     store (one launch), attention over `position` + 1 cached positions (two
     launches), o, residual + NaN check + FFN RMSNorm (one launch), gate/up
-    (grouped), SiLU x up, down, residual + NaN check + the next layer's
-    attention RMSNorm (one launch) -- 10 launches, no host round trip.  Steps cycle over 32 layers' distinct weights and
+    with SiLU x up (one launch over the interleaved gate/up pair), down,
+    residual + NaN check + the next layer's attention RMSNorm (one launch)
+    -- 9 launches, no host round trip.  Steps cycle over 32 layers' distinct weights and
     KV caches (2.9 GB), so neither stays in the MALL.  Bytes per step: the
     layer's weight payloads, the KV rows attention reads, activations."""
     qt, bs, mats = cfg2_layer()
     log("layer: weights quantised")
     hid, nh, hd, eid, max_seq, n_layers = 4096, 32, 128, 11008, position + 1, 32
-    layers = [[hip.Tensor(p, qt, r, c, bs) for _, p, r, c in mats] for _ in range(n_layers)]
+    # q, k, v, o and down as tensors; gate and up as one interleaved pair
+    layers = [[hip.Tensor(p, qt, r, c, bs) for _, p, r, c in mats[:4] + mats[6:7]]
+              for _ in range(n_layers)]
+    pairs = [hip.TensorPair(mats[4][1], mats[5][1], qt, mats[4][2], mats[4][3], bs)
+             for _ in range(n_layers)]
     g = torch.Generator(device="cuda:0").manual_seed(40)
     kcs = [torch.randint(-127, 128, (nh, max_seq, hd), dtype=torch.int8, device="cuda:0", generator=g)
            for _ in range(n_layers)]
@@ -501,9 +506,8 @@ def bench_decode_layer(torch, hip, steps, warmup, position=1023):
                       stream=stream)
         hip.matvec_group(ts[3:4], attn, [ys["o"]], stream=stream)
         hip.residual_norm(res, ys["o"], fn_w, 1e-5, x, stream=stream)
-        hip.matvec_group(ts[4:6], x, [ys["gate"], ys["up"]], stream=stream)
-        hip.act_mul(ys["gate"], ys["up"], 2, stream=stream)
-        hip.matvec_group(ts[6:7], ys["gate"], [ys["down"]], stream=stream)
+        pairs[li].gate_up_act(x, ys["gate"], 2, stream=stream)
+        hip.matvec_group(ts[4:5], ys["gate"], [ys["down"]], stream=stream)
         hip.residual_norm(res, ys["down"], an_w, 1e-5, x, bad=bad, stream=stream)
 
     hip.rms_norm(res, x, an_w, 1e-5, stream=torch.cuda.current_stream())   # the first layer's input
@@ -516,6 +520,8 @@ def bench_decode_layer(torch, hip, steps, warmup, position=1023):
     for ts in layers:
         for t in ts:
             t.free()
+    for pr in pairs:
+        pr.free()
     kv_bytes = 2 * nh * max_seq * (hd + 4)
     total = algo_bytes(mats) + kv_bytes
     return {"value": total / (ms * 1e-3) / 1e9, "ms_per_step": ms, "bytes_per_step": total,
@@ -746,7 +752,7 @@ def run_config(torch, hip, key: str, args, cpu_budget: float, cache: dict) -> di
                          "int8 KV cache)",
                     config={"workload": f"device-resident 7B decoder layer step (3-bit block 128), "
                                         f"attention over {r['position'] + 1} cached positions, "
-                                        f"10 launches (residual + norm and RoPE + KV store fused)",
+                                        f"9 launches (residual + norm, RoPE + KV store and gate/up + act*mul fused)",
                             "us_per_layer": round(r["ms_per_step"] * 1e3, 3),
                             "bytes_per_step": r["bytes_per_step"], "weight_bytes": r["weight_bytes"],
                             "kv_bytes": r["kv_bytes"],

@@ -105,6 +105,14 @@ typedef struct qsf_hip_tensor qsf_hip_tensor;   /* opaque */
  * run from HBM.  Returns NULL on error. */
 qsf_hip_tensor* qsf_hip_tensor_upload(const void* host_payload, int quant_type,
                                       int rows, int cols, int block_size);
+/* Gate and up weights of one FFN (two payloads of the same plain block
+ * format and shape, no outlier table) uploaded as one interleaved tensor of
+ * 2 * rows rows for qsf_hip_gate_up_act_dev.  Not registered for any host
+ * pointer.  No counterpart in the reference: the engine's two matvecs and
+ * activation product (src/engine.c:1118-1140) in one launch, for a
+ * device-resident engine.  Returns NULL on error. */
+qsf_hip_tensor* qsf_hip_tensor_upload_pair(const void* gate_payload, const void* up_payload,
+                                           int quant_type, int rows, int cols, int block_size);
 /* Tensor registered for this host pointer, or NULL. */
 qsf_hip_tensor* qsf_hip_tensor_lookup(const void* host_payload);
 void            qsf_hip_tensor_free(qsf_hip_tensor* t);
@@ -298,6 +306,12 @@ int qsf_hip_attention_dev(const float* d_q, const int8_t* d_kc, const int8_t* d_
 /* gate = act(gate) * up, src/engine.c:1128-1140 (QSFActivation: 2 SiLU,
  * 0/1 GELU, else ReLU) */
 int qsf_hip_act_mul_dev(float* d_gate, const float* d_up, int n, int activation, void* stream);
+/* d_out[i] = act(gate_i . x) * (up_i . x) over a tensor from
+ * qsf_hip_tensor_upload_pair, in one GEMV launch: the results equal the
+ * gate/up GEMV followed by qsf_hip_act_mul_dev bit for bit.  Replaces
+ * src/engine.c:1118-1140 for a device-resident engine. */
+int qsf_hip_gate_up_act_dev(const qsf_hip_tensor* pair, const float* d_x, float* d_out, int activation,
+                            void* stream);
 /* res += x, src/engine.c:937 and 1174; with d_bad, the NaN/Inf check of
  * src/engine.c:1176-1187: *d_bad = first index holding NaN or |v| > 1e30,
  * or -1 (written on every call; nothing to clear beforehand). */

@@ -305,16 +305,7 @@ __global__ __launch_bounds__(256) void act_mul_kernel(float* gate, const float* 
                                                       int n, int act) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
-    float x = gate[i];
-    if (act == 2) {
-        x = __fdiv_rn(x, __fadd_rn(1.0f, expf(-x)));
-    } else if (act == 0 || act == 1) {
-        const float inner = __fmul_rn(0.7978845608f, __fadd_rn(x, __fmul_rn(__fmul_rn(__fmul_rn(0.044715f, x), x), x)));
-        x = __fmul_rn(__fmul_rn(0.5f, x), __fadd_rn(1.0f, tanhf(inner)));
-    } else if (x < 0.0f) {
-        x = 0.0f;
-    }
-    gate[i] = __fmul_rn(x, up[i]);
+    gate[i] = qsf::act_mul(act, gate[i], up[i]);
 }
 
 // res += x, then the first index whose value is NaN or beyond +-1e30 (or

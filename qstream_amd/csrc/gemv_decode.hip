@@ -441,6 +441,9 @@ struct GemvArgs {
     const uint32_t* xq;            // prepared digits (stride DWS), or null: prepare here
     const float2* xmeta;
     const float* x;
+    // paired rows (row 2i gate_i, row 2i+1 up_i; two-row tiles, one matrix):
+    // 1 + the activation, and y[i] = act(gate_i x) * (up_i x); 0: plain rows
+    int act1;
 };
 
 
@@ -1029,7 +1032,19 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
         }
     }
 
-    // 9. stores
+    // 9. stores (paired rows: the gate/up activation product,
+    //    src/engine.c:1128-1140, as the act-mul kernel computes it)
+    if constexpr (R == 2) {
+        if (a.act1) {
+#pragma unroll
+            for (int j = 0; j < MT; j++) {
+                const int row0 = row_of(j);
+                if (j < nt && lig == lpg - 1 && row0 < rows)
+                    Y[row0 >> 1] = qsf::act_mul(a.act1 - 1, stash[j * rpt + grp * R], stash[j * rpt + grp * R + 1]);
+            }
+            return;
+        }
+    }
 #pragma unroll
     for (int j = 0; j < MT; j++) {
         if (j < nt) {
@@ -1356,6 +1371,10 @@ int plan_rt(const qsf_hip_tensor* const* t, int n, int cols, int mode, float* co
     return 0;
 }
 
+// Paired-rows request of the calling thread for the launch being planned
+// (qk_gemv_pair_act sets it around its one call): 1 + activation, or 0.
+thread_local int tl_pair_act1 = 0;
+
 template <int FMT, int BS, int R, bool DREG = false, bool SPLIT = false>
 int launch_rt(const qsf_hip_tensor* const* t, int n, int cols, const float* d_x,
               float* const* d_y, void* d_ws, int mode, hipStream_t s) {
@@ -1376,6 +1395,10 @@ int launch_rt(const qsf_hip_tensor* const* t, int n, int cols, const float* d_x,
     Plan p;
     const int rc = plan_rt<FMT, BS, R, DREG, SPLIT>(t, n, cols, mode, d_y, a, p);
     if (rc) return rc < 0 ? rc : 0;
+    // paired rows: the whole-row kernel with two-row tiles only (a tile's
+    // two rows, a gate row and its up row, end in the same lane's stash)
+    a.act1 = tl_pair_act1;
+    if (a.act1 && (R != 2 || DREG || p.kid == 0 || n != 1 || t[0]->d_row_ptr)) return -2;
     const bool prepared = !(mode & QK_RUN_XPREP) || (mode & QK_RUN_STANDALONE_PREP);
     a.xq = prepared ? xq : nullptr;
     a.xmeta = xmeta;
@@ -1458,6 +1481,12 @@ template <int FMT, int BS, bool SPLIT = false>
 int launch_t(const qsf_hip_tensor* const* t, int n, int cols, const float* d_x,
              float* const* d_y, void* d_ws, int mode, hipStream_t s) {
     constexpr bool kDreg = FMT != QK_FMT_3 && Fmt<FMT, BS>::CW * Fmt<FMT, BS>::NC * ND <= 48;
+    if (tl_pair_act1) {
+        // paired rows take two-row tiles whatever the row count
+        if constexpr (tile_rows<FMT, BS>() == 2)
+            return launch_rt<FMT, BS, 2, false, SPLIT>(t, n, cols, d_x, d_y, d_ws, mode, s);
+        return -2;
+    }
     const int k = pick_tiles<FMT, BS>(t, n, cols);
     if constexpr (kDreg)
         if (k == 0) return launch_rt<FMT, BS, 1, true, SPLIT>(t, n, cols, d_x, d_y, d_ws, mode, s);
@@ -1642,6 +1671,16 @@ extern "C" int qk_gemv_group(const qsf_hip_tensor* const* t, int n, const float*
         }
     }
     return launch_fmt(fmt, bs, t, n, cols, d_x, d_y, d_ws, mode, s);
+}
+
+extern "C" int qk_gemv_pair_act(const qsf_hip_tensor* t, const float* d_x, float* d_y, int act,
+                                hipStream_t s) {
+    if (!t || t->rows % 2 || t->cols <= 0 || t->fmt < 0 || act < 0) return -2;
+    tl_pair_act1 = act + 1;
+    float* const y[1] = {d_y};
+    const int rc = qk_gemv_group(&t, 1, d_x, y, nullptr, QK_RUN_BOTH, s);
+    tl_pair_act1 = 0;
+    return rc;
 }
 
 extern "C" uint64_t qk_gemv_signature(const qsf_hip_tensor* const* t, int n, int mode) {

@@ -33,6 +33,23 @@ __device__ __forceinline__ int sdot8_z(uint32_t a, uint32_t b) {
     return r;
 }
 
+// act(g) * u with QSFActivation act: 2 SiLU, 0/1 GELU (tanh form), else
+// ReLU (src/kernels_scalar.c:129-147, src/engine.c:1128-1140).  Every
+// operation is rounded on its own (no contraction into FMAs), so the
+// act-mul kernel and the gate/up GEMV's fused epilogue give the same bits.
+__device__ __forceinline__ float act_mul(int act, float g, float u) {
+    float x = g;
+    if (act == 2) {
+        x = __fdiv_rn(x, __fadd_rn(1.0f, expf(-x)));
+    } else if (act == 0 || act == 1) {
+        const float inner = __fmul_rn(0.7978845608f, __fadd_rn(x, __fmul_rn(__fmul_rn(__fmul_rn(0.044715f, x), x), x)));
+        x = __fmul_rn(__fmul_rn(0.5f, x), __fadd_rn(1.0f, tanhf(inner)));
+    } else if (x < 0.0f) {
+        x = 0.0f;
+    }
+    return __fmul_rn(x, u);
+}
+
 // Butterfly sum over groups of `width` consecutive lanes (power of two).
 __device__ __forceinline__ float group_sum(float v, int width) {
     for (int off = width >> 1; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);

@@ -70,6 +70,10 @@ int qk_xprep(int fmt, int bs, int cols, const float* d_x, void* d_ws, hipStream_
 enum { QK_RUN_XPREP = 1, QK_RUN_GEMV = 2, QK_RUN_BOTH = 3, QK_RUN_STANDALONE_PREP = 4 };
 int qk_gemv_group(const qsf_hip_tensor* const* t, int n, const float* d_x,
                   float* const* d_y, void* d_ws, int mode, hipStream_t s);
+/* One-launch GEMV over a paired tensor (row 2i gate_i, row 2i+1 up_i, no
+ * outliers): y[i] = act(gate_i x) * (up_i x), act a QSFActivation >= 0.
+ * -2 when the plan cannot take two-row tiles. */
+int qk_gemv_pair_act(const qsf_hip_tensor* t, const float* d_x, float* d_y, int act, hipStream_t s);
 /* What fixes a row's arithmetic in qk_gemv_group(t, n, ..., mode): the
  * kernel instantiation, row-group width, tile rows and chunk.  A tensor's
  * rows come out bit-identical in two launches whose signatures are equal

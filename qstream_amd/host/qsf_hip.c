@@ -471,6 +471,36 @@ qsf_hip_tensor* qsf_hip_tensor_upload(const void* host, int qt, int rows, int co
     return t;
 }
 
+/* Gate and up weights of one FFN as one tensor of 2 * rows rows, block rows
+ * interleaved (row 2i = gate row i, row 2i+1 = up row i), so that one
+ * two-row GEMV tile holds both rows of an output.  Not registered: no host
+ * pointer stands for it.  Plain block formats only (no outlier table). */
+qsf_hip_tensor* qsf_hip_tensor_upload_pair(const void* gate, const void* up, int qt, int rows,
+                                           int cols, int bs) {
+    if (!gate || !up || rows <= 0 || cols <= 0 || kernel_fmt(qt) < 0 || is_outlier(qt) ||
+        !(bs == 32 || bs == 64 || bs == 128 || bs == 256)) {
+        fail(E_INVALID, "qsf_hip_tensor_upload_pair: bad arguments (type %d, %dx%d, block %d)", qt,
+             rows, cols, bs);
+        return NULL;
+    }
+    const size_t row_bytes = (size_t)((cols + bs - 1) / bs) * (4 + (bs * fmt_bits(kernel_fmt(qt)) + 7) / 8);
+    uint8_t* both = malloc(2 * (size_t)rows * row_bytes);
+    if (!both) {
+        fail(E_OOM, "qsf_hip_tensor_upload_pair: host staging");
+        return NULL;
+    }
+    for (int r = 0; r < rows; r++) {
+        memcpy(both + (2 * (size_t)r) * row_bytes, (const uint8_t*)gate + (size_t)r * row_bytes, row_bytes);
+        memcpy(both + (2 * (size_t)r + 1) * row_bytes, (const uint8_t*)up + (size_t)r * row_bytes, row_bytes);
+    }
+    pthread_mutex_lock(&g_lock);
+    qsf_hip_tensor* t = upload_locked(both, qt, 2 * rows, cols, bs);
+    if (t) t->host_key = NULL;
+    pthread_mutex_unlock(&g_lock);
+    free(both);
+    return t;
+}
+
 qsf_hip_tensor* qsf_host_upload_owned(const void* host, int qt, int rows, int cols, int bs) {
     pthread_mutex_lock(&g_lock);
     qsf_hip_tensor* t = upload_locked(host, qt, rows, cols, bs);
@@ -857,6 +887,15 @@ int qsf_hip_act_mul_dev(float* d_gate, const float* d_up, int n, int activation,
     if (n < 0 || (n > 0 && (!d_gate || !d_up)))
         return fail(E_INVALID, "qsf_hip_act_mul_dev: bad arguments");
     return glue_rc("qsf_hip_act_mul_dev", qk_act_mul(d_gate, d_up, n, activation, pick_stream(stream)));
+}
+
+int qsf_hip_gate_up_act_dev(const qsf_hip_tensor* pair, const float* d_x, float* d_out, int activation,
+                            void* stream) {
+    if (!pair || !d_x || !d_out || pair->rows % 2 || activation < 0)
+        return fail(E_INVALID, "qsf_hip_gate_up_act_dev: bad arguments");
+    const int rc = qk_gemv_pair_act(pair, d_x, d_out, activation, pick_stream(stream));
+    if (rc == -2) return fail(E_INVALID, "qsf_hip_gate_up_act_dev: no two-row plan for this tensor");
+    return rc ? fail(E_INTERNAL, "qsf_hip_gate_up_act_dev: launch failed") : E_OK;
 }
 
 int qsf_hip_residual_dev(float* d_res, const float* d_x, int n, int* d_bad, void* stream) {

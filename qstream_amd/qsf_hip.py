@@ -28,7 +28,7 @@ EXPORTS = (
     "qsf_matvec_2bit_hip", "qsf_matvec_3bit_hip", "qsf_matvec_4bit_hip",
     "qsf_matvec_4bit_sym_hip", "qsf_matvec_outlier_2bit_hip", "qsf_matvec_outlier_4bit_hip",
     "qsf_matvec_mxfp4_hip", "qsf_kernels_init_hip", "qsf_hip_slot_lookahead",
-    "qsf_hip_tensor_upload", "qsf_hip_tensor_lookup", "qsf_hip_tensor_free",
+    "qsf_hip_tensor_upload", "qsf_hip_tensor_upload_pair", "qsf_hip_tensor_lookup", "qsf_hip_tensor_free",
     "qsf_hip_arena_forget", "qsf_hip_arena_forget_range", "qsf_hip_arena_bytes", "qsf_hip_tensor_payload_bytes",
     "qsf_hip_matvec_dev", "qsf_hip_matvec_group_dev", "qsf_hip_xprep_bytes",
     "qsf_hip_xprep_dev", "qsf_hip_matvec_group_prepared_dev",
@@ -37,7 +37,7 @@ EXPORTS = (
     "qsf_hip_prefill_4bit_dev", "qsf_hip_prefill_4bit_dev_noalloc",
     "qsf_hip_rms_norm_dev", "qsf_hip_layer_norm_dev", "qsf_hip_rope_create", "qsf_hip_rope_free",
     "qsf_hip_rope_dev", "qsf_hip_kv_store_dev", "qsf_hip_attention_dev", "qsf_hip_act_mul_dev",
-    "qsf_hip_residual_dev", "qsf_hip_embed_row_dev", "qsf_hip_embed_row_fp16_dev",
+    "qsf_hip_gate_up_act_dev", "qsf_hip_residual_dev", "qsf_hip_embed_row_dev", "qsf_hip_embed_row_fp16_dev",
     "qsf_hip_residual_norm_dev", "qsf_hip_rope_kv_store_dev",
     "qsf_hip_crc32", "qsf_hip_model_load", "qsf_hip_model_free", "qsf_hip_model_get_info",
     "qsf_hip_model_tensor", "qsf_hip_model_vector", "qsf_hip_model_embedding",
@@ -118,6 +118,9 @@ def load(path: str = LIB_PATH) -> C.CDLL:
     L.qsf_hip_kv_store_dev.argtypes = [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _vp, _vp]
     L.qsf_hip_attention_dev.argtypes = [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp, _vp]
     L.qsf_hip_act_mul_dev.argtypes = [_vp, _vp, _i, _i, _vp]
+    L.qsf_hip_gate_up_act_dev.argtypes = [_vp, _vp, _vp, _i, _vp]
+    L.qsf_hip_tensor_upload_pair.argtypes = [_vp, _vp, _i, _i, _i, _i]
+    L.qsf_hip_tensor_upload_pair.restype = _vp
     L.qsf_hip_residual_dev.argtypes = [_vp, _vp, _i, _vp, _vp]
     L.qsf_hip_embed_row_dev.argtypes = [_vp, _i, _vp, _vp]
     L.qsf_hip_embed_row_fp16_dev.argtypes = [_vp, _i, _i, _vp, _vp]
@@ -125,7 +128,7 @@ def load(path: str = LIB_PATH) -> C.CDLL:
     L.qsf_hip_rope_kv_store_dev.argtypes = [_vp, _vp, _vp, _vp, _i, _i, _i, _vp, _vp, _vp, _vp, _i, _vp]
     for n in ("qsf_hip_rms_norm_dev", "qsf_hip_layer_norm_dev", "qsf_hip_rope_dev",
               "qsf_hip_kv_store_dev", "qsf_hip_attention_dev", "qsf_hip_act_mul_dev",
-              "qsf_hip_residual_dev", "qsf_hip_embed_row_dev", "qsf_hip_embed_row_fp16_dev",
+              "qsf_hip_gate_up_act_dev", "qsf_hip_residual_dev", "qsf_hip_embed_row_dev", "qsf_hip_embed_row_fp16_dev",
               "qsf_hip_residual_norm_dev", "qsf_hip_rope_kv_store_dev"):
         getattr(L, n).restype = _i
     L.qsf_hip_crc32.argtypes = [_vp, C.c_size_t]
@@ -278,6 +281,27 @@ class Tensor:
         if self.handle:
             load().qsf_hip_tensor_free(self.handle)
             self.handle = None
+
+
+class TensorPair(Tensor):
+    """Gate and up payloads of one FFN as one interleaved HBM tensor
+    (2 * rows rows) for gate_up_act."""
+
+    def __init__(self, gate, up, qt: int, rows: int, cols: int, bs: int):
+        as_u8 = lambda p: np.frombuffer(p, np.uint8) if isinstance(p, (bytes, bytearray)) \
+            else np.ascontiguousarray(p)
+        g, u = as_u8(gate), as_u8(up)
+        self.qt, self.rows, self.cols, self.bs = qt, rows, cols, bs
+        L = load()
+        self.handle = L.qsf_hip_tensor_upload_pair(g.ctypes.data, u.ctypes.data, qt, rows, cols, bs)
+        if not self.handle:
+            _check(-1, "qsf_hip_tensor_upload_pair")
+        self.payload_bytes = L.qsf_hip_tensor_payload_bytes(self.handle)
+
+    def gate_up_act(self, x, out, activation, stream=None) -> None:
+        """out[i] = act(gate_i . x) * (up_i . x) in one launch."""
+        _check(load().qsf_hip_gate_up_act_dev(self.handle, _addr(x), _addr(out), activation,
+                                              _stream(stream)), "qsf_hip_gate_up_act_dev")
 
 
 def matvec_group(tensors, x, ys, stream=None) -> None:
