@@ -128,66 +128,32 @@ struct PrefillArgs {
 //    {0, 2, 4, 6, 1, 3, 5, 7} of the codes (codes8).
 // Zeros past m, k and nb.  The GEMM then loads each fragment as one
 // contiguous 1 KB read instead of 64 scattered 16-byte pieces.  One
-// workgroup per (row group, 8 k-steps): the code part reads a 16 x 256 tile
-// row-contiguously into LDS and writes it back in fragment order.
+// workgroup per (row group, 8 code k-steps) reads its 16 x 256 tile of x
+// row-contiguously into LDS and writes it back in fragment order; the same
+// workgroup sums the tile's blocks (256 / bs of each row) from LDS for the
+// zero-point part.  Workgroup 0 of a row group also writes the zero chunks
+// of the blocks past nb.  (Summing the blocks in workgroups of their own,
+// which read x again from memory with 16-byte pieces scattered over rows,
+// cost 3 us of config 4's 74 us step.)
 constexpr int XP_PITCH = 256 + 8;      // LDS row pitch of the pack tile, bf16
+
+// The zero-point chunk {X1, X2, X3, X1, X2, 0, 0, 0} of a block sum X
+// (X = X1 + X2 + X3 exactly, each part bf16).
+__device__ __forceinline__ u32x4 xchunk(float X) {
+    const bf16x2 p1 = to_bf16x2(X, 0.f);
+    const float r1 = X - bf16_f32(p1[0]);
+    const bf16x2 p2 = to_bf16x2(r1, 0.f);
+    const bf16x2 p3 = to_bf16x2(r1 - bf16_f32(p2[0]), 0.f);
+    const __bf16 zero = p1[1];
+    return __builtin_bit_cast(u32x4, bf16x8{p1[0], p2[0], p3[0], p1[0], p2[0], zero, zero, zero});
+}
+
 __global__ __launch_bounds__(256) void xpack_kernel(const uint16_t* __restrict__ x, u32x4* xp,
                                                    int m, int k, int ksp_total, int kz,
                                                    int bs, int nb) {
     __shared__ __align__(16) uint16_t tile[16 * XP_PITCH];
     const int g = blockIdx.y, t = threadIdx.x;
-    if ((int)blockIdx.x < kz / 8) {
-        // 32 blocks of each of the 16 rows; a lane sums one block in order,
-        // for two rows.  Each 64-value piece of both rows' blocks is
-        // requested before any of it is summed (one memory round trip a
-        // piece instead of one a 16-byte load).
-        const int b = (int)blockIdx.x * 32 + (t & 31);
-        float Xs[2] = {0.f, 0.f};
-        const uint16_t* xr[2];
-        int cnt[2];
-#pragma unroll
-        for (int h = 0; h < 2; h++) {
-            const int row = g * 16 + (t >> 5) + 8 * h;
-            const bool live = row < m && b < nb;
-            xr[h] = x + (size_t)(live ? row : 0) * k + (size_t)(live ? b : 0) * bs;
-            cnt[h] = live ? min(bs, k - b * bs) : 0;   // a multiple of 8
-        }
-        for (int e0 = 0; e0 < max(cnt[0], cnt[1]); e0 += 64) {
-            u32x4 v[2][8];
-#pragma unroll
-            for (int h = 0; h < 2; h++)
-#pragma unroll
-                for (int q = 0; q < 8; q++)
-                    v[h][q] = e0 + 8 * q < cnt[h] ? *reinterpret_cast<const u32x4*>(xr[h] + e0 + 8 * q)
-                                                  : u32x4{0u, 0u, 0u, 0u};
-#pragma unroll
-            for (int h = 0; h < 2; h++)
-#pragma unroll
-                for (int q = 0; q < 8; q++) {
-                    if (e0 + 8 * q >= cnt[h]) continue;
-#pragma unroll
-                    for (int j = 0; j < 4; j++) {
-                        Xs[h] += __builtin_bit_cast(float, v[h][q][j] << 16);
-                        Xs[h] += __builtin_bit_cast(float, v[h][q][j] & 0xFFFF0000u);
-                    }
-                }
-        }
-#pragma unroll
-        for (int h = 0; h < 2; h++) {
-            const int r = (t >> 5) + 8 * h;
-            const float X = Xs[h];
-            const bf16x2 p1 = to_bf16x2(X, 0.f);
-            const float r1 = X - bf16_f32(p1[0]);
-            const bf16x2 p2 = to_bf16x2(r1, 0.f);
-            const bf16x2 p3 = to_bf16x2(r1 - bf16_f32(p2[0]), 0.f);
-            const __bf16 zero = p1[1];
-            const bf16x8 c = {p1[0], p2[0], p3[0], p1[0], p2[0], zero, zero, zero};
-            xp[((size_t)g * ksp_total + (b >> 2)) * 64 + r + 16 * (b & 3)] =
-                __builtin_bit_cast(u32x4, c);
-        }
-        return;
-    }
-    const int kk0 = ((int)blockIdx.x - kz / 8) * 8;
+    const int kk0 = (int)blockIdx.x * 8;
     const int c = t & 31;                      // 16-byte chunk of a 256-wide row piece
 #pragma unroll
     for (int h = 0; h < 2; h++) {
@@ -203,6 +169,36 @@ __global__ __launch_bounds__(256) void xpack_kernel(const uint16_t* __restrict__
         xp[((size_t)g * ksp_total + kz + kk0 + kk) * 64 + l] =
             *reinterpret_cast<const u32x4*>(&tile[(l & 15) * XP_PITCH + kk * 32 + 8 * (l >> 4)]);
     }
+    // Zero-point part: thread (row r, tile block jb) sums its block's
+    // elements in index order from the tile (a chunk's slots hold elements
+    // {0, 2, 4, 6, 1, 3, 5, 7}: dword 0 = x0 | x2, 1 = x4 | x6, 2 = x1 | x3,
+    // 3 = x5 | x7).  Rows past m and blocks past nb get zero chunks, and
+    // workgroup 0 writes those of the blocks past nb that no tile holds.
+    const int nbt = 256 / bs;                  // blocks of the tile a row
+    if (t < 16 * nbt) {
+        const int r = t & 15, jb = t >> 4;
+        const int b = kk0 * 32 / bs + jb, row = g * 16 + r;
+        const int cnt = row < m && b < nb ? min(bs, k - b * bs) : 0;   // a multiple of 8
+        const uint16_t* src = &tile[r * XP_PITCH + jb * bs];
+        float X = 0.f;
+        for (int e = 0; e < cnt; e += 8) {
+            const u32x4 q = *reinterpret_cast<const u32x4*>(src + e);
+            X += __builtin_bit_cast(float, q[0] << 16);           // x0
+            X += __builtin_bit_cast(float, q[2] << 16);           // x1
+            X += __builtin_bit_cast(float, q[0] & 0xFFFF0000u);   // x2
+            X += __builtin_bit_cast(float, q[2] & 0xFFFF0000u);   // x3
+            X += __builtin_bit_cast(float, q[1] << 16);           // x4
+            X += __builtin_bit_cast(float, q[3] << 16);           // x5
+            X += __builtin_bit_cast(float, q[1] & 0xFFFF0000u);   // x6
+            X += __builtin_bit_cast(float, q[3] & 0xFFFF0000u);   // x7
+        }
+        if (b < 4 * kz) xp[((size_t)g * ksp_total + (b >> 2)) * 64 + r + 16 * (b & 3)] = xchunk(X);
+    }
+    if (blockIdx.x == 0)
+        for (int i = t; i < 16 * (4 * kz - nb); i += 256) {
+            const int b = nb + (i >> 4), r = i & 15;
+            xp[((size_t)g * ksp_total + (b >> 2)) * 64 + r + 16 * (b & 3)] = u32x4{0u, 0u, 0u, 0u};
+        }
 }
 
 // Raw buffer descriptor (gfx9 family word 3): loads at offsets >= `bytes`
@@ -535,7 +531,7 @@ extern "C" int qk_prefill_4bit(const qsf_hip_tensor* t, const uint16_t* d_x_bf16
         return -2;
     const int tiles_n = (t->rows + BN - 1) / BN;
     const bool ragged = t->cols % (2 * SK) != 0;
-    hipLaunchKernelGGL(xpack_kernel, dim3(ksp_total / 8, (m + 15) / 16), dim3(256), 0, s,
+    hipLaunchKernelGGL(xpack_kernel, dim3((ksp_total - kz) / 8, (m + 15) / 16), dim3(256), 0, s,
                        d_x_bf16, static_cast<u32x4*>(d_ws), m, t->cols, ksp_total, kz, t->bs, t->nb);
     PrefillArgs a = {t->d_blocks, static_cast<const u32x4*>(d_ws), d_y, m, t->rows, t->cols, t->nb,
                      tiles_n, st.sz, st.sz + st.sc, (uint32_t)((uint64_t)t->rows * row_bytes),
