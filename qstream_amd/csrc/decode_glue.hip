@@ -46,8 +46,8 @@ __global__ __launch_bounds__(NORM_THREADS) void norm_kernel(const float* __restr
         float ss = 0.f;
         for (int i = threadIdx.x; i < dim; i += blockDim.x) ss = fmaf(in[i], in[i], ss);
         ss = block_sum(ss, red);
-        const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)dim), eps)));
-        for (int i = threadIdx.x; i < dim; i += blockDim.x) out[i] = __fmul_rn(__fmul_rn(in[i], inv), w[i]);
+        const float inv = __fdiv_rn(1.0f, __fsqrt_rn(qsf::add_rn(__fdiv_rn(ss, (float)dim), eps)));
+        for (int i = threadIdx.x; i < dim; i += blockDim.x) out[i] = qsf::mul_rn(qsf::mul_rn(in[i], inv), w[i]);
     } else {
         float s = 0.f;
         for (int i = threadIdx.x; i < dim; i += blockDim.x) s += in[i];
@@ -58,10 +58,10 @@ __global__ __launch_bounds__(NORM_THREADS) void norm_kernel(const float* __restr
             v = fmaf(d, d, v);
         }
         const float var = __fdiv_rn(block_sum(v, red), (float)dim);
-        const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(var, eps)));
+        const float inv = __fdiv_rn(1.0f, __fsqrt_rn(qsf::add_rn(var, eps)));
         for (int i = threadIdx.x; i < dim; i += blockDim.x) {
-            float o = __fmul_rn(__fmul_rn(__fsub_rn(in[i], mean), inv), w[i]);
-            if (b) o = __fadd_rn(o, b[i]);
+            float o = qsf::mul_rn(qsf::mul_rn(qsf::sub_rn(in[i], mean), inv), w[i]);
+            if (b) o = qsf::add_rn(o, b[i]);
             out[i] = o;
         }
     }
@@ -82,8 +82,8 @@ __global__ __launch_bounds__(256) void rope_kernel(float* q, float* k, const flo
     ang = fmod(ang, 2.0 * 3.14159265358979323846);
     const float c = cosf((float)ang), s = sinf((float)ang);
     const float a0 = v[0], a1 = v[1];
-    v[0] = __fsub_rn(__fmul_rn(a0, c), __fmul_rn(a1, s));
-    v[1] = __fadd_rn(__fmul_rn(a0, s), __fmul_rn(a1, c));
+    v[0] = qsf::sub_rn(qsf::mul_rn(a0, c), qsf::mul_rn(a1, s));
+    v[1] = qsf::add_rn(qsf::mul_rn(a0, s), qsf::mul_rn(a1, c));
 }
 
 // int8 KV store: one wave per (kv head, K or V).  absmax, scale =
@@ -110,10 +110,10 @@ __global__ __launch_bounds__(64) void kv_store_kernel(int8_t* kc, int8_t* vc, fl
     if (amax > 1e-30f) {
         const float inv = __fdiv_rn(127.0f, amax);
         for (int i = lane; i < head_dim; i += 64) {
-            float x = __fmul_rn(src[i], inv);
+            float x = qsf::mul_rn(src[i], inv);
             if (x > 127.0f) x = 127.0f;
             if (x < -127.0f) x = -127.0f;
-            dst[i] = (int8_t)(int)__fadd_rn(x, x >= 0 ? 0.5f : -0.5f);
+            dst[i] = (int8_t)(int)qsf::add_rn(x, x >= 0 ? 0.5f : -0.5f);
         }
     } else {
         for (int i = lane; i < head_dim; i += 64) dst[i] = 0;
@@ -161,9 +161,9 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_part_kernel(
             const att_u32x4 w = kr[c];
 #pragma unroll
             for (int j = 0; j < 16; j++)
-                dot = fmaf(qs[16 * c + j], __fmul_rn(sbyte(w[j >> 2], j & 3), kscale), dot);
+                dot = fmaf(qs[16 * c + j], qsf::mul_rn(sbyte(w[j >> 2], j & 3), kscale), dot);
         }
-        sc = __fmul_rn(dot, inv_sqrt_d);
+        sc = qsf::mul_rn(dot, inv_sqrt_d);
     }
     float m = sc;
     for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
@@ -171,7 +171,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_part_kernel(
     __syncthreads();
     m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     const float e = t < np ? expf(sc - m) : 0.f;
-    if (t < np) ew[t] = __fmul_rn(e, vs[(size_t)kvh * max_seq + p0 + t]);
+    if (t < np) ew[t] = qsf::mul_rn(e, vs[(size_t)kvh * max_seq + p0 + t]);
     const float l = block_sum(e, red);                   // also orders the ew writes
     // weighted V: thread (d, part) over positions part, part + P, ...
     const int P = ATT_THREADS / head_dim, d = t % head_dim, part = t / head_dim;
@@ -241,17 +241,17 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_part_fast_kernel(
     for (int j = 0; j < KH; j++)
 #pragma unroll
         for (int b = 0; b < 16; b++)
-            dot = fmaf(qs[16 * (kh * KH + j) + b], __fmul_rn(sbyte(kv[j][b >> 2], b & 3), kscale), dot);
+            dot = fmaf(qs[16 * (kh * KH + j) + b], qsf::mul_rn(sbyte(kv[j][b >> 2], b & 3), kscale), dot);
     dot += __shfl_xor(dot, 1, 64);
     const bool mine = kh == 0 && kp < np;
-    const float sc = kp < np ? __fmul_rn(dot, inv_sqrt_d) : -INFINITY;
+    const float sc = kp < np ? qsf::mul_rn(dot, inv_sqrt_d) : -INFINITY;
     float m = sc;
     for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
     if ((t & 63) == 0) red[t >> 6] = m;
     __syncthreads();
     m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     const float e = mine ? expf(sc - m) : 0.f;
-    if (mine) ew[kp] = __fmul_rn(e, vscale);
+    if (mine) ew[kp] = qsf::mul_rn(e, vscale);
     const float l = block_sum(e, red);                   // also orders the ew writes
     // 3. weighted V: dims 16 (t % HC) .. +15 of the thread's pieces
     float acc[16];
@@ -316,7 +316,7 @@ __global__ __launch_bounds__(1024) void residual_kernel(float* res, const float*
     __shared__ int red[1024 / 64];
     int first = n;
     for (int i = threadIdx.x; i < n; i += blockDim.x) {
-        const float r = __fadd_rn(res[i], x[i]);
+        const float r = qsf::add_rn(res[i], x[i]);
         res[i] = r;
         if ((r != r || r > 1e30f || r < -1e30f) && i < first) first = i;
     }
@@ -345,7 +345,7 @@ __global__ __launch_bounds__(NORM_THREADS) void residual_norm_kernel(
     int first = n;
     float acc = 0.f;
     for (int i = threadIdx.x; i < n; i += blockDim.x) {
-        const float r = __fadd_rn(res[i], x[i]);
+        const float r = qsf::add_rn(res[i], x[i]);
         res[i] = r;
         if ((r != r || r > 1e30f || r < -1e30f) && i < first) first = i;
         acc = LAYER ? acc + r : fmaf(r, r, acc);
@@ -362,8 +362,8 @@ __global__ __launch_bounds__(NORM_THREADS) void residual_norm_kernel(
     }
     if (!LAYER) {
         const float ss = block_sum(acc, red);
-        const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)n), eps)));
-        for (int i = threadIdx.x; i < n; i += blockDim.x) out[i] = __fmul_rn(__fmul_rn(res[i], inv), w[i]);
+        const float inv = __fdiv_rn(1.0f, __fsqrt_rn(qsf::add_rn(__fdiv_rn(ss, (float)n), eps)));
+        for (int i = threadIdx.x; i < n; i += blockDim.x) out[i] = qsf::mul_rn(qsf::mul_rn(res[i], inv), w[i]);
     } else {
         const float mean = __fdiv_rn(block_sum(acc, red), (float)n);
         float v = 0.f;
@@ -372,10 +372,10 @@ __global__ __launch_bounds__(NORM_THREADS) void residual_norm_kernel(
             v = fmaf(d, d, v);
         }
         const float var = __fdiv_rn(block_sum(v, red), (float)n);
-        const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(var, eps)));
+        const float inv = __fdiv_rn(1.0f, __fsqrt_rn(qsf::add_rn(var, eps)));
         for (int i = threadIdx.x; i < n; i += blockDim.x) {
-            float o = __fmul_rn(__fmul_rn(__fsub_rn(res[i], mean), inv), w[i]);
-            if (b) o = __fadd_rn(o, b[i]);
+            float o = qsf::mul_rn(qsf::mul_rn(qsf::sub_rn(res[i], mean), inv), w[i]);
+            if (b) o = qsf::add_rn(o, b[i]);
             out[i] = o;
         }
     }
@@ -393,15 +393,15 @@ __device__ __forceinline__ void rope_pair(float& a0, float& a1, const float* __r
     ang = fmod(ang, 2.0 * 3.14159265358979323846);
     const float c = cosf((float)ang), sn = sinf((float)ang);
     const float x0 = a0, x1 = a1;
-    a0 = __fsub_rn(__fmul_rn(x0, c), __fmul_rn(x1, sn));
-    a1 = __fadd_rn(__fmul_rn(x0, sn), __fmul_rn(x1, c));
+    a0 = qsf::sub_rn(qsf::mul_rn(x0, c), qsf::mul_rn(x1, sn));
+    a1 = qsf::add_rn(qsf::mul_rn(x0, sn), qsf::mul_rn(x1, c));
 }
 
 __device__ __forceinline__ int8_t kv_code(float x, float inv) {
-    x = __fmul_rn(x, inv);
+    x = qsf::mul_rn(x, inv);
     if (x > 127.0f) x = 127.0f;
     if (x < -127.0f) x = -127.0f;
-    return (int8_t)(int)__fadd_rn(x, x >= 0 ? 0.5f : -0.5f);
+    return (int8_t)(int)qsf::add_rn(x, x >= 0 ? 0.5f : -0.5f);
 }
 
 __global__ __launch_bounds__(64) void rope_kv_kernel(float* q, float* k, const float* __restrict__ v,
@@ -481,9 +481,9 @@ __global__ __launch_bounds__(256) void embed_row_kernel(const uint8_t* __restric
     const unsigned c = code_of(fmt, blk + 4, i % bs);
     const float s = qsf::f16_lo(meta);
     if (fmt == QK_FMT_4SYM) {
-        out[i] = __fmul_rn(s, (float)(c >= 8u ? (int)c - 16 : (int)c));
+        out[i] = qsf::mul_rn(s, (float)(c >= 8u ? (int)c - 16 : (int)c));
     } else {
-        out[i] = __fadd_rn(__fmul_rn(s, (float)c), qsf::f16_hi(meta));
+        out[i] = qsf::add_rn(qsf::mul_rn(s, (float)c), qsf::f16_hi(meta));
     }
 }
 

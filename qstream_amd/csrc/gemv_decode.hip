@@ -1584,8 +1584,8 @@ __global__ void unpack_kernel(const uint8_t* __restrict__ blocks, int nblocks,
         if constexpr (FMT == QK_FMT_4) q += 8;            // undo the ^0x8 centring
         if (codes) codes[(size_t)b * BS + k] = (int8_t)q;
         if (deq) {
-            const float prod = __fmul_rn(sc, (float)q);
-            deq[(size_t)b * BS + k] = FMT == QK_FMT_4SYM ? prod : __fadd_rn(prod, z);
+            const float prod = qsf::mul_rn(sc, (float)q);
+            deq[(size_t)b * BS + k] = FMT == QK_FMT_4SYM ? prod : qsf::add_rn(prod, z);
         }
     }
     if (meta) meta[b] = m0;

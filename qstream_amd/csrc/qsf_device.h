@@ -33,6 +33,25 @@ __device__ __forceinline__ int sdot8_z(uint32_t a, uint32_t b) {
     return r;
 }
 
+// fp32 multiply, add and subtract, each rounded on its own to nearest even,
+// as the reference's scalar C code performs them.  HIP's __fmul_rn and
+// __fadd_rn are plain operators, which the compiler's default contraction
+// mode may fuse into an FMA once inlined; these carry the contraction pragma
+// at the operation itself, so they stay separate wherever they are inlined.
+// (fmaf and __builtin_fmaf remain single-rounding FMAs.)
+__device__ __forceinline__ float mul_rn(float a, float b) {
+#pragma clang fp contract(off)
+    return a * b;
+}
+__device__ __forceinline__ float add_rn(float a, float b) {
+#pragma clang fp contract(off)
+    return a + b;
+}
+__device__ __forceinline__ float sub_rn(float a, float b) {
+#pragma clang fp contract(off)
+    return a - b;
+}
+
 // act(g) * u with QSFActivation act: 2 SiLU, 0/1 GELU (tanh form), else
 // ReLU (src/kernels_scalar.c:129-147, src/engine.c:1128-1140).  Every
 // operation is rounded on its own (no contraction into FMAs), so the
@@ -40,14 +59,14 @@ __device__ __forceinline__ int sdot8_z(uint32_t a, uint32_t b) {
 __device__ __forceinline__ float act_mul(int act, float g, float u) {
     float x = g;
     if (act == 2) {
-        x = __fdiv_rn(x, __fadd_rn(1.0f, expf(-x)));
+        x = __fdiv_rn(x, add_rn(1.0f, expf(-x)));
     } else if (act == 0 || act == 1) {
-        const float inner = __fmul_rn(0.7978845608f, __fadd_rn(x, __fmul_rn(__fmul_rn(__fmul_rn(0.044715f, x), x), x)));
-        x = __fmul_rn(__fmul_rn(0.5f, x), __fadd_rn(1.0f, tanhf(inner)));
+        const float inner = mul_rn(0.7978845608f, add_rn(x, mul_rn(mul_rn(mul_rn(0.044715f, x), x), x)));
+        x = mul_rn(mul_rn(0.5f, x), add_rn(1.0f, tanhf(inner)));
     } else if (x < 0.0f) {
         x = 0.0f;
     }
-    return __fmul_rn(x, u);
+    return mul_rn(x, u);
 }
 
 // Butterfly sum over groups of `width` consecutive lanes (power of two).
