@@ -464,12 +464,14 @@ def bench_layers(torch, hip, steps, warmup, with_cpu=True, cpu_budget=10.0):
 def bench_decode_layer(torch, hip, steps, warmup, position=1023):
     """One device-resident 7B decoder layer step per step (LLaMA-7B shapes:
     hidden 4096, 32 heads of 128, intermediate 11008, 3-bit block 128
-    weights): q/k/v (one grouped launch) on the normed input, RoPE + int8 KV
-    store (one launch), attention over `position` + 1 cached positions (two
-    launches), o, residual + NaN check + FFN RMSNorm (one launch), gate/up
-    with SiLU x up (one launch over the interleaved gate/up pair), down,
-    residual + NaN check + the next layer's attention RMSNorm (one launch)
-    -- 9 launches, no host round trip.  Steps cycle over 32 layers' distinct weights and
+    weights): residual + NaN check + attention RMSNorm + q/k/v (one grouped
+    launch: the previous layer's down output joins the residual, whose norm
+    the q/k/v rows multiply), RoPE + int8 KV store (one launch), attention
+    over `position` + 1 cached positions (two launches), o, residual + FFN
+    RMSNorm + gate/up with SiLU x up (one launch over the interleaved gate/up
+    pair), down -- 7 launches, no host round trip.  The residual alternates
+    between two buffers (a fused launch reads one while it writes the
+    other).  Steps cycle over 32 layers' distinct weights and
     KV caches (2.9 GB), so neither stays in the MALL.  Bytes per step: the
     layer's weight payloads, the KV rows attention reads, activations."""
     qt, bs, mats = cfg2_layer()
@@ -491,26 +493,24 @@ def bench_decode_layer(torch, hip, steps, warmup, position=1023):
     fn_w = torch.ones(hid, device="cuda:0")
     rope = hip.Rope(hd, 10000.0)
     res = torch.randn(hid, device="cuda:0", generator=g)
-    x = torch.empty(hid, device="cuda:0")
+    res2 = torch.empty(hid, device="cuda:0")
     ys = {n: torch.empty(r, device="cuda:0") for n, _, r, _ in mats}
+    ys["down"].zero_()                        # the first layer's residual increment
     attn = torch.empty(nh * hd, device="cuda:0")
     bad = torch.zeros(1, dtype=torch.int32, device="cuda:0")
 
     def step(i, stream):
         li = i % n_layers
         ts = layers[li]
-        hip.matvec_group(ts[0:3], x, [ys["q"], ys["k"], ys["v"]], stream=stream)
+        hip.residual_norm_matvec_group(ts[0:3], res, res2, ys["down"], an_w, 1e-5,
+                                       [ys["q"], ys["k"], ys["v"]], bad=bad, stream=stream)
         rope.apply_and_store(ys["q"], ys["k"], ys["v"], nh, nh, position, kcs[li], vcs[li], kss[li],
                              vss[li], max_seq, stream=stream)
         hip.attention(ys["q"], kcs[li], vcs[li], kss[li], vss[li], max_seq, nh, nh, hd, position, attn,
                       stream=stream)
         hip.matvec_group(ts[3:4], attn, [ys["o"]], stream=stream)
-        hip.residual_norm(res, ys["o"], fn_w, 1e-5, x, stream=stream)
-        pairs[li].gate_up_act(x, ys["gate"], 2, stream=stream)
+        pairs[li].residual_norm_gate_up_act(res2, res, ys["o"], fn_w, 1e-5, ys["gate"], 2, stream=stream)
         hip.matvec_group(ts[4:5], ys["gate"], [ys["down"]], stream=stream)
-        hip.residual_norm(res, ys["down"], an_w, 1e-5, x, bad=bad, stream=stream)
-
-    hip.rms_norm(res, x, an_w, 1e-5, stream=torch.cuda.current_stream())   # the first layer's input
 
     for i in range(warmup):
         step(i, torch.cuda.current_stream())
@@ -752,7 +752,7 @@ def run_config(torch, hip, key: str, args, cpu_budget: float, cache: dict) -> di
                          "int8 KV cache)",
                     config={"workload": f"device-resident 7B decoder layer step (3-bit block 128), "
                                         f"attention over {r['position'] + 1} cached positions, "
-                                        f"9 launches (residual + norm, RoPE + KV store and gate/up + act*mul fused)",
+                                        f"7 launches (residual + norm fused into q/k/v and into gate/up + act*mul; RoPE + KV store fused)",
                             "us_per_layer": round(r["ms_per_step"] * 1e3, 3),
                             "bytes_per_step": r["bytes_per_step"], "weight_bytes": r["weight_bytes"],
                             "kv_bytes": r["kv_bytes"],

@@ -323,6 +323,24 @@ int qsf_hip_residual_dev(float* d_res, const float* d_x, int n, int* d_bad, void
  * (RMS, or layer norm with d_b when layer_norm != 0; 940-948, 805-815). */
 int qsf_hip_residual_norm_dev(float* d_res, const float* d_x, int n, int* d_bad, const float* d_w,
                               const float* d_b, float eps, int layer_norm, float* d_out, void* stream);
+/* Residual + NaN check + RMS norm fused into the matvec that consumes the
+ * norm (src/engine.c:1174-1187 and 940-948 ahead of the q/k/v matvecs at
+ * 848-866, or 937 and 805-815 ahead of gate/up at 1118-1125): d_res_out =
+ * d_res + d_x, *d_bad as in qsf_hip_residual_dev (d_bad may be NULL), and
+ * the rows multiply rms_norm(d_res_out) * d_w.  Equal bit for bit to
+ * qsf_hip_residual_norm_dev followed by qsf_hip_matvec_group_dev /
+ * qsf_hip_gate_up_act_dev, in one launch instead of two.  No counterpart in
+ * the reference, which runs these steps one after another.  d_res_out is a
+ * second residual buffer (not d_res or d_x: every workgroup reads d_res
+ * while one writes d_res_out), and d_y / d_out alias none of the three.
+ * Blockwise tensors without outliers, cols <= 8192; otherwise
+ * QSF_ERR_INVALID_INPUT and nothing runs. */
+int qsf_hip_residual_norm_matvec_group_dev(const qsf_hip_tensor* const* t, int n, const float* d_res,
+                                           float* d_res_out, const float* d_x, int* d_bad,
+                                           const float* d_w, float eps, float* const* d_y, void* stream);
+int qsf_hip_residual_norm_gate_up_act_dev(const qsf_hip_tensor* pair, const float* d_res, float* d_res_out,
+                                          const float* d_x, int* d_bad, const float* d_w, float eps,
+                                          float* d_out, int activation, void* stream);
 /* RoPE of q and k (apply_rope, src/engine.c:204-235) and the int8 KV store
  * of the rotated k and of v at `position` (kv_cache_store, 240-300);
  * head_dim <= 256. */

@@ -20,18 +20,7 @@ namespace {
 
 constexpr int NORM_THREADS = 1024;
 
-// Sum over the workgroup (blockDim.x a multiple of 64, <= 1024); every
-// thread gets the total.  `red` holds one float per wave.
-__device__ __forceinline__ float block_sum(float v, float* red) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-    __syncthreads();                       // `red` free from any earlier use
-    if (lane == 0) red[wave] = v;
-    __syncthreads();
-    float t = 0.f;
-    for (int w = 0; w < nw; w++) t += red[w];
-    return t;
-}
+__device__ __forceinline__ float block_sum(float v, float* red) { return qsf::wg_sum(v, red); }
 
 // RMS norm (LAYER = false) or layer norm over one vector of `dim` floats,
 // one workgroup.  Output rounding order as src/kernels_scalar.c:148-185:

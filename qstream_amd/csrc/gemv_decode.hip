@@ -444,7 +444,18 @@ struct GemvArgs {
     // paired rows (row 2i gate_i, row 2i+1 up_i; two-row tiles, one matrix):
     // 1 + the activation, and y[i] = act(gate_i x) * (up_i x); 0: plain rows
     int act1;
+    // NORM kernels: x is a residual increment.  r = res_in + x (workgroup
+    // (0, 0) stores it to res_out and the NaN check to *bad), and the rows
+    // multiply rms_norm(r) * nw, kept in LDS
+    const float* res_in;
+    float* res_out;
+    const float* nw;
+    int* bad;
+    float eps;
 };
+
+// NORM kernels: elements of x a thread holds in the norm prologue
+constexpr int kNormPerThread = 8;
 
 
 // Main-kernel limits: x as XV (1 or kXvMax) float4 a thread, prepared digits
@@ -662,7 +673,8 @@ __device__ __forceinline__ void flush_tile(const GemvArgs& a, int m, int row0, i
 // tile; the barrier; the rest of the first D weight items; then the item loop
 // (the first entries join the row sums before the one reduction a row), the
 // remaining outlier entries and the stores.
-template <int FMT, int BS, int R, int D, bool OUT, bool PREP, bool DREG, bool SPLIT = false>
+template <int FMT, int BS, int R, int D, bool OUT, bool PREP, bool DREG, bool SPLIT = false,
+          bool NORM = false>
 __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
     constexpr int XV = kXvMax;
     constexpr int MT = tiles_per_wave(DREG);
@@ -746,6 +758,73 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
         rpl = rp[has ? min(row_of(bj) + br, rows) : min(br, (int)F::BB / 4 - 1)];
     }
 
+    // 1b. NORM: the residual add and the RMS norm of src/engine.c:1174-1187
+    //    and 940-948 / 805-815 ahead of the matvec, as residual_norm_kernel
+    //    computes them (same thread count, elements and order, so the same
+    //    bits): every workgroup loads res_in, x and the norm weights, issues
+    //    its first weight item behind them, reduces, and leaves the normed
+    //    x in LDS (xs), where the preparation reads it.  Workgroup (0, 0)
+    //    stores the residual and the NaN check.  Only the passes that hold
+    //    elements load (a wave-uniform guard; every such load comes before
+    //    the weight item, so the waits stay exact); a pass's lanes past the
+    //    end re-read their own first element.
+    static_assert(!NORM || (!OUT && !PREP && WAVES * 64 == 1024), "NORM: one-launch, no outliers");
+    const float* xsrc = a.x;
+    uint32_t wv[D][R][1 + F::CW];
+    if constexpr (NORM) {
+        constexpr int KN = kNormPerThread;
+        const int t_id = (int)threadIdx.x, n = a.cols;
+        float nr[KN], nx[KN], nwv[KN];
+#pragma unroll
+        for (int k = 0; k < KN; k++) {
+            nr[k] = nx[k] = nwv[k] = 0.f;
+            if (k * NT < n) {
+                const int i = t_id + k * NT < n ? t_id + k * NT : min(t_id, n - 1);
+                nr[k] = a.res_in[i];
+                nx[k] = a.x[i];
+                nwv[k] = a.nw[i];
+            }
+        }
+        issue(wv[0]);
+        float acc = 0.f;
+        int first = n;
+#pragma unroll
+        for (int k = 0; k < KN; k++) {
+            const int i = t_id + k * NT;
+            const float r = qsf::add_rn(nr[k], nx[k]);
+            nr[k] = r;
+            if (i < n) {
+                if ((r != r || r > 1e30f || r < -1e30f) && i < first) first = i;
+                acc = fmaf(r, r, acc);
+            }
+        }
+        float* red = reinterpret_cast<float*>(lds + a.st_off);
+        const float ss = qsf::wg_sum(acc, red);
+        const float inv = __fdiv_rn(1.0f, __fsqrt_rn(qsf::add_rn(__fdiv_rn(ss, (float)n), a.eps)));
+        if (blockIdx.x == 0 && blockIdx.y == 0) {
+#pragma unroll
+            for (int k = 0; k < KN; k++)
+                if (t_id + k * NT < n) a.res_out[t_id + k * NT] = nr[k];
+            if (a.bad) {
+                for (int off = 32; off > 0; off >>= 1) first = min(first, __shfl_xor(first, off, 64));
+                int* ired = reinterpret_cast<int*>(red);
+                __syncthreads();                      // every wave past wg_sum's reads of red
+                if (lane == 0) ired[wave] = first;
+                __syncthreads();
+                if (t_id == 0) {
+                    int f = n;
+                    for (int w = 0; w < WAVES; w++) f = min(f, ired[w]);
+                    *a.bad = f < n ? f : -1;
+                }
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < KN; k++)
+            if (t_id + k * NT < n) xs[t_id + k * NT] = qsf::mul_rn(qsf::mul_rn(nr[k], inv), nwv[k]);
+        __syncthreads();
+        xsrc = xs;
+    }
+
     // 2. Preparing here: the prep waves load the x of their first two passes
     //    of blocks, issue their first weight item, and then turn x into
     //    digits in LDS.  The x loads go ahead of every weight load of the
@@ -763,7 +842,6 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
     const int pw = t_id & (F::LPB - 1), pb = t_id / F::LPB;
     const bool prep_wave = !PREP && wave * (64 / F::LPB) < a.nb;
     float* xcopy = OUT ? xs : nullptr;
-    uint32_t wv[D][R][1 + F::CW];
     if constexpr (!PREP) {
         // 2/4-bit: the first two passes load their x together (the second
         // pass is the 7B down projection's: 172 4-bit blocks); 3-bit: one
@@ -780,16 +858,16 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
         // theirs at once.  2/4-bit: the first item goes first (measured:
         // config 0 5.25 -> 5.04 us, config 1 12.7 -> 12.45 us).
         constexpr bool kItemFirst = FMT != QK_FMT_3;
-        if (prep_wave) prep_load<FMT, BS, true>(a.x, a.cols, pb, pb < a.nb, pw, xv0);
+        if (prep_wave) prep_load<FMT, BS, true>(xsrc, a.cols, pb, pb < a.nb, pw, xv0);
         if constexpr (AHEAD == 2)
-            if (two) prep_load<FMT, BS, true>(a.x, a.cols, pb1, pb1 < a.nb, pw, xv1);
-        if constexpr (kItemFirst) issue(wv[0]);              // 3. the first weight item
+            if (two) prep_load<FMT, BS, true>(xsrc, a.cols, pb1, pb1 < a.nb, pw, xv1);
+        if constexpr (kItemFirst && !NORM) issue(wv[0]);     // 3. the first weight item
         if (prep_wave) {
             const int b0 = pb < a.nb ? pb : 0;
             prep_settle<FMT, BS>(pb, pb < a.nb, pw, a.cols, xv0);
             prep_finish<FMT, BS>(xv0, pb, pb < a.nb, pw, dig + b0 * F::DWS, meta + b0, xcopy, a.cols);
         }
-        if constexpr (!kItemFirst) issue(wv[0]);
+        if constexpr (!kItemFirst && !NORM) issue(wv[0]);
         if constexpr (AHEAD == 2) {
             if (two) {
                 const int b1 = pb1 < a.nb ? pb1 : 0;
@@ -803,7 +881,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
             const int b = base + pb;
             const bool live = b < a.nb;
             const int bb = live ? b : 0;
-            prep_block<FMT, BS>(a.x, a.cols, b, live, pw, dig + bb * F::DWS, meta + bb, xcopy);
+            prep_block<FMT, BS>(xsrc, a.cols, b, live, pw, dig + bb * F::DWS, meta + bb, xcopy);
         }
     }
     constexpr bool XS = PREP && OUT;
@@ -1374,6 +1452,8 @@ int plan_rt(const qsf_hip_tensor* const* t, int n, int cols, int mode, float* co
 // Paired-rows request of the calling thread for the launch being planned
 // (qk_gemv_pair_act sets it around its one call): 1 + activation, or 0.
 thread_local int tl_pair_act1 = 0;
+// set by qk_gemv_group_norm / qk_gemv_pair_act_norm for the call's launches
+thread_local const qk_norm_args* tl_norm = nullptr;
 
 template <int FMT, int BS, int R, bool DREG = false, bool SPLIT = false>
 int launch_rt(const qsf_hip_tensor* const* t, int n, int cols, const float* d_x,
@@ -1403,6 +1483,17 @@ int launch_rt(const qsf_hip_tensor* const* t, int n, int cols, const float* d_x,
     a.xq = prepared ? xq : nullptr;
     a.xmeta = xmeta;
     a.x = d_x;
+    // fused residual + norm: the one-launch whole-row kernel without
+    // outliers; any other plan is refused (never run without the norm)
+    const qk_norm_args* const nm = tl_norm;
+    a.res_in = nm ? nm->res_in : nullptr;
+    a.res_out = nm ? nm->res_out : nullptr;
+    a.nw = nm ? nm->w : nullptr;
+    a.bad = nm ? nm->bad : nullptr;
+    a.eps = nm ? nm->eps : 0.f;
+    if (nm && (prepared || !(p.kid == 2 || p.kid == 3 || p.kid == 4 || p.kid >= 8) ||
+               cols > kNormPerThread * WAVES * 64))
+        return -2;
 
     constexpr bool kHasOut = FMT == QK_FMT_2 || FMT == QK_FMT_4;
     // one item a wave at most (a 4096-row matrix of up to 64 blocks): one
@@ -1415,6 +1506,22 @@ int launch_rt(const qsf_hip_tensor* const* t, int n, int cols, const float* d_x,
     constexpr int D = DREG ? 2 : prefetch_depth<FMT, BS, R, false>();
     constexpr int DO = DREG ? 2 : prefetch_depth<FMT, BS, R, kHasOut>();
     const dim3 g(p.grid, p.ny), b(WAVES * 64);
+    if (nm) {
+        if constexpr (SPLIT) {
+            switch (p.kid) {
+            case 2: launch_main<gemv_kernel<FMT, BS, R, 1, false, false, DREG, true, true>>(g, b, p.lds, s, a); break;
+            case 3: launch_main<gemv_kernel<FMT, BS, R, (D > 2 ? 2 : D), false, false, DREG, true, true>>(g, b, p.lds, s, a); break;
+            default: launch_main<gemv_kernel<FMT, BS, R, D, false, false, DREG, true, true>>(g, b, p.lds, s, a); break;
+            }
+        } else {
+            switch (p.kid) {
+            case 8: launch_main<gemv_kernel<FMT, BS, R, 1, false, false, DREG, false, true>>(g, b, p.lds, s, a); break;
+            case 9: launch_main<gemv_kernel<FMT, BS, R, (D > 2 ? 2 : D), false, false, DREG, false, true>>(g, b, p.lds, s, a); break;
+            default: launch_main<gemv_kernel<FMT, BS, R, D, false, false, DREG, false, true>>(g, b, p.lds, s, a); break;
+            }
+        }
+        return hipGetLastError() == hipSuccess ? 0 : -1;
+    }
     if constexpr (SPLIT) {
         // one-launch decode only (the split view prepares x in its own parts)
         switch (p.kid) {
@@ -1680,6 +1787,39 @@ extern "C" int qk_gemv_pair_act(const qsf_hip_tensor* t, const float* d_x, float
     float* const y[1] = {d_y};
     const int rc = qk_gemv_group(&t, 1, d_x, y, nullptr, QK_RUN_BOTH, s);
     tl_pair_act1 = 0;
+    return rc;
+}
+
+// The fused forms' checks: a norm needs its arguments, every matrix rows
+// (a launch with no tiles would skip the residual store), and buffers that
+// no workgroup writes while another still reads them.
+static bool norm_ok(const qsf_hip_tensor* const* t, int n, const qk_norm_args* nm, const float* d_x,
+                    float* const* d_y) {
+    if (!nm || !nm->res_in || !nm->res_out || !nm->w || !d_x || n <= 0 || n > QK_MAX_GROUP) return false;
+    if (nm->res_out == nm->res_in || nm->res_out == d_x) return false;
+    for (int i = 0; i < n; i++) {
+        if (!t[i] || t[i]->rows <= 0 || t[i]->cols <= 0 || t[i]->cols > kNormPerThread * WAVES * 64) return false;
+        if (d_y[i] == nm->res_in || d_y[i] == nm->res_out || d_y[i] == d_x) return false;
+    }
+    return true;
+}
+
+extern "C" int qk_gemv_group_norm(const qsf_hip_tensor* const* t, int n, const qk_norm_args* nm,
+                                  const float* d_x, float* const* d_y, hipStream_t s) {
+    if (!norm_ok(t, n, nm, d_x, d_y)) return -2;
+    tl_norm = nm;
+    const int rc = qk_gemv_group(t, n, d_x, d_y, nullptr, QK_RUN_BOTH, s);
+    tl_norm = nullptr;
+    return rc;
+}
+
+extern "C" int qk_gemv_pair_act_norm(const qsf_hip_tensor* t, const qk_norm_args* nm, const float* d_x,
+                                     float* d_y, int act, hipStream_t s) {
+    float* const y[1] = {d_y};
+    if (!norm_ok(&t, 1, nm, d_x, y)) return -2;
+    tl_norm = nm;
+    const int rc = qk_gemv_pair_act(t, d_x, d_y, act, s);
+    tl_norm = nullptr;
     return rc;
 }
 

@@ -69,6 +69,21 @@ __device__ __forceinline__ float act_mul(int act, float g, float u) {
     return mul_rn(x, u);
 }
 
+// Sum over the workgroup (blockDim.x a multiple of 64, <= 1024); every
+// thread gets the total.  `red` holds one float per wave.  The norm launches
+// and the GEMV's fused norm prologue both reduce through this, so equal
+// thread counts give equal sums.
+__device__ __forceinline__ float wg_sum(float v, float* red) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    __syncthreads();                       // `red` free from any earlier use
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float t = 0.f;
+    for (int w = 0; w < nw; w++) t += red[w];
+    return t;
+}
+
 // Butterfly sum over groups of `width` consecutive lanes (power of two).
 __device__ __forceinline__ float group_sum(float v, int width) {
     for (int off = width >> 1; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);

@@ -74,6 +74,23 @@ int qk_gemv_group(const qsf_hip_tensor* const* t, int n, const float* d_x,
  * outliers): y[i] = act(gate_i x) * (up_i x), act a QSFActivation >= 0.
  * -2 when the plan cannot take two-row tiles. */
 int qk_gemv_pair_act(const qsf_hip_tensor* t, const float* d_x, float* d_y, int act, hipStream_t s);
+/* Residual + RMS norm fused ahead of a one-launch GEMV: res_out = res_in +
+ * x (the matvec's x argument is the increment), the NaN check into *bad
+ * (may be NULL), then the rows multiply rms_norm(res_out) * w.  Equal bit
+ * for bit to qk_residual_norm followed by the plain GEMV.  res_out must
+ * differ from res_in and x, and y from all three.  -2 when the plan is not
+ * the one-launch whole-row kernel without outliers, or cols > 8192. */
+typedef struct {
+    const float* res_in;
+    float* res_out;
+    const float* w;
+    int* bad;
+    float eps;
+} qk_norm_args;
+int qk_gemv_group_norm(const qsf_hip_tensor* const* t, int n, const qk_norm_args* nm,
+                       const float* d_x, float* const* d_y, hipStream_t s);
+int qk_gemv_pair_act_norm(const qsf_hip_tensor* t, const qk_norm_args* nm, const float* d_x,
+                          float* d_y, int act, hipStream_t s);
 /* What fixes a row's arithmetic in qk_gemv_group(t, n, ..., mode): the
  * kernel instantiation, row-group width, tile rows and chunk.  A tensor's
  * rows come out bit-identical in two launches whose signatures are equal

@@ -898,6 +898,35 @@ int qsf_hip_gate_up_act_dev(const qsf_hip_tensor* pair, const float* d_x, float*
     return rc ? fail(E_INTERNAL, "qsf_hip_gate_up_act_dev: launch failed") : E_OK;
 }
 
+static int norm_rc(const char* fn, int rc) {
+    if (rc == -2)
+        return fail(E_INVALID, "%s: no fused plan (outliers, cols > 8192, no rows, or aliased buffers)", fn);
+    return rc ? fail(E_INTERNAL, "%s: launch failed", fn) : E_OK;
+}
+
+int qsf_hip_residual_norm_matvec_group_dev(const qsf_hip_tensor* const* t, int n, const float* d_res,
+                                           float* d_res_out, const float* d_x, int* d_bad,
+                                           const float* d_w, float eps, float* const* d_y, void* stream) {
+    static const char fn[] = "qsf_hip_residual_norm_matvec_group_dev";
+    if (!t || n <= 0 || n > QK_MAX_GROUP || !d_res || !d_res_out || !d_x || !d_w || !d_y)
+        return fail(E_INVALID, "%s: bad arguments", fn);
+    for (int i = 0; i < n; i++)
+        if (!t[i] || t[i]->fmt < 0 || !d_y[i]) return fail(E_INVALID, "%s: blockwise QSF tensors only", fn);
+    const qk_norm_args nm = {d_res, d_res_out, d_w, d_bad, eps};
+    return norm_rc(fn, qk_gemv_group_norm(t, n, &nm, d_x, d_y, pick_stream(stream)));
+}
+
+int qsf_hip_residual_norm_gate_up_act_dev(const qsf_hip_tensor* pair, const float* d_res, float* d_res_out,
+                                          const float* d_x, int* d_bad, const float* d_w, float eps,
+                                          float* d_out, int activation, void* stream) {
+    static const char fn[] = "qsf_hip_residual_norm_gate_up_act_dev";
+    if (!pair || pair->fmt < 0 || pair->rows % 2 || activation < 0 || !d_res || !d_res_out || !d_x || !d_w ||
+        !d_out)
+        return fail(E_INVALID, "%s: bad arguments", fn);
+    const qk_norm_args nm = {d_res, d_res_out, d_w, d_bad, eps};
+    return norm_rc(fn, qk_gemv_pair_act_norm(pair, &nm, d_x, d_out, activation, pick_stream(stream)));
+}
+
 int qsf_hip_residual_dev(float* d_res, const float* d_x, int n, int* d_bad, void* stream) {
     if (n < 0 || (n > 0 && (!d_res || !d_x)))
         return fail(E_INVALID, "qsf_hip_residual_dev: bad arguments");

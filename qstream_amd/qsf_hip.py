@@ -39,6 +39,7 @@ EXPORTS = (
     "qsf_hip_rope_dev", "qsf_hip_kv_store_dev", "qsf_hip_attention_dev", "qsf_hip_act_mul_dev",
     "qsf_hip_gate_up_act_dev", "qsf_hip_residual_dev", "qsf_hip_embed_row_dev", "qsf_hip_embed_row_fp16_dev",
     "qsf_hip_residual_norm_dev", "qsf_hip_rope_kv_store_dev",
+    "qsf_hip_residual_norm_matvec_group_dev", "qsf_hip_residual_norm_gate_up_act_dev",
     "qsf_hip_crc32", "qsf_hip_model_load", "qsf_hip_model_free", "qsf_hip_model_get_info",
     "qsf_hip_model_tensor", "qsf_hip_model_vector", "qsf_hip_model_embedding",
     "qsf_hip_model_embedding_fp16", "qsf_hip_model_output_head", "qsf_hip_model_final_norm", "qsf_hip_model_moe",
@@ -125,11 +126,14 @@ def load(path: str = LIB_PATH) -> C.CDLL:
     L.qsf_hip_embed_row_dev.argtypes = [_vp, _i, _vp, _vp]
     L.qsf_hip_embed_row_fp16_dev.argtypes = [_vp, _i, _i, _vp, _vp]
     L.qsf_hip_residual_norm_dev.argtypes = [_vp, _vp, _i, _vp, _vp, _vp, _f, _i, _vp, _vp]
+    L.qsf_hip_residual_norm_matvec_group_dev.argtypes = [_vp, _i, _vp, _vp, _vp, _vp, _vp, _f, _vp, _vp]
+    L.qsf_hip_residual_norm_gate_up_act_dev.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _f, _vp, _i, _vp]
     L.qsf_hip_rope_kv_store_dev.argtypes = [_vp, _vp, _vp, _vp, _i, _i, _i, _vp, _vp, _vp, _vp, _i, _vp]
     for n in ("qsf_hip_rms_norm_dev", "qsf_hip_layer_norm_dev", "qsf_hip_rope_dev",
               "qsf_hip_kv_store_dev", "qsf_hip_attention_dev", "qsf_hip_act_mul_dev",
               "qsf_hip_gate_up_act_dev", "qsf_hip_residual_dev", "qsf_hip_embed_row_dev", "qsf_hip_embed_row_fp16_dev",
-              "qsf_hip_residual_norm_dev", "qsf_hip_rope_kv_store_dev"):
+              "qsf_hip_residual_norm_dev", "qsf_hip_rope_kv_store_dev",
+              "qsf_hip_residual_norm_matvec_group_dev", "qsf_hip_residual_norm_gate_up_act_dev"):
         getattr(L, n).restype = _i
     L.qsf_hip_crc32.argtypes = [_vp, C.c_size_t]
     L.qsf_hip_crc32.restype = C.c_uint32
@@ -298,6 +302,15 @@ class TensorPair(Tensor):
             _check(-1, "qsf_hip_tensor_upload_pair")
         self.payload_bytes = L.qsf_hip_tensor_payload_bytes(self.handle)
 
+    def residual_norm_gate_up_act(self, res, res_out, x, w, eps, out, activation, bad=None,
+                                  stream=None) -> None:
+        """res_out = res + x (NaN check into `bad`), then out = act(gate n) * (up n) for
+        n = rms_norm(res_out) * w, in one launch."""
+        _check(load().qsf_hip_residual_norm_gate_up_act_dev(self.handle, _addr(res), _addr(res_out),
+                                                            _addr(x), _addr(bad), _addr(w), eps,
+                                                            _addr(out), activation, _stream(stream)),
+               "qsf_hip_residual_norm_gate_up_act_dev")
+
     def gate_up_act(self, x, out, activation, stream=None) -> None:
         """out[i] = act(gate_i . x) * (up_i . x) in one launch."""
         _check(load().qsf_hip_gate_up_act_dev(self.handle, _addr(x), _addr(out), activation,
@@ -310,6 +323,17 @@ def matvec_group(tensors, x, ys, stream=None) -> None:
     yh = (_vp * n)(*[_addr(y) for y in ys])
     _check(load().qsf_hip_matvec_group_dev(th, n, _addr(x), yh, _stream(stream)),
            "qsf_hip_matvec_group_dev")
+
+
+def residual_norm_matvec_group(tensors, res, res_out, x, w, eps, ys, bad=None, stream=None) -> None:
+    """res_out = res + x (NaN check into `bad`), then ys[i] = tensors[i] . (rms_norm(res_out) * w),
+    in one launch."""
+    n = len(tensors)
+    th = (_vp * n)(*[t.handle for t in tensors])
+    yh = (_vp * n)(*[_addr(y) for y in ys])
+    _check(load().qsf_hip_residual_norm_matvec_group_dev(th, n, _addr(res), _addr(res_out), _addr(x),
+                                                         _addr(bad), _addr(w), eps, yh, _stream(stream)),
+           "qsf_hip_residual_norm_matvec_group_dev")
 
 
 def xprep_bytes(qt: int, bs: int, cols: int) -> int:
