@@ -762,8 +762,11 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
     //    and 940-948 / 805-815 ahead of the matvec, as residual_norm_kernel
     //    computes them (same thread count, elements and order, so the same
     //    bits): every workgroup loads res_in, x and the norm weights, issues
-    //    its first weight item behind them, reduces, and leaves the normed
-    //    x in LDS (xs), where the preparation reads it.  Workgroup (0, 0)
+    //    its first weight item behind them (3-bit: after the digits, as
+    //    without the norm; issued here it held the norm's arithmetic back
+    //    behind the CU's weight loads, 3.2 us more a 7B layer step),
+    //    reduces, and leaves the normed x in LDS (xs), where the preparation
+    //    reads it.  Workgroup (0, 0)
     //    stores the residual and the NaN check.  Only the passes that hold
     //    elements load (a wave-uniform guard; every such load comes before
     //    the weight item, so the waits stay exact); a pass's lanes past the
@@ -785,7 +788,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
                 nwv[k] = a.nw[i];
             }
         }
-        issue(wv[0]);
+        if constexpr (FMT != QK_FMT_3) issue(wv[0]);
         float acc = 0.f;
         int first = n;
 #pragma unroll
@@ -867,7 +870,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
             prep_settle<FMT, BS>(pb, pb < a.nb, pw, a.cols, xv0);
             prep_finish<FMT, BS>(xv0, pb, pb < a.nb, pw, dig + b0 * F::DWS, meta + b0, xcopy, a.cols);
         }
-        if constexpr (!kItemFirst && !NORM) issue(wv[0]);
+        if constexpr (!kItemFirst) issue(wv[0]);
         if constexpr (AHEAD == 2) {
             if (two) {
                 const int b1 = pb1 < a.nb ? pb1 : 0;
