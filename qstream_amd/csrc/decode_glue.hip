@@ -449,25 +449,31 @@ __global__ __launch_bounds__(64) void rope_kv_kernel(float* q, float* k, const f
 
 // One row of a blockwise table: value i = scale * q + zero (4-bit sym:
 // scale * q), each product and sum rounded as in src/quant.c:95-177.
-__device__ __forceinline__ unsigned code_of(int fmt, const uint8_t* packed, int i) {
-    if (fmt == QK_FMT_2) return (packed[i >> 2] >> ((i & 3) * 2)) & 3u;
-    if (fmt == QK_FMT_3) {
-        const int bit = 3 * i, byte = bit >> 3, off = bit & 7;
-        unsigned v = packed[byte] >> off;
-        if (off > 5) v |= (unsigned)packed[byte + 1] << (8 - off);
-        return v & 7u;
-    }
-    return (packed[i >> 1] >> ((i & 1) * 4)) & 15u;
-}
-
 __global__ __launch_bounds__(256) void embed_row_kernel(const uint8_t* __restrict__ blocks, int fmt,
-                                                        int bs, int bb, int hd, float* out) {
+                                                        int bs, int bb, int hd, float* out,
+                                                        int frag_row, int nq) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= hd) return;
-    const uint8_t* blk = blocks + (size_t)(i / bs) * bb;
-    const uint32_t meta = (uint32_t)blk[0] | ((uint32_t)blk[1] << 8) | ((uint32_t)blk[2] << 16) |
-                          ((uint32_t)blk[3] << 24);
-    const unsigned c = code_of(fmt, blk + 4, i % bs);
+    // byte j of the value's block: on-disk order (`blocks` is the row), or
+    // fragment order (`blocks` is the tensor, frag_row the row)
+    const int b = i / bs;
+    auto byte_at = [&](int j) -> unsigned {
+        return frag_row >= 0 ? blocks[qsf::frag_off((size_t)frag_row, b, j, nq, bb)]
+                             : blocks[(size_t)b * bb + j];
+    };
+    const uint32_t meta = byte_at(0) | (byte_at(1) << 8) | (byte_at(2) << 16) | (byte_at(3) << 24);
+    const int k = i % bs;
+    unsigned c;
+    if (fmt == QK_FMT_2) {
+        c = (byte_at(4 + (k >> 2)) >> ((k & 3) * 2)) & 3u;
+    } else if (fmt == QK_FMT_3) {
+        const int bit = 3 * k, byte = bit >> 3, off = bit & 7;
+        unsigned v = byte_at(4 + byte) >> off;
+        if (off > 5) v |= byte_at(4 + byte + 1) << (8 - off);
+        c = v & 7u;
+    } else {
+        c = (byte_at(4 + (k >> 1)) >> ((k & 1) * 4)) & 15u;
+    }
     const float s = qsf::f16_lo(meta);
     if (fmt == QK_FMT_4SYM) {
         out[i] = qsf::mul_rn(s, (float)(c >= 8u ? (int)c - 16 : (int)c));
@@ -588,9 +594,9 @@ extern "C" int qk_rope_kv_store(float* q, float* k, const float* v, const float*
 extern "C" int qk_embed_row(const qsf_hip_tensor* t, int token, float* out, hipStream_t s) {
     if (t->fmt < 0 || token < 0 || token >= t->rows) return -2;
     if (t->cols <= 0) return 0;
-    const uint8_t* row = t->d_blocks + (size_t)token * t->nb * t->block_bytes;
+    const uint8_t* row = t->frag ? t->d_blocks : t->d_blocks + (size_t)token * t->nb * t->block_bytes;
     hipLaunchKernelGGL(embed_row_kernel, dim3((t->cols + 255) / 256), dim3(256), 0, s, row, t->fmt, t->bs,
-                       t->block_bytes, t->cols, out);
+                       t->block_bytes, t->cols, out, t->frag ? token : -1, t->frag_nq);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

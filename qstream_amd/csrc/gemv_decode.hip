@@ -1771,6 +1771,11 @@ extern "C" int qk_gemv_group(const qsf_hip_tensor* const* t, int n, const float*
                                    d_y[i], t[i]->rows, 0.0f);
         return hipGetLastError() == hipSuccess ? 0 : -1;
     }
+    // tensors in fragment order take the matrix-core kernel (from the fp32 x
+    // in every mode) and nothing else
+    bool frag = false, disk = false;
+    for (int i = 0; i < n; i++) (t[i]->frag ? frag : disk) = true;
+    if (frag) return disk ? -2 : qk_gemv_mfma(t, n, d_x, d_y, tl_pair_act1, tl_norm, s);
     if (mode == QK_RUN_BOTH && (bs == 128 || bs == 256)) {
         switch (fmt) {
         case QK_FMT_2: return launch_split<QK_FMT_2>(t, n, cols, d_x, d_y, d_ws, mode, s);
@@ -1830,8 +1835,16 @@ extern "C" uint64_t qk_gemv_signature(const qsf_hip_tensor* const* t, int n, int
     if (n <= 0 || n > QK_MAX_GROUP) return 0;
     const int fmt = t[0]->fmt, bs = t[0]->bs, cols = t[0]->cols;
     for (int i = 1; i < n; i++)
-        if (t[i]->fmt != fmt || t[i]->bs != bs || t[i]->cols != cols) return 0;
+        if (t[i]->fmt != fmt || t[i]->bs != bs || t[i]->cols != cols || t[i]->frag != t[0]->frag) return 0;
     if (cols <= 0) return 2;
+    if (t[0]->frag) {
+        // the matrix-core kernel: a row's arithmetic depends on its matrix
+        // alone; groups mix no outlier and plain tables
+        const bool o = t[0]->d_row_ptr != nullptr;
+        for (int i = 1; i < n; i++)
+            if ((t[i]->d_row_ptr != nullptr) != o) return 0;
+        return 1ull | (1ull << 62) | (uint64_t)o << 1 | (uint64_t)fmt << 8 | (uint64_t)bs << 16;
+    }
     if (mode == QK_RUN_BOTH && (bs == 128 || bs == 256)) {
         switch (fmt) {
         case QK_FMT_2: return sig_t<QK_FMT_2, 64, true>(t, n, cols, mode);

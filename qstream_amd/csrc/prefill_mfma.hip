@@ -116,6 +116,7 @@ struct PrefillArgs {
     int tiles_n;
     int sz, s;               // zero-point stages; all stages (both even)
     uint32_t w_bytes, xp_bytes;
+    int nq;                  // FRAG: 4-block quads a row (the blocks are in fragment order)
 };
 
 // x bf16 [m][k] -> A-fragment order.  For each group of 16 rows, ksp_total
@@ -221,7 +222,7 @@ __device__ __forceinline__ void tile_of(int id, int nwg, int tiles_n, int& tm, i
 
 // RAGGED: k is not a multiple of 2 SK, so code stages reach past the last
 // column; their B items are zeroed (and x is zero there).
-template <int BS, bool RAGGED>
+template <int BS, bool RAGGED, bool FRAG = false>
 __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
     constexpr int BB = 4 + BS / 2;             // block bytes
     // two B buffers and their scales during the main loop; the output
@@ -254,7 +255,48 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
         const uint32_t lane_code = lane_meta + 4 + (BS == 64 ? 0u : (uint32_t)h * 32);
         const uint32_t wv = (uint32_t)(n0 + col) * row_bytes;
         const int it_base = col * PITCH + 64 * h;
+        // FRAG: block b of row n0 + col sits in tile (row / 16, b / 4) at
+        // lane 16 (b % 4) + row % 16; its 16-byte planes are 1 KB apart, the
+        // 4-byte tail plane after them (rows and blocks past the tensor read
+        // zero or are masked below, as in on-disk order)
+        constexpr int KP = BB / 16;            // 16-byte planes a block
+        const uint32_t frow = (uint32_t)(n0 + col);
+        auto fbase = [&](uint32_t b) __attribute__((always_inline)) {
+            return (((frow >> 4) * (uint32_t)a.nq + (b >> 2)) * 64u) * (uint32_t)BB +
+                   ((b & 3u) * 16u + (frow & 15u)) * 16u;
+        };
+        auto ftail = [&](uint32_t b) __attribute__((always_inline)) {
+            return (((frow >> 4) * (uint32_t)a.nq + (b >> 2)) * 64u) * (uint32_t)BB + KP * 1024u +
+                   ((b & 3u) * 16u + (frow & 15u)) * 4u;
+        };
         auto load = [&](int s, u32x4 (&c)[2], uint32_t& meta) __attribute__((always_inline)) {
+            if constexpr (FRAG) {
+                static_assert(BS == 64 || BS == 128, "fragment order: blocks of 64 or 128");
+                if (s < a.sz) {
+                    const uint32_t b0 = (uint32_t)(16 * s + 8 * h);
+#pragma unroll
+                    for (int j = 0; j < 8; j++)
+                        c[j >> 2][j & 3] = __builtin_amdgcn_raw_buffer_load_b32(wr, fbase(b0 + j), 0, 0);
+                    meta = 0;
+                } else {
+                    // the 32 code bytes from byte 4 + 32 (h or 0) of the block:
+                    // dwords 1-3 of plane pa, plane pa + 1, dword 0 of plane
+                    // pa + 2 (or of the tail plane)
+                    const int sc = s - a.sz;
+                    const uint32_t b = BS == 64 ? (uint32_t)(2 * sc + h) : (uint32_t)sc;
+                    const uint32_t pa = BS == 64 ? 0u : 2u * (uint32_t)h;
+                    const uint32_t o = fbase(b);
+                    const u32x4 pA = __builtin_amdgcn_raw_buffer_load_b128(wr, o + pa * 1024u, 0, 0);
+                    const u32x4 pB = __builtin_amdgcn_raw_buffer_load_b128(wr, o + (pa + 1) * 1024u, 0, 0);
+                    const uint32_t pC = pa + 2 < (uint32_t)KP
+                                            ? __builtin_amdgcn_raw_buffer_load_b32(wr, o + (pa + 2) * 1024u, 0, 0)
+                                            : __builtin_amdgcn_raw_buffer_load_b32(wr, ftail(b), 0, 0);
+                    meta = pa == 0 ? pA.x : __builtin_amdgcn_raw_buffer_load_b32(wr, o, 0, 0);
+                    c[0] = u32x4{pA.y, pA.z, pA.w, pB.x};
+                    c[1] = u32x4{pB.y, pB.z, pB.w, pC};
+                }
+                return;
+            }
             if (s < a.sz) {
                 const uint32_t b0 = (uint32_t)(16 * s + 8 * h);
 #pragma unroll
@@ -533,19 +575,25 @@ extern "C" int qk_prefill_4bit(const qsf_hip_tensor* t, const uint16_t* d_x_bf16
     const bool ragged = t->cols % (2 * SK) != 0;
     hipLaunchKernelGGL(xpack_kernel, dim3((ksp_total - kz) / 8, (m + 15) / 16), dim3(256), 0, s,
                        d_x_bf16, static_cast<u32x4*>(d_ws), m, t->cols, ksp_total, kz, t->bs, t->nb);
+    const uint64_t w_bytes = t->frag ? (uint64_t)qk_frag_bytes(t->rows, t->nb, bb) : (uint64_t)t->rows * row_bytes;
+    if (t->frag && (uint64_t)((t->rows + BN) / 16 + 1) * t->frag_nq * 64 * bb >= (1ull << 32)) return -2;
     PrefillArgs a = {t->d_blocks, static_cast<const u32x4*>(d_ws), d_y, m, t->rows, t->cols, t->nb,
-                     tiles_n, st.sz, st.sz + st.sc, (uint32_t)((uint64_t)t->rows * row_bytes),
-                     (uint32_t)xp_bytes};
+                     tiles_n, st.sz, st.sz + st.sc, (uint32_t)w_bytes, (uint32_t)xp_bytes, t->frag_nq};
     const dim3 grid(tiles_n * tiles_m), block(512);
-#define QK_PREFILL_CASE(B)                                                   \
-    case B:                                                                  \
-        if (ragged) launch<prefill_kernel<B, true>>(grid, block, s, a);      \
-        else launch<prefill_kernel<B, false>>(grid, block, s, a);            \
-        break;
+#define QK_PREFILL_CASE(B, F)                                                   \
+    if (ragged) launch<prefill_kernel<B, true, F>>(grid, block, s, a);          \
+    else launch<prefill_kernel<B, false, F>>(grid, block, s, a);
     switch (t->bs) {
-        QK_PREFILL_CASE(64)
-        QK_PREFILL_CASE(128)
-        QK_PREFILL_CASE(256)
+    case 64:
+        if (t->frag) { QK_PREFILL_CASE(64, true) } else { QK_PREFILL_CASE(64, false) }
+        break;
+    case 128:
+        if (t->frag) { QK_PREFILL_CASE(128, true) } else { QK_PREFILL_CASE(128, false) }
+        break;
+    case 256:
+        if (t->frag) return -2;
+        QK_PREFILL_CASE(256, false)
+        break;
     default: return -2;
     }
 #undef QK_PREFILL_CASE

@@ -19,6 +19,19 @@ __device__ __forceinline__ float f16_bits(uint16_t v) {
     return (float)__builtin_bit_cast(_Float16, v);
 }
 
+// Byte j of block b of row `row` of a tensor in fragment order (the tile
+// layout of qk_frag_offset in qsf_hip_internal.h): tile (row / 16, b / 4) of
+// 64 * bb bytes, lane 16 (b % 4) + row % 16, 16-byte planes then a tail
+// plane of bb % 16 bytes a lane.
+__device__ __forceinline__ size_t frag_off(size_t row, int b, int j, int nq, int bb) {
+    const size_t tile = (row >> 4) * (size_t)nq + (size_t)(b >> 2);
+    const int lane = (b & 3) * 16 + (int)(row & 15);
+    const int k = bb >> 4;
+    const size_t base = tile * 64 * (size_t)bb;
+    return j < 16 * k ? base + (size_t)(j >> 4) * 1024 + (size_t)lane * 16 + (size_t)(j & 15)
+                      : base + (size_t)k * 1024 + (size_t)lane * (size_t)(bb & 15) + (size_t)(j - 16 * k);
+}
+
 // Signed 4-bit x signed 4-bit dot of 8 nibble pairs, accumulated in int32
 // (v_dot8_i32_i4).
 __device__ __forceinline__ int sdot8(uint32_t a, uint32_t b, int c) {

@@ -42,6 +42,8 @@ typedef struct qsf_hip_tensor {
     uint32_t* d_ocol;           /* else n_csr column indices ... */
     uint16_t* d_oval;           /* ... and n_csr fp16 values */
     void*    d_alloc;           /* base of the single device allocation */
+    int      frag;              /* 1: d_blocks in fragment order (below), 0: on-disk order */
+    int      frag_nq;           /* fragment order: 4-block quads a row, ceil(nb / 4) */
     int      registry_owned;    /* uploaded implicitly by a table-slot call */
     const void* succ;           /* table slots: the key called next with the same x ... */
     int      succ_hits;         /* ... this many times since it last differed */
@@ -50,6 +52,22 @@ typedef struct qsf_hip_tensor {
 } qsf_hip_tensor;
 
 #define QK_MAX_GROUP 8
+
+/* Fragment order: the device layout of a dense tensor the matrix-core GEMV
+ * covers (qk_mfma_layout).  The on-disk blocks, unchanged, regrouped into
+ * tiles of 16 rows x 4 blocks: tile t = (row / 16) * nq + b / 4 (nq =
+ * ceil(nb / 4)) holds 64 blocks, lane L = 16 (b % 4) + row % 16 holding block
+ * b of row `row`.  A tile is 64 * bb bytes: bb / 16 planes of 64 x 16 bytes
+ * (plane i: bytes [16 i, 16 i + 16) of every lane's block, lane-major), then
+ * a plane of 64 x (bb % 16) bytes with the rest.  Blocks past nb and rows
+ * past `rows` in a tile are zero.  So a wave reads a tile with 16-byte loads
+ * that each cover 1 KB of contiguous memory. */
+size_t qk_frag_bytes(int rows, int nb, int block_bytes);
+/* byte j of block b of row `row` in fragment order */
+size_t qk_frag_offset(size_t row, int b, int j, int nq, int block_bytes);
+/* 1 when the matrix-core GEMV covers tensors of this format (QK_FMT_*),
+ * block size and column count, so that they are uploaded in fragment order */
+int qk_mfma_layout(int fmt, int bs, int cols);
 
 /* Per-call prepared activation: block-fixed-point digits of x. */
 size_t qk_xprep_bytes(int fmt, int bs, int cols);
@@ -91,6 +109,22 @@ int qk_gemv_group_norm(const qsf_hip_tensor* const* t, int n, const qk_norm_args
                        const float* d_x, float* const* d_y, hipStream_t s);
 int qk_gemv_pair_act_norm(const qsf_hip_tensor* t, const qk_norm_args* nm, const float* d_x,
                           float* d_y, int act, hipStream_t s);
+/* One-launch decode GEMV on the int8 matrix cores (gemv_mfma.hip) over n
+ * tensors in fragment order sharing fp32 x in HBM: the path qk_gemv_group
+ * takes for them in every mode (a prepared x is not used).  A group's
+ * matrices must all have outlier tables or none.  act1: paired rows
+ * (qk_gemv_pair_act); nm: the fused residual + norm (qk_gemv_group_norm), or
+ * NULL.  Returns -2 when the call is not covered.  A row's arithmetic
+ * depends on its matrix's shape and its outlier entries only, never on the
+ * group or the grid. */
+int qk_gemv_mfma(const qsf_hip_tensor* const* t, int n, const float* d_x, float* const* d_y,
+                 int act1, const qk_norm_args* nm, hipStream_t s);
+/* Engine for tensors uploaded from now on: 1 (default) the matrix-core GEMV
+ * and fragment order for the 3-bit formats where qk_mfma_layout covers the
+ * shape, 2 the same for every format, 0 the dot-product kernels and on-disk
+ * order for all; < 0 only queries.  Returns the previous setting. */
+int qk_gemv_mfma_enable(int on);
+
 /* What fixes a row's arithmetic in qk_gemv_group(t, n, ..., mode): the
  * kernel instantiation, row-group width, tile rows and chunk.  A tensor's
  * rows come out bit-identical in two launches whose signatures are equal

@@ -318,6 +318,34 @@ static void reg_drop(const void* key) {
 
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
+/* Fragment order (qsf_hip_internal.h): 16-row x 4-block tiles of 64 blocks,
+ * each block's bytes spread over 16-byte planes and a tail plane. */
+size_t qk_frag_bytes(int rows, int nb, int block_bytes) {
+    return (size_t)((rows + 15) / 16) * (size_t)((nb + 3) / 4) * 64 * (size_t)block_bytes;
+}
+
+size_t qk_frag_offset(size_t row, int b, int j, int nq, int block_bytes) {
+    const size_t tile = (row >> 4) * (size_t)nq + (size_t)(b >> 2);
+    const size_t lane = (size_t)((b & 3) * 16) + (row & 15);
+    const int k = block_bytes >> 4;
+    const size_t base = tile * 64 * (size_t)block_bytes;
+    return j < 16 * k ? base + (size_t)(j >> 4) * 1024 + lane * 16 + (size_t)(j & 15)
+                      : base + (size_t)k * 1024 + lane * (size_t)(block_bytes & 15) + (size_t)(j - 16 * k);
+}
+
+/* The on-disk blocks [rows][nb][bb] into fragment order (dst zeroed). */
+static void frag_permute(uint8_t* dst, const uint8_t* src, int rows, int nb, int bb) {
+    const int nq = (nb + 3) / 4, k = bb / 16, tb = bb % 16;
+    for (int r = 0; r < rows; r++)
+        for (int b = 0; b < nb; b++) {
+            const uint8_t* s = src + ((size_t)r * nb + b) * bb;
+            uint8_t* tile = dst + (((size_t)(r >> 4) * nq + (size_t)(b >> 2)) * 64) * bb;
+            const size_t lane = (size_t)((b & 3) * 16 + (r & 15));
+            for (int i = 0; i < k; i++) memcpy(tile + (size_t)i * 1024 + lane * 16, s + 16 * i, 16);
+            if (tb) memcpy(tile + (size_t)k * 1024 + lane * tb, s + 16 * k, (size_t)tb);
+        }
+}
+
 static qsf_hip_tensor* upload_locked(const void* host, int qt, int rows, int cols, int bs) {
     if (init_locked(g_dev.ready ? g_dev.device : 0) != E_OK) return NULL;
     if (!host || rows < 0 || cols < 0) {
@@ -353,6 +381,15 @@ static qsf_hip_tensor* upload_locked(const void* host, int qt, int rows, int col
         }
     }
     t->n_outliers = n_out;
+    /* device order of the blocks: fragment order where the matrix-core GEMV
+     * is the engine for the format and covers the shape, else the on-disk
+     * order.  Engine 1 takes it for the 3-bit formats, whose unpack is the
+     * costliest on the vector units; 2 for every format. */
+    const int engine = qk_gemv_mfma_enable(-1);
+    t->frag = fmt >= 0 && rows > 0 && (engine == 2 || (engine == 1 && fmt == QK_FMT_3)) &&
+              qk_mfma_layout(fmt, bs, cols);
+    t->frag_nq = (t->nb + 3) / 4;
+    const size_t dev_blocks_bytes = t->frag ? qk_frag_bytes(rows, t->nb, t->block_bytes) : blocks_bytes;
 
     /* CSR of the outlier table: stable counting sort by row keeps file order
      * within a row; entries with row >= rows are dropped (src/quant.c:432-434). */
@@ -405,7 +442,7 @@ static qsf_hip_tensor* upload_locked(const void* host, int qt, int rows, int col
 
     /* one allocation: [blocks][scales][row_ptr][ocol][oval], 256-B aligned parts */
     size_t off_blocks = 0;
-    size_t off_scales = align256(blocks_bytes);
+    size_t off_scales = align256(dev_blocks_bytes);
     size_t off_rp = off_scales + align256(scales_bytes);
     size_t rp_bytes = row_ptr ? ((size_t)rows + 1) * 4 : 0;
     size_t off_oc = off_rp + align256(rp_bytes);
@@ -424,7 +461,20 @@ static qsf_hip_tensor* upload_locked(const void* host, int qt, int rows, int col
     uint8_t* base = (uint8_t*)t->d_alloc;
     t->d_blocks = base + off_blocks;
     const uint8_t* host_blocks = is_outlier(qt) ? p + 4 + 6 * (size_t)n_out : p;
-    he = hipMemcpy(t->d_blocks, host_blocks, blocks_bytes, hipMemcpyHostToDevice);
+    if (t->frag) {
+        uint8_t* fb = calloc(dev_blocks_bytes ? dev_blocks_bytes : 1, 1);
+        if (!fb) {
+            hipFree(t->d_alloc);
+            free(row_ptr); free(ocol); free(oval); free(t);
+            fail(E_OOM, "qsf_hip: fragment-order staging (%zu bytes)", dev_blocks_bytes);
+            return NULL;
+        }
+        frag_permute(fb, host_blocks, rows, t->nb, t->block_bytes);
+        he = hipMemcpy(t->d_blocks, fb, dev_blocks_bytes, hipMemcpyHostToDevice);
+        free(fb);
+    } else {
+        he = hipMemcpy(t->d_blocks, host_blocks, blocks_bytes, hipMemcpyHostToDevice);
+    }
     if (he == hipSuccess && scales_bytes) {
         t->d_scales = base + off_scales;
         he = hipMemcpy(t->d_scales, p + blocks_bytes, scales_bytes, hipMemcpyHostToDevice);
@@ -1156,6 +1206,10 @@ static int ahead_plan(const qsf_hip_tensor* t, const void* w, const qsf_hip_tens
         if (ok) break;
     }
     return n;
+}
+
+int qsf_hip_gemv_engine(int engine) {
+    return qk_gemv_mfma_enable(engine);
 }
 
 int qsf_hip_slot_lookahead(int n) {

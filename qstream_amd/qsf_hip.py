@@ -33,7 +33,7 @@ EXPORTS = (
     "qsf_hip_matvec_dev", "qsf_hip_matvec_group_dev", "qsf_hip_xprep_bytes",
     "qsf_hip_xprep_dev", "qsf_hip_matvec_group_prepared_dev",
     "qsf_hip_moe_create", "qsf_hip_moe_free", "qsf_hip_moe_forward_dev",
-    "qsf_hip_unpack_dev", "qsf_hip_kernel_timing", "qsf_hip_kernel_timing_read",
+    "qsf_hip_unpack_dev", "qsf_hip_kernel_timing", "qsf_hip_kernel_timing_read", "qsf_hip_gemv_engine",
     "qsf_hip_prefill_4bit_dev", "qsf_hip_prefill_4bit_dev_noalloc",
     "qsf_hip_rms_norm_dev", "qsf_hip_layer_norm_dev", "qsf_hip_rope_create", "qsf_hip_rope_free",
     "qsf_hip_rope_dev", "qsf_hip_kv_store_dev", "qsf_hip_attention_dev", "qsf_hip_act_mul_dev",
@@ -157,8 +157,18 @@ def load(path: str = LIB_PATH) -> C.CDLL:
     L.qsf_hip_kernel_timing.restype = _i
     L.qsf_hip_kernel_timing_read.argtypes = [C.POINTER(C.c_float), _i]
     L.qsf_hip_kernel_timing_read.restype = _i
+    L.qsf_hip_gemv_engine.argtypes = [_i]
+    L.qsf_hip_gemv_engine.restype = _i
     _lib = L
     return L
+
+
+def gemv_engine(engine: int = -1) -> int:
+    """Decode GEMV engine for tensors uploaded from now on: 1 (default) the
+    int8 matrix-core kernel for 3-bit tensors, 2 for every format it covers,
+    0 the dot-product kernels for all; < 0 queries.  Returns the previous
+    setting."""
+    return int(load().qsf_hip_gemv_engine(engine))
 
 
 def kernel_timing(enable: bool) -> None:
@@ -220,6 +230,12 @@ def arena_forget_range(buf) -> int:
     """Forget every registered pointer inside a host buffer; returns how many."""
     a = buf if isinstance(buf, np.ndarray) else np.frombuffer(buf, np.uint8)
     return load().qsf_hip_arena_forget_range(a.ctypes.data, a.nbytes)
+
+
+def arena_forget_all() -> int:
+    """Forget every registered host pointer (the table slots upload their
+    payloads afresh); returns how many."""
+    return load().qsf_hip_arena_forget_range(None, C.c_size_t(-1).value)
 
 
 def slot_lookahead(n: int = -1) -> int:

@@ -46,3 +46,24 @@ def device_floats(ptr: int, n: int) -> np.ndarray:
     assert rt.hipMemcpy(out.ctypes.data, ptr, 4 * n, 2) == 0       # 2 = device to host
     return out
 
+
+
+# Decode GEMV engines a parity module runs under (the setting applies to the
+# tensors uploaded while it holds): 0 the dot-product kernels for every
+# format, 2 the int8 matrix-core kernel wherever it covers the shape.  The
+# default, 1, is the matrix-core kernel for the 3-bit formats and the
+# dot-product kernels for the rest: the two together cover it.
+ENGINES = [0, 2]
+
+
+def engine_hip(request):
+    """Body of a module-scoped `hip` fixture parametrized over ENGINES.  The
+    table slots' registered payloads are dropped on entry and exit, so that
+    no slot serves a tensor uploaded under another engine."""
+    from qstream_amd import qsf_hip
+    qsf_hip.init(0)
+    qsf_hip.arena_forget_all()
+    old = qsf_hip.gemv_engine(request.param)
+    yield qsf_hip
+    qsf_hip.arena_forget_all()
+    qsf_hip.gemv_engine(old)

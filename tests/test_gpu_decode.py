@@ -12,7 +12,7 @@ import numpy as np
 import pytest
 
 from qstream_amd import qsf_format as F
-from tests.gpu_util import REL_L2, dev, host, rel_l2, torch_cuda
+from tests.gpu_util import ENGINES, REL_L2, dev, engine_hip, host, rel_l2, torch_cuda
 
 pytestmark = pytest.mark.gpu
 
@@ -20,11 +20,9 @@ DENSE = [F.Q2, F.Q3, F.Q4, F.Q4SYM]
 ALL = DENSE + [F.Q2_OUTLIER, F.Q4_OUTLIER]
 
 
-@pytest.fixture(scope="module")
-def hip():
-    from qstream_amd import qsf_hip
-    qsf_hip.init(0)
-    return qsf_hip
+@pytest.fixture(scope="module", params=ENGINES, ids=lambda e: f"engine{e}")
+def hip(request):
+    yield from engine_hip(request)
 
 
 def _stream():
@@ -390,6 +388,10 @@ def test_slot_reused_buffer_forget_and_volatile(hip, oracle, qt):
     x = F.gaussian(rng, cols)
     slot = _slot(hip, qt)
     buf = a.copy()
+    # a fresh buffer: entries that earlier, freed arrays left at these
+    # addresses (this test under another engine wrote the same bytes there)
+    # are the caller's to drop
+    hip.arena_forget_range(buf)
     out = np.full(rows, np.nan, np.float32)
 
     def run_and_check(content):
@@ -416,6 +418,7 @@ def test_slot_reused_buffer_forget_and_volatile(hip, oracle, qt):
     # >= 1: keys that earlier, freed arrays left inside this address range go too
     assert hip.arena_forget_range(buf) >= 1 and hip.arena_forget_range(buf) == 0
     run_and_check(b)
+    hip.arena_forget_range(buf)                  # before the buffer is freed
 
 
 def test_slot_x_reuse_between_calls(hip, oracle):

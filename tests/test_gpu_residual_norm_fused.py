@@ -17,18 +17,16 @@ import numpy as np
 import pytest
 
 from qstream_amd import qsf_format as F
-from tests.gpu_util import REL_L2, dev, host, rel_l2, torch_cuda
+from tests.gpu_util import ENGINES, REL_L2, dev, engine_hip, host, rel_l2, torch_cuda
 
 pytestmark = pytest.mark.gpu
 
 EPS = 1e-5
 
 
-@pytest.fixture(scope="module")
-def hip():
-    from qstream_amd import qsf_hip
-    qsf_hip.init(0)
-    return qsf_hip
+@pytest.fixture(scope="module", params=ENGINES, ids=lambda e: f"engine{e}")
+def hip(request):
+    yield from engine_hip(request)
 
 
 def _vectors(rng, cols, poison):

@@ -18,18 +18,17 @@ import numpy as np
 import pytest
 
 from qstream_amd import qsf_format as F
-from tests.gpu_util import REL_L2, rel_l2
+from tests.gpu_util import ENGINES, REL_L2, engine_hip, rel_l2
 
 pytestmark = pytest.mark.gpu
 
 
-@pytest.fixture(scope="module")
-def hip():
-    from qstream_amd import qsf_hip
-    qsf_hip.init(0)
-    old = qsf_hip.slot_lookahead(-1)
-    yield qsf_hip
-    qsf_hip.slot_lookahead(old)
+@pytest.fixture(scope="module", params=ENGINES, ids=lambda e: f"engine{e}")
+def hip(request):
+    for h in engine_hip(request):
+        old = h.slot_lookahead(-1)
+        yield h
+        h.slot_lookahead(old)
 
 
 def _slot(hip, qt):
