@@ -362,7 +362,10 @@ int qsf_hip_rope_kv_store_dev(const qsf_hip_rope* r, float* d_q, float* d_k, con
                               float* d_ks, float* d_vs, int max_seq, void* stream);
 /* Embedding lookup, src/engine.c:709-765: row `token` of a blockwise table
  * uploaded with qsf_hip_tensor_upload (rows = vocab, cols = hidden),
- * dequantised bit-exactly; or of an FP16 table [vocab][hd] in device memory. */
+ * dequantised bit-exactly; or of an FP16 table [vocab][hd] in device memory.
+ * Blockwise types 0, 2, 3 and 4 only, the ones the engine's lookup reads
+ * (its row size, qsf_quant_block_size, is 0 for the outlier and MXFP4 types,
+ * and type 1 rows are dequantised as 4-bit): others fail with E_INVALID. */
 int qsf_hip_embed_row_dev(const qsf_hip_tensor* table, int token, float* d_out, void* stream);
 int qsf_hip_embed_row_fp16_dev(const uint16_t* d_table, int hd, int token, float* d_out,
                                void* stream);

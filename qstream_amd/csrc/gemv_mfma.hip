@@ -218,7 +218,6 @@ __global__ __launch_bounds__(NT) void gemv_mfma_kernel(MfArgs a) {
     const int rows = M.rows, nb = a.nb, nq = a.nq;
     const uint8_t* __restrict__ W = M.w;
     const int row_a = rg0 * 16, row_b = min(row_a + nrg * 16, rows);
-    const int nbp = 4 * nq;                                   // blocks incl. quad padding
 
     // this wave's tiles: the workgroup's T = nrg * nq tiles in quad-major
     // order (u -> quad u / nrg, group u % nrg), contiguous runs a wave
@@ -626,7 +625,7 @@ template <int FMT, int BS>
 int launch_mf(const qsf_hip_tensor* const* t, int n, int cols, const float* d_x, float* const* d_y,
               int act1, const qk_norm_args* nm, hipStream_t s) {
     using F = MF<FMT, BS>;
-    const int nb = (cols + BS - 1) / BS, nq = (nb + 3) / 4, nbp = 4 * nq;
+    const int nb = (cols + BS - 1) / BS, nq = (nb + 3) / 4;
     if (!covers_mf<FMT, BS>(cols)) return -2;
     MfArgs a{};
     a.x = d_x;

@@ -1005,8 +1005,15 @@ int qsf_hip_rope_kv_store_dev(const qsf_hip_rope* r, float* d_q, float* d_k, con
 }
 
 int qsf_hip_embed_row_dev(const qsf_hip_tensor* t, int token, float* d_out, void* stream) {
-    if (!t || !d_out || t->fmt < 0 || token < 0 || token >= t->rows)
+    if (!t || !d_out || token < 0 || token >= t->rows)
         return fail(E_INVALID, "qsf_hip_embed_row_dev: bad arguments (token %d)", token);
+    /* the engine's lookup reads rows of qsf_quant_block_size(type) blocks
+     * and dequantises types 0, 2, 3 and 4 (src/engine.c:718-753,
+     * src/quant.c:68-85); for every other blockwise type its row size is 0
+     * or its dequantiser reads 4-bit blocks over 2-bit ones */
+    if (t->qt != QK_Q2 && t->qt != QK_Q3 && t->qt != QK_Q4 && t->qt != QK_Q4SYM)
+        return fail(E_INVALID, "qsf_hip_embed_row_dev: quant type %d has no embedding lookup in the "
+                               "engine (types 0, 2, 3, 4; FP16 tables take qsf_hip_embed_row_fp16_dev)", t->qt);
     return glue_rc("qsf_hip_embed_row_dev", qk_embed_row(t, token, d_out, pick_stream(stream)));
 }
 

@@ -22,6 +22,7 @@
 
 #include <fcntl.h>
 #include <pthread.h>
+#include <stdint.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
@@ -78,16 +79,25 @@ static size_t block_bytes_of(int qt, int bs) {
     }
 }
 
+/* a * b * c, or 0 when it does not fit a size_t */
+static size_t mul3(size_t a, size_t b, size_t c) {
+    size_t ab, abc;
+    if (__builtin_mul_overflow(a, b, &ab) || __builtin_mul_overflow(ab, c, &abc)) return 0;
+    return abc;
+}
+
+/* Bytes the upload of a [rows][cols] matrix of type qt reads from `data`
+ * (avail bytes there): MXFP4 records, or the dense blocks behind the
+ * outlier table of types 9 and 10.  0 when it cannot be sized. */
 static size_t matrix_bytes(int qt, const uint8_t* data, size_t avail, uint32_t rows, uint32_t cols,
                            int bs) {
-    if (qt == QSF_HIP_QUANT_MXFP4) {
-        size_t nb = (cols + 31) / 32;
-        return (size_t)rows * nb * 17;
-    }
-    size_t dense = (size_t)rows * ((cols + (uint32_t)bs - 1) / (uint32_t)bs) * block_bytes_of(qt, bs);
+    if (qt == QSF_HIP_QUANT_MXFP4) return mul3(rows, ((size_t)cols + 31) / 32, 17);
+    const size_t dense = mul3(rows, ((size_t)cols + (uint32_t)bs - 1) / (uint32_t)bs, block_bytes_of(qt, bs));
+    if (dense == 0 && rows > 0 && cols > 0) return 0;
     if (qt == 9 || qt == 10) {
         if (avail < 4) return 0;
-        return 4 + 6 * (size_t)le32(data) + dense;
+        const size_t table = 4 + 6 * (size_t)le32(data);
+        return dense > SIZE_MAX - table ? 0 : table + dense;
     }
     return dense;
 }
@@ -310,6 +320,7 @@ static int load_mapped(qsf_hip_model* m, const uint8_t* f, size_t fsize) {
     /* embedding section (types.h:276-286; engine.c:709-765) */
     const uint8_t* emb = NULL;
     uint32_t emb_qt = 0;
+    size_t emb_row_bytes = 0;
     uint64_t eo = le64(f + 72);
     if (eo) {
         if (eo > fsize || fsize - eo < 32)
@@ -323,10 +334,18 @@ static int load_mapped(qsf_hip_model* m, const uint8_t* f, size_t fsize) {
             return qsf_host_fail(E_INVALID_MODEL, "qsf_hip_model_load: embedding %ux%u, model %ux%u", nvec,
                                  dim, in->vocab_size, in->hidden_dim);
         uint64_t dofs = eo + 32 + (nchunks > 1 ? 8ull * nchunks : 0);
-        size_t esize = emb_qt == 7 ? (size_t)nvec * dim * 2
-                                   : (size_t)nvec * ((dim + (uint32_t)bs - 1) / (uint32_t)bs) *
-                                         block_bytes_of((int)emb_qt, bs);
-        if (dofs > fsize || esize > fsize - dofs)
+        if (dofs > fsize)
+            return qsf_host_fail(E_CORRUPTED, "qsf_hip_model_load: embedding data past the end");
+        /* the span the upload reads: FP16 rows at the engine's stride of
+         * ceil(dim / bs) blocks of 2 * bs bytes (engine.c:718-721 with
+         * quant.c:82), else the table as a matrix of its type (outlier
+         * table and MXFP4 records included) */
+        if (emb_qt == 7) emb_row_bytes = (((size_t)dim + (uint32_t)bs - 1) / (uint32_t)bs) * (uint32_t)bs * 2;
+        size_t esize = emb_qt == 7 ? mul3(nvec, emb_row_bytes, 1)
+                                   : matrix_bytes((int)emb_qt, f + dofs, fsize - dofs, nvec, dim, bs);
+        if (esize == 0 && nvec > 0 && dim > 0)
+            return qsf_host_fail(E_CORRUPTED, "qsf_hip_model_load: embedding size cannot be computed");
+        if (esize > fsize - dofs)
             return qsf_host_fail(E_CORRUPTED, "qsf_hip_model_load: embedding data past the end");
         emb = f + dofs;
         uint32_t got = qsf_hip_crc32(emb, esize);
@@ -435,8 +454,19 @@ static int load_mapped(qsf_hip_model* m, const uint8_t* f, size_t fsize) {
     }
     if (emb) {
         if (emb_qt == 7) {
-            size_t nb = (size_t)in->vocab_size * hd * 2;
-            m->d_embedding_fp16 = (uint16_t*)qsf_host_device_bytes(emb, nb);
+            /* [vocab][hd] on the device: rows padded to whole blocks in the
+             * file are packed (sizes checked above) */
+            const size_t nb = (size_t)in->vocab_size * hd * 2;
+            if (emb_row_bytes == (size_t)hd * 2) {
+                m->d_embedding_fp16 = (uint16_t*)qsf_host_device_bytes(emb, nb);
+            } else {
+                uint8_t* packed = malloc(nb ? nb : 1);
+                if (!packed) return qsf_host_fail(E_OOM, "qsf_hip_model_load: FP16 embedding staging");
+                for (size_t r = 0; r < in->vocab_size; r++)
+                    memcpy(packed + r * hd * 2, emb + r * emb_row_bytes, (size_t)hd * 2);
+                m->d_embedding_fp16 = (uint16_t*)qsf_host_device_bytes(packed, nb);
+                free(packed);
+            }
             if (!m->d_embedding_fp16) return upload_failed();
             in->device_bytes += nb;
         } else {

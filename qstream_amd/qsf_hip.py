@@ -541,6 +541,10 @@ class Model:
         h = load().qsf_hip_model_embedding(self.handle)
         return _Ref(h) if h else None
 
+    def embedding_fp16(self) -> int | None:
+        """Device address of an FP16 embedding table [vocab][hidden], or None."""
+        return load().qsf_hip_model_embedding_fp16(self.handle) or None
+
     def output_head(self):
         h = load().qsf_hip_model_output_head(self.handle)
         return _Ref(h) if h else None

@@ -113,3 +113,60 @@ def test_crc_mismatch_warns_and_loads_the_bytes(hip, oracle, tmp_path):
     assert m.info.crc_mismatches == 2            # the header (no CRC written) and layer 1
     check_model(hip, oracle, m, kw)
     m.free()
+
+
+def test_fp16_embedding_rows_at_the_engine_stride(hip, tmp_path):
+    """An FP16 table whose width is not a whole number of blocks: the
+    engine reads token t at t * ceil(hd / bs) * bs * 2 bytes and converts hd
+    values (src/engine.c:718-737, src/quant.c:82), so the file's rows are
+    padded to whole blocks and the device table holds the first hd of
+    each."""
+    torch = torch_cuda()
+    rng = np.random.default_rng(13)
+    kw = build(rng, True)
+    hidden, vocab, bs = 96, 260, 64
+    q4 = lambda r, c: F.quantize_matrix(F.gaussian(rng, (r, c), 0.02), F.Q4, bs)  # noqa: E731
+    kw.update(hidden=hidden, vocab=vocab, inter=128, heads=4, kv_heads=2, output_head=q4(vocab, hidden),
+              tied=False, final_norm=F.gaussian(rng, hidden).astype(np.float16),
+              layers=[[(F.T_ATTN_Q, F.Q4, hidden, hidden, q4(hidden, hidden))]])
+    padded = F.gaussian(rng, (vocab, 128)).astype(np.float16)
+    kw["embedding"] = (F.FP16, padded.tobytes())
+    path = tmp_path / "f16.qsf"
+    F.write_qsf(str(path), **kw)
+    m = hip.Model(str(path))
+    assert m.info.crc_mismatches == 0
+    table = m.embedding_fp16()
+    out = torch.empty(hidden, device="cuda:0")
+    for token in (0, 1, vocab - 1):
+        hip.embed_row_fp16(table, hidden, token, out, stream=torch.cuda.current_stream())
+        assert np.array_equal(host(out), padded[token, :hidden].astype(np.float32))
+    m.free()
+
+
+def test_outlier_embedding_tied_head(hip, oracle, tmp_path):
+    """A 2-bit + outlier model with a tied head, as the converter writes it
+    (the embedding in the model's type, outlier table first,
+    tools/convert_hf.py:206-208): its checked span is the whole table (no
+    CRC warning), the tied logits are the outlier matvec over it
+    (src/engine.c:1200-1226), and the row lookup, which the engine sizes as
+    0 bytes for this type (src/engine.c:718-721), is refused."""
+    torch = torch_cuda()
+    rng = np.random.default_rng(17)
+    kw = build(rng, True)
+    hidden, vocab, bs = kw["hidden"], kw["vocab"], kw["block_size"]
+    epay = F.quantize_matrix(F.heavy_tail_weights(rng, vocab, hidden), F.Q2_OUTLIER, bs)
+    for recs in kw["layers"]:                    # the layer default is now type 9
+        recs[:] = [r for r in recs if r[1] != 0xFF]
+    kw.update(quant_type=F.Q2_OUTLIER, embedding=(F.Q2_OUTLIER, epay))
+    path = tmp_path / "t9.qsf"
+    F.write_qsf(str(path), **kw)
+    m = hip.Model(str(path))
+    assert m.info.crc_mismatches == 0 and m.info.size_mismatch == 0
+    x = F.gaussian(rng, hidden)
+    y = torch.full((vocab,), float("nan"), device="cuda:0")
+    m.output_head().matvec(dev(x), y, stream=torch.cuda.current_stream())
+    assert rel_l2(host(y), oracle.matvec(F.Q2_OUTLIER, epay, x, vocab, hidden, bs)) <= REL_L2
+    out = torch.empty(hidden, device="cuda:0")
+    with pytest.raises(hip.QsfHipError, match="no embedding lookup"):
+        hip.embed_row(m.embedding(), 0, out, stream=torch.cuda.current_stream())
+    m.free()

@@ -35,13 +35,21 @@ def _vectors(rng, cols, poison):
     if poison == "nan":
         x[cols // 3] = np.nan
     elif poison == "big":
-        x[7] = 3e30
+        x[7] = 3e30                       # finite, past the 1e30 check
+    elif poison == "res_nan":
+        res[cols // 2] = np.nan           # in the residual, not the increment
     w = (1 + 0.1 * rng.standard_normal(cols)).astype(np.float32)
     return res, x, w
 
 
 def _bits(a):
     return host(a).view(np.uint32)
+
+
+def _bad_index(poison, cols):
+    """First element the residual check flags (src/engine.c:1174-1187): -1,
+    or the poisoned one."""
+    return {None: -1, "nan": cols // 3, "big": 7, "res_nan": cols // 2}[poison]
 
 
 # (qt, bs, [rows...], cols): q/k/v-like groups and single matrices, split
@@ -56,7 +64,7 @@ GROUPS = [
 ]
 
 
-@pytest.mark.parametrize("poison", [None, "nan"])
+@pytest.mark.parametrize("poison", [None, "nan", "big", "res_nan"])
 @pytest.mark.parametrize("shape", GROUPS, ids=lambda s: f"qt{s[0]}_bs{s[1]}_{'-'.join(map(str, s[2]))}x{s[3]}")
 def test_fused_group_equals_separate(hip, oracle, shape, poison):
     qt, bs, rows_list, cols = shape
@@ -82,8 +90,8 @@ def test_fused_group_equals_separate(hip, oracle, shape, poison):
         y2 = [torch.full((r,), float("nan"), device="cuda:0") for r in rows_list]
         hip.residual_norm_matvec_group(ts, r_in, r2, dev(x), dev(w), EPS, y2, bad=bad2)
         assert np.array_equal(_bits(r1), _bits(r2))
-        assert np.array_equal(host(r_in), res)                    # the input residual is untouched
-        assert int(host(bad1)[0]) == int(host(bad2)[0]) == {None: -1, "nan": cols // 3}[poison]
+        assert np.array_equal(_bits(r_in), res.view(np.uint32))   # the input residual is untouched
+        assert int(host(bad1)[0]) == int(host(bad2)[0]) == _bad_index(poison, cols)
         for a, b in zip(y1, y2):
             assert np.array_equal(_bits(a), _bits(b))
         if poison is None:
@@ -97,22 +105,24 @@ def test_fused_group_equals_separate(hip, oracle, shape, poison):
             t.free()
 
 
+@pytest.mark.parametrize("poison", [None, "nan", "big", "res_nan"])
 @pytest.mark.parametrize("shape", [(F.Q3, 128, 11008, 4096), (F.Q4, 64, 300, 1000), (F.Q2, 256, 64, 2048)],
                          ids=lambda s: f"qt{s[0]}_bs{s[1]}_{s[2]}x{s[3]}")
-def test_fused_gate_up_act_equals_separate(hip, oracle, shape):
+def test_fused_gate_up_act_equals_separate(hip, oracle, shape, poison):
     qt, bs, rows, cols = shape
     torch = torch_cuda()
     rng = np.random.default_rng(rows)
     pg = np.frombuffer(F.quantize_matrix(F.gaussian(rng, (rows, cols), 0.02), qt, bs), np.uint8).copy()
     pu = np.frombuffer(F.quantize_matrix(F.gaussian(rng, (rows, cols), 0.02), qt, bs), np.uint8).copy()
     pair = hip.TensorPair(pg, pu, qt, rows, cols, bs)
-    res, x, w = _vectors(rng, cols, None)
+    res, x, w = _vectors(rng, cols, poison)
     try:
         for act in (0, 2):
-            print(f"fused gate/up qt {qt} bs {bs} {rows}x{cols} act {act}", flush=True)
+            print(f"fused gate/up qt {qt} bs {bs} {rows}x{cols} act {act} poison {poison}", flush=True)
             r1 = dev(res)
             n1 = torch.empty(cols, device="cuda:0")
-            hip.residual_norm(r1, dev(x), dev(w), EPS, n1)
+            bad1 = torch.full((1,), 7, dtype=torch.int32, device="cuda:0")
+            hip.residual_norm(r1, dev(x), dev(w), EPS, n1, bad=bad1)
             o1 = torch.full((rows,), float("nan"), device="cuda:0")
             pair.gate_up_act(n1, o1, act)
             r2 = torch.full((cols,), float("nan"), device="cuda:0")
@@ -121,7 +131,9 @@ def test_fused_gate_up_act_equals_separate(hip, oracle, shape):
             pair.residual_norm_gate_up_act(dev(res), r2, dev(x), dev(w), EPS, o2, act, bad=bad)
             assert np.array_equal(_bits(r1), _bits(r2))
             assert np.array_equal(_bits(o1), _bits(o2))
-            assert int(host(bad)[0]) == -1
+            assert int(host(bad)[0]) == int(host(bad1)[0]) == _bad_index(poison, cols)
+            if poison is not None:
+                continue
             nv = oracle.rms_norm((res + x).astype(np.float32), w, EPS)
             g = oracle.matvec(qt, pg.tobytes(), nv, rows, cols, bs)
             u = oracle.matvec(qt, pu.tobytes(), nv, rows, cols, bs)

@@ -87,3 +87,40 @@ def test_rejects_malformed_files(hip, tmp_path):
         mutate(str(p))
         expect(hip, p, code, words)
     expect(hip, tmp_path / "missing.qsf", 1, ["cannot open"])
+
+
+def test_embedding_span_is_what_the_upload_reads(hip, tmp_path):
+    """The embedding is sized as its upload reads it, before any device
+    work: the outlier table of a type-9 table (its count from the file),
+    17-byte MXFP4 records at any block size, FP16 rows at the engine's
+    stride of whole blocks (src/engine.c:718-721, src/quant.c:68-85).  A
+    file shorter than that span is rejected, never read past its end."""
+    rng = np.random.default_rng(3)
+    hidden, vocab = 256, 300
+    # type 9, the embedding last in the file, its outlier count past the end
+    kw = small_model(rng, hidden=hidden, vocab=vocab)
+    kw.update(final_norm=None, output_head=None,
+              embedding=(F.Q2_OUTLIER, F.quantize_matrix(F.heavy_tail_weights(rng, vocab, hidden), F.Q2_OUTLIER, 64)))
+    p = tmp_path / "emb9.qsf"
+    offs = F.write_qsf(str(p), **kw)
+    n_out = struct.unpack_from("<I", p.read_bytes(), offs["embedding"] + 32)[0]
+    assert n_out > 0
+    patch(str(p), offs["embedding"] + 32, "<I", 0xFFFFFFFF)
+    expect(hip, p, 2, ["embedding data past the end"])
+    # one outlier more than the file holds
+    patch(str(p), offs["embedding"] + 32, "<I", n_out + 1)
+    expect(hip, p, 2, ["embedding data past the end"])
+    # type 11 at block 256: 132-byte blocks written where 17-byte records of 32 are read
+    kw = small_model(rng, hidden=hidden, vocab=vocab, bs=256)
+    kw.update(final_norm=None, output_head=None,
+              embedding=(F.MXFP4, rng.integers(0, 256, vocab * 132, dtype=np.uint8).tobytes()))
+    p = tmp_path / "emb11.qsf"
+    F.write_qsf(str(p), **kw)
+    expect(hip, p, 2, ["embedding data past the end"])
+    # FP16 rows of 96 values with block 64: the engine reads rows of 128
+    kw = small_model(rng, hidden=96, vocab=vocab)
+    kw.update(final_norm=None, output_head=None,
+              embedding=(F.FP16, F.gaussian(rng, (vocab, 96)).astype(np.float16).tobytes()))
+    p = tmp_path / "emb7.qsf"
+    F.write_qsf(str(p), **kw)
+    expect(hip, p, 2, ["embedding data past the end"])
