@@ -303,3 +303,49 @@ def ref_strict() -> RefLib | None:
 
 def ref_avx2() -> RefLib | None:
     return RefLib(REF_AVX2_SO) if os.path.exists(REF_AVX2_SO) else None
+
+
+REF_CONTAINER_SO = os.path.join(HERE, "_ref", "libqsf_ref_container.so")
+
+
+class _RefSummary(C.Structure):
+    _fields_ = [("rc", C.c_int32), ("head_dim", C.c_uint32), ("num_kv_heads", C.c_uint32)] + [
+        (n, C.c_int32) for n in ("is_gated_ffn", "uses_rope", "uses_alibi", "has_bias_attn_qkv",
+                                 "has_bias_attn_o", "has_bias_ffn", "has_bias_norm", "weight_tied")] + [
+        ("file_size", C.c_uint64), ("header", C.c_uint8 * 256)]
+
+
+class RefContainer:
+    """QStream's own QSF reader (src/format.c, src/file_access.c, src/error.c
+    compiled into oracle/_ref behind oracle/ref_container.c)."""
+
+    def __init__(self, path: str = REF_CONTAINER_SO):
+        if not os.path.exists(path):
+            raise FileNotFoundError(path)
+        L = self.lib = C.CDLL(path)
+        L.ref_container_load.argtypes = [C.c_char_p, C.POINTER(_RefSummary), _vp, C.c_uint32, _vp]
+        L.ref_container_load.restype = _i
+        L.ref_container_error.restype = C.c_char_p
+        L.ref_layout_count.restype = _i
+        L.ref_layout_name.argtypes = [_i]
+        L.ref_layout_name.restype = C.c_char_p
+        L.ref_layout_value.argtypes = [_i]
+        L.ref_layout_value.restype = C.c_long
+        self.layout = {L.ref_layout_name(i).decode(): L.ref_layout_value(i) for i in range(L.ref_layout_count())}
+
+    def load(self, path: str, max_layers: int = 256) -> dict:
+        """qsf_model_load (+ qsf_decompress_layer of every layer): the QSFError,
+        the header bytes and derived fields as the reference holds them, the
+        layer-index entries and each layer's data offset in the file."""
+        s = _RefSummary()
+        li = np.zeros(max_layers * self.layout["QSFLayerIndex"], np.uint8)
+        offs = np.full(max_layers, -2, np.int64)
+        rc = self.lib.ref_container_load(path.encode(), C.byref(s), _ptr(li), max_layers, _ptr(offs))
+        out = {k: getattr(s, k) for k, _ in _RefSummary._fields_ if k != "header"}
+        out.update(rc=rc, error=self.lib.ref_container_error().decode(errors="replace"),
+                   header=bytes(s.header), layer_index=li.tobytes(), layer_data_off=offs)
+        return out
+
+
+def ref_container() -> RefContainer | None:
+    return RefContainer() if os.path.exists(REF_CONTAINER_SO) else None

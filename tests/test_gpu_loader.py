@@ -170,3 +170,49 @@ def test_outlier_embedding_tied_head(hip, oracle, tmp_path):
     with pytest.raises(hip.QsfHipError, match="no embedding lookup"):
         hip.embed_row(m.embedding(), 0, out, stream=torch.cuda.current_stream())
     m.free()
+
+
+@pytest.mark.parametrize("name", ["dense", "dense_tied", "outlier_tied", "moe"])
+def test_model_info_equals_reference_parse(hip, tmp_path, name):
+    """What this build's loader reports equals what QStream's own reader
+    (src/format.c:99-201, compiled into oracle/_ref) parses from the same
+    file: header fields, its zero defaults resolved (src/format.c:145-162),
+    tensor records per layer and no CRC or size warning in either."""
+    from oracle.oracle import ref_container
+    import struct
+    from tests import container_models as CM
+    rc = ref_container()
+    if rc is None:
+        pytest.skip("oracle/_ref not built")
+    kw = CM.all_models()[name]
+    path = tmp_path / f"{name}.qsf"
+    F.write_qsf(str(path), **kw)
+    ref = rc.load(str(path))
+    assert ref["rc"] == 0
+    L, hb = rc.layout, ref["header"]
+
+    def h(f, t="I"):
+        return struct.unpack_from("<" + t, hb, L[f"QSFHeader.{f}"])[0]
+
+    m = hip.Model(str(path))
+    try:
+        i = m.info
+        assert (i.num_layers, i.hidden_dim, i.num_heads, i.vocab_size, i.max_seq_len, i.intermediate_dim,
+                i.block_size) == (h("num_layers"), h("hidden_dim"), h("num_heads"), h("vocab_size"),
+                                  h("max_seq_len"), h("intermediate_dim"), h("block_size"))
+        assert (i.num_kv_heads, i.head_dim, i.weight_tied) == (ref["num_kv_heads"], ref["head_dim"],
+                                                               ref["weight_tied"])
+        assert (i.quant_type, i.activation, i.norm_type, i.pos_enc_type, i.ffn_type, i.attn_type, i.has_bias) == \
+            (h("quant_type", "B"), h("activation", "B"), h("norm_type", "B"), h("pos_enc_type", "B"),
+             h("ffn_type", "B"), h("attn_type", "B"), h("has_bias", "B"))
+        assert (i.num_experts, i.num_active_experts, i.moe_norm_topk, i.expert_intermediate_dim) == \
+            (h("num_experts", "B"), h("num_active_experts", "B"), h("moe_norm_topk", "B"),
+             h("expert_intermediate_dim"))
+        assert (i.rope_theta, i.norm_epsilon) == (h("rope_theta", "f"), h("norm_epsilon", "f"))
+        n_rec = sum(struct.unpack_from("<H", ref["layer_index"], k * L["QSFLayerIndex"] +
+                                       L["QSFLayerIndex.num_tensors"])[0] for k in range(i.num_layers))
+        assert i.num_tensors == n_rec
+        assert i.crc_mismatches == 0 and i.size_mismatch == 0 and i.has_embedding == 1
+        assert i.moe_layers == (i.num_layers if name == "moe" else 0)
+    finally:
+        m.free()
