@@ -359,6 +359,44 @@ def test_nonfinite_input_gives_nan(hip, qt, bad):
     assert np.all(np.isnan(out)), out
 
 
+@pytest.mark.parametrize("qt", ALL)
+@pytest.mark.parametrize("bs", [64, 128])
+def test_nonfinite_meta_rows(hip, oracle, qt, bs):
+    """Blocks whose fp16 scale or zero is Inf or NaN.  Decided behaviour:
+    exactly the rows the reference makes non-finite are non-finite here,
+    and every other row keeps the 1e-5 bar.  Which of NaN and +-Inf such a
+    row holds can differ: the reference takes Inf * 0 per element
+    ((scale * q + zero) * x, src/kernels_scalar.c:16-109), this path
+    multiplies the block's sums by scale and zero once."""
+    from tests import meta_cases as MC
+    torch = torch_cuda()
+    rows, cols = 40, 1000
+    rng = np.random.default_rng(41 + qt + bs)
+    w = F.heavy_tail_weights(rng, rows, cols) if qt in (F.Q2_OUTLIER, F.Q4_OUTLIER) else \
+        F.gaussian(rng, (rows, cols), 0.02)
+    p = MC.poison(F.quantize_matrix(w, qt, bs), qt, rows, cols, bs)
+    x = F.gaussian(rng, cols)
+    ref = oracle.matvec(qt, p, x, rows, cols, bs)
+    bad = MC.poisoned_rows(qt, rows, cols, bs)
+    assert np.all(~np.isfinite(ref[bad])) and np.all(np.isfinite(ref[~bad]))
+    print(f"nonfinite meta qt {qt} bs {bs}", flush=True)
+    t = hip.Tensor(np.frombuffer(p, np.uint8).copy(), qt, rows, cols, bs)
+    try:
+        y = torch.full((rows,), 0.5, device="cuda:0")
+        t.matvec(dev(x), y, stream=_stream())
+        outs = [host(y)]
+    finally:
+        t.free()
+    slot = np.zeros(rows, np.float32)
+    getattr(hip.KernelTable(), {F.Q2: "matvec_2bit", F.Q3: "matvec_3bit", F.Q4: "matvec_4bit",
+                                 F.Q4SYM: "matvec_4bit_sym", F.Q2_OUTLIER: "matvec_outlier_2bit",
+                                 F.Q4_OUTLIER: "matvec_outlier_4bit"}[qt])(p, x, slot, rows, cols, bs)
+    outs.append(slot)
+    for got in outs:
+        assert np.array_equal(~np.isfinite(got), bad), (got, bad)
+        assert rel_l2(got[~bad], ref[~bad]) <= REL_L2
+
+
 def _unsampled_edit(payload: np.ndarray) -> np.ndarray:
     """A copy of `payload` changed in one byte that none of the slot's nine
     sampled 8-byte words covers (offset n/16, inside the first eighth)."""

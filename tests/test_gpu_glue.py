@@ -83,6 +83,25 @@ def test_kv_store_bit_exact(hip, oracle):
     assert np.array_equal(host(dvs).view(np.uint32), vs.view(np.uint32))
 
 
+def test_kv_store_exact_ties(hip):
+    """Exact .5 ties and the 0.5 - 2^-25 case of the reference's
+    truncating rounding (src/engine.c:265,287), known answers pinned in
+    tests/test_oracle_glue.py, in every head of a 128-wide store."""
+    from tests.test_oracle_glue import KV_TIE_CODES, KV_TIE_ROW
+    torch = torch_cuda()
+    nkv, hd, max_seq, pos = 4, 128, 8, 3
+    k = np.tile(KV_TIE_ROW, nkv * hd // 16).astype(np.float32)
+    dkc = dev(np.zeros((nkv, max_seq, hd), np.int8))
+    dvc = dev(np.zeros((nkv, max_seq, hd), np.int8))
+    dks, dvs = dev(np.zeros((nkv, max_seq), np.float32)), dev(np.zeros((nkv, max_seq), np.float32))
+    hip.kv_store(dkc, dvc, dks, dvs, max_seq, nkv, hd, pos, dev(k), dev(-k), stream=_s())
+    torch.cuda.synchronize()
+    want = np.tile(KV_TIE_CODES, hd // 16)
+    for h in range(nkv):
+        assert np.array_equal(host(dkc)[h, pos], want) and np.array_equal(host(dvc)[h, pos], -want)
+    assert np.all(host(dks)[:, pos] == 1.0) and np.all(host(dvs)[:, pos] == 1.0)
+
+
 # head_dim 64, 128 and 256 take the load-everything-first kernel, others the
 # general one; positions 129 and 300 leave a partial last chunk of 128
 @pytest.mark.parametrize("nh,nkv,hd,position", [(32, 32, 128, 0), (32, 32, 128, 1023),

@@ -29,7 +29,10 @@ def _stream():
 def test_mxfp4_unpack_every_code_and_scale(hip, oracle):
     """All 16 E2M1 codes in both nibble positions x a sweep of E8M0 scales,
     through the table slot with one-hot activations: output row r, input
-    col c gives exactly e2m1(code) * 2^(E-127)."""
+    col c gives exactly e2m1(code) * 2^(E-127).  The ends of the scale
+    range are OCP MX's special cases: E = 0 is 2^-127 (an fp32 subnormal,
+    kept, not flushed) and E = 255 is NaN, which every product carries,
+    code 0 included."""
     rows, cols = 16, 32
     codes = np.zeros((rows, 1, 16), np.uint8)
     for r in range(rows):
@@ -37,7 +40,7 @@ def test_mxfp4_unpack_every_code_and_scale(hip, oracle):
             lo, hi = (r + 2 * j) % 16, (r + 2 * j + 1) % 16
             codes[r, 0, j] = lo | (hi << 4)
     kt = hip.KernelTable()
-    for e in (1, 100, 127, 130, 200, 254):
+    for e in (0, 1, 100, 127, 130, 200, 254, 255):
         scales = np.full((rows, 1), e, np.uint8)
         payload = codes.tobytes() + scales.tobytes()
         got = np.zeros((cols, rows), np.float32)
@@ -48,6 +51,9 @@ def test_mxfp4_unpack_every_code_and_scale(hip, oracle):
         for r in range(rows):
             for c in range(cols):
                 nib = (codes[r, 0, c // 2] >> (4 * (c % 2))) & 15
+                if e == 255:
+                    assert np.isnan(got[c, r]), (e, r, c, got[c, r])
+                    continue
                 want = np.float32(oracle.lib.orc_e2m1_to_fp32(int(nib))) * np.float32(2.0 ** (e - 127))
                 assert got[c, r] == want, (e, r, c, got[c, r], want)
 

@@ -322,3 +322,22 @@ def test_e2m1_encoder_matches_brute_force():
     idx = np.where(even.any(axis=1), even.argmax(axis=1), best.argmax(axis=1)).astype(np.uint8)
     want = idx | ((np.signbit(v) & (idx != 0)).astype(np.uint8) << 3)
     assert np.array_equal(F._e2m1_encode(v), want)
+
+
+def test_nonfinite_meta_matches_compiled_reference(oracle, ref):
+    """Blocks with Inf or NaN fp16 scale or zero: the oracle's rows equal
+    the compiled reference's bit for bit (NaN where Inf * 0 or Inf - Inf
+    occurs, the Inf's sign otherwise), and only the poisoned rows go
+    non-finite."""
+    from tests import meta_cases as MC
+    rng = np.random.default_rng(29)
+    rows, cols = 24, 700
+    for qt in (F.Q2, F.Q3, F.Q4, F.Q4SYM, F.Q2_OUTLIER, F.Q4_OUTLIER):
+        for bs in (64, 128):
+            p = MC.poison(F.quantize_matrix(F.gaussian(rng, (rows, cols), 0.02), qt, bs), qt, rows, cols, bs)
+            x = F.gaussian(rng, cols)
+            a = oracle.matvec(qt, p, x, rows, cols, bs)
+            b = ref.matvec(qt, p, x, rows, cols, bs)
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), (qt, bs)
+            bad = MC.poisoned_rows(qt, rows, cols, bs)
+            assert np.all(~np.isfinite(a[bad])) and np.all(np.isfinite(a[~bad])), (qt, bs)

@@ -134,6 +134,27 @@ def test_kv_store_invariants(oracle):
             assert np.all(np.sign(codes[codes != 0]) == np.sign(row[codes != 0]))
 
 
+# Exact ties of the int8 KV code.  With |max| = 127 the scale 127/amax is
+# exactly 1, so each value reaches the rounding as written.  The reference
+# rounds by truncating v +- 0.5f in fp32 (src/engine.c:265,287): halves go
+# away from zero (2.5 -> 3, where half-to-even gives 2), and 0.5 - 2^-25
+# goes to 1, because v + 0.5f rounds up to 1.0f before the truncation.
+KV_TIE_ROW = np.array([127.0, 2.5, -2.5, 0.5, -0.5, 3.5, -3.5, 126.5, -126.5, 0.25, -0.25,
+                       0.5 - 2.0 ** -25, -(0.5 - 2.0 ** -25), 2.5 - 2.0 ** -22, 1.5, -1.5], np.float32)
+KV_TIE_CODES = np.array([127, 3, -3, 1, -1, 4, -4, 127, -127, 0, 0, 1, -1, 2, 2, -2], np.int8)
+
+
+def test_kv_store_exact_ties(oracle):
+    hd = 16
+    kc = np.zeros((1, 2, hd), np.int8)
+    vc = np.zeros_like(kc)
+    ks = np.zeros((1, 2), np.float32)
+    vs = np.zeros_like(ks)
+    oracle.kv_store(kc, vc, ks, vs, 2, 1, hd, 1, KV_TIE_ROW, -KV_TIE_ROW)
+    assert np.array_equal(kc[0, 1], KV_TIE_CODES) and np.array_equal(vc[0, 1], -KV_TIE_CODES)
+    assert ks[0, 1] == vs[0, 1] == np.float32(1.0)
+
+
 # ---- attention: fp64 brute force ---------------------------------------------
 @pytest.mark.parametrize("nh,nkv,position", [(4, 4, 0), (4, 4, 9), (8, 2, 30)])
 def test_attention_vs_fp64(oracle, nh, nkv, position):
