@@ -98,3 +98,19 @@ def _load_fresh(mod, path):
         return mod.load(path)
     finally:
         mod._lib = saved
+
+
+DROPIN = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "oracle", "_ref",
+                      "dropin_table")
+
+
+@pytest.mark.skipif(not os.path.exists(DROPIN), reason="oracle/_ref not built (reference sources absent)")
+def test_real_kernel_table_takeover():
+    """oracle/dropin_table: the reference's qsf_kernels_init fills a real
+    QSFKernelTable (src/kernels.c:7-65), qsf_kernels_init_hip takes over the
+    six matvec members and the MXFP4 slot, and the other twelve members stay
+    the CPU kernels (no GPU call)."""
+    from qstream_amd import qsf_hip
+    r = subprocess.run([DROPIN, qsf_hip.LIB_PATH, "--slots-only"], capture_output=True, text=True,
+                       timeout=60)
+    assert r.returncode == 0 and r.stdout.strip().endswith("OK"), r.stdout + r.stderr
