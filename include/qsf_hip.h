@@ -206,6 +206,11 @@ typedef struct {
  * (qsf_hip_last_error: 1 not found, 2 corrupted, 3 version, 6 invalid
  * model, 15 LZ4-compressed layers, which this build does not read). */
 qsf_hip_model* qsf_hip_model_load(const char* path);
+/* The same load from a QSF file already in memory (size bytes at data, read
+ * only during the call; nothing in the model points into it afterwards).
+ * No counterpart in the reference: for engines that hold the file in
+ * their own buffers, and for checking the parse under a sanitizer. */
+qsf_hip_model* qsf_hip_model_load_mem(const void* data, size_t size);
 void qsf_hip_model_free(qsf_hip_model* m);
 int qsf_hip_model_get_info(const qsf_hip_model* m, qsf_hip_model_info* out);
 /* Matrix (tensor_type of include/qsf/types.h:118-162) of a layer, or NULL. */

@@ -524,6 +524,20 @@ qsf_hip_model* qsf_hip_model_load(const char* path) {
     return m;
 }
 
+qsf_hip_model* qsf_hip_model_load_mem(const void* data, size_t size) {
+    if (!data || size == 0) {
+        qsf_host_fail(E_CORRUPTED, "qsf_hip_model_load_mem: empty buffer");
+        return NULL;
+    }
+    qsf_hip_model* m = calloc(1, sizeof *m);
+    int rc = m ? load_mapped(m, (const uint8_t*)data, size) : qsf_host_fail(E_OOM, "qsf_hip_model_load_mem");
+    if (rc) {
+        free_model(m);
+        return NULL;
+    }
+    return m;
+}
+
 int qsf_hip_model_get_info(const qsf_hip_model* m, qsf_hip_model_info* out) {
     if (!m || !out) return qsf_host_fail(11, "qsf_hip_model_get_info: null argument");
     *out = m->info;

@@ -40,7 +40,7 @@ EXPORTS = (
     "qsf_hip_gate_up_act_dev", "qsf_hip_residual_dev", "qsf_hip_embed_row_dev", "qsf_hip_embed_row_fp16_dev",
     "qsf_hip_residual_norm_dev", "qsf_hip_rope_kv_store_dev",
     "qsf_hip_residual_norm_matvec_group_dev", "qsf_hip_residual_norm_gate_up_act_dev",
-    "qsf_hip_crc32", "qsf_hip_model_load", "qsf_hip_model_free", "qsf_hip_model_get_info",
+    "qsf_hip_crc32", "qsf_hip_model_load", "qsf_hip_model_load_mem", "qsf_hip_model_free", "qsf_hip_model_get_info",
     "qsf_hip_model_tensor", "qsf_hip_model_vector", "qsf_hip_model_embedding",
     "qsf_hip_model_embedding_fp16", "qsf_hip_model_output_head", "qsf_hip_model_final_norm", "qsf_hip_model_moe",
 )
@@ -139,6 +139,8 @@ def load(path: str = LIB_PATH) -> C.CDLL:
     L.qsf_hip_crc32.restype = C.c_uint32
     L.qsf_hip_model_load.argtypes = [C.c_char_p]
     L.qsf_hip_model_load.restype = _vp
+    L.qsf_hip_model_load_mem.argtypes = [_vp, C.c_size_t]
+    L.qsf_hip_model_load_mem.restype = _vp
     L.qsf_hip_model_free.argtypes = [_vp]
     L.qsf_hip_model_get_info.argtypes = [_vp, _vp]
     L.qsf_hip_model_get_info.restype = _i
