@@ -2,32 +2,40 @@
 """Benchmark of QStream's quantized matvec hot path on one MI355X.
 
 Metric: quant matvec HBM GB/s (% of ~8 TB/s peak) + us/call
-at 7B decode shapes.  The default workload is BASELINE.json config 1: the
+at 7B decode shapes.  The headline workload is BASELINE.json config 1: the
 2-bit+outlier FFN gate and up projections (11008x4096 each, block 64), batch-1
 decode.  A step is one pass over one activation vector: one grouped GEMV
 launch over gate and up that prepares x inside its workgroups.  Weights
 rotate over >= 512 MiB of distinct copies in HBM so the 256 MB Infinity Cache
 cannot serve them; inputs are resident in HBM before the timed region.
 
-    python bench.py [--steps K] [--warmup W] [--config 1|0|2|3|4|all]
+    python bench.py [--steps K] [--warmup W] [--config 1|headline|0|2|3|4|layer|copy]
 
 Prints one JSON line.  `value` is algorithmic bytes per step (on-disk QSF
 payload + x read once + y written, per matrix) / wall time per step, over K
 steps captured once into a HIP graph and replayed between two HIP events on
 the replay stream, after W untimed eager steps and at least 0.2 s of untimed
 replays (the clocks settle after about 40 ms of sustained work).  For the
-one-launch decode steps (configs 0 and 1) that
-timed region is also the kernel's time: `roofline.kernel_us` is the region
-time per launch, so it never exceeds the step.  Configs 2-4 time their
-dominant kernel separately (see each function).  `roofline.traffic` is the
-HBM bytes per launch measured with rocprofv3 counters (profiles/traffic.json),
-used only while the kernel source it was measured on is unchanged, else
-null.  `cpu_baseline` times QStream's own AVX2 kernel (oracle/_ref,
-reference release flags, 1 thread) on a bounded sample.
-The default line also carries config 0 (the 4-bit matvec north_star's
-target names) under "config0"; `--config all` nests every config under
-"configs".  `--profile` runs eager launches only, for rocprofv3 counter
-passes; `--no-slot` skips the PCIe-inclusive table-slot timing.
+one-launch decode steps (configs 0 and 1) that timed region is also the
+kernel's time: `roofline.kernel_us` is the region time per launch, so it
+never exceeds the step.  Configs 2, 4 and the layer step time their
+dominant kernel by a graph of that kernel's launches alone; config 3 by
+kernel-edge HIP event pairs (`roofline.timing` says which).
+`roofline.traffic` is the HBM bytes per launch measured with rocprofv3
+counters (profiles/traffic.json), used only while the kernel source it was
+measured on is unchanged, else null.  Configs 0 and 1 also carry
+`read_floor`: one launch per step that only streams the same rotated
+tensors' device bytes, timed the same way.  `cpu_baseline` times QStream's
+own CPU kernel (oracle/_ref, reference release flags, 1 thread) on a
+bounded sample whose weights rotate over >= 768 MiB of host copies.
+
+The default run (`--config 1`) prints the headline line with every other
+config (0, 2, 3 at batch 1 and 8, 4, the layer step) nested under
+"configs", each with its roofline and cpu_baseline: about 2-4 minutes in
+all (data generation and about 34 s of CPU baselines included; the GPU
+timed work is under 10 s).  `--config headline` runs config 1 alone.
+`--profile` runs eager launches only, for rocprofv3 counter passes;
+`--no-slot` skips the PCIe-inclusive table-slot timing.
 """
 from __future__ import annotations
 
@@ -46,6 +54,7 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0
 BF16_MFMA_PEAK_TFS = 2500.0     # dense bf16 MFMA, MI355X
 ROTATE_BYTES = 512 << 20
+HOST_ROTATE_BYTES = 768 << 20   # CPU baselines: past the largest host LLC (EPYC: up to 512 MB L3)
 METRIC = "quant matvec HBM GB/s (% of ~8 TB/s peak) + µs/call at 7B decode shapes"
 
 
@@ -151,10 +160,22 @@ def run_dense(torch, hip, qt, bs, mats, x, steps, warmup, split=False):
         step(i, torch.cuda.current_stream())
     torch.cuda.synchronize()
     ms = graph_ms(torch, step, steps)
+    # the bare-read floor: one launch per step that only streams the same
+    # tensors' device bytes, over the same rotation, timed the same way
+    sink = torch.zeros(1, dtype=torch.int32, device="cuda:0")
+
+    def read_step(i, stream):
+        hip.stream_read(copies[i % n_copies], sink, stream=stream)
+
+    for i in range(warmup):
+        read_step(i, torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    read_ms = graph_ms(torch, read_step, steps)
     for ts in copies:
         for t in ts:
             t.free()
-    return {"ms_per_step": ms, "n_copies": n_copies, "rotation_mib": n_copies * per_copy / (1 << 20)}
+    return {"ms_per_step": ms, "read_ms_per_step": read_ms, "n_copies": n_copies,
+            "rotation_mib": n_copies * per_copy / (1 << 20)}
 
 
 def cpu_baseline_dense(qt, bs, mats, x, budget_s=10.0):
@@ -174,15 +195,17 @@ def cpu_baseline_dense(qt, bs, mats, x, budget_s=10.0):
         def fn(p, r, c):
             return o.matvec(qt, p, x, r, c, bs)
         name = "oracle scalar"
-    # 4 distinct host copies per matrix so the rotation exceeds the LLC
-    hcopies = [[(np.array(p, copy=True), r, c) for _, p, r, c in mats] for _ in range(4)]
+    # distinct host copies, rotated, >= HOST_ROTATE_BYTES in all: past the
+    # host's last-level cache, so every step reads its weights from DRAM
     per_step = algo_bytes(mats)
+    n_host = max(4, math.ceil(HOST_ROTATE_BYTES / per_step))
+    hcopies = [[(np.array(p, copy=True), r, c) for _, p, r, c in mats] for _ in range(n_host)]
     times = []
     t_start = time.perf_counter()
     i = 0
     while time.perf_counter() - t_start < budget_s or len(times) < 3:
         t = time.perf_counter()
-        for p, r, c in hcopies[i % 4]:
+        for p, r, c in hcopies[i % n_host]:
             fn(p, r, c)
         times.append(time.perf_counter() - t)
         i += 1
@@ -190,8 +213,9 @@ def cpu_baseline_dense(qt, bs, mats, x, budget_s=10.0):
             break
     med = float(np.median(times))
     return {"value": per_step / med / 1e9, "unit": "GB/s", "cores": 1, "kind": kind,
-            "sample": f"{name}, {len(times)} steps ({len(mats)} matrices per step) over 4 host "
-                      f"copies, median {med * 1e3:.1f} ms/step, {time.perf_counter() - t_start:.1f} s"}
+            "sample": f"{name}, {len(times)} steps ({len(mats)} matrices per step) over {n_host} host "
+                      f"copies ({n_host * per_step / (1 << 20):.0f} MiB rotated), median "
+                      f"{med * 1e3:.1f} ms/step, {time.perf_counter() - t_start:.1f} s"}
 
 
 def _sha16(path: str):
@@ -293,12 +317,19 @@ def bench_dense(torch, hip, cfg, steps, warmup, with_cpu=True, split=False, slot
     if not split:
         # one GEMV launch per step: the graph-replayed timed region per
         # launch is the kernel's time (launch gaps included, so it errs low)
-        out["roofline"] = {"bound": "hbm", "kernel": "gemv_kernel (one launch per step)",
+        out["roofline"] = {"bound": "hbm", "kernel": "decode GEMV (one launch per step)",
+                           "timing": "graph replay of the steps",
                            "achieved": round(value, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                            "frac": round(value / HBM_PEAK_GBS, 4),
                            "traffic": measured_traffic(f"cfg{cfg}"),
                            "kernel_us": round(us_step, 3), "launches_timed": steps,
                            "bytes_per_launch": bytes_step}
+    read_us = res["read_ms_per_step"] * 1e3
+    out["read_floor"] = {"kernel": "stream_read_kernel (one launch per step, same rotated tensors)",
+                         "us_per_step": round(read_us, 3),
+                         "achieved": round(bytes_step / (read_us * 1e-6) / 1e9, 2), "unit": "GB/s",
+                         "frac": round(bytes_step / (read_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                         "gemv_over_floor": round(us_step / read_us, 3)}
     if slot:
         out["table_slot_us_per_step"] = table_slot_step_us(hip, qt, bs, mats, x)
         out["table_slot_alone_us_per_step"] = table_slot_step_us(hip, qt, bs, mats, x, lookahead=0)
@@ -315,24 +346,28 @@ def cpu_baseline_prefill(payload, xb, m, n, k, bs, budget_s=10.0):
     from qstream_amd import qsf_format as F
     ref = ref_avx2()
     xf = (xb.astype(np.uint32) << 16).view(np.float32)
+    # host copies of the weights in rotation, past the host LLC
+    n_host = max(2, math.ceil(HOST_ROTATE_BYTES / len(payload)))
+    hcopies = [np.array(np.frombuffer(payload, np.uint8), copy=True) for _ in range(n_host)]
     if ref is not None:
         kind, name = "reference", "qsf_matvec_4bit_avx2"
 
-        def fn(x):
-            return ref.matvec(F.Q4, payload, x, n, k, bs, isa="avx2")
+        def fn(w, x):
+            return ref.matvec(F.Q4, w, x, n, k, bs, isa="avx2")
     else:
         kind, name, o = "port", "oracle scalar", Oracle()
 
-        def fn(x):
-            return o.matvec(F.Q4, payload, x, n, k, bs)
+        def fn(w, x):
+            return o.matvec(F.Q4, w, x, n, k, bs)
     t0 = time.perf_counter()
     done = 0
     while done < m and (time.perf_counter() - t0 < budget_s or done < 2):
-        fn(xf[done])
+        fn(hcopies[done % n_host], xf[done])
         done += 1
     el = time.perf_counter() - t0
     return {"value": 2.0 * n * k * done / el / 1e12, "unit": "TFLOP/s", "cores": 1, "kind": kind,
-            "sample": f"{name}, {done} of {m} tokens (one {n}x{k} matvec each), {el:.1f} s"}
+            "sample": f"{name}, {done} of {m} tokens (one {n}x{k} matvec each) over {n_host} host "
+                      f"weight copies ({n_host * len(payload) / (1 << 20):.0f} MiB rotated), {el:.1f} s"}
 
 
 def profile_prefill(torch, hip, steps, warmup):
@@ -351,9 +386,9 @@ def profile_prefill(torch, hip, steps, warmup):
 
 def bench_prefill(torch, hip, steps, warmup, with_cpu=True, cpu_budget=10.0):
     """Config 4: one MFMA prefill (x repack + GEMM launch) per step over a
-    rotating weight copy.  The GEMM's own time comes from HIP event pairs
-    at its start and end on its launch stream (qsf_hip_kernel_timing), over
-    eager steps after the graph-timed region."""
+    rotating weight copy.  The GEMM's own time: a graph of GEMM-only
+    launches (the packed-x half of the prefill, qsf_hip_prefill_4bit_packed_dev)
+    over the same rotation, x packed once before it, timed like the steps."""
     from qstream_amd import qsf_format as F
     payload, xb, m, n, k, bs = cfg4_data()
     log(f"config 4: data ready ({m}x{n}x{k}, block {bs})")
@@ -369,24 +404,29 @@ def bench_prefill(torch, hip, steps, warmup, with_cpu=True, cpu_budget=10.0):
         step(i, torch.cuda.current_stream())
     torch.cuda.synchronize()
     ms = graph_ms(torch, step, steps)
-    hip.kernel_timing(True)
-    for i in range(steps):
-        step(i, torch.cuda.current_stream())
+    packed = torch.empty(hip.prefill_pack_bytes(m, k, bs) + 256, dtype=torch.uint8, device="cuda:0")
+    paddr = (packed.data_ptr() + 255) & ~255
+    hip.prefill_pack(dx, m, k, bs, paddr, stream=torch.cuda.current_stream())
+
+    def gemm_step(i, stream):
+        copies[i % n_copies].prefill_packed(paddr, m, y, stream=stream)
+
+    for i in range(warmup):
+        gemm_step(i, torch.cuda.current_stream())
     torch.cuda.synchronize()
-    kern_us = hip.kernel_timing_read(steps)
-    hip.kernel_timing(False)
+    kus = graph_ms(torch, gemm_step, steps) * 1e3
     for t in copies:
         t.free()
     flops = 2.0 * m * n * k
-    kus = float(np.mean(kern_us))
     out = {"value": flops / (ms * 1e-3) / 1e12, "ms_per_step": ms, "us_kernel": kus,
            "flops_per_step": flops, "weight_bytes": len(payload),
-           "roofline": {"bound": "mfma", "kernel": "prefill_kernel",
+           "roofline": {"bound": "mfma", "kernel": "prefill_kernel (the GEMM half)",
+                        "timing": "graph of GEMM-only launches over the rotation",
                         "achieved": round(flops / (kus * 1e-6) / 1e12, 2),
                         "peak": BF16_MFMA_PEAK_TFS, "unit": "TFLOP/s",
                         "frac": round(flops / (kus * 1e-6) / 1e12 / BF16_MFMA_PEAK_TFS, 4),
                         "traffic": measured_traffic("cfg4"), "kernel_us": round(kus, 3),
-                        "launches_timed": len(kern_us)},
+                        "launches_timed": steps},
            "rotation_mib": n_copies * len(payload) / (1 << 20), "m": m, "n": n, "k": k}
     if with_cpu:
         out["cpu_baseline"] = cpu_baseline_prefill(payload, xb, m, n, k, bs, cpu_budget)
@@ -450,7 +490,8 @@ def bench_layers(torch, hip, steps, warmup, with_cpu=True, cpu_budget=10.0):
     total = 32 * per_layer
     gu_bytes = algo_bytes(mats[4:6])
     out = {"value": total / (ms * 1e-3) / 1e9, "ms_per_step": ms, "bytes_per_step": total}
-    out["roofline"] = {"bound": "hbm", "kernel": "gemv_kernel, gate/up launch (2 x 11008x4096 3-bit)",
+    out["roofline"] = {"bound": "hbm", "kernel": "decode GEMV, gate/up launch (2 x 11008x4096 3-bit)",
+                       "timing": "graph of 32 gate/up launches (one a layer)",
                        "achieved": round(gu_bytes / (gu_us * 1e-6) / 1e9, 2),
                        "peak": HBM_PEAK_GBS, "unit": "GB/s",
                        "frac": round(gu_bytes / (gu_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
@@ -516,6 +557,14 @@ def bench_decode_layer(torch, hip, steps, warmup, position=1023):
         step(i, torch.cuda.current_stream())
     torch.cuda.synchronize()
     ms = graph_ms(torch, step, steps)
+    # Dominant kernel: the fused residual + FFN norm + gate/up + SiLU x up
+    # launch (45% of the layer's weight bytes), a graph of one such launch
+    # per layer over the 32 layers' pairs, timed like the steps.
+    def gu_step(i, stream):
+        pairs[i % n_layers].residual_norm_gate_up_act(res2, res, ys["o"], fn_w, 1e-5, ys["gate"], 2,
+                                                      stream=stream)
+
+    gu_us = graph_ms(torch, gu_step, n_layers) * 1e3
     rope.free()
     for ts in layers:
         for t in ts:
@@ -524,8 +573,16 @@ def bench_decode_layer(torch, hip, steps, warmup, position=1023):
         pr.free()
     kv_bytes = 2 * nh * max_seq * (hd + 4)
     total = algo_bytes(mats) + kv_bytes
+    gu_bytes = algo_bytes(mats[4:6]) + 3 * 4 * hid     # + residual in/out and norm weights
     return {"value": total / (ms * 1e-3) / 1e9, "ms_per_step": ms, "bytes_per_step": total,
-            "weight_bytes": algo_bytes(mats), "kv_bytes": kv_bytes, "position": position}
+            "weight_bytes": algo_bytes(mats), "kv_bytes": kv_bytes, "position": position,
+            "roofline": {"bound": "hbm",
+                         "kernel": "residual + norm + gate/up + act launch (2 x 11008x4096 3-bit, interleaved)",
+                         "timing": "graph of 32 such launches (one a layer)",
+                         "achieved": round(gu_bytes / (gu_us * 1e-6) / 1e9, 2), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(gu_bytes / (gu_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                         "traffic": measured_traffic("layer"), "kernel_us": round(gu_us, 3),
+                         "bytes_per_launch": gu_bytes}}
 
 
 def cpu_baseline_layer(qt, bs, mats, budget_s=10.0):
@@ -537,21 +594,26 @@ def cpu_baseline_layer(qt, bs, mats, budget_s=10.0):
     rng = np.random.default_rng(21)
     kind = "reference" if ref is not None else "port"
     o = None if ref is not None else Oracle()
+    # host copies of the layer in rotation, past the host LLC
+    n_host = max(2, math.ceil(HOST_ROTATE_BYTES / algo_bytes(mats)))
+    hcopies = [[(np.array(np.frombuffer(p, np.uint8), copy=True), r, c) for _, p, r, c in mats]
+               for _ in range(n_host)]
+    xs = {c: rng.standard_normal(c).astype(np.float32) for _, _, _, c in mats}
     t0 = time.perf_counter()
     done = 0
     nbytes = 0
     while time.perf_counter() - t0 < budget_s or done == 0:
-        for _, p, r, c in mats:
-            x = rng.standard_normal(c).astype(np.float32)
+        for p, r, c in hcopies[done % n_host]:
             if ref is not None:
-                ref.matvec(qt, p, x, r, c, bs, isa="scalar")
+                ref.matvec(qt, p, xs[c], r, c, bs, isa="scalar")
             else:
-                o.matvec(qt, p, x, r, c, bs)
+                o.matvec(qt, p, xs[c], r, c, bs)
             nbytes += len(p) + 4 * c + 4 * r
         done += 1
     el = time.perf_counter() - t0
     return {"value": nbytes / el / 1e9, "unit": "GB/s", "cores": 1, "kind": kind,
-            "sample": f"qsf_matvec_3bit_scalar over {done} layer(s) of 7 matrices, {el:.1f} s"}
+            "sample": f"qsf_matvec_3bit_scalar over {done} layer(s) of 7 matrices, {n_host} host copies "
+                      f"rotated ({n_host * algo_bytes(mats) / (1 << 20):.0f} MiB), {el:.1f} s"}
 
 
 def profile_moe(torch, hip, steps, warmup, ntok):
@@ -635,7 +697,9 @@ def bench_moe(torch, hip, steps, warmup, ntok, with_cpu=True, cpu_budget=10.0, e
             t.free()
     res = {"value": bytes_step / (ms * 1e-3) / 1e9, "ms_per_step": ms, "bytes_per_step": bytes_step,
            "distinct_experts_mean": float(np.mean(distinct))}
-    res["roofline"] = {"bound": "hbm", "kernel": "moe_gate_up_kernel", "achieved": round(roof, 2),
+    res["roofline"] = {"bound": "hbm", "kernel": "moe_gate_up_kernel",
+                       "timing": "kernel-edge HIP event pairs on the launch stream, eager steps",
+                       "achieved": round(roof, 2),
                        "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(roof / HBM_PEAK_GBS, 4),
                        "traffic": measured_traffic(f"cfg3_b{ntok}"),
                        "kernel_us": round(float(np.mean(gu_us)), 3),
@@ -709,6 +773,8 @@ def run_config(torch, hip, key: str, args, cpu_budget: float, cache: dict) -> di
                 "bytes_per_step": r["bytes_per_step"],
                 "hbm_frac_of_8TBs": round(r["value"] / HBM_PEAK_GBS, 4),
                 "rotation_mib": round(r["rotation_mib"], 1)}
+        if "read_floor" in r:
+            conf["read_floor"] = r["read_floor"]
         if "table_slot_us_per_step" in r:
             conf["table_slot_us_per_step_pcie"] = round(r["table_slot_us_per_step"], 3)
             conf["table_slot_lookahead_off_us_per_step_pcie"] = round(
@@ -746,6 +812,10 @@ def run_config(torch, hip, key: str, args, cpu_budget: float, cache: dict) -> di
                             "hbm_frac_of_8TBs": round(r["value"] / HBM_PEAK_GBS, 4)})
     elif key == "layer":
         r = bench_decode_layer(torch, hip, args.steps, args.warmup)
+        if with_cpu:
+            qt, bs, mats = cfg2_layer()
+            r["cpu_baseline"] = cpu_baseline_layer(qt, bs, mats, cpu_budget)
+            r["cpu_baseline"]["sample"] += " (the layer's matvecs; the glue is under 1% of its bytes)"
         line = dict(base, value=round(r["value"], 2), ms_per_step=round(r["ms_per_step"], 5),
                     dtype=DIGIT_DTYPE + "; glue fp32",
                     data="synthetic (seeded N(0,0.02) weights quantised to 3-bit block 128; random "
@@ -792,7 +862,9 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--config", default="1", help="1 (default), 0, 2, 3, 4, layer, all, or copy")
+    ap.add_argument("--config", default="1",
+                    help="1 (default: config 1 with every other config nested), headline (config 1 "
+                         "alone), 0, 2, 3, 4, layer, or copy")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-slot", action="store_true", help="skip the table-slot (PCIe) timing")
     ap.add_argument("--data-workers", type=int, default=None,
@@ -827,13 +899,17 @@ def main():
             run_profile(torch, qsf_hip, cfg, args.steps, args.warmup)
         return
     cache: dict = {}
-    if args.config == "all":
+    if args.config in ("1", "all"):
+        # the headline (config 1) with every other config nested under "configs"
+        t0 = time.perf_counter()
         line = run_config(torch, qsf_hip, "1", args, 10.0, cache)
-        line["configs"] = {k.replace("3b", "3_b"): nested(run_config(torch, qsf_hip, k, args, 4.0, cache))
-                           for k in ("0", "2", "3b1", "3b8", "4", "layer")}
-    elif args.config == "1":
+        line["configs"] = {}
+        for k in ("0", "2", "3b1", "3b8", "4", "layer"):
+            line["configs"][k.replace("3b", "3_b")] = nested(run_config(torch, qsf_hip, k, args, 4.0, cache))
+            log(f"config {k} done, {time.perf_counter() - t0:.0f} s in all")
+        line["bench_wall_s"] = round(time.perf_counter() - t0, 1)
+    elif args.config == "headline":
         line = run_config(torch, qsf_hip, "1", args, 10.0, cache)
-        line["config0"] = nested(run_config(torch, qsf_hip, "0", args, 5.0, cache))
     else:
         line = run_config(torch, qsf_hip, args.config, args, 10.0, cache)
     print(json.dumps(line), flush=True)

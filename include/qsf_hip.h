@@ -286,6 +286,25 @@ int qsf_hip_prefill_4bit_dev(const qsf_hip_tensor* t, const uint16_t* d_x_bf16, 
 int qsf_hip_prefill_4bit_dev_noalloc(const qsf_hip_tensor* t, const uint16_t* d_x_bf16, int m,
                                      float* d_y, void* stream);
 
+/* qsf_hip_prefill_4bit_dev in two halves (no counterpart in the reference):
+ * pack x (bf16 [m][cols]) once into a caller buffer of
+ * qsf_hip_prefill_pack_bytes(m, cols, bs) bytes (16-byte aligned), then run
+ * the GEMM of every 4-bit tensor with those cols and block size that
+ * shares this x (q/k/v, gate/up) over it.  Results are those of
+ * qsf_hip_prefill_4bit_dev.  Asynchronous on `stream`. */
+size_t qsf_hip_prefill_pack_bytes(int m, int cols, int block_size);
+int qsf_hip_prefill_pack_dev(const uint16_t* d_x_bf16, int m, int cols, int block_size, void* d_packed,
+                             void* stream);
+int qsf_hip_prefill_4bit_packed_dev(const qsf_hip_tensor* t, const void* d_packed, int m, float* d_y,
+                                    void* stream);
+
+/* Diagnostic (no counterpart in the reference): one launch that streams the
+ * device bytes of n <= 8 tensors once (blocks, scales, outlier CSR) and does
+ * nothing else, the floor a one-launch GEMV over them is measured against.
+ * d_sink: one uint32 of device memory, written only in the unlikely case a
+ * workgroup's checksum equals a fixed constant.  Asynchronous. */
+int qsf_hip_stream_read_dev(const qsf_hip_tensor* const* t, int n, uint32_t* d_sink, void* stream);
+
 /* ---- device-resident decode glue ------------------------------------------
  * The per-layer work between the projections of one decode step
  * (src/engine.c:709-1187), so an engine that keeps its activations in HBM

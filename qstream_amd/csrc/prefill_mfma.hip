@@ -553,30 +553,54 @@ extern "C" size_t qk_prefill_ws_bytes(int m, int cols, int bs) {
     return (size_t)((m + 15) / 16) * (size_t)(4 * (st.sz + st.sc)) * 1024;
 }
 
-extern "C" int qk_prefill_4bit(const qsf_hip_tensor* t, const uint16_t* d_x_bf16, int m,
-                               float* d_y, void* d_ws, hipStream_t s) {
+// x bf16 [m][cols] -> the packed activations (qk_prefill_ws_bytes) a
+// prefill of any 4-bit tensor with these cols and block size reads.
+extern "C" int qk_prefill_pack(const uint16_t* d_x_bf16, int m, int cols, int bs, void* d_ws, hipStream_t s) {
+    if (m <= 0) return 0;
+    if (cols < 32 || cols % 8 || !(bs == 64 || bs == 128 || bs == 256)) return -2;
+    const Stages st = stages_of(cols, bs);
+    const int ksp_total = 4 * (st.sz + st.sc), kz = 4 * st.sz, nb = (cols + bs - 1) / bs;
+    if ((uint64_t)((m + BM - 1) / BM) * (BM / 16) * ksp_total * 1024 + 8 * 1024 >= (1ull << 32)) return -2;
+    hipLaunchKernelGGL(xpack_kernel, dim3((ksp_total - kz) / 8, (m + 15) / 16), dim3(256), 0, s,
+                       d_x_bf16, static_cast<u32x4*>(d_ws), m, cols, ksp_total, kz, bs, nb);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+namespace {
+// 0 when qk_prefill_gemm takes (t, m): a 4-bit tensor without outliers and
+// 32-bit byte offsets inside the weight payload (including the columns of
+// the last tile past the end, and the zero-point stages' block reads up to
+// 16 sz blocks a row) and the packed activations (including the row groups
+// of the last tile and the prefetch past the last stage); else -2.
+int gemm_check(const qsf_hip_tensor* t, int m) {
     if (t->fmt != QK_FMT_4 || t->n_outliers) return -2;
     if (m <= 0 || t->rows <= 0) return 0;
     if (t->cols < 32 || t->cols % 8) return -2;
+    if (t->bs == 256 && t->frag) return -2;
     const int bb = 4 + t->bs / 2;
     const Stages st = stages_of(t->cols, t->bs);
-    const int ksp_total = 4 * (st.sz + st.sc), kz = 4 * st.sz;
-    const size_t xp_bytes = qk_prefill_ws_bytes(m, t->cols, t->bs);
-    // 32-bit byte offsets inside the weight payload (including the columns
-    // of the last tile past the end, and the zero-point stages' block reads
-    // up to 16 sz blocks a row) and the packed activations (including the
-    // row groups of the last tile and the prefetch past the last stage)
-    const int tiles_m = (m + BM - 1) / BM;
+    const int ksp_total = 4 * (st.sz + st.sc);
     const uint64_t row_bytes = (uint64_t)t->nb * bb;
     if ((uint64_t)(t->rows + BN) * row_bytes + (uint64_t)16 * st.sz * bb >= (1ull << 32) ||
-        (uint64_t)tiles_m * (BM / 16) * ksp_total * 1024 + 8 * 1024 >= (1ull << 32))
+        (uint64_t)((m + BM - 1) / BM) * (BM / 16) * ksp_total * 1024 + 8 * 1024 >= (1ull << 32))
         return -2;
+    if (t->frag && (uint64_t)((t->rows + BN) / 16 + 1) * t->frag_nq * 64 * bb >= (1ull << 32)) return -2;
+    return 0;
+}
+}  // namespace
+
+// The GEMM over activations qk_prefill_pack wrote for m tokens.
+extern "C" int qk_prefill_gemm(const qsf_hip_tensor* t, const void* d_ws, int m, float* d_y, hipStream_t s) {
+    if (gemm_check(t, m)) return -2;
+    if (m <= 0 || t->rows <= 0) return 0;
+    const int bb = 4 + t->bs / 2;
+    const Stages st = stages_of(t->cols, t->bs);
+    const size_t xp_bytes = qk_prefill_ws_bytes(m, t->cols, t->bs);
+    const int tiles_m = (m + BM - 1) / BM;
+    const uint64_t row_bytes = (uint64_t)t->nb * bb;
     const int tiles_n = (t->rows + BN - 1) / BN;
     const bool ragged = t->cols % (2 * SK) != 0;
-    hipLaunchKernelGGL(xpack_kernel, dim3((ksp_total - kz) / 8, (m + 15) / 16), dim3(256), 0, s,
-                       d_x_bf16, static_cast<u32x4*>(d_ws), m, t->cols, ksp_total, kz, t->bs, t->nb);
     const uint64_t w_bytes = t->frag ? (uint64_t)qk_frag_bytes(t->rows, t->nb, bb) : (uint64_t)t->rows * row_bytes;
-    if (t->frag && (uint64_t)((t->rows + BN) / 16 + 1) * t->frag_nq * 64 * bb >= (1ull << 32)) return -2;
     PrefillArgs a = {t->d_blocks, static_cast<const u32x4*>(d_ws), d_y, m, t->rows, t->cols, t->nb,
                      tiles_n, st.sz, st.sz + st.sc, (uint32_t)w_bytes, (uint32_t)xp_bytes, t->frag_nq};
     const dim3 grid(tiles_n * tiles_m), block(512);
@@ -591,13 +615,20 @@ extern "C" int qk_prefill_4bit(const qsf_hip_tensor* t, const uint16_t* d_x_bf16
         if (t->frag) { QK_PREFILL_CASE(128, true) } else { QK_PREFILL_CASE(128, false) }
         break;
     case 256:
-        if (t->frag) return -2;
         QK_PREFILL_CASE(256, false)
         break;
     default: return -2;
     }
 #undef QK_PREFILL_CASE
     return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+extern "C" int qk_prefill_4bit(const qsf_hip_tensor* t, const uint16_t* d_x_bf16, int m,
+                               float* d_y, void* d_ws, hipStream_t s) {
+    if (gemm_check(t, m)) return -2;
+    if (m <= 0 || t->rows <= 0) return 0;
+    const int r = qk_prefill_pack(d_x_bf16, m, t->cols, t->bs, d_ws, s);
+    return r ? r : qk_prefill_gemm(t, d_ws, m, d_y, s);
 }
 
 // ---- allocation-free form -------------------------------------------------

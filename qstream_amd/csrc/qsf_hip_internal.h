@@ -42,6 +42,7 @@ typedef struct qsf_hip_tensor {
     uint32_t* d_ocol;           /* else n_csr column indices ... */
     uint16_t* d_oval;           /* ... and n_csr fp16 values */
     void*    d_alloc;           /* base of the single device allocation */
+    size_t   alloc_bytes;       /* its parts (blocks, scales, CSR) up to the tail pad */
     int      frag;              /* 1: d_blocks in fragment order (below), 0: on-disk order */
     int      frag_nq;           /* fragment order: 4-block quads a row, ceil(nb / 4) */
     int      registry_owned;    /* uploaded implicitly by a table-slot call */
@@ -176,6 +177,17 @@ size_t qk_prefill_ws_bytes(int m, int cols, int bs);
 int qk_prefill_scratch_init(void);
 int qk_prefill_4bit_noalloc(const qsf_hip_tensor* t, const uint16_t* d_x_bf16, int m,
                             float* d_y, hipStream_t s);
+/* One streaming read of n device ranges (16-byte aligned), the floor of a
+ * launch that reads those bytes once.  A workgroup stores its checksum to
+ * *sink only if it equals a fixed 32-bit constant, which keeps every load
+ * live and in practice stores nothing. */
+int qk_stream_read(const void* const* ptr, const size_t* bytes, int n, uint32_t* sink, hipStream_t s);
+
+/* The two halves of qk_prefill_4bit: x bf16 [m][cols] packed into d_ws
+ * (qk_prefill_ws_bytes), and the GEMM of a 4-bit tensor with those cols and
+ * block size over it. */
+int qk_prefill_pack(const uint16_t* d_x_bf16, int m, int cols, int bs, void* d_ws, hipStream_t s);
+int qk_prefill_gemm(const qsf_hip_tensor* t, const void* d_ws, int m, float* d_y, hipStream_t s);
 int qk_prefill_4bit(const qsf_hip_tensor* t, const uint16_t* d_x_bf16, int m,
                     float* d_y, void* d_ws, hipStream_t s);
 

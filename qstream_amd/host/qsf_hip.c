@@ -452,6 +452,7 @@ static qsf_hip_tensor* upload_locked(const void* host, int qt, int rows, int col
     /* blocks are read with 16-byte vector loads that may reach 12 bytes past
      * the last block: keep a tail pad */
     total += 256;
+    t->alloc_bytes = total - 256;    /* the parts, without the tail pad */
     hipError_t he = hipMalloc(&t->d_alloc, total);
     if (he != hipSuccess) {
         free(row_ptr); free(ocol); free(oval); free(t);
@@ -767,7 +768,8 @@ static int prefill_check(const char* who, const qsf_hip_tensor* t, const uint16_
     if (t->fmt != QK_FMT_4 || t->n_outliers || !(t->bs == 64 || t->bs == 128 || t->bs == 256))
         return fail(E_INVALID, "%s: needs a 4-bit asymmetric tensor with "
                                "block 64, 128 or 256 and no outliers", who);
-    if (m < 0 || t->cols < 32 || t->cols % 8 != 0 || ((uintptr_t)d_x_bf16 & 15u) != 0)
+    if (m < 0 || t->cols < 32 || t->cols % 8 != 0 || ((uintptr_t)d_x_bf16 & 15u) != 0 ||
+        (m > 0 && !d_x_bf16 && !strstr(who, "packed")))
         return fail(E_INVALID, "%s: m >= 0, cols >= 32, cols %% 8 == 0 "
                                "and a 16-byte aligned x are required", who);
     return E_OK;
@@ -801,6 +803,53 @@ int qsf_hip_prefill_4bit_dev_noalloc(const qsf_hip_tensor* t, const uint16_t* d_
         if (r) rc = fail(E_INTERNAL, "qsf_hip_prefill_4bit_dev_noalloc: %s",
                          r == -1 ? "no address for this device's scratch array" : "launch failed");
     }
+    pthread_mutex_unlock(&g_lock);
+    return rc;
+}
+
+size_t qsf_hip_prefill_pack_bytes(int m, int cols, int bs) { return qk_prefill_ws_bytes(m, cols, bs); }
+
+int qsf_hip_prefill_pack_dev(const uint16_t* d_x_bf16, int m, int cols, int bs, void* d_packed,
+                             void* stream) {
+    if (m < 0 || cols < 32 || cols % 8 != 0 || !(bs == 64 || bs == 128 || bs == 256) ||
+        ((uintptr_t)d_x_bf16 & 15u) != 0 || ((uintptr_t)d_packed & 15u) != 0 || (m > 0 && !d_packed))
+        return fail(E_INVALID, "qsf_hip_prefill_pack_dev: m >= 0, cols >= 32, cols %% 8 == 0, block "
+                               "64/128/256 and 16-byte aligned x and packed buffer are required");
+    pthread_mutex_lock(&g_lock);
+    int rc = g_dev.ready ? E_OK : fail(E_INVALID, "qsf_hip: not initialised");
+    if (rc == E_OK && qk_prefill_pack(d_x_bf16, m, cols, bs, d_packed, pick_stream(stream)))
+        rc = fail(E_INTERNAL, "qsf_hip_prefill_pack_dev: %d tokens x %d columns: launch failed", m, cols);
+    pthread_mutex_unlock(&g_lock);
+    return rc;
+}
+
+int qsf_hip_prefill_4bit_packed_dev(const qsf_hip_tensor* t, const void* d_packed, int m, float* d_y,
+                                    void* stream) {
+    if (prefill_check("qsf_hip_prefill_4bit_packed_dev", t, NULL, m)) return g_err;
+    if (((uintptr_t)d_packed & 15u) != 0 || (m > 0 && !d_packed))
+        return fail(E_INVALID, "qsf_hip_prefill_4bit_packed_dev: a 16-byte aligned packed buffer is required");
+    pthread_mutex_lock(&g_lock);
+    int rc = g_dev.ready ? E_OK : fail(E_INVALID, "qsf_hip: not initialised");
+    if (rc == E_OK && qk_prefill_gemm(t, d_packed, m, d_y, pick_stream(stream)))
+        rc = fail(E_INTERNAL, "qsf_hip_prefill_4bit_packed_dev: launch failed");
+    pthread_mutex_unlock(&g_lock);
+    return rc;
+}
+
+int qsf_hip_stream_read_dev(const qsf_hip_tensor* const* t, int n, uint32_t* d_sink, void* stream) {
+    if (!t || n <= 0 || n > QK_MAX_GROUP || !d_sink)
+        return fail(E_INVALID, "qsf_hip_stream_read_dev: 1..%d tensors and a sink are required", QK_MAX_GROUP);
+    const void* ptr[QK_MAX_GROUP];
+    size_t bytes[QK_MAX_GROUP];
+    for (int i = 0; i < n; i++) {
+        if (!t[i]) return fail(E_INVALID, "qsf_hip_stream_read_dev: null tensor %d", i);
+        ptr[i] = t[i]->d_alloc;
+        bytes[i] = t[i]->alloc_bytes;
+    }
+    pthread_mutex_lock(&g_lock);
+    int rc = g_dev.ready ? E_OK : fail(E_INVALID, "qsf_hip: not initialised");
+    if (rc == E_OK && qk_stream_read(ptr, bytes, n, d_sink, pick_stream(stream)))
+        rc = fail(E_INTERNAL, "qsf_hip_stream_read_dev: launch failed");
     pthread_mutex_unlock(&g_lock);
     return rc;
 }

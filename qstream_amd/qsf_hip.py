@@ -34,7 +34,8 @@ EXPORTS = (
     "qsf_hip_xprep_dev", "qsf_hip_matvec_group_prepared_dev",
     "qsf_hip_moe_create", "qsf_hip_moe_free", "qsf_hip_moe_forward_dev",
     "qsf_hip_unpack_dev", "qsf_hip_kernel_timing", "qsf_hip_kernel_timing_read", "qsf_hip_gemv_engine",
-    "qsf_hip_prefill_4bit_dev", "qsf_hip_prefill_4bit_dev_noalloc",
+    "qsf_hip_prefill_4bit_dev", "qsf_hip_prefill_4bit_dev_noalloc", "qsf_hip_prefill_pack_bytes",
+    "qsf_hip_prefill_pack_dev", "qsf_hip_prefill_4bit_packed_dev", "qsf_hip_stream_read_dev",
     "qsf_hip_rms_norm_dev", "qsf_hip_layer_norm_dev", "qsf_hip_rope_create", "qsf_hip_rope_free",
     "qsf_hip_rope_dev", "qsf_hip_kv_store_dev", "qsf_hip_attention_dev", "qsf_hip_act_mul_dev",
     "qsf_hip_gate_up_act_dev", "qsf_hip_residual_dev", "qsf_hip_embed_row_dev", "qsf_hip_embed_row_fp16_dev",
@@ -109,6 +110,14 @@ def load(path: str = LIB_PATH) -> C.CDLL:
     L.qsf_hip_prefill_4bit_dev.restype = _i
     L.qsf_hip_prefill_4bit_dev_noalloc.argtypes = [_vp, _vp, _i, _vp, _vp]
     L.qsf_hip_prefill_4bit_dev_noalloc.restype = _i
+    L.qsf_hip_prefill_pack_bytes.argtypes = [_i, _i, _i]
+    L.qsf_hip_prefill_pack_bytes.restype = C.c_size_t
+    L.qsf_hip_prefill_pack_dev.argtypes = [_vp, _i, _i, _i, _vp, _vp]
+    L.qsf_hip_prefill_pack_dev.restype = _i
+    L.qsf_hip_prefill_4bit_packed_dev.argtypes = [_vp, _vp, _i, _vp, _vp]
+    L.qsf_hip_prefill_4bit_packed_dev.restype = _i
+    L.qsf_hip_stream_read_dev.argtypes = [C.POINTER(_vp), _i, _vp, _vp]
+    L.qsf_hip_stream_read_dev.restype = _i
     _f = C.c_float
     L.qsf_hip_rms_norm_dev.argtypes = [_vp, _vp, _vp, _i, _f, _vp]
     L.qsf_hip_layer_norm_dev.argtypes = [_vp, _vp, _vp, _vp, _i, _f, _vp]
@@ -295,6 +304,11 @@ class Tensor:
                                                        _stream(stream)),
                "qsf_hip_prefill_4bit_dev_noalloc")
 
+    def prefill_packed(self, packed, m: int, y, stream=None) -> None:
+        """The GEMM half of prefill over activations prefill_pack wrote."""
+        _check(load().qsf_hip_prefill_4bit_packed_dev(self.handle, _addr(packed), m, _addr(y),
+                                                      _stream(stream)), "qsf_hip_prefill_4bit_packed_dev")
+
     def matvec(self, x, y, stream=None) -> None:
         _check(load().qsf_hip_matvec_dev(self.handle, _addr(x), _addr(y), _stream(stream)),
                "qsf_hip_matvec_dev")
@@ -333,6 +347,24 @@ class TensorPair(Tensor):
         """out[i] = act(gate_i . x) * (up_i . x) in one launch."""
         _check(load().qsf_hip_gate_up_act_dev(self.handle, _addr(x), _addr(out), activation,
                                               _stream(stream)), "qsf_hip_gate_up_act_dev")
+
+
+def prefill_pack_bytes(m: int, cols: int, bs: int) -> int:
+    return int(load().qsf_hip_prefill_pack_bytes(m, cols, bs))
+
+
+def prefill_pack(x_bf16, m: int, cols: int, bs: int, packed, stream=None) -> None:
+    """x bf16 [m][cols] into `packed` (prefill_pack_bytes bytes, 16-byte
+    aligned), shared by every 4-bit tensor of these cols and block size."""
+    _check(load().qsf_hip_prefill_pack_dev(_addr(x_bf16), m, cols, bs, _addr(packed), _stream(stream)),
+           "qsf_hip_prefill_pack_dev")
+
+
+def stream_read(tensors, sink, stream=None) -> None:
+    """One launch streaming the tensors' device bytes once (the bare-read floor)."""
+    n = len(tensors)
+    th = (_vp * n)(*[t.handle for t in tensors])
+    _check(load().qsf_hip_stream_read_dev(th, n, _addr(sink), _stream(stream)), "qsf_hip_stream_read_dev")
 
 
 def matvec_group(tensors, x, ys, stream=None) -> None:

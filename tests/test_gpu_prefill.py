@@ -157,3 +157,51 @@ def test_prefill_rejects_bad_input(hip):
     with pytest.raises(hip.QsfHipError):
         t4.prefill(xs[1:], 4, y)                # x not 16-byte aligned
     t4.free()
+
+
+@pytest.mark.parametrize("m,n,k,bs", [(37, 100, 256, 64), (513, 129, 4096, 64), (64, 96, 768, 256)])
+def test_packed_halves_equal_one_call(hip, m, n, k, bs):
+    """prefill_pack once + the packed GEMM of two tensors that share x give
+    the bits of one qsf_hip_prefill_4bit_dev call per tensor."""
+    torch = torch_cuda()
+    stream = torch.cuda.current_stream()
+    pa, xb = case(7 + m, m, n, k, bs)
+    pb, _ = case(8 + m, m, n, k, bs)
+    dx = torch.from_numpy(xb.view(np.int16).copy()).to("cuda:0")
+    ta, tb = hip.Tensor(pa, F.Q4, n, k, bs), hip.Tensor(pb, F.Q4, n, k, bs)
+    try:
+        packed = torch.empty(hip.prefill_pack_bytes(m, k, bs) + 256, dtype=torch.uint8, device="cuda:0")
+        paddr = (packed.data_ptr() + 255) & ~255
+        hip.prefill_pack(dx, m, k, bs, paddr, stream=stream)
+        outs = []
+        for t in (ta, tb):
+            y1 = torch.full((m, n), float("nan"), device="cuda:0")
+            y2 = torch.full((m, n), float("nan"), device="cuda:0")
+            t.prefill(dx, m, y1, stream=stream)
+            t.prefill_packed(paddr, m, y2, stream=stream)
+            outs.append((y1, y2))
+        torch.cuda.synchronize()
+        for y1, y2 in outs:
+            assert np.array_equal(y1.cpu().numpy().view(np.uint32), y2.cpu().numpy().view(np.uint32))
+    finally:
+        ta.free()
+        tb.free()
+
+
+def test_stream_read_floor_runs(hip):
+    """The bare-read diagnostic launch completes over tensors of every kind
+    (dense, outlier CSR, MXFP4) and stores nothing to its sink."""
+    torch = torch_cuda()
+    rng = np.random.default_rng(3)
+    ts = [hip.Tensor(F.quantize_matrix(F.gaussian(rng, (300, 1000), 0.02), F.Q4, 64), F.Q4, 300, 1000, 64),
+          hip.Tensor(F.quantize_matrix(F.heavy_tail_weights(rng, 64, 4096), F.Q2_OUTLIER, 64), F.Q2_OUTLIER,
+                     64, 4096, 64),
+          hip.Tensor(F.random_mxfp4(rng, 96, 2880), F.MXFP4, 96, 2880, 32)]
+    try:
+        sink = torch.zeros(1, dtype=torch.int32, device="cuda:0")
+        hip.stream_read(ts, sink, stream=torch.cuda.current_stream())
+        torch.cuda.synchronize()
+        assert int(sink.cpu()[0]) == 0
+    finally:
+        for t in ts:
+            t.free()
