@@ -283,12 +283,16 @@ __global__ __launch_bounds__(NT) void gemv_mfma_kernel(MfArgs a) {
         }
     } else {
         // every chunk loaded, at min(c, cols - 4) (cols >= 16), whatever the
-        // wave's quad count: no branch, so nothing waits for x here
+        // wave's quad count: no branch, so nothing waits for x here.  Slots
+        // past the wave's quads re-read its last quad (first-level cache
+        // hits), so the L2 serves each wave only the x it uses.
+        const int qlast = qspan > 0 ? qspan - 1 : 0;
 #pragma unroll
         for (int qi = 0; qi < QX; qi++)
 #pragma unroll
             for (int k = 0; k < XPQ / 4; k++)
-                xc[qi][k] = *reinterpret_cast<const f32x4_a4*>(a.x + min(xcol0(qi) + 4 * k, a.cols - 4));
+                xc[qi][k] = *reinterpret_cast<const f32x4_a4*>(
+                    a.x + min(xcol0(min(qi, qlast)) + 4 * k, a.cols - 4));
     }
     __builtin_amdgcn_sched_barrier(0);
     // every wave's x requests ahead of any wave's weights: the CU issues
