@@ -450,6 +450,26 @@ def profile_layers(torch, hip, steps, warmup):
     log(f"profile run: config 2 gate/up, {warmup} + {steps} launches done")
 
 
+def profile_decode_layer(torch, hip, steps, warmup):
+    """Eager launches of the layer step's dominant kernel only (the fused
+    residual + norm + gate/up + act launch over 32 layers' pairs), for
+    rocprofv3 counter passes."""
+    qt, bs, mats = cfg2_layer()
+    pairs = [hip.TensorPair(mats[4][1], mats[5][1], qt, mats[4][2], mats[4][3], bs) for _ in range(32)]
+    g = torch.Generator(device="cuda:0").manual_seed(41)
+    res, res2 = torch.randn(4096, device="cuda:0", generator=g), torch.empty(4096, device="cuda:0")
+    x = torch.randn(4096, device="cuda:0", generator=g)
+    w = torch.ones(4096, device="cuda:0")
+    out = torch.empty(mats[4][2], device="cuda:0")
+    stream = torch.cuda.current_stream()
+    for i in range(warmup + steps):
+        pairs[i % 32].residual_norm_gate_up_act(res, res2, x, w, 1e-5, out, 2, stream=stream)
+    torch.cuda.synchronize()
+    log(f"profile run: layer step gate/up, {warmup} + {steps} launches done")
+    for pr in pairs:
+        pr.free()
+
+
 def bench_layers(torch, hip, steps, warmup, with_cpu=True, cpu_budget=10.0):
     """Config 2: 32 decoder layers at 3-bit back to back.  A step is the
     whole stack: per layer q/k/v in one grouped launch, o, gate/up grouped,
@@ -888,6 +908,9 @@ def main():
         print(json.dumps(copy_calibration(torch, args.steps, args.warmup, args.copy_mib)), flush=True)
         return
     if args.profile:
+        if args.config == "layer":
+            profile_decode_layer(torch, qsf_hip, args.steps, args.warmup)
+            return
         cfg = int(args.config)
         if cfg == 2:
             profile_layers(torch, qsf_hip, args.steps, args.warmup)
