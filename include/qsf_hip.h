@@ -163,13 +163,12 @@ int qsf_hip_kernel_timing(int enable);
 int qsf_hip_kernel_timing_read(float* us, int max);
 
 /* Decode GEMV engine for the tensors uploaded from now on (no counterpart
- * in the reference).  1 (default): 3-bit tensors of at least 2^25 weights
- * (the 7B FFN projections) whose shape the int8 matrix-core kernel covers
- * (cols 16..16384) are stored in its fragment
+ * in the reference).  1 (default): 3-bit tensors whose shape the int8
+ * matrix-core kernel covers (cols 16..16384) are stored in its fragment
  * order and every decode GEMV over them (one-launch, gate/up, fused
  * residual + norm, table slots, prepared-x) takes that kernel; all other
  * tensors keep the on-disk order and the dot-product kernels.  2: the same
- * for every format and size.  0: on-disk order and dot-product
+ * for the 2- and 4-bit formats too.  0: on-disk order and dot-product
  * kernels for every tensor.  A tensor keeps the engine it was uploaded
  * with.  For A/B comparisons and tests; both engines meet the same 1e-5
  * bound, their results differ in fp32 rounding.  engine < 0 only queries.

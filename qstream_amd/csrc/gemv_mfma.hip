@@ -34,11 +34,12 @@
 //
 // Launch.  1024-thread workgroups, about one per CU.  A workgroup owns whole
 // 16-row groups of one matrix (so every row's sum is finished in LDS), its
-// 16 waves split the groups' tiles in quad-major order.  Every wave requests
-// x for its own quads first (all waves' x ahead of any weights), then its
-// first tile once x is in, turns x into digits in LDS while that tile
-// streams, and then keeps D tiles in flight in a register ring.  The fp16 outliers
-// of the workgroup's rows (CSR entries, contiguous) are requested after the
+// 16 waves split the groups' tiles in quad-major order.  The workgroup loads
+// x once, every thread a few columns (all of it ahead of any weights), each
+// wave requests its first tile once x is in, and the 1024 threads turn x
+// into digits in LDS together while those tiles stream; every wave then keeps
+// D tiles in flight in a register ring.  The fp16 outliers of the
+// workgroup's rows (CSR entries, contiguous) are requested after the
 // weights, turned into products in LDS, and summed per row in the final pass.
 #include "qsf_device.h"
 #include "qsf_hip_internal.h"
@@ -184,17 +185,7 @@ __device__ __forceinline__ int group_all(int v, OP op) {
     return v;
 }
 
-// LDS writes of this wave visible to its other lanes' reads: wait for the
-// wave's LDS operations alone (lgkmcnt(0); not vmcnt: the weight loads in
-// flight must not be waited for here), and keep the compiler from moving
-// LDS accesses across.
-__device__ __forceinline__ void wave_lds_sync() {
-    __builtin_amdgcn_s_waitcnt(0xC07F);                        // lgkmcnt(0), vmcnt/expcnt untouched
-    __builtin_amdgcn_wave_barrier();
-    asm volatile("" ::: "memory");
-}
-
-template <int FMT, int BS, int D, int QX, bool OUT, bool NORM>
+template <int FMT, int BS, int D, bool OUT, bool NORM>
 __global__ __launch_bounds__(NT) void gemv_mfma_kernel(MfArgs a) {
     static_assert(!(OUT && NORM), "NORM: no outlier tables");
     using F = MF<FMT, BS>;
@@ -211,7 +202,12 @@ __global__ __launch_bounds__(NT) void gemv_mfma_kernel(MfArgs a) {
     const MfArgs::Mat& M = a.mat[blockIdx.y];
     const int wgm = (int)blockIdx.x;
     asm volatile("" ::"s"(M.w), "s"(M.y), "s"(M.rows), "s"(M.gpm), "s"(M.rq), "s"(M.rr), "s"(a.x),
-                 "s"(a.cols), "s"(a.nq), "s"(a.nb));
+                 "s"(a.cols), "s"(a.nq), "s"(a.nb), "s"(a.o_dig), "s"(a.o_zero), "s"(a.o_meta), "s"(a.o_xq),
+                 "s"(a.o_xs), "s"(a.o_stash), "s"(a.o_rp), "s"(a.o_prod), "s"(a.prod_cap), "s"(a.act1));
+    if constexpr (OUT) asm volatile("" ::"s"(M.rp), "s"(M.oe), "s"(M.nent));
+    if constexpr (NORM)
+        asm volatile("" ::"s"(a.res_in), "s"(a.res_out), "s"(a.nw), "s"(a.bad), "s"(a.eps), "s"(a.o_xn),
+                     "s"(a.o_red));
     if (wgm >= M.gpm) return;                                 // (whole workgroup)
     const int rg0 = wgm * M.rq + min(wgm, M.rr);
     const int nrg = M.rq + (wgm < M.rr ? 1 : 0);
@@ -243,32 +239,24 @@ __global__ __launch_bounds__(NT) void gemv_mfma_kernel(MfArgs a) {
         for (int i = 0; i < TB / 4; i++) wv[k][4 * KP + i] = __builtin_nontemporal_load(tl + i);
     };
 
-    // 1. outliers: the workgroup's CSR bounds (its entries are contiguous)
-    uint32_t e0 = 0, e1 = 0, rpv = 0;
-    if constexpr (OUT) {
-        e0 = M.rp[row_a];
-        e1 = M.rp[row_b];
-        rpv = M.rp[min(row_a + t, row_b)];
-    }
-
-    // 2. x for the wave's own quads [qa, qa + qspan) (at most QX; the host
-    //    sees to it), XPQ columns a lane a quad: lane L holds columns
-    //    16 (L % 16)... of block L / 16.  Issued ahead of every weight load
-    //    (loads return in order, and x is waited for first); a wave with
-    //    fewer quads loads fewer, which does not disturb the waits for the
-    //    weights behind them.  NORM: the residual, the increment and the norm
-    //    weights of elements t + k * NT instead, as the residual + norm launch
-    //    loads them (only the passes that hold elements load; past the end a
+    // 2. x, cooperatively: in pass p thread t holds XPQ columns of block
+    //    64 p + t / 16 (lane t % 16 of it), the layout the digit rows are
+    //    built from; a workgroup covers 64 blocks a pass and every block in
+    //    at most kMaxCols / (64 BS) passes (XC 4-vectors a thread in all).
+    //    Issued ahead of every weight load (loads return in order, and x is
+    //    waited for first); chunks of passes past the blocks re-read the
+    //    thread's first (first-level cache hits: no branch, so the waits stay
+    //    exact).  NORM: the residual, the increment and the norm weights of
+    //    elements t + k * NT instead, as the residual + norm launch loads
+    //    them (only the passes that hold elements load; past the end a
     //    thread re-reads its first).
-    constexpr int XPQ = BS / 16;                              // x values a lane a quad
-    const int qa = nmy > 0 ? u0 / nrg : 0;
-    const int qspan = nmy > 0 ? (u1 - 1) / nrg - qa + 1 : 0;
-    // x chunks as 4-vectors (kept in registers; fixed up after the
-    // weights are issued, with element selects)
-    f32x4 xc[QX][XPQ / 4];
+    constexpr int XPQ = BS / 16;                              // x values a thread a pass
+    constexpr int NPASS = kMaxCols / (64 * BS);               // passes at most
+    const int nbp = 4 * nq;                                   // blocks incl. quad padding
+    const int npass = (nbp + 63) >> 6;
+    const int xl0 = (t >> 4) * BS + (t & 15) * XPQ;           // the thread's first column in pass 0
+    f32x4 xc[NPASS][XPQ / 4];
     float nr[kNormPerThread], nx[kNormPerThread], nwv[kNormPerThread];
-    const int xl0 = (lane >> 4) * BS + (lane & 15) * XPQ;   // the lane's first column in a quad
-    auto xcol0 = [=](int qi) __attribute__((always_inline)) { return 4 * (qa + qi) * BS + xl0; };
     if constexpr (NORM) {
         const int n = a.cols;
 #pragma unroll
@@ -282,17 +270,22 @@ __global__ __launch_bounds__(NT) void gemv_mfma_kernel(MfArgs a) {
             }
         }
     } else {
-        // every chunk loaded, at min(c, cols - 4) (cols >= 16), whatever the
-        // wave's quad count: no branch, so nothing waits for x here.  Slots
-        // past the wave's quads re-read its last quad (first-level cache
-        // hits), so the L2 serves each wave only the x it uses.
-        const int qlast = qspan > 0 ? qspan - 1 : 0;
 #pragma unroll
-        for (int qi = 0; qi < QX; qi++)
+        for (int p = 0; p < NPASS; p++)
 #pragma unroll
             for (int k = 0; k < XPQ / 4; k++)
-                xc[qi][k] = *reinterpret_cast<const f32x4_a4*>(
-                    a.x + min(xcol0(min(qi, qlast)) + 4 * k, a.cols - 4));
+                xc[p][k] = *reinterpret_cast<const f32x4_a4*>(
+                    a.x + min((p < npass ? p * 64 * BS : 0) + xl0 + 4 * k, a.cols - 4));
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // 2b. outliers: the workgroup's CSR bounds (its entries are contiguous),
+    //     behind x: they come from HBM, and x, waited for first, must not
+    //     wait for them
+    uint32_t e0 = 0, e1 = 0, rpv = 0;
+    if constexpr (OUT) {
+        e0 = M.rp[row_a];
+        e1 = M.rp[row_b];
+        rpv = M.rp[min(row_a + t, row_b)];
     }
     __builtin_amdgcn_sched_barrier(0);
     // every wave's x requests ahead of any wave's weights: the CU issues
@@ -300,18 +293,19 @@ __global__ __launch_bounds__(NT) void gemv_mfma_kernel(MfArgs a) {
     // x would queue behind the first waves' tiles
     if constexpr (!NORM) __syncthreads();
 
-    // 3. the first tile's weights, once x is in (requested earlier, a tile
-    //    of weights ahead of it delays the digits by its own latency); the
-    //    other slots once the digits are done
-    if constexpr (!NORM) __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): x is in
+    // 3. the first tile's weights, once x is in (issued with x, the whole
+    //    ring ahead of the digits measured slower); the other slots once the
+    //    digits are built
+    if constexpr (OUT) __builtin_amdgcn_s_waitcnt(0x0F73);   // vmcnt(3): x is in, the bounds may not be
+    else if constexpr (!NORM) __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): x is in
     issue(0, u0);
     __builtin_amdgcn_sched_barrier(0);
 
     // 3b. NORM: the residual add and the RMS norm of src/engine.c:1174-1187
     //     and 940-948 / 805-815 as residual_norm_kernel computes them (same
     //     thread count, elements and order, so the same bits); the normed x
-    //     goes to LDS, where the waves' preparation reads it.  Workgroup
-    //     (0, 0) stores the residual and the NaN check.
+    //     goes to LDS, where the preparation reads it.  Workgroup (0, 0)
+    //     stores the residual and the NaN check.
     if constexpr (NORM) {
         const int n = a.cols;
         float acc = 0.f;
@@ -352,35 +346,32 @@ __global__ __launch_bounds__(NT) void gemv_mfma_kernel(MfArgs a) {
             if (t + k * NT < n) xn[t + k * NT] = qsf::mul_rn(qsf::mul_rn(nr[k], inv), nwv[k]);
         __syncthreads();
     }
-    // NORM: the normed x from LDS
-    auto xn_v = [&](int qi, int k) __attribute__((always_inline)) {
-        return reinterpret_cast<const float*>(lds + a.o_xn)[xcol0(qi) + k];
-    };
 
-    // 4. the wave's own digits, quad by quad, wave-local (two waves sharing a
-    //    quad write the same bytes).  Phase 1: x -> X.  A lane's XPQ columns
-    //    lie in block 4q + L/16; block max of |x| as bits (Inf/NaN above every
-    //    finite value), shift, X = rint(x 2^sh) (exact: |x 2^sh| < 2^XB),
-    //    block sum of X in two exact halves, meta {f, f sum X}.  Phase 2:
-    //    one lane a (block, MFMA j, 4-position slice tq): the 4 multipliers of
-    //    the slice, biased by 0x80808080 so that byte d is digit d + 128,
-    //    byte-transposed into one dword of each digit row, re-biased to int8.
+    // 4. the digits, cooperatively.  Phase 1, a pass at a time: x -> X.  A
+    //    thread's XPQ columns lie in block 64 p + t / 16; block max of |x| as
+    //    bits (Inf/NaN above every finite value), shift, X = rint(x 2^sh)
+    //    (exact: |x 2^sh| < 2^XB), block sum of X in two exact halves, meta
+    //    {f, f sum X}.  Phase 2: one thread a (block, MFMA j, 4-position
+    //    slice tq): the 4 multipliers of the slice, biased by 0x80808080 so
+    //    that byte d is digit d + 128, byte-transposed into one dword of
+    //    each digit row, re-biased to int8.
     float2* meta = reinterpret_cast<float2*>(lds + a.o_meta);
     int* xq = reinterpret_cast<int*>(lds + a.o_xq);
     float* xs = reinterpret_cast<float*>(lds + a.o_xs);
     uint8_t* dig = lds + a.o_dig;
 #pragma unroll
-    for (int qi = 0; qi < QX; qi++) {
-      if (qi < qspan) {                                       // (uniform)
-        const int c0 = xcol0(qi);
+    for (int p = 0; p < NPASS; p++) {
+      if (p < npass) {                                        // (uniform)
+        const int c0 = p * 64 * BS + xl0;
         float v8[XPQ];
         if constexpr (NORM) {
+            const float* xn = reinterpret_cast<const float*>(lds + a.o_xn);
 #pragma unroll
-            for (int k = 0; k < XPQ; k++) v8[k] = c0 + k < a.cols ? xn_v(qi, k) : 0.0f;
+            for (int k = 0; k < XPQ; k++) v8[k] = c0 + k < a.cols ? xn[c0 + k] : 0.0f;
         } else {
 #pragma unroll
             for (int k = 0; k < XPQ / 4; k++) {
-                const f32x4 ch = xc[qi][k];
+                const f32x4 ch = xc[p][k];
                 const int c = c0 + 4 * k;
                 // in range: the chunk as read; straddling the last column: it
                 // was read at cols - 4, so column c + i sits at i + sh; past it: 0
@@ -414,51 +405,49 @@ __global__ __launch_bounds__(NT) void gemv_mfma_kernel(MfArgs a) {
         }
         hs = group_all<16>(hs, [](int u, int v) { return u + v; });
         ls = group_all<16>(ls, [](int u, int v) { return u + v; });
+        if (c0 < nbp * BS) {
 #pragma unroll
-        for (int k = 0; k < XPQ / 4; k++) {
-            reinterpret_cast<i32x4*>(xq + c0)[k] = i32x4{X[4 * k], X[4 * k + 1], X[4 * k + 2], X[4 * k + 3]};
-            if constexpr (OUT)
-                reinterpret_cast<f32x4*>(xs + c0)[k] = f32x4{v8[4 * k], v8[4 * k + 1], v8[4 * k + 2], v8[4 * k + 3]};
-        }
-        if ((lane & 15) == 0) {
-            const double tot = (double)hs * 65536.0 + (double)ls;           // exact
-            const float f = bad ? __builtin_nanf("") : ldexpf(FMT == QK_FMT_3 ? 0.25f : 1.0f, -sh);
-            meta[4 * (qa + qi) + (lane >> 4)] = make_float2(f, bad ? 0.0f : (float)(tot * ldexp(1.0, -sh)));
-        }
-        wave_lds_sync();
-#pragma unroll
-        for (int pz = 0; pz < NJ; pz += 4) {
-            const int idx = lane + 64 * (pz / 4);
-            if (idx < 16 * NJ) {
-                const int tq = idx & 3, bj = idx >> 2;        // bj = block-in-quad * NJ + j
-                const int bq = bj / NJ, j = bj - bq * NJ;
-                const int b = 4 * (qa + qi) + bq;
-                uint32_t V[4];
-#pragma unroll
-                for (int s4 = 0; s4 < 4; s4++) {
-                    int code, shift;
-                    pos_code<FMT>(j, 4 * tq + s4, code, shift);
-                    const uint32_t mlt = (uint32_t)xq[b * BS + code] << shift;
-                    V[s4] = (mlt + 0x80808080u) ^ 0x80808080u;
-                }
-                const uint32_t l01 = __builtin_amdgcn_perm(V[1], V[0], 0x05010400u);
-                const uint32_t h01 = __builtin_amdgcn_perm(V[1], V[0], 0x07030602u);
-                const uint32_t l23 = __builtin_amdgcn_perm(V[3], V[2], 0x05010400u);
-                const uint32_t h23 = __builtin_amdgcn_perm(V[3], V[2], 0x07030602u);
-                uint32_t* out = reinterpret_cast<uint32_t*>(dig + (size_t)(b * NJ + j) * 64) + tq;
-                out[0] = __builtin_amdgcn_perm(l23, l01, 0x05040100u);
-                out[4] = __builtin_amdgcn_perm(l23, l01, 0x07060302u);
-                out[8] = __builtin_amdgcn_perm(h23, h01, 0x05040100u);
-                out[12] = __builtin_amdgcn_perm(h23, h01, 0x07060302u);
+            for (int k = 0; k < XPQ / 4; k++) {
+                reinterpret_cast<i32x4*>(xq + c0)[k] = i32x4{X[4 * k], X[4 * k + 1], X[4 * k + 2], X[4 * k + 3]};
+                if constexpr (OUT)
+                    reinterpret_cast<f32x4*>(xs + c0)[k] =
+                        f32x4{v8[4 * k], v8[4 * k + 1], v8[4 * k + 2], v8[4 * k + 3]};
+            }
+            if ((t & 15) == 0) {
+                const double tot = (double)hs * 65536.0 + (double)ls;           // exact
+                const float f = bad ? __builtin_nanf("") : ldexpf(FMT == QK_FMT_3 ? 0.25f : 1.0f, -sh);
+                meta[c0 / BS] = make_float2(f, bad ? 0.0f : (float)(tot * ldexp(1.0, -sh)));
             }
         }
       }
     }
+    // the zero rows of the A operands
+    if (t < NJ * 4) reinterpret_cast<u32x4*>(lds + a.o_zero)[t] = u32x4{0u, 0u, 0u, 0u};
+    __syncthreads();
+    for (int idx = t; idx < nbp * NJ * 4; idx += NT) {
+        const int tq = idx & 3, bj = idx >> 2;                // bj = block * NJ + j
+        const int b = bj / NJ, j = bj - b * NJ;
+        uint32_t V[4];
+#pragma unroll
+        for (int s4 = 0; s4 < 4; s4++) {
+            int code, shift;
+            pos_code<FMT>(j, 4 * tq + s4, code, shift);
+            const uint32_t mlt = (uint32_t)xq[b * BS + code] << shift;
+            V[s4] = (mlt + 0x80808080u) ^ 0x80808080u;
+        }
+        const uint32_t l01 = __builtin_amdgcn_perm(V[1], V[0], 0x05010400u);
+        const uint32_t h01 = __builtin_amdgcn_perm(V[1], V[0], 0x07030602u);
+        const uint32_t l23 = __builtin_amdgcn_perm(V[3], V[2], 0x05010400u);
+        const uint32_t h23 = __builtin_amdgcn_perm(V[3], V[2], 0x07030602u);
+        uint32_t* out = reinterpret_cast<uint32_t*>(dig + (size_t)(b * NJ + j) * 64) + tq;
+        out[0] = __builtin_amdgcn_perm(l23, l01, 0x05040100u);
+        out[4] = __builtin_amdgcn_perm(l23, l01, 0x07060302u);
+        out[8] = __builtin_amdgcn_perm(h23, h01, 0x05040100u);
+        out[12] = __builtin_amdgcn_perm(h23, h01, 0x07060302u);
+    }
 #pragma unroll
     for (int k = 1; k < D; k++) issue(k, u0 + k);
-    // the zero rows of the A operands (every wave writes the same zeros)
-    for (int i = lane; i < NJ * 4; i += 64) reinterpret_cast<u32x4*>(lds + a.o_zero)[i] = u32x4{0u, 0u, 0u, 0u};
-    wave_lds_sync();
+    __syncthreads();
 
     // 5. outlier entries of the workgroup's rows, kEntAhead a thread
     //    (clamped indices: always loaded, so the waits stay exact)
@@ -665,9 +654,6 @@ int launch_mf(const qsf_hip_tensor* const* t, int n, int cols, const float* d_x,
         const int by_lds = (int)((room - fixed) / ((size_t)nq * 256 + (out ? 64 : 0)));
         nrg_fit = by_lds < nrg_fit ? by_lds : nrg_fit;
     }
-    // (a wave's run spans at most floor(nq / 16) + 2 quads; past 32 quads a
-    // row, one 16-row group a workgroup keeps it within ceil(nq / 16) <= 4)
-    if (nq > 32) nrg_fit = 1;
     if (nrg_fit < 1) return -2;
     // workgroups per matrix in proportion to its 16-row groups, about one a
     // CU in all; each takes whole groups, spread evenly
@@ -714,34 +700,16 @@ int launch_mf(const qsf_hip_tensor* const* t, int n, int cols, const float* d_x,
         else
             hipLaunchKernelGGL(kern, dim3(g, n), dim3(NT), off, s, a);
     };
-    // ring depth: the slots a wave's tiles need, up to the format's budget;
-    // quads a wave prepares x for: the most any wave's run spans
+    // ring depth: the slots a wave's tiles need, up to the format's budget
     const int per = (nrg_max * nq + NWAVE - 1) / NWAVE;
-    int span = 0;
-    for (int i = 0; i < n; i++)
-        for (int nr = a.mat[i].rq; nr <= a.mat[i].rq + (a.mat[i].rr ? 1 : 0); nr++) {
-            if (nr <= 0) continue;
-            const int tt = nr * nq;
-            for (int w = 0; w < NWAVE; w++) {
-                const int w0 = (w * tt) / NWAVE, w1 = ((w + 1) * tt) / NWAVE;
-                if (w1 > w0) span = (w1 - 1) / nr - w0 / nr + 1 > span ? (w1 - 1) / nr - w0 / nr + 1 : span;
-            }
-        }
-    if (span > 4) return -2;
-    auto go_d = [&](auto dc, auto qc) {
+    auto go_d = [&](auto dc) {
         constexpr int DD = decltype(dc)::value < F::DFIT ? decltype(dc)::value : F::DFIT;
-        constexpr int QQ = decltype(qc)::value;
-        if (out) go(gemv_mfma_kernel<FMT, BS, DD, QQ, true, false>);
-        else if (nm) go(gemv_mfma_kernel<FMT, BS, DD, QQ, false, true>);
-        else go(gemv_mfma_kernel<FMT, BS, DD, QQ, false, false>);
+        if (out) go(gemv_mfma_kernel<FMT, BS, DD, true, false>);
+        else if (nm) go(gemv_mfma_kernel<FMT, BS, DD, false, true>);
+        else go(gemv_mfma_kernel<FMT, BS, DD, false, false>);
     };
-    using I2 = std::integral_constant<int, 2>;
-    using I4 = std::integral_constant<int, 4>;
-    if (per <= 2) {
-        if (span <= 2) go_d(I2{}, I2{}); else go_d(I2{}, I4{});
-    } else {
-        if (span <= 2) go_d(I4{}, I2{}); else go_d(I4{}, I4{});
-    }
+    if (per <= 2) go_d(std::integral_constant<int, 2>{});
+    else go_d(std::integral_constant<int, 4>{});
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

@@ -121,8 +121,8 @@ int qk_gemv_pair_act_norm(const qsf_hip_tensor* t, const qk_norm_args* nm, const
 int qk_gemv_mfma(const qsf_hip_tensor* const* t, int n, const float* d_x, float* const* d_y,
                  int act1, const qk_norm_args* nm, hipStream_t s);
 /* Engine for tensors uploaded from now on: 1 (default) the matrix-core GEMV
- * and fragment order for 3-bit matrices of at least 2^25 weights where
- * qk_mfma_layout covers the shape, 2 the same for every format and size, 0 the dot-product kernels and on-disk
+ * and fragment order for the 3-bit formats where qk_mfma_layout covers the
+ * shape, 2 the same for every format, 0 the dot-product kernels and on-disk
  * order for all; < 0 only queries.  Returns the previous setting. */
 int qk_gemv_mfma_enable(int on);
 

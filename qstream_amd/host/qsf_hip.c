@@ -383,13 +383,11 @@ static qsf_hip_tensor* upload_locked(const void* host, int qt, int rows, int col
     t->n_outliers = n_out;
     /* device order of the blocks: fragment order where the matrix-core GEMV
      * is the engine for the format and covers the shape, else the on-disk
-     * order.  Engine 1 takes it for 3-bit matrices of at least 2^25 weights
-     * (the 7B FFN projections), where the 3-bit unpack is the costliest on
-     * the vector units and the launch is long enough to amortise the
-     * matrix-core kernel's longer prologue; 2 for every format and size. */
+     * order.  Engine 1 takes it for the 3-bit formats, whose unpack is the
+     * costliest on the vector units; 2 for every format. */
     const int engine = qk_gemv_mfma_enable(-1);
-    const int big3 = fmt == QK_FMT_3 && (uint64_t)rows * (uint64_t)cols >= ((uint64_t)1 << 25);
-    t->frag = fmt >= 0 && rows > 0 && (engine == 2 || (engine == 1 && big3)) && qk_mfma_layout(fmt, bs, cols);
+    t->frag = fmt >= 0 && rows > 0 && (engine == 2 || (engine == 1 && fmt == QK_FMT_3)) &&
+              qk_mfma_layout(fmt, bs, cols);
     t->frag_nq = (t->nb + 3) / 4;
     const size_t dev_blocks_bytes = t->frag ? qk_frag_bytes(rows, t->nb, t->block_bytes) : blocks_bytes;
 

@@ -176,8 +176,7 @@ def load(path: str = LIB_PATH) -> C.CDLL:
 
 def gemv_engine(engine: int = -1) -> int:
     """Decode GEMV engine for tensors uploaded from now on: 1 (default) the
-    int8 matrix-core kernel for 3-bit tensors of >= 2^25 weights, 2 for
-    every format and size it covers,
+    int8 matrix-core kernel for 3-bit tensors, 2 for every format it covers,
     0 the dot-product kernels for all; < 0 queries.  Returns the previous
     setting."""
     return int(load().qsf_hip_gemv_engine(engine))

@@ -51,7 +51,7 @@ def device_floats(ptr: int, n: int) -> np.ndarray:
 # Decode GEMV engines a parity module runs under (the setting applies to the
 # tensors uploaded while it holds): 0 the dot-product kernels for every
 # format, 2 the int8 matrix-core kernel wherever it covers the shape.  The
-# default, 1, is the matrix-core kernel for large 3-bit matrices and the
+# default, 1, is the matrix-core kernel for the 3-bit formats and the
 # dot-product kernels for the rest: the two together cover it.
 ENGINES = [0, 2]
 
