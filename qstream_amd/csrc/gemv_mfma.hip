@@ -296,8 +296,10 @@ __global__ __launch_bounds__(NT) void gemv_mfma_kernel(MfArgs a) {
     // 3. the first tile's weights, once x is in (issued with x, the whole
     //    ring ahead of the digits measured slower); the other slots once the
     //    digits are built
+#ifndef QSF_MF_T0_EARLY
     if constexpr (OUT) __builtin_amdgcn_s_waitcnt(0x0F73);   // vmcnt(3): x is in, the bounds may not be
     else if constexpr (!NORM) __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): x is in
+#endif
     issue(0, u0);
     __builtin_amdgcn_sched_barrier(0);
 
@@ -604,14 +606,16 @@ size_t lds_plan(MfArgs& a, int cols, int nrg_max, bool out, bool norm) {
 }
 
 template <int FMT, int BS>
-bool covers_mf(int cols) {
+bool covers_mf(int cols, bool outliers) {
     const int nb = (cols + BS - 1) / BS, nq = (nb + 3) / 4;
     if (cols < 16 || 4 * nq * BS > kMaxCols) return false;
     MfArgs a{};
     a.nq = nq;
-    // one 16-row group a workgroup, outliers (the larger plan) and the norm
-    return lds_plan<FMT, BS>(a, cols, 1, true, false) + (size_t)NT * 4 <= lds_cap_mf() &&
-           lds_plan<FMT, BS>(a, cols, 1, false, true) <= lds_cap_mf();
+    // one 16-row group a workgroup: plain, with the norm, and with outliers
+    // (the larger plan) where the tensor has an outlier table
+    return lds_plan<FMT, BS>(a, cols, 1, false, false) <= lds_cap_mf() &&
+           lds_plan<FMT, BS>(a, cols, 1, false, true) <= lds_cap_mf() &&
+           (!outliers || lds_plan<FMT, BS>(a, cols, 1, true, false) + (size_t)NT * 4 <= lds_cap_mf());
 }
 
 template <int FMT, int BS>
@@ -619,7 +623,7 @@ int launch_mf(const qsf_hip_tensor* const* t, int n, int cols, const float* d_x,
               int act1, const qk_norm_args* nm, hipStream_t s) {
     using F = MF<FMT, BS>;
     const int nb = (cols + BS - 1) / BS, nq = (nb + 3) / 4;
-    if (!covers_mf<FMT, BS>(cols)) return -2;
+    if (!covers_mf<FMT, BS>(cols, false)) return -2;
     MfArgs a{};
     a.x = d_x;
     a.n = n;
@@ -725,22 +729,22 @@ int launch_mf_bs(int bs, const qsf_hip_tensor* const* t, int n, int cols, const 
 }
 
 template <int FMT>
-bool covers_bs(int bs, int cols) {
+bool covers_bs(int bs, int cols, bool outliers) {
     switch (bs) {
-    case 64: return covers_mf<FMT, 64>(cols);
-    case 128: return covers_mf<FMT, 128>(cols);
+    case 64: return covers_mf<FMT, 64>(cols, outliers);
+    case 128: return covers_mf<FMT, 128>(cols, outliers);
     default: return false;
     }
 }
 
 }  // namespace
 
-extern "C" int qk_mfma_layout(int fmt, int bs, int cols) {
+extern "C" int qk_mfma_layout(int fmt, int bs, int cols, int outliers) {
     switch (fmt) {
-    case QK_FMT_2: return covers_bs<QK_FMT_2>(bs, cols);
-    case QK_FMT_3: return covers_bs<QK_FMT_3>(bs, cols);
-    case QK_FMT_4: return covers_bs<QK_FMT_4>(bs, cols);
-    case QK_FMT_4SYM: return covers_bs<QK_FMT_4SYM>(bs, cols);
+    case QK_FMT_2: return covers_bs<QK_FMT_2>(bs, cols, outliers != 0);
+    case QK_FMT_3: return covers_bs<QK_FMT_3>(bs, cols, outliers != 0);
+    case QK_FMT_4: return covers_bs<QK_FMT_4>(bs, cols, outliers != 0);
+    case QK_FMT_4SYM: return covers_bs<QK_FMT_4SYM>(bs, cols, outliers != 0);
     default: return 0;
     }
 }

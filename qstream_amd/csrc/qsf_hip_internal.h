@@ -67,8 +67,9 @@ size_t qk_frag_bytes(int rows, int nb, int block_bytes);
 /* byte j of block b of row `row` in fragment order */
 size_t qk_frag_offset(size_t row, int b, int j, int nq, int block_bytes);
 /* 1 when the matrix-core GEMV covers tensors of this format (QK_FMT_*),
- * block size and column count, so that they are uploaded in fragment order */
-int qk_mfma_layout(int fmt, int bs, int cols);
+ * block size and column count (with an outlier table when `outliers`), so
+ * that they are uploaded in fragment order */
+int qk_mfma_layout(int fmt, int bs, int cols, int outliers);
 
 /* Per-call prepared activation: block-fixed-point digits of x. */
 size_t qk_xprep_bytes(int fmt, int bs, int cols);

@@ -387,7 +387,7 @@ static qsf_hip_tensor* upload_locked(const void* host, int qt, int rows, int col
      * costliest on the vector units; 2 for every format. */
     const int engine = qk_gemv_mfma_enable(-1);
     t->frag = fmt >= 0 && rows > 0 && (engine == 2 || (engine == 1 && fmt == QK_FMT_3)) &&
-              qk_mfma_layout(fmt, bs, cols);
+              qk_mfma_layout(fmt, bs, cols, is_outlier(qt));
     t->frag_nq = (t->nb + 3) / 4;
     const size_t dev_blocks_bytes = t->frag ? qk_frag_bytes(rows, t->nb, t->block_bytes) : blocks_bytes;
 
