@@ -527,10 +527,11 @@ def bench_decode_layer(torch, hip, steps, warmup, position=1023):
     hidden 4096, 32 heads of 128, intermediate 11008, 3-bit block 128
     weights): residual + NaN check + attention RMSNorm + q/k/v (one grouped
     launch: the previous layer's down output joins the residual, whose norm
-    the q/k/v rows multiply), RoPE + int8 KV store (one launch), attention
-    over `position` + 1 cached positions (two launches), o, residual + FFN
-    RMSNorm + gate/up with SiLU x up (one launch over the interleaved gate/up
-    pair), down -- 7 launches, no host round trip.  The residual alternates
+    the q/k/v rows multiply), RoPE + int8 KV store + attention over
+    `position` + 1 cached positions (two launches: rotation, store and the
+    chunk pass in one, then the chunk combine), o, residual + FFN RMSNorm +
+    gate/up with SiLU x up (one launch over the interleaved gate/up pair),
+    down -- 6 launches, no host round trip.  The residual alternates
     between two buffers (a fused launch reads one while it writes the
     other).  Steps cycle over 32 layers' distinct weights and
     KV caches (2.9 GB), so neither stays in the MALL.  Bytes per step: the
@@ -565,10 +566,8 @@ def bench_decode_layer(torch, hip, steps, warmup, position=1023):
         ts = layers[li]
         hip.residual_norm_matvec_group(ts[0:3], res, res2, ys["down"], an_w, 1e-5,
                                        [ys["q"], ys["k"], ys["v"]], bad=bad, stream=stream)
-        rope.apply_and_store(ys["q"], ys["k"], ys["v"], nh, nh, position, kcs[li], vcs[li], kss[li],
-                             vss[li], max_seq, stream=stream)
-        hip.attention(ys["q"], kcs[li], vcs[li], kss[li], vss[li], max_seq, nh, nh, hd, position, attn,
-                      stream=stream)
+        rope.apply_store_attend(ys["q"], ys["k"], ys["v"], nh, nh, position, kcs[li], vcs[li], kss[li],
+                                vss[li], max_seq, attn, stream=stream)
         hip.matvec_group(ts[3:4], attn, [ys["o"]], stream=stream)
         pairs[li].residual_norm_gate_up_act(res2, res, ys["o"], fn_w, 1e-5, ys["gate"], 2, stream=stream)
         hip.matvec_group(ts[4:5], ys["gate"], [ys["down"]], stream=stream)
@@ -842,7 +841,8 @@ def run_config(torch, hip, key: str, args, cpu_budget: float, cache: dict) -> di
                          "int8 KV cache)",
                     config={"workload": f"device-resident 7B decoder layer step (3-bit block 128), "
                                         f"attention over {r['position'] + 1} cached positions, "
-                                        f"7 launches (residual + norm fused into q/k/v and into gate/up + act*mul; RoPE + KV store fused)",
+                                        f"6 launches (residual + norm fused into q/k/v and into gate/up + "
+                                        f"act*mul; RoPE + KV store fused into the attention chunk pass)",
                             "us_per_layer": round(r["ms_per_step"] * 1e3, 3),
                             "bytes_per_step": r["bytes_per_step"], "weight_bytes": r["weight_bytes"],
                             "kv_bytes": r["kv_bytes"],

@@ -384,6 +384,18 @@ int qsf_hip_residual_norm_gate_up_act_dev(const qsf_hip_tensor* pair, const floa
 int qsf_hip_rope_kv_store_dev(const qsf_hip_rope* r, float* d_q, float* d_k, const float* d_v,
                               int n_heads, int n_kv_heads, int position, int8_t* d_kc, int8_t* d_vc,
                               float* d_ks, float* d_vs, int max_seq, void* stream);
+/* qsf_hip_rope_kv_store_dev followed by qsf_hip_attention_dev (the
+ * sequence src/engine.c:870-923 runs: apply_rope, kv_cache_store, the
+ * attention loop), in two launches instead of three for head_dim 64, 128
+ * and 256: the cache rows, scales and d_out equal the two calls' bit for
+ * bit.  On return d_q and d_k hold either their inputs or the rotated
+ * values (rotated only for other head dims, which run the two calls):
+ * neither is read after this step.  Same limits and workspace as
+ * qsf_hip_attention_dev.  No counterpart in the reference, which runs the
+ * three steps one after another. */
+int qsf_hip_rope_kv_attention_dev(const qsf_hip_rope* r, float* d_q, float* d_k, const float* d_v,
+                                  int n_heads, int n_kv_heads, int position, int8_t* d_kc, int8_t* d_vc,
+                                  float* d_ks, float* d_vs, int max_seq, float* d_out, void* stream);
 /* Embedding lookup, src/engine.c:709-765: row `token` of a blockwise table
  * uploaded with qsf_hip_tensor_upload (rows = vocab, cols = hidden),
  * dequantised bit-exactly; or of an FP16 table [vocab][hd] in device memory.

@@ -447,6 +447,179 @@ __global__ __launch_bounds__(64) void rope_kv_kernel(float* q, float* k, const f
     }
 }
 
+// RoPE + int8 KV store + the chunk pass of attention in one launch, for
+// head_dim = 16 HC in {64, 128, 256}: the cache rows, scales and chunk
+// records of rope_kv_kernel followed by attention_part_fast_kernel, bit for
+// bit.  Every workgroup (head, chunk) rotates its head's q itself, into LDS.
+// The position being decoded lies in the last chunk: its workgroups rotate
+// the new k and quantise k and v with the KV store's arithmetic, and use
+// those codes for that row instead of reading the cache; the first head of
+// each KV group also stores them, with the scales.  No other workgroup
+// needs that row, so the store orders with nothing.  q and k stay as they
+// were: several workgroups read each of them, so none may rotate them in
+// place.
+template <int HC>
+__global__ __launch_bounds__(ATT_THREADS) void rope_attention_part_kernel(
+    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
+    const float* __restrict__ freq, int8_t* kc, int8_t* vc, float* ks, float* vs, int max_seq, int groups,
+    int position, int nsplit, float* __restrict__ ws) {
+    constexpr int HD = 16 * HC, KH = HC / 2, VJ = ATT_CHUNK * HC / ATT_THREADS, HP = HD / 2;
+    static_assert(HD <= ATT_THREADS && ATT_THREADS % HC == 0 && HP <= 128, "one q pair a thread");
+    __shared__ float qs[HD];
+    __shared__ float ew[ATT_CHUNK];                      // exp(score - m) * v_scale per position
+    __shared__ float red[ATT_THREADS / 64];
+    __shared__ float part[ATT_THREADS][17];
+    __shared__ __align__(16) int8_t newc[2][HD];         // the new row's K and V codes
+    __shared__ float news[2];                            // and their scales
+    const int h = blockIdx.x, chunk = blockIdx.y, kvh = h / groups, t = threadIdx.x;
+    const int p0 = chunk * ATT_CHUNK, np = min(ATT_CHUNK, position + 1 - p0);
+    const bool last = chunk == nsplit - 1;               // holds the new row, np - 1
+    const size_t row0 = (size_t)kvh * max_seq + p0;
+    // 1. all loads.  In the last chunk the rows before the new one; its own
+    //    slot loads the row before it (or, when it starts the chunk, the
+    //    slot itself, whatever it holds) and is replaced below.
+    const int kp = t >> 1, kh = t & 1;
+    const int nold = last ? max(np - 1, 1) : np;
+    const int kpc = min(kp, nold - 1);
+    const att_u32x4* kr = reinterpret_cast<const att_u32x4*>(kc + (row0 + kpc) * HD) + kh * KH;
+    att_u32x4 kv[KH];
+#pragma unroll
+    for (int j = 0; j < KH; j++) kv[j] = kr[j];
+    float kscale = ks[row0 + kpc];
+    float vscale = vs[row0 + kpc];
+    const att_u32x4* vr = reinterpret_cast<const att_u32x4*>(vc + row0 * HD);
+    att_u32x4 vv[VJ];
+#pragma unroll
+    for (int j = 0; j < VJ; j++) {
+        const int i = t + ATT_THREADS * j;
+        vv[j] = vr[min(i / HC, nold - 1) * HC + i % HC];
+    }
+    // q pair t of the head, and in the last chunk k and v pair t
+    float q0 = 0.f, q1 = 0.f, nk[2] = {0.f, 0.f}, nv[2] = {0.f, 0.f};
+    if (t < HP) {
+        q0 = q[(size_t)h * HD + 2 * t];
+        q1 = q[(size_t)h * HD + 2 * t + 1];
+        if (last) {
+            nk[0] = k[(size_t)kvh * HD + 2 * t];
+            nk[1] = k[(size_t)kvh * HD + 2 * t + 1];
+            nv[0] = v[(size_t)kvh * HD + 2 * t];
+            nv[1] = v[(size_t)kvh * HD + 2 * t + 1];
+        }
+        rope_pair(q0, q1, freq, t, position);
+        qs[2 * t] = q0;
+        qs[2 * t + 1] = q1;
+    }
+    if (last) {
+        if (t < HP) rope_pair(nk[0], nk[1], freq, t, position);
+        // absmax as the KV store takes it (NaN compares false and drops out)
+        float ak = 0.f, av = 0.f;
+#pragma unroll
+        for (int e = 0; e < 2; e++) {
+            const float a = nk[e] < 0 ? -nk[e] : nk[e], b = nv[e] < 0 ? -nv[e] : nv[e];
+            ak = a > ak ? a : ak;
+            av = b > av ? b : av;
+        }
+        for (int off = 32; off > 0; off >>= 1) {
+            const float ok = __shfl_xor(ak, off, 64), ov = __shfl_xor(av, off, 64);
+            ak = ok > ak ? ok : ak;
+            av = ov > av ? ov : av;
+        }
+        if (HP > 64) {                                   // pairs in waves 0 and 1
+            if (t == 0 || t == 64) {
+                red[t >> 5] = ak;
+                red[(t >> 5) + 1] = av;
+            }
+            __syncthreads();
+            ak = red[2] > red[0] ? red[2] : red[0];
+            av = red[3] > red[1] ? red[3] : red[1];
+        }
+        const bool lk = ak > 1e-30f, lv = av > 1e-30f;
+        const float ik = lk ? __fdiv_rn(127.0f, ak) : 0.f, iv = lv ? __fdiv_rn(127.0f, av) : 0.f;
+        const bool store = h % groups == 0;
+        const size_t row = (size_t)kvh * max_seq + position;
+        if (t < HP) {
+#pragma unroll
+            for (int e = 0; e < 2; e++) {
+                const int8_t ck = lk ? kv_code(nk[e], ik) : (int8_t)0, cv = lv ? kv_code(nv[e], iv) : (int8_t)0;
+                newc[0][2 * t + e] = ck;
+                newc[1][2 * t + e] = cv;
+                if (store) {
+                    kc[row * HD + 2 * t + e] = ck;
+                    vc[row * HD + 2 * t + e] = cv;
+                }
+            }
+        }
+        if (t == 0) {
+            news[0] = __fdiv_rn(ak, 127.0f);
+            news[1] = __fdiv_rn(av, 127.0f);
+            if (store) {
+                ks[row] = news[0];
+                vs[row] = news[1];
+            }
+        }
+    }
+    __syncthreads();
+    if (last) {                                          // the new row in place of the loaded one
+        if (kp == np - 1) {
+            const att_u32x4* nkr = reinterpret_cast<const att_u32x4*>(newc[0]) + kh * KH;
+#pragma unroll
+            for (int j = 0; j < KH; j++) kv[j] = nkr[j];
+            kscale = news[0];
+            vscale = news[1];
+        }
+#pragma unroll
+        for (int j = 0; j < VJ; j++) {
+            const int i = t + ATT_THREADS * j;
+            if (i / HC == np - 1) vv[j] = reinterpret_cast<const att_u32x4*>(newc[1])[i % HC];
+        }
+    }
+    // 2. scores and the chunk's softmax terms, as attention_part_fast_kernel
+    const float inv_sqrt_d = __fdiv_rn(1.0f, __fsqrt_rn((float)HD));
+    float dot = 0.f;
+#pragma unroll
+    for (int j = 0; j < KH; j++)
+#pragma unroll
+        for (int b = 0; b < 16; b++)
+            dot = fmaf(qs[16 * (kh * KH + j) + b], qsf::mul_rn(sbyte(kv[j][b >> 2], b & 3), kscale), dot);
+    dot += __shfl_xor(dot, 1, 64);
+    const bool mine = kh == 0 && kp < np;
+    const float sc = kp < np ? qsf::mul_rn(dot, inv_sqrt_d) : -INFINITY;
+    float m = sc;
+    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+    if ((t & 63) == 0) red[t >> 6] = m;                  // red's absmax use ended at the barrier
+    __syncthreads();
+    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    const float e = mine ? expf(sc - m) : 0.f;
+    if (mine) ew[kp] = qsf::mul_rn(e, vscale);
+    const float l = block_sum(e, red);                   // also orders the ew writes
+    // 3. weighted V
+    float acc[16];
+#pragma unroll
+    for (int b = 0; b < 16; b++) acc[b] = 0.f;
+#pragma unroll
+    for (int j = 0; j < VJ; j++) {
+        const int p = (t + ATT_THREADS * j) / HC;
+        const float w = p < np ? ew[p] : 0.f;
+#pragma unroll
+        for (int b = 0; b < 16; b++) acc[b] = fmaf(w, sbyte(vv[j][b >> 2], b & 3), acc[b]);
+    }
+#pragma unroll
+    for (int b = 0; b < 16; b++) part[t][b] = acc[b];
+    __syncthreads();
+    float* rec = ws + ((size_t)h * nsplit + chunk) * (HD + 2);
+    if (t < HD) {
+        const int c = t >> 4, b = t & 15;
+        float o = 0.f;
+#pragma unroll
+        for (int r = 0; r < ATT_THREADS / HC; r++) o += part[c + HC * r][b];
+        rec[2 + t] = o;
+    }
+    if (t == 0) {
+        rec[0] = m;
+        rec[1] = l;
+    }
+}
+
 // One row of a blockwise table: value i = scale * q + zero (4-bit sym:
 // scale * q), each product and sum rounded as in src/quant.c:95-177.
 __global__ __launch_bounds__(256) void embed_row_kernel(const uint8_t* __restrict__ blocks, int fmt,
@@ -588,6 +761,35 @@ extern "C" int qk_rope_kv_store(float* q, float* k, const float* v, const float*
         return -2;
     hipLaunchKernelGGL(rope_kv_kernel, dim3(n_heads + 2 * n_kv), dim3(64), 0, s, q, k, v, freq, head_dim,
                        n_heads, position, kc, vc, ks, vs, max_seq);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+extern "C" int qk_rope_kv_attention(float* q, float* k, const float* v, const float* freq, int head_dim,
+                                    int n_heads, int n_kv, int position, int8_t* kc, int8_t* vc, float* ks,
+                                    float* vs, int max_seq, float* out, void* ws, hipStream_t s) {
+    const int seq = position + 1;
+    if (head_dim <= 0 || head_dim > 256 || head_dim % 16 || n_heads <= 0 || n_kv <= 0 || n_heads % n_kv ||
+        position < 0 || position >= max_seq || seq > ATT_MAX_SEQ)
+        return -2;
+    if (head_dim != 64 && head_dim != 128 && head_dim != 256) {
+        const int rc = qk_rope_kv_store(q, k, v, freq, head_dim, n_heads, n_kv, position, kc, vc, ks, vs,
+                                        max_seq, s);
+        return rc ? rc : qk_attention(q, kc, vc, ks, vs, max_seq, n_heads, n_kv, head_dim, position, out, ws, s);
+    }
+    const int nsplit = (seq + ATT_CHUNK - 1) / ATT_CHUNK, groups = n_heads / n_kv;
+    const dim3 grid(n_heads, nsplit), block(ATT_THREADS);
+    float* part = (float*)ws;
+    if (head_dim == 64)
+        hipLaunchKernelGGL(rope_attention_part_kernel<4>, grid, block, 0, s, q, k, v, freq, kc, vc, ks, vs,
+                           max_seq, groups, position, nsplit, part);
+    else if (head_dim == 128)
+        hipLaunchKernelGGL(rope_attention_part_kernel<8>, grid, block, 0, s, q, k, v, freq, kc, vc, ks, vs,
+                           max_seq, groups, position, nsplit, part);
+    else
+        hipLaunchKernelGGL(rope_attention_part_kernel<16>, grid, block, 0, s, q, k, v, freq, kc, vc, ks, vs,
+                           max_seq, groups, position, nsplit, part);
+    hipLaunchKernelGGL(attention_combine_kernel, dim3(n_heads), dim3(256), 0, s, (const float*)ws, head_dim,
+                       nsplit, out);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

@@ -296,10 +296,8 @@ __global__ __launch_bounds__(NT) void gemv_mfma_kernel(MfArgs a) {
     // 3. the first tile's weights, once x is in (issued with x, the whole
     //    ring ahead of the digits measured slower); the other slots once the
     //    digits are built
-#ifndef QSF_MF_T0_EARLY
     if constexpr (OUT) __builtin_amdgcn_s_waitcnt(0x0F73);   // vmcnt(3): x is in, the bounds may not be
     else if constexpr (!NORM) __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): x is in
-#endif
     issue(0, u0);
     __builtin_amdgcn_sched_barrier(0);
 

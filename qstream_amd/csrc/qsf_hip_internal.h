@@ -217,6 +217,13 @@ int qk_residual_norm(float* res, const float* x, int n, int* bad, const float* w
 int qk_rope_kv_store(float* q, float* k, const float* v, const float* freq, int head_dim, int n_heads,
                      int n_kv, int position, int8_t* kc, int8_t* vc, float* ks, float* vs, int max_seq,
                      hipStream_t s);
+/* qk_rope_kv_store then qk_attention, for head_dim 64, 128 or 256 in two
+ * launches (RoPE, KV store and the chunk pass in one); other head dims run
+ * the two calls.  The cache, scales and out are theirs bit for bit; q and
+ * k are rotated in place only on the two-call path. */
+int qk_rope_kv_attention(float* q, float* k, const float* v, const float* freq, int head_dim, int n_heads,
+                         int n_kv, int position, int8_t* kc, int8_t* vc, float* ks, float* vs, int max_seq,
+                         float* out, void* ws, hipStream_t s);
 int qk_embed_row(const qsf_hip_tensor* t, int token, float* out, hipStream_t s);
 int qk_embed_row_fp16(const uint16_t* table, int hd, int token, float* out, hipStream_t s);
 

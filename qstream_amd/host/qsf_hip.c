@@ -1053,6 +1053,26 @@ int qsf_hip_rope_kv_store_dev(const qsf_hip_rope* r, float* d_q, float* d_k, con
                                     d_kc, d_vc, d_ks, d_vs, max_seq, pick_stream(stream)));
 }
 
+int qsf_hip_rope_kv_attention_dev(const qsf_hip_rope* r, float* d_q, float* d_k, const float* d_v,
+                                  int n_heads, int n_kv_heads, int position, int8_t* d_kc, int8_t* d_vc,
+                                  float* d_ks, float* d_vs, int max_seq, float* d_out, void* stream) {
+    static const char fn[] = "qsf_hip_rope_kv_attention_dev";
+    if (!r || n_heads <= 0 || n_kv_heads <= 0 || !d_q || !d_k || !d_v || !d_kc || !d_vc || !d_ks || !d_vs ||
+        !d_out || position < 0 || position >= max_seq)
+        return fail(E_INVALID, "%s: bad arguments (position %d of %d)", fn, position, max_seq);
+    pthread_mutex_lock(&g_lock);
+    int rc = g_dev.ready ? E_OK : fail(E_INVALID, "qsf_hip: not initialised");
+    if (rc == E_OK)
+        rc = ensure_dev(&g_dev.att_ws, &g_dev.att_ws_bytes,
+                        qk_attention_ws_bytes(n_heads, r->head_dim, position));
+    if (rc == E_OK)
+        rc = glue_rc(fn, qk_rope_kv_attention(d_q, d_k, d_v, r->d_freq, r->head_dim, n_heads, n_kv_heads,
+                                              position, d_kc, d_vc, d_ks, d_vs, max_seq, d_out, g_dev.att_ws,
+                                              pick_stream(stream)));
+    pthread_mutex_unlock(&g_lock);
+    return rc;
+}
+
 int qsf_hip_embed_row_dev(const qsf_hip_tensor* t, int token, float* d_out, void* stream) {
     if (!t || !d_out || token < 0 || token >= t->rows)
         return fail(E_INVALID, "qsf_hip_embed_row_dev: bad arguments (token %d)", token);

@@ -39,7 +39,7 @@ EXPORTS = (
     "qsf_hip_rms_norm_dev", "qsf_hip_layer_norm_dev", "qsf_hip_rope_create", "qsf_hip_rope_free",
     "qsf_hip_rope_dev", "qsf_hip_kv_store_dev", "qsf_hip_attention_dev", "qsf_hip_act_mul_dev",
     "qsf_hip_gate_up_act_dev", "qsf_hip_residual_dev", "qsf_hip_embed_row_dev", "qsf_hip_embed_row_fp16_dev",
-    "qsf_hip_residual_norm_dev", "qsf_hip_rope_kv_store_dev",
+    "qsf_hip_residual_norm_dev", "qsf_hip_rope_kv_store_dev", "qsf_hip_rope_kv_attention_dev",
     "qsf_hip_residual_norm_matvec_group_dev", "qsf_hip_residual_norm_gate_up_act_dev",
     "qsf_hip_crc32", "qsf_hip_model_load", "qsf_hip_model_load_mem", "qsf_hip_model_free", "qsf_hip_model_get_info",
     "qsf_hip_model_tensor", "qsf_hip_model_vector", "qsf_hip_model_embedding",
@@ -138,10 +138,12 @@ def load(path: str = LIB_PATH) -> C.CDLL:
     L.qsf_hip_residual_norm_matvec_group_dev.argtypes = [_vp, _i, _vp, _vp, _vp, _vp, _vp, _f, _vp, _vp]
     L.qsf_hip_residual_norm_gate_up_act_dev.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _f, _vp, _i, _vp]
     L.qsf_hip_rope_kv_store_dev.argtypes = [_vp, _vp, _vp, _vp, _i, _i, _i, _vp, _vp, _vp, _vp, _i, _vp]
+    L.qsf_hip_rope_kv_attention_dev.argtypes = [_vp, _vp, _vp, _vp, _i, _i, _i, _vp, _vp, _vp, _vp, _i, _vp,
+                                                _vp]
     for n in ("qsf_hip_rms_norm_dev", "qsf_hip_layer_norm_dev", "qsf_hip_rope_dev",
               "qsf_hip_kv_store_dev", "qsf_hip_attention_dev", "qsf_hip_act_mul_dev",
               "qsf_hip_gate_up_act_dev", "qsf_hip_residual_dev", "qsf_hip_embed_row_dev", "qsf_hip_embed_row_fp16_dev",
-              "qsf_hip_residual_norm_dev", "qsf_hip_rope_kv_store_dev",
+              "qsf_hip_residual_norm_dev", "qsf_hip_rope_kv_store_dev", "qsf_hip_rope_kv_attention_dev",
               "qsf_hip_residual_norm_matvec_group_dev", "qsf_hip_residual_norm_gate_up_act_dev"):
         getattr(L, n).restype = _i
     L.qsf_hip_crc32.argtypes = [_vp, C.c_size_t]
@@ -474,6 +476,16 @@ class Rope:
                                                 n_kv, position, _addr(kc), _addr(vc), _addr(ks),
                                                 _addr(vs), max_seq, _stream(stream)),
                "qsf_hip_rope_kv_store_dev")
+
+    def apply_store_attend(self, q, k, v, n_heads, n_kv, position, kc, vc, ks, vs, max_seq, out,
+                           stream=None) -> None:
+        """apply_and_store then attention(), with the RoPE, the KV store and
+        the attention's chunk pass in one launch for head_dim 64/128/256;
+        q and k are not read afterwards (rotated in place or not)."""
+        _check(load().qsf_hip_rope_kv_attention_dev(self.handle, _addr(q), _addr(k), _addr(v), n_heads, n_kv,
+                                                    position, _addr(kc), _addr(vc), _addr(ks), _addr(vs),
+                                                    max_seq, _addr(out), _stream(stream)),
+               "qsf_hip_rope_kv_attention_dev")
 
     def free(self) -> None:
         if self.handle:

@@ -351,3 +351,48 @@ def test_rope_kv_store_equals_separate_calls(hip, nh, nkv, hd, position):
         outs.append([host(a).view(np.uint8) for a in (dq, dk, kc, vc, ks, vs)])
     for name, a, c in zip(("q", "k", "kc", "vc", "ks", "vs"), *outs):
         assert np.array_equal(a, c), name
+
+
+@pytest.mark.parametrize("nh,nkv,hd,position", [(32, 32, 128, 1023), (32, 8, 128, 127), (32, 8, 128, 128),
+                                                (8, 2, 64, 300), (8, 8, 64, 0), (4, 4, 256, 77),
+                                                (4, 2, 256, 256), (16, 4, 256, 2050), (6, 2, 80, 130)])
+def test_rope_kv_attention_equals_separate_calls(hip, nh, nkv, hd, position):
+    """RoPE + KV store + attention in one call (two launches for head_dim
+    64/128/256, the new row's codes used from LDS) against the RoPE + KV
+    store launch followed by attention: the cache row, the scales and the
+    attention output bit for bit, the older rows untouched.  Positions at a
+    chunk's first row (128, 256, 0) and last (127), GQA and MHA; hd 80 runs
+    the two-call path."""
+    torch = torch_cuda()
+    rng = np.random.default_rng(3 * nh + hd + position)
+    max_seq = position + 3
+    q = rng.standard_normal(nh * hd).astype(np.float32)
+    k = rng.standard_normal(nkv * hd).astype(np.float32)
+    v = rng.standard_normal(nkv * hd).astype(np.float32)
+    k[:hd] = 0.0                               # a zero head: scale 0, codes 0
+    v[-hd:] *= 1e3                             # a large one
+    kc0 = rng.integers(-127, 128, (nkv, max_seq, hd), dtype=np.int8)
+    vc0 = rng.integers(-127, 128, (nkv, max_seq, hd), dtype=np.int8)
+    ks0 = (0.02 * rng.random((nkv, max_seq))).astype(np.float32)
+    vs0 = (0.02 * rng.random((nkv, max_seq))).astype(np.float32)
+    rope = hip.Rope(hd, 500000.0)
+    outs = []
+    for fused in (False, True):
+        dq, dk, dv = dev(q), dev(k), dev(v)
+        kc, vc, ks, vs = (torch.from_numpy(a.copy()).to("cuda:0") for a in (kc0, vc0, ks0, vs0))
+        out = torch.full((nh * hd,), np.nan, device="cuda:0")
+        if fused:
+            rope.apply_store_attend(dq, dk, dv, nh, nkv, position, kc, vc, ks, vs, max_seq, out, stream=_s())
+        else:
+            rope.apply_and_store(dq, dk, dv, nh, nkv, position, kc, vc, ks, vs, max_seq, stream=_s())
+            hip.attention(dq, kc, vc, ks, vs, max_seq, nh, nkv, hd, position, out, stream=_s())
+        outs.append([host(a).view(np.uint8) for a in (kc, vc, ks, vs, out)])
+    for name, a, c in zip(("kc", "vc", "ks", "vs", "out"), *outs):
+        assert np.array_equal(a, c), name
+    kc1 = outs[1][0].view(np.int8).reshape(nkv, max_seq, hd)
+    keep = np.ones(max_seq, bool)
+    keep[position] = False
+    assert np.array_equal(kc1[:, keep], kc0[:, keep])
+    assert not kc1[0, position].any()          # the zero head
+    assert np.isfinite(outs[1][4].view(np.float32)).all()
+    rope.free()
