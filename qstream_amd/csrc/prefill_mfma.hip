@@ -13,7 +13,7 @@
 //    sum restarts every 64 k (a "sub-block"; the scale is constant inside
 //    one) and is folded into the output in fp32: out = fma(s, acc, out).
 //  * The zero-point term sum_b z_b X_b is itself a small contraction over
-//    the blocks.  It runs on the same MFMA as extra k-steps ahead of the
+//    the blocks.  It runs on the same MFMA as extra k-steps after the
 //    codes, on exact bf16 splits: z = zh + zl (fp16 has 11 significant
 //    bits, bf16 8, so the remainder has at most 3) and X_b = X1 + X2 + X3
 //    (fp32 sum of the block, 24 bits in three 8-bit parts).  Each block
@@ -25,13 +25,21 @@
 //
 // Tiling.  One 512-thread workgroup per 256 (m) x 112 (n) tile of Y; at
 // config-4 shape (M 512, N 14336) that is exactly one workgroup per CU.  K
-// advances in stages of 128 (4 MFMA k-steps): first the zero-point stages
-// (8 k positions per block, padded to an even stage count), then the code
-// stages.  The waves split by role, one of each per SIMD, so the VALU work
+// advances in stages of 128 (4 MFMA k-steps): first the code stages, then
+// the zero-point stages (8 k positions per block, padded to an even stage
+// count).  The waves split by role, one of each per SIMD, so the VALU work
 // (code conversion, scale epilogue) and MFMAs overlap in the hardware:
 //  * 4 producer waves write stage s+1's 112 x 128 B tile into LDS (bf16,
 //    [112][128 + 8 pad], two buffers) with each column's sub-block scales,
-//    while stage s is contracted; their loads run two stages ahead;
+//    while stage s is contracted; their loads run two stages ahead.  The
+//    code stages read each block's meta dword for its scale and keep its
+//    fp16 zero in an LDS stash [112][16 per zero-point stage], from which
+//    the zero-point stages build their B tiles: every weight byte is
+//    fetched once.  (With the zero-point stages first, reading the meta
+//    from memory, they pulled every 64-byte line of the tile's rows through
+//    the cache, and the code stages fetched them all again: 2x the weight
+//    bytes.)  Rows of more than 448 blocks, too long for the stash, read the
+//    meta dwords from memory again in the zero-point stages;
 //  * 4 consumer waves each own 64 rows x 112 columns (4 x 7 MFMA tiles).
 //    A fragments come from x repacked into fragment order (xpack_kernel:
 //    one contiguous 1 KB load per fragment), one stage ahead in registers;
@@ -63,6 +71,12 @@ constexpr int EP_FLOATS = 4 * 64 * EP_PITCH;
 constexpr int LDS_MAIN = 2 * BUF * 2 + 2 * SCN * 4;
 constexpr int LDS_BYTES = LDS_MAIN > EP_FLOATS * 4 ? LDS_MAIN : EP_FLOATS * 4;
 constexpr int ZK = 8;                  // zero-point k positions per block
+// Zero stash: fp16 zeros [BN][16 sz] after the B buffers, in LDS left free
+// up to 160 KB (the epilogue tile reuses it): rows of up to 448 blocks.
+constexpr int ZP_MAX = 448;
+constexpr int LDS_STASH = LDS_MAIN + BN * ZP_MAX * 2;
+constexpr int LDS_TOTAL = LDS_STASH > LDS_BYTES ? LDS_STASH : LDS_BYTES;
+static_assert(LDS_TOTAL <= 160 * 1024, "LDS of a CU");
 
 __device__ __forceinline__ float bf16_f32(__bf16 v) {
     return __builtin_bit_cast(float, (uint32_t)__builtin_bit_cast(uint16_t, v) << 16);
@@ -115,6 +129,7 @@ struct PrefillArgs {
     int m, n, k, nb;
     int tiles_n;
     int sz, s;               // zero-point stages; all stages (both even)
+    int zp;                  // zero stash entries a column (16 sz), or 0: zeros re-read from memory
     uint32_t w_bytes, xp_bytes;
     int nq;                  // FRAG: 4-block quads a row (the blocks are in fragment order)
 };
@@ -227,9 +242,11 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
     constexpr int BB = 4 + BS / 2;             // block bytes
     // two B buffers and their scales during the main loop; the output
     // staging tile after it
-    __shared__ __align__(16) uint8_t lds_raw[LDS_BYTES];
+    __shared__ __align__(16) uint8_t lds_raw[LDS_TOTAL];
     __bf16* const lds = reinterpret_cast<__bf16*>(lds_raw);
     float* const scl = reinterpret_cast<float*>(lds_raw + 2 * BUF * 2);
+    uint16_t* const zst = reinterpret_cast<uint16_t*>(lds_raw + LDS_MAIN);
+    const int ncode = a.s - a.sz;              // code stages 0..ncode-1, then the zero-point ones
 
     const int t = threadIdx.x, lane = t & 63;
     const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
@@ -240,11 +257,13 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
     if (wave >= 4) {
         // ---- producer waves: write stage s+1's B tile during stage s.
         // Item p < 2 BN: column p/2, k positions 64 (p%2)..+63 of the stage.
-        //  * zero-point stage: the 8 blocks 16 s + 8 (p%2) + j of the
-        //    column, one meta dword each -> one 16-byte chunk each;
-        //  * code stage: one meta dword and two 16-byte code loads; the
-        //    codes become 8 chunks of 8 bf16 integers and the scale goes to
-        //    the stage's scale row (p%2 = the stage's 64-wide sub-block).
+        //  * code stage c: one meta dword and two 16-byte code loads; the
+        //    codes become 8 chunks of 8 bf16 integers, the scale goes to the
+        //    stage's scale row (p%2 = the stage's 64-wide sub-block) and the
+        //    zero to the stash;
+        //  * zero-point stage z: the 8 blocks 16 z + 8 (p%2) + j of the
+        //    column, one stashed zero (or meta dword) each -> one 16-byte
+        //    chunk each.
         // Byte offsets in a row: the lane part is fixed, the stage part
         // uniform; columns past n read zeros.
         const uint32_t row_bytes = (uint32_t)a.nb * BB;
@@ -270,10 +289,11 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
                    ((b & 3u) * 16u + (frow & 15u)) * 4u;
         };
         auto load = [&](int s, u32x4 (&c)[2], uint32_t& meta) __attribute__((always_inline)) {
+            if (s >= a.s || (s >= ncode && a.zp)) return;   // past the end; zeros from the stash
             if constexpr (FRAG) {
                 static_assert(BS == 64 || BS == 128, "fragment order: blocks of 64 or 128");
-                if (s < a.sz) {
-                    const uint32_t b0 = (uint32_t)(16 * s + 8 * h);
+                if (s >= ncode) {
+                    const uint32_t b0 = (uint32_t)(16 * (s - ncode) + 8 * h);
 #pragma unroll
                     for (int j = 0; j < 8; j++)
                         c[j >> 2][j & 3] = __builtin_amdgcn_raw_buffer_load_b32(wr, fbase(b0 + j), 0, 0);
@@ -282,7 +302,7 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
                     // the 32 code bytes from byte 4 + 32 (h or 0) of the block:
                     // dwords 1-3 of plane pa, plane pa + 1, dword 0 of plane
                     // pa + 2 (or of the tail plane)
-                    const int sc = s - a.sz;
+                    const int sc = s;
                     const uint32_t b = BS == 64 ? (uint32_t)(2 * sc + h) : (uint32_t)sc;
                     const uint32_t pa = BS == 64 ? 0u : 2u * (uint32_t)h;
                     const uint32_t o = fbase(b);
@@ -297,14 +317,14 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
                 }
                 return;
             }
-            if (s < a.sz) {
-                const uint32_t b0 = (uint32_t)(16 * s + 8 * h);
+            if (s >= ncode) {
+                const uint32_t b0 = (uint32_t)(16 * (s - ncode) + 8 * h);
 #pragma unroll
                 for (int j = 0; j < 8; j++)
                     c[j >> 2][j & 3] = __builtin_amdgcn_raw_buffer_load_b32(wr, wv + (b0 + j) * BB, 0, 0);
                 meta = 0;
             } else {
-                const int sc = s - a.sz;
+                const int sc = s;
                 const uint32_t sm = BS <= SK ? (uint32_t)sc * (SK / BS) * BB : (uint32_t)(sc / (BS / SK)) * BB;
                 const uint32_t so = BS <= SK ? sm : sm + (uint32_t)(sc % (BS / SK)) * (SK / 2);
                 meta = __builtin_amdgcn_raw_buffer_load_b32(wr, wv + lane_meta + sm, 0, 0);
@@ -314,17 +334,25 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
         };
         auto produce = [&](int s, const u32x4 (&c)[2], uint32_t meta, __bf16* buf, float* sc)
             __attribute__((always_inline)) {
-            if (!active) return;
-            if (s < a.sz) {
+            if (!active || s >= a.s) return;
+            if (s >= ncode) {
+                const int b0 = 16 * (s - ncode) + 8 * h;
+                u32x4 zs = {0u, 0u, 0u, 0u};            // stashed zeros b0..b0+7
+                if (a.zp) zs = *reinterpret_cast<const u32x4*>(zst + col * a.zp + b0);
 #pragma unroll
                 for (int j = 0; j < 8; j++) {
-                    const int b = 16 * s + 8 * h + j;
-                    bf16x8 v = zchunk(c[j >> 2][j & 3]);
+                    const int b = b0 + j;
+                    const uint32_t m = a.zp ? (zs[j >> 1] >> (16 * (j & 1))) << 16 : c[j >> 2][j & 3];
+                    bf16x8 v = zchunk(m);
                     if (b >= a.nb) v = bf16x8{};
                     *reinterpret_cast<bf16x8*>(buf + it_base + 8 * j) = v;
                 }
             } else {
-                const int k0 = (s - a.sz) * SK + 64 * h;
+                // the block's zero into the stash, once a block
+                const int zb = BS == 64 ? 2 * s + h : BS == 128 ? s : s >> 1;
+                if (a.zp && zb < a.nb && (BS == 64 || (h == 0 && (BS == 128 || (s & 1) == 0))))
+                    zst[col * a.zp + zb] = (uint16_t)(meta >> 16);
+                const int k0 = s * SK + 64 * h;
                 // a sub-block wholly past k has zero codes and x; a zero
                 // scale keeps junk meta (Inf, NaN) out of the sum
                 sc[h * BN + col] = RAGGED && k0 >= a.k ? 0.f : qsf::f16_lo(meta);
@@ -369,10 +397,12 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
     // B fragment of n-tile nt, k-step ks: column 16 nt + l%16, k 32 ks + 8 (l/16)
     const int bf_base = l16 * PITCH + 8 * g4;
 
+    // stage s's k-steps in the packed x: its zero-point part first, then x
     auto load_a = [&](int s, int ks, u32x4 (&A)[MT][4]) __attribute__((always_inline)) {
+        const int xs = s < ncode ? s + a.sz : s - ncode;
 #pragma unroll
         for (int mt = 0; mt < MT; mt++)
-            A[mt][ks] = __builtin_amdgcn_raw_buffer_load_b128(xr, xv[mt] + (uint32_t)(s * 4 + ks) * 1024u, 0, 0);
+            A[mt][ks] = __builtin_amdgcn_raw_buffer_load_b128(xr, xv[mt] + (uint32_t)(xs * 4 + ks) * 1024u, 0, 0);
     };
     auto load_b = [&](const __bf16* src, int nt, int ks) __attribute__((always_inline)) {
         return *reinterpret_cast<const bf16x8*>(src + bf_base + nt * 16 * PITCH + ks * 32);
@@ -479,11 +509,7 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
     b0 = load_b(lds, 0, 0);
     b1 = load_b(lds, 0, 1);
     int s = 0;
-    for (; s < a.sz; s += 2) {
-        stage.template operator()<true>(s, lds, scl, lds + BUF);
-        stage.template operator()<true>(s + 1, lds + BUF, scl + SCN, lds);
-    }
-    for (; s < a.s; s += 2) {
+    for (; s < ncode; s += 2) {
         stage.template operator()<false>(s, lds, scl, lds + BUF);
         stage.template operator()<false>(s + 1, lds + BUF, scl + SCN, lds);
     }
@@ -492,6 +518,10 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
 #pragma unroll
         for (int i = 0; i < 4; i++)
             out[mt][NT - 1][i] = __builtin_fmaf(scp, accp[mt][i], out[mt][NT - 1][i]);
+    for (; s < a.s; s += 2) {
+        stage.template operator()<true>(s, lds, scl, lds + BUF);
+        stage.template operator()<true>(s + 1, lds + BUF, scl + SCN, lds);
+    }
 
     // Epilogue: each wave stages its 64 x 112 fp32 tile in LDS (once every
     // wave is past its last B read) and writes whole row pieces with 16-byte
@@ -602,7 +632,8 @@ extern "C" int qk_prefill_gemm(const qsf_hip_tensor* t, const void* d_ws, int m,
     const bool ragged = t->cols % (2 * SK) != 0;
     const uint64_t w_bytes = t->frag ? (uint64_t)qk_frag_bytes(t->rows, t->nb, bb) : (uint64_t)t->rows * row_bytes;
     PrefillArgs a = {t->d_blocks, static_cast<const u32x4*>(d_ws), d_y, m, t->rows, t->cols, t->nb,
-                     tiles_n, st.sz, st.sz + st.sc, (uint32_t)w_bytes, (uint32_t)xp_bytes, t->frag_nq};
+                     tiles_n, st.sz, st.sz + st.sc, 16 * st.sz <= ZP_MAX ? 16 * st.sz : 0,
+                     (uint32_t)w_bytes, (uint32_t)xp_bytes, t->frag_nq};
     const dim3 grid(tiles_n * tiles_m), block(512);
 #define QK_PREFILL_CASE(B, F)                                                   \
     if (ragged) launch<prefill_kernel<B, true, F>>(grid, block, s, a);          \
