@@ -721,13 +721,20 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
         return reinterpret_cast<const uint32_t*>(W + (size_t)min(row_of(j), rows - 1) * row_bytes);
     };
 
-    // issue cursor: tile ij, step iq; row offsets of that tile
+    // issue cursor: tile ij, step iq; row offsets of that tile, clamped to
+    // the last row in bytes (the tile's first row times row_bytes is
+    // wave-uniform, the group's row within the tile a per-lane constant: no
+    // vector multiply a tile; the host keeps (rows + 128) * row_bytes within
+    // 32 bits)
     int ij = 0, iq = 0;
     uint32_t ioff[R];
+    uint32_t goff = (uint32_t)(grp * R) * row_bytes;
+    asm volatile("" : "+v"(goff));   // opaque: else folded back into (row + grp R) * row_bytes
+    const uint32_t olim = (uint32_t)max(rows - 1, 0) * row_bytes;
     auto at_tile = [&](int j) __attribute__((always_inline)) {
-        const int r0 = row_of(j);
+        const uint32_t base = (uint32_t)((tl + WAVES * min(j, ntl - 1)) * rpt) * row_bytes + goff;
 #pragma unroll
-        for (int r = 0; r < R; r++) ioff[r] = (uint32_t)min(r0 + r, rows - 1) * row_bytes;
+        for (int r = 0; r < R; r++) ioff[r] = min(base + (uint32_t)r * row_bytes, olim);
     };
     at_tile(0);
     // The matrix record is materialised here, with the other arguments, in
@@ -1043,17 +1050,68 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
     // before the end); the last block issues nothing, since a wave cannot
     // retire before its loads return.
     const int nblk = (ni + D - 1) / D;
-    for (int q = 0; q + 1 < nblk; q++) {
+    if constexpr (DREG) {
+        // One block a lane (nb <= lpg): every item is a whole tile, and the
+        // lane's block, hence its byte offset in a row, is the same in every
+        // item.  Item k of a block of D items reads its tile's first outlier
+        // entries from e0[k] and mask bits k*R..; the block then shifts them
+        // down by D (a shift each item cost MT - 1 moves an item: config 1
+        // 9.45-9.82 -> 9.26-9.32 us with this loop and the multiply-free row
+        // offsets, on one box; runs of 2 D items with one shift were slower,
+        // 10.0-10.2 us).
+        const bool live = lig < a.nb;
+        const int bl = min(lig, a.nb - 1);
+        auto issue_d = [&](WV& wv) __attribute__((always_inline)) {
+            load_block<FMT, BS, R, SPLIT>(W, ioff, bl, wv, a.pbb, a.lsplit);
+            ++ij;
+            at_tile(min(ij, ntl - 1));
+        };
+        auto item = [&](const WV& w, int k) __attribute__((always_inline)) {
+            if (live) compute_block<FMT, BS, R>(w, dreg, mreg, rs);
+            if constexpr (OUT) {
+                const uint32_t e = e0[k], mb = (omask >> (k * R)) & ((1u << R) - 1);
+                const float p = qsf::f16_bits(e >> 16) * xs[mb ? e & 0xFFFFu : 0u];
 #pragma unroll
-        for (int k = 0; k < D; k++) {
-            compute(wv[k]);
-            issue(wv[k]);
+                for (int r = 0; r < R; r++) rs[r] += (mb >> r) & 1u ? p : 0.0f;
+            }
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                const float v = group_reduce(rs[r], lpg);
+                rs[r] = 0.0f;
+                if (lig == lpg - 1) stash[cj * rpt + grp * R + r] = v;
+            }
+            ++cj;
+        };
+        for (int q = 0; q + 1 < nblk; q++) {
+#pragma unroll
+            for (int k = 0; k < D; k++) {
+                item(wv[k], k);
+                issue_d(wv[k]);
+            }
+            if constexpr (OUT) {
+#pragma unroll
+                for (int j = 0; j + D < MT; j++) e0[j] = e0[j + D];
+                omask >>= D * R;
+            }
         }
-    }
-    if (nblk > 0) {
+        if (nblk > 0) {
 #pragma unroll
-        for (int k = 0; k < D; k++)
-            if ((nblk - 1) * D + k < ni) compute(wv[k]);
+            for (int k = 0; k < D; k++)
+                if ((nblk - 1) * D + k < ni) item(wv[k], k);
+        }
+    } else {
+        for (int q = 0; q + 1 < nblk; q++) {
+#pragma unroll
+            for (int k = 0; k < D; k++) {
+                compute(wv[k]);
+                issue(wv[k]);
+            }
+        }
+        if (nblk > 0) {
+#pragma unroll
+            for (int k = 0; k < D; k++)
+                if ((nblk - 1) * D + k < ni) compute(wv[k]);
+        }
     }
 
     // 8. remaining outlier entries of each tile, one per lane each step;
@@ -1359,7 +1417,7 @@ int plan_rt(const qsf_hip_tensor* const* t, int n, int cols, int mode, float* co
     bool any_out = false, split = false;
     a.tile0[0] = 0;
     for (int i = 0; i < n; i++) {
-        if ((size_t)t[i]->rows * nb * F::BB > 0xFFFFFFF0ull) return -2;   // 32-bit offsets
+        if ((size_t)(t[i]->rows + 128) * nb * F::BB > 0xFFFFFFF0ull) return -2;   // 32-bit offsets
         float* y = d_y ? d_y[i] : nullptr;
         a.w[i] = t[i]->d_blocks;
         a.y[i] = y;
