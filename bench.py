@@ -470,13 +470,30 @@ def profile_decode_layer(torch, hip, steps, warmup):
         pr.free()
 
 
+def upload_layer_tensors(hip, qt, bs, mats):
+    """One layer's tensors, each on the decode engine that runs its launch
+    fastest: o, a 4096 x 4096 matrix launched alone, on the dot-product
+    kernels (4.8 against 5.8 us a launch on the matrix core, which needs
+    more rows a launch to fill its workgroups), the others (q/k/v launched
+    as a group, gate/up, down) on the library's default engine."""
+    out = []
+    for name, p, r, c in mats:
+        prev = hip.gemv_engine(0) if name == "o" else None
+        try:
+            out.append(hip.Tensor(p, qt, r, c, bs))
+        finally:
+            if prev is not None:
+                hip.gemv_engine(prev)
+    return out
+
+
 def bench_layers(torch, hip, steps, warmup, with_cpu=True, cpu_budget=10.0):
     """Config 2: 32 decoder layers at 3-bit back to back.  A step is the
     whole stack: per layer q/k/v in one grouped launch, o, gate/up grouped,
     down -- 128 launches, each on its own fresh x."""
     qt, bs, mats = cfg2_layer()
     log("config 2: layer quantised")
-    layers = [[hip.Tensor(p, qt, r, c, bs) for _, p, r, c in mats] for _ in range(32)]
+    layers = [upload_layer_tensors(hip, qt, bs, mats) for _ in range(32)]
     rng = np.random.default_rng(20)
     xs = [torch.from_numpy(rng.standard_normal((4, 11008)).astype(np.float32)).to("cuda:0")
           for _ in range(32)]
@@ -540,8 +557,7 @@ def bench_decode_layer(torch, hip, steps, warmup, position=1023):
     log("layer: weights quantised")
     hid, nh, hd, eid, max_seq, n_layers = 4096, 32, 128, 11008, position + 1, 32
     # q, k, v, o and down as tensors; gate and up as one interleaved pair
-    layers = [[hip.Tensor(p, qt, r, c, bs) for _, p, r, c in mats[:4] + mats[6:7]]
-              for _ in range(n_layers)]
+    layers = [upload_layer_tensors(hip, qt, bs, mats[:4] + mats[6:7]) for _ in range(n_layers)]
     pairs = [hip.TensorPair(mats[4][1], mats[5][1], qt, mats[4][2], mats[4][3], bs)
              for _ in range(n_layers)]
     g = torch.Generator(device="cuda:0").manual_seed(40)
