@@ -18,9 +18,10 @@ the replay stream, after W untimed eager steps and at least 0.2 s of untimed
 replays (the clocks settle after about 40 ms of sustained work).  For the
 one-launch decode steps (configs 0 and 1) that timed region is also the
 kernel's time: `roofline.kernel_us` is the region time per launch, so it
-never exceeds the step.  Configs 2, 4 and the layer step time their
-dominant kernel by a graph of that kernel's launches alone; config 3 by
-kernel-edge HIP event pairs (`roofline.timing` says which).
+never exceeds the step.  Configs 2, 3, 4 and the layer step time their
+dominant kernel by a graph of that kernel's launches alone (config 3 at
+batch 8: routing + gate/up less routing alone; `roofline.timing` says
+which).
 `roofline.traffic` is the HBM bytes per launch measured with rocprofv3
 counters (profiles/traffic.json), used only while the kernel source it was
 measured on is unchanged, else null.  Configs 0 and 1 also carry
@@ -714,18 +715,22 @@ def bench_moe(torch, hip, steps, warmup, ntok, with_cpu=True, cpu_budget=10.0, e
         distinct.append(len(sel))
     bytes_step = float(np.mean(distinct)) * 3 * per_mat + ntok * dim * 4 * 2
     # Dominant kernel: the gate/up expert launch (two of the three matrices
-    # of every distinct expert), timed at its own start and end over eager
-    # steps; algorithmic bytes = its expert codes and scales + x + h written.
-    stream = torch.cuda.current_stream()
-    nt = min(steps, 256)
-    hip.kernel_timing(True)
-    for i in range(nt):
-        step(i, stream)
-    torch.cuda.synchronize()
-    gu_us = np.asarray(hip.kernel_timing_read(4096), np.float64)
-    hip.kernel_timing(False)
-    gu_bytes = np.asarray(distinct[:nt], np.float64) * 2 * per_mat + ntok * dim * 4 * 2
-    roof = float(np.mean(gu_bytes)) / (float(np.mean(gu_us)) * 1e-6) / 1e9
+    # of every distinct expert), timed like the steps, by graph replay of
+    # steps that launch only it (qsf_hip_moe_stages: one token routes inside
+    # it); with several tokens, a graph of routing + gate/up less one of the
+    # routing launch alone.  Algorithmic bytes = its expert codes and scales
+    # + x + h written.
+    prev = hip.moe_stages(3)
+    try:
+        gu_ms = graph_ms(torch, step, steps)
+        if ntok > 1:
+            hip.moe_stages(1)
+            gu_ms -= graph_ms(torch, step, steps)
+    finally:
+        hip.moe_stages(prev)
+    gu_us = gu_ms * 1e3
+    gu_bytes = np.asarray(distinct, np.float64) * 2 * per_mat + ntok * dim * 4 * 2
+    roof = float(np.mean(gu_bytes)) / (gu_us * 1e-6) / 1e9
     moe.free()
     for ts in tens.values():
         for t in ts:
@@ -733,11 +738,12 @@ def bench_moe(torch, hip, steps, warmup, ntok, with_cpu=True, cpu_budget=10.0, e
     res = {"value": bytes_step / (ms * 1e-3) / 1e9, "ms_per_step": ms, "bytes_per_step": bytes_step,
            "distinct_experts_mean": float(np.mean(distinct))}
     res["roofline"] = {"bound": "hbm", "kernel": "moe_gate_up_kernel",
-                       "timing": "kernel-edge HIP event pairs on the launch stream, eager steps",
+                       "timing": ("graph of gate/up-only steps (routing inside the launch)" if ntok == 1 else
+                                  "graph of routing + gate/up steps less a graph of routing-only steps"),
                        "achieved": round(roof, 2),
                        "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(roof / HBM_PEAK_GBS, 4),
                        "traffic": measured_traffic(f"cfg3_b{ntok}"),
-                       "kernel_us": round(float(np.mean(gu_us)), 3),
+                       "kernel_us": round(gu_us, 3),
                        "bytes_per_launch": round(float(np.mean(gu_bytes)))}
     if with_cpu:
         res["cpu_baseline"] = cpu_baseline_moe(ex, ntok, k, dim, logits_h, xs.cpu().numpy(),

@@ -252,6 +252,17 @@ void qsf_hip_moe_free(qsf_hip_moe* m);
 int qsf_hip_moe_forward_dev(qsf_hip_moe* m, int top_k, int norm_topk, int activation,
                             int ntok, const float* d_x, const float* d_logits,
                             float* d_out, void* stream);
+/* Measurement aid (no counterpart in the reference): the stages
+ * qsf_hip_moe_forward_dev launches from now on, bit 0 the routing launch
+ * (batches of more than one token; one token routes inside its gate/up
+ * launch), bit 1 gate/up, bit 2 down and the weighted sum.  Default 7 (the
+ * whole FFN).  A stage left out leaves the object's workspace as the last
+ * call that ran it wrote it, so forward calls with masks 1, 2, 4 in turn on
+ * the same inputs give the output of one call with 7; any other mask leaves
+ * d_out unwritten or stale, for timing one stage's launches on their own.
+ * Masks other than 7 need ntok <= 8.  mask < 0 only queries; returns the
+ * previous mask. */
+int qsf_hip_moe_stages(int mask);
 
 /* Batched prefill through the 4-bit format (no reference kernel: the engine
  * runs one qsf_matvec_4bit call per token, src/engine.c:1289-1295):

@@ -814,7 +814,8 @@ extern "C" size_t qk_moe_ws_bytes(int n_exp, int k, int ntok, int hidden, int ei
 
 extern "C" int qk_moe_launch(const qk_mx_expert* d_experts, int n_exp, int k, int norm, int act,
                              int hidden, int eid, int ntok, const float* d_x,
-                             const float* d_logits, float* d_out, void* d_ws, hipStream_t s) {
+                             const float* d_logits, float* d_out, void* d_ws, int stages,
+                             hipStream_t s) {
     if (ntok < 1 || ntok > MAX_TOK || k < 1 || k > MAX_K || n_exp < 1 || n_exp > MAX_EXP ||
         hidden < 1 || eid < 1 || (hidden % 4) || (eid % 4) || hidden > 4096 || eid > 4096)
         return -2;
@@ -837,7 +838,7 @@ extern "C" int qk_moe_launch(const qk_mx_expert* d_experts, int n_exp, int k, in
     const dim3 g_gu((eid + rows_gu - 1) / rows_gu, items), g_dn((hidden + rows_dn - 1) / rows_dn, items);
     // one token with the fused down: gate/up routes in-kernel (no route launch)
     const bool one = ntok == 1 && k <= FG;
-    if (!one) hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(MAX_TOK * 64), 0, s, a);
+    if (!one && (stages & 1)) hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(MAX_TOK * 64), 0, s, a);
     const int tch = ntok < TCH ? ntok : TCH;
     // inputs (one token: then the expert table's gate/up pointers)
     const size_t lds_gu = (size_t)tch * ((hidden + 31) / 32) * XBP * 4 + (one ? (size_t)n_exp * 6 * 8 : 0),
@@ -846,13 +847,16 @@ extern "C" int qk_moe_launch(const qk_mx_expert* d_experts, int n_exp, int k, in
 #define QK_GU(NI)                                                                        \
     if (one) launch_lds<moe_gate_up_kernel<NI, true>>(g_gu, block_gu, lds_gu, s, a, true); \
     else launch_lds<moe_gate_up_kernel<NI, false>>(g_gu, block_gu, lds_gu, s, a, true);
-    switch (ni_gu) {
-    case 1: QK_GU(1) break;
-    case 2: QK_GU(2) break;
-    case 3: QK_GU(3) break;
-    default: QK_GU(4) break;
+    if (stages & 2) {
+        switch (ni_gu) {
+        case 1: QK_GU(1) break;
+        case 2: QK_GU(2) break;
+        case 3: QK_GU(3) break;
+        default: QK_GU(4) break;
+        }
     }
 #undef QK_GU
+    if (!(stages & 4)) return hipGetLastError() == hipSuccess ? 0 : -1;
     if (one) {
         // one token: down and combine in one launch
         const dim3 g_f((hidden + FROWS - 1) / FROWS), b_f(FG * FGW * 64);

@@ -159,9 +159,12 @@ typedef struct {
     const uint8_t* dc; const uint8_t* ds; const uint16_t* db;
 } qk_mx_expert;
 size_t qk_moe_ws_bytes(int n_exp, int k, int ntok, int hidden, int eid);
+/* stages: bit 0 the routing launch (more than one token; one token routes
+ * in the gate/up launch), bit 1 gate/up, bit 2 down and combine; a stage
+ * left out leaves the workspace as the previous call's stage wrote it. */
 int qk_moe_launch(const qk_mx_expert* d_experts, int n_exp, int k, int norm, int act,
                   int hidden, int eid, int ntok, const float* d_x, const float* d_logits,
-                  float* d_out, void* d_ws, hipStream_t s);
+                  float* d_out, void* d_ws, int stages, hipStream_t s);
 
 /* 4-bit prefill on MFMA: y[m][n] = W[n] . float(x_bf16[m]).  d_ws holds
  * the per-block sums of x and x itself in MFMA fragment order:

@@ -1183,15 +1183,28 @@ void qsf_hip_moe_free(qsf_hip_moe* m) {
 /* Tokens go through in chunks of at most 8 (the kernels' batch), one after
  * another on `stream`, which orders their use of the object's workspace;
  * each token's result does not depend on the others in its chunk. */
+static int g_moe_stages = 7;
+
+int qsf_hip_moe_stages(int mask) {
+    pthread_mutex_lock(&g_lock);
+    const int prev = g_moe_stages;
+    if (mask >= 0) g_moe_stages = mask & 7;
+    pthread_mutex_unlock(&g_lock);
+    return prev;
+}
+
 int qsf_hip_moe_forward_dev(qsf_hip_moe* m, int k, int norm, int act, int ntok,
                             const float* d_x, const float* d_logits, float* d_out, void* stream) {
     if (!m || ntok < 1 || k < 1 || k > 8 || !d_x || !d_logits || !d_out)
         return fail(E_INVALID, "qsf_hip_moe_forward_dev: bad arguments (ntok %d, k %d)", ntok, k);
+    const int stages = qsf_hip_moe_stages(-1);
+    if (stages != 7 && ntok > 8)
+        return fail(E_INVALID, "qsf_hip_moe_forward_dev: stages 0x%x need ntok <= 8 (one launch group)", stages);
     for (int t0 = 0; t0 < ntok; t0 += 8) {
         const int nt = ntok - t0 < 8 ? ntok - t0 : 8;
         if (qk_moe_launch(m->d_table, m->n_exp, k, norm, act, m->hidden, m->eid, nt,
                           d_x + (size_t)t0 * m->hidden, d_logits + (size_t)t0 * m->n_exp,
-                          d_out + (size_t)t0 * m->hidden, m->d_ws, pick_stream(stream)))
+                          d_out + (size_t)t0 * m->hidden, m->d_ws, stages, pick_stream(stream)))
             return fail(E_INTERNAL, "qsf_hip_moe_forward_dev: launch failed (tokens %d..%d)", t0,
                         t0 + nt - 1);
     }

@@ -33,7 +33,7 @@ EXPORTS = (
     "qsf_hip_matvec_dev", "qsf_hip_matvec_group_dev", "qsf_hip_xprep_bytes",
     "qsf_hip_xprep_dev", "qsf_hip_matvec_group_prepared_dev",
     "qsf_hip_moe_create", "qsf_hip_moe_free", "qsf_hip_moe_forward_dev",
-    "qsf_hip_unpack_dev", "qsf_hip_kernel_timing", "qsf_hip_kernel_timing_read", "qsf_hip_gemv_engine",
+    "qsf_hip_unpack_dev", "qsf_hip_kernel_timing", "qsf_hip_kernel_timing_read", "qsf_hip_gemv_engine", "qsf_hip_moe_stages",
     "qsf_hip_prefill_4bit_dev", "qsf_hip_prefill_4bit_dev_noalloc", "qsf_hip_prefill_pack_bytes",
     "qsf_hip_prefill_pack_dev", "qsf_hip_prefill_4bit_packed_dev", "qsf_hip_stream_read_dev",
     "qsf_hip_rms_norm_dev", "qsf_hip_layer_norm_dev", "qsf_hip_rope_create", "qsf_hip_rope_free",
@@ -172,6 +172,8 @@ def load(path: str = LIB_PATH) -> C.CDLL:
     L.qsf_hip_kernel_timing_read.restype = _i
     L.qsf_hip_gemv_engine.argtypes = [_i]
     L.qsf_hip_gemv_engine.restype = _i
+    L.qsf_hip_moe_stages.argtypes = [_i]
+    L.qsf_hip_moe_stages.restype = _i
     _lib = L
     return L
 
@@ -182,6 +184,13 @@ def gemv_engine(engine: int = -1) -> int:
     0 the dot-product kernels for all; < 0 queries.  Returns the previous
     setting."""
     return int(load().qsf_hip_gemv_engine(engine))
+
+
+def moe_stages(mask: int = -1) -> int:
+    """Stages Moe.forward launches from now on (measurement aid): bit 0
+    routing, bit 1 gate/up, bit 2 down + combine; 7 by default; < 0
+    queries.  Returns the previous mask."""
+    return int(load().qsf_hip_moe_stages(mask))
 
 
 def kernel_timing(enable: bool) -> None:

@@ -176,6 +176,44 @@ def test_moe_repeated_calls_reuse_workspace(hip, oracle):
             t.free()
 
 
+@pytest.mark.parametrize("ntok", [1, 8])
+def test_moe_stages_one_at_a_time_equal_the_forward(hip, ntok):
+    """The measurement switch qsf_hip_moe_stages: forward calls with masks
+    1, 2 and 4 in turn (routing, gate/up, down + combine; one token routes
+    inside gate/up) leave the same output as one call with 7, bit for bit,
+    and a call without the down stage leaves the output untouched."""
+    torch = torch_cuda()
+    rng = np.random.default_rng(90 + ntok)
+    n_exp, k, hidden, eid = 32, 4, 512, 384
+    ex = _experts(rng, n_exp, hidden, eid, True)
+    tens = {n: [hip.Tensor(e[n], F.MXFP4, *((eid, hidden) if n != "down" else (hidden, eid)), 32)
+                for e in ex] for n in ("gate", "up", "down")}
+    biases = {n: [e[n] for e in ex] for n in ("gate_bias", "up_bias", "down_bias")}
+    moe = hip.Moe(tens["gate"], tens["up"], tens["down"], hidden, eid, **biases)
+    x, logits = dev(F.gaussian(rng, (ntok, hidden))), dev(F.gaussian(rng, (ntok, n_exp)))
+    full = torch.full((ntok, hidden), float("nan"), device="cuda:0")
+    moe.forward(k, 1, 2, ntok, x, logits, full, stream=_stream())
+    # other inputs in between, so the workspace holds another call's state
+    moe.forward(k, 1, 2, ntok, dev(F.gaussian(rng, (ntok, hidden))), dev(F.gaussian(rng, (ntok, n_exp))),
+                torch.empty((ntok, hidden), device="cuda:0"), stream=_stream())
+    staged = torch.full((ntok, hidden), float("nan"), device="cuda:0")
+    try:
+        assert hip.moe_stages(1) == 7
+        moe.forward(k, 1, 2, ntok, x, logits, staged, stream=_stream())
+        hip.moe_stages(2)
+        moe.forward(k, 1, 2, ntok, x, logits, staged, stream=_stream())
+        assert np.isnan(host(staged)).all()          # no down stage yet: untouched
+        hip.moe_stages(4)
+        moe.forward(k, 1, 2, ntok, x, logits, staged, stream=_stream())
+    finally:
+        assert hip.moe_stages(7) == 4
+    assert np.array_equal(host(staged).view(np.uint32), host(full).view(np.uint32))
+    moe.free()
+    for ts in tens.values():
+        for t in ts:
+            t.free()
+
+
 @pytest.mark.parametrize("ntok,all_nan", [(1, False), (3, False), (3, True)])
 def test_moe_nan_logits_pick_nothing(hip, oracle, ntok, all_nan):
     """A NaN router logit makes every softmax probability NaN (the sum
