@@ -73,9 +73,11 @@ def row_slice(payload, r0, r1, k, bs):
 
 # (m, n, k, bs): single tile, ragged k and partial blocks, several m and n
 # tiles, every block size, n and m past a tile edge
+# the last two: rows of 448 blocks (the most the zero-point stash holds) and
+# of 449, whose zero-point stages read the meta from memory again
 SHAPES = [(1, 64, 64, 64), (37, 100, 256, 64), (128, 64, 512, 64), (200, 300, 1000, 64),
           (130, 70, 512, 128), (64, 96, 768, 256), (513, 129, 4096, 64), (16, 112, 200, 128),
-          (300, 224, 1280, 256)]
+          (300, 224, 1280, 256), (24, 120, 28672, 64), (20, 112, 28736, 64)]
 
 
 @pytest.mark.parametrize("m,n,k,bs", SHAPES)
