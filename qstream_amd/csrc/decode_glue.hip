@@ -475,24 +475,32 @@ __global__ __launch_bounds__(ATT_THREADS) void rope_attention_part_kernel(
     const int p0 = chunk * ATT_CHUNK, np = min(ATT_CHUNK, position + 1 - p0);
     const bool last = chunk == nsplit - 1;               // holds the new row, np - 1
     const size_t row0 = (size_t)kvh * max_seq + p0;
-    // 1. all loads.  In the last chunk the rows before the new one; its own
-    //    slot loads the row before it (or, when it starts the chunk, the
-    //    slot itself, whatever it holds) and is replaced below.
+    // 1. all loads.  In the last chunk only the rows before the new one:
+    //    its own slot loads the row before it and is replaced below, and
+    //    when the new row starts the chunk nothing is loaded (no workgroup
+    //    reads the row the first head of the group is storing).
     const int kp = t >> 1, kh = t & 1;
-    const int nold = last ? max(np - 1, 1) : np;
-    const int kpc = min(kp, nold - 1);
-    const att_u32x4* kr = reinterpret_cast<const att_u32x4*>(kc + (row0 + kpc) * HD) + kh * KH;
-    att_u32x4 kv[KH];
+    const int nold = last ? np - 1 : np;                 // rows already in the cache
+    const int kpc = min(kp, max(nold, 1) - 1);
+    att_u32x4 kv[KH], vv[VJ];
+    float kscale = 0.f, vscale = 0.f;
+    if (nold > 0) {                                      // (uniform)
+        const att_u32x4* kr = reinterpret_cast<const att_u32x4*>(kc + (row0 + kpc) * HD) + kh * KH;
 #pragma unroll
-    for (int j = 0; j < KH; j++) kv[j] = kr[j];
-    float kscale = ks[row0 + kpc];
-    float vscale = vs[row0 + kpc];
-    const att_u32x4* vr = reinterpret_cast<const att_u32x4*>(vc + row0 * HD);
-    att_u32x4 vv[VJ];
+        for (int j = 0; j < KH; j++) kv[j] = kr[j];
+        kscale = ks[row0 + kpc];
+        vscale = vs[row0 + kpc];
+        const att_u32x4* vr = reinterpret_cast<const att_u32x4*>(vc + row0 * HD);
 #pragma unroll
-    for (int j = 0; j < VJ; j++) {
-        const int i = t + ATT_THREADS * j;
-        vv[j] = vr[min(i / HC, nold - 1) * HC + i % HC];
+        for (int j = 0; j < VJ; j++) {
+            const int i = t + ATT_THREADS * j;
+            vv[j] = vr[min(i / HC, nold - 1) * HC + i % HC];
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < KH; j++) kv[j] = att_u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int j = 0; j < VJ; j++) vv[j] = att_u32x4{0u, 0u, 0u, 0u};
     }
     // q pair t of the head, and in the last chunk k and v pair t
     float q0 = 0.f, q1 = 0.f, nk[2] = {0.f, 0.f}, nv[2] = {0.f, 0.f};
