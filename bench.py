@@ -418,6 +418,18 @@ def bench_prefill(torch, hip, steps, warmup, with_cpu=True, cpu_budget=10.0):
     kus = graph_ms(torch, gemm_step, steps) * 1e3
     for t in copies:
         t.free()
+    # the matrix-core ceiling on this box, beside the published peak: a graph
+    # of launches of independent v_mfma_f32_16x16x32_bf16 chains, no memory
+    sink = torch.zeros(4, dtype=torch.int32, device="cuda:0")
+    probe_iters = 512
+    probe_flop = hip.mfma_peak(probe_iters, sink)
+    torch.cuda.synchronize()
+    probe_us = graph_ms(torch, lambda i, st: hip.mfma_peak(probe_iters, sink, stream=st), 20) * 1e3
+    probe = {"kernel": "mfma_peak_kernel (independent v_mfma_f32_16x16x32_bf16 chains on every SIMD, "
+                       "no memory traffic)",
+             "timing": "graph of 20 launches", "us_per_launch": round(probe_us, 3),
+             "tflops": round(probe_flop / (probe_us * 1e-6) / 1e12, 1)}
+    probe["frac_of_published_peak"] = round(probe["tflops"] / BF16_MFMA_PEAK_TFS, 4)
     flops = 2.0 * m * n * k
     out = {"value": flops / (ms * 1e-3) / 1e12, "ms_per_step": ms, "us_kernel": kus,
            "flops_per_step": flops, "weight_bytes": len(payload),
@@ -428,7 +440,8 @@ def bench_prefill(torch, hip, steps, warmup, with_cpu=True, cpu_budget=10.0):
                         "frac": round(flops / (kus * 1e-6) / 1e12 / BF16_MFMA_PEAK_TFS, 4),
                         "traffic": measured_traffic("cfg4"), "kernel_us": round(kus, 3),
                         "launches_timed": steps},
-           "rotation_mib": n_copies * len(payload) / (1 << 20), "m": m, "n": n, "k": k}
+           "rotation_mib": n_copies * len(payload) / (1 << 20), "m": m, "n": n, "k": k,
+           "mfma_probe": probe}
     if with_cpu:
         out["cpu_baseline"] = cpu_baseline_prefill(payload, xb, m, n, k, bs, cpu_budget)
     return out
@@ -748,13 +761,20 @@ def bench_moe(torch, hip, steps, warmup, ntok, with_cpu=True, cpu_budget=10.0, e
     if with_cpu:
         res["cpu_baseline"] = cpu_baseline_moe(ex, ntok, k, dim, logits_h, xs.cpu().numpy(),
                                                cpu_budget)
+        # the reference's own GPT-OSS path, beside the port of the MXFP4 math
+        # (per token, so batch 1 and batch 8 share one measurement)
+        key = (k, dim)
+        if key not in _MOE_REF4:
+            _MOE_REF4[key] = cpu_baseline_moe_ref4(k, dim, min(3.0, cpu_budget))
+        res["cpu_baseline"]["reference_4bit_path"] = _MOE_REF4[key]
     return res
 
 
 def cpu_baseline_moe(ex, ntok, k, dim, logits_h, xs, budget_s=10.0):
     """No reference CPU kernel reads MXFP4 (the reference re-quantises GPT-OSS
-    experts to its own formats).  This times this build's scalar restatement
-    of the same MoE token (oracle, strict fp32, 1 thread)."""
+    experts to its own formats: cpu_baseline_moe_ref4 times that path).  This
+    times this build's scalar restatement of the same MoE token (oracle,
+    strict fp32, 1 thread)."""
     from oracle.oracle import Oracle
     o = Oracle()
     t0 = time.perf_counter()
@@ -769,6 +789,49 @@ def cpu_baseline_moe(ex, ntok, k, dim, logits_h, xs, budget_s=10.0):
     el = time.perf_counter() - t0
     return {"value": nbytes / el / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
             "sample": f"oracle MoE token (scalar MXFP4), {toks} tokens, {el:.1f} s"}
+
+
+_MOE_REF4 = {}
+
+
+def cpu_baseline_moe_ref4(k, dim, budget_s=3.0):
+    """The reference's own path for GPT-OSS experts: its converter re-quantises
+    them to its 4-bit format (block 64), and each token then runs k experts'
+    gate, up and down as qsf_matvec_4bit_avx2 calls (src/engine.c:1024-1107),
+    1 thread.  Timed on synthetic 4-bit payloads of the experts' shape (codes
+    random, every block's scale and zero a fixed normal fp16 pair: the AVX2
+    kernel's time does not depend on the values), rotated over >= 768 MiB of
+    distinct host matrices.  None without oracle/_ref."""
+    from oracle.oracle import ref_avx2
+    ref = ref_avx2()
+    if ref is None:
+        return None
+    bs, bb = 64, 36
+    nb = (dim + bs - 1) // bs
+    per_mat = dim * nb * bb
+    n_mats = max(3 * k, math.ceil(HOST_ROTATE_BYTES / per_mat))
+    rng = np.random.default_rng(7)
+    meta = np.frombuffer(np.array([0.003, -0.01], np.float16).tobytes(), np.uint8)
+    mats = []
+    for _ in range(n_mats):
+        m = rng.integers(0, 256, (dim * nb, bb), dtype=np.uint8)
+        m[:, :4] = meta
+        mats.append(m.reshape(-1))
+    x = rng.standard_normal(dim).astype(np.float32)
+    times, i = [], 0
+    t_start = time.perf_counter()
+    while time.perf_counter() - t_start < budget_s or len(times) < 3:
+        t = time.perf_counter()
+        for _ in range(3 * k):
+            ref.matvec(3, mats[i % n_mats], x, dim, dim, bs, isa="avx2")
+            i += 1
+        times.append(time.perf_counter() - t)
+    med = float(np.median(times))
+    return {"value": 3 * k * per_mat / med / 1e9, "unit": "GB/s", "us_per_token": round(med * 1e6, 1),
+            "cores": 1, "kind": "reference",
+            "sample": f"qsf_matvec_4bit_avx2 x {3 * k} a token (k = {k} experts' gate, up, down re-quantised "
+                      f"to 4-bit block 64, {dim}x{dim}), {len(times)} tokens over {n_mats} host matrices "
+                      f"({n_mats * per_mat / (1 << 20):.0f} MiB rotated), median {med * 1e3:.2f} ms/token"}
 
 
 def copy_calibration(torch, steps, warmup, mib=512):
@@ -883,7 +946,10 @@ def run_config(torch, hip, key: str, args, cpu_budget: float, cache: dict) -> di
                             "us_per_step_graph": round(r["ms_per_step"] * 1e3, 3),
                             "mfma_util_of_peak": round(r["value"] / BF16_MFMA_PEAK_TFS, 4),
                             "flops_per_step": r["flops_per_step"],
-                            "rotation_mib": round(r["rotation_mib"], 1)})
+                            "rotation_mib": round(r["rotation_mib"], 1),
+                            "measured_mfma_ceiling": r["mfma_probe"],
+                            "gemm_frac_of_measured_ceiling": round(
+                                r["roofline"]["achieved"] / r["mfma_probe"]["tflops"], 4)})
     else:
         raise SystemExit(f"unknown --config {key}")
     if "roofline" in r:

@@ -315,6 +315,13 @@ int qsf_hip_prefill_4bit_packed_dev(const qsf_hip_tensor* t, const void* d_packe
  * d_sink: one uint32 of device memory, written only in the unlikely case a
  * workgroup's checksum equals a fixed constant.  Asynchronous. */
 int qsf_hip_stream_read_dev(const qsf_hip_tensor* const* t, int n, uint32_t* d_sink, void* stream);
+/* The bf16 matrix-core ceiling the prefill is set beside (a diagnostic, no
+ * counterpart in the reference): one launch in which every CU runs
+ * independent v_mfma_f32_16x16x32_bf16 chains `iters` long with no memory
+ * traffic.  d_sink: one uint32 of device memory, written only if the sum of
+ * the accumulators has a fixed bit pattern.  Asynchronous; returns the
+ * launch's FLOP, or a negative value on error. */
+double qsf_hip_mfma_peak_dev(int iters, uint32_t* d_sink, void* stream);
 
 /* ---- device-resident decode glue ------------------------------------------
  * The per-layer work between the projections of one decode step

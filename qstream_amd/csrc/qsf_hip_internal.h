@@ -186,6 +186,10 @@ int qk_prefill_4bit_noalloc(const qsf_hip_tensor* t, const uint16_t* d_x_bf16, i
  * *sink only if it equals a fixed 32-bit constant, which keeps every load
  * live and in practice stores nothing. */
 int qk_stream_read(const void* const* ptr, const size_t* bytes, int n, uint32_t* sink, hipStream_t s);
+/* The bf16 matrix-core ceiling: every CU runs independent
+ * v_mfma_f32_16x16x32_bf16 chains `iters` long, with no memory traffic.
+ * Returns the launch's FLOP (< 0 on a bad argument or launch failure). */
+double qk_mfma_peak(int iters, uint32_t* sink, hipStream_t s);
 
 /* The two halves of qk_prefill_4bit: x bf16 [m][cols] packed into d_ws
  * (qk_prefill_ws_bytes), and the GEMM of a 4-bit tensor with those cols and

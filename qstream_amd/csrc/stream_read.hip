@@ -1,7 +1,10 @@
-// stream_read.hip - the bare-read floor of a decode launch: one launch that
-// streams the device bytes of a step's tensors once and does nothing else.
-// A diagnostic with no counterpart in the reference: the bench sets the
-// GEMV's time beside it, on the same rotated bytes.
+// stream_read.hip - the measured ceilings the bench sets its kernels
+// beside, diagnostics with no counterpart in the reference:
+//  * the bare-read floor of a decode launch: one launch that streams the
+//    device bytes of a step's tensors once and does nothing else, on the
+//    same rotated bytes as the GEMV;
+//  * the bf16 matrix-core peak: v_mfma_f32_16x16x32_bf16 (the prefill's
+//    instruction) in independent chains on every SIMD, no memory traffic.
 //
 // Layout of the work: the ranges are cut into 16 KB chunks (256 threads x
 // 4 x 16-byte nontemporal loads, each load covering 4 KB of contiguous
@@ -51,7 +54,56 @@ __global__ __launch_bounds__(kThreads) void stream_read_kernel(ReadArgs a) {
     if (acc == kMagic) *a.sink = acc;
 }
 
+// kMfmaChains independent accumulators a wave, each advanced `iters` times
+// (operands from the thread id, so nothing folds); the sum of every
+// accumulator is stored only if its bits equal a fixed constant.
+constexpr int kMfmaChains = 8, kMfmaWgPerCu = 4;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// (four waves a SIMD, as launched: with the hint the accumulators stay in
+// place in VGPRs; without it the compiler routed them through AGPR moves,
+// 20-50 an iteration, and measured those instead of the matrix core)
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4, 4))) void mfma_peak_kernel(
+    int iters, uint32_t* sink) {
+    const float f = (float)(threadIdx.x & 7) * 0.125f;
+    bf16x8 a, b;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        a[i] = (__bf16)(f + (float)i);
+        b[i] = (__bf16)(f - (float)i);
+    }
+    f32x4 c0 = {f, f, f, f}, c1 = c0 + 1.f, c2 = c0 + 2.f, c3 = c0 + 3.f, c4 = c0 + 4.f, c5 = c0 + 5.f,
+          c6 = c0 + 6.f, c7 = c0 + 7.f;
+    static_assert(kMfmaChains == 8, "eight chains");
+    for (int it = 0; it < iters; it++) {
+        c0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c0, 0, 0, 0);
+        c1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c1, 0, 0, 0);
+        c2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c2, 0, 0, 0);
+        c3 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c3, 0, 0, 0);
+        c4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c4, 0, 0, 0);
+        c5 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c5, 0, 0, 0);
+        c6 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c6, 0, 0, 0);
+        c7 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c7, 0, 0, 0);
+    }
+    const f32x4 t = ((c0 + c1) + (c2 + c3)) + ((c4 + c5) + (c6 + c7));
+    const float sum = (t[0] + t[1]) + (t[2] + t[3]);
+    if (__builtin_bit_cast(uint32_t, sum) == kMagic) *sink = 1u;
+}
+
 }  // namespace
+
+extern "C" double qk_mfma_peak(int iters, uint32_t* sink, hipStream_t s) {
+    if (iters <= 0 || !sink) return -2;
+    int dev = 0, cus = 256;
+    if (hipGetDevice(&dev) == hipSuccess)
+        (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    const unsigned g = (unsigned)cus * kMfmaWgPerCu;
+    hipLaunchKernelGGL(mfma_peak_kernel, dim3(g), dim3(kThreads), 0, s, iters, sink);
+    if (hipGetLastError() != hipSuccess) return -1;
+    // FLOP of the launch: every wave's chains, 2 * 16 * 16 * 32 a MFMA
+    return (double)g * (kThreads / 64) * (double)iters * kMfmaChains * 2.0 * 16 * 16 * 32;
+}
 
 extern "C" int qk_stream_read(const void* const* ptr, const size_t* bytes, int n, uint32_t* sink,
                               hipStream_t s) {

@@ -854,6 +854,20 @@ int qsf_hip_stream_read_dev(const qsf_hip_tensor* const* t, int n, uint32_t* d_s
     return rc;
 }
 
+double qsf_hip_mfma_peak_dev(int iters, uint32_t* d_sink, void* stream) {
+    if (iters <= 0 || !d_sink) {
+        fail(E_INVALID, "qsf_hip_mfma_peak_dev: iters > 0 and a sink are required");
+        return -1.0;
+    }
+    pthread_mutex_lock(&g_lock);
+    double flop = -1.0;
+    if (!g_dev.ready) fail(E_INVALID, "qsf_hip: not initialised");
+    else if ((flop = qk_mfma_peak(iters, d_sink, pick_stream(stream))) < 0)
+        fail(E_INTERNAL, "qsf_hip_mfma_peak_dev: launch failed");
+    pthread_mutex_unlock(&g_lock);
+    return flop;
+}
+
 int qsf_hip_unpack_dev(int qt, const void* d_blocks, int nblocks, int bs, int8_t* d_codes,
                        uint32_t* d_meta, float* d_deq, void* stream) {
     if (kernel_fmt(qt) < 0 || !(bs == 32 || bs == 64 || bs == 128 || bs == 256))

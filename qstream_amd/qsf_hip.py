@@ -35,7 +35,7 @@ EXPORTS = (
     "qsf_hip_moe_create", "qsf_hip_moe_free", "qsf_hip_moe_forward_dev",
     "qsf_hip_unpack_dev", "qsf_hip_kernel_timing", "qsf_hip_kernel_timing_read", "qsf_hip_gemv_engine", "qsf_hip_moe_stages",
     "qsf_hip_prefill_4bit_dev", "qsf_hip_prefill_4bit_dev_noalloc", "qsf_hip_prefill_pack_bytes",
-    "qsf_hip_prefill_pack_dev", "qsf_hip_prefill_4bit_packed_dev", "qsf_hip_stream_read_dev",
+    "qsf_hip_prefill_pack_dev", "qsf_hip_prefill_4bit_packed_dev", "qsf_hip_stream_read_dev", "qsf_hip_mfma_peak_dev",
     "qsf_hip_rms_norm_dev", "qsf_hip_layer_norm_dev", "qsf_hip_rope_create", "qsf_hip_rope_free",
     "qsf_hip_rope_dev", "qsf_hip_kv_store_dev", "qsf_hip_attention_dev", "qsf_hip_act_mul_dev",
     "qsf_hip_gate_up_act_dev", "qsf_hip_residual_dev", "qsf_hip_embed_row_dev", "qsf_hip_embed_row_fp16_dev",
@@ -118,6 +118,8 @@ def load(path: str = LIB_PATH) -> C.CDLL:
     L.qsf_hip_prefill_4bit_packed_dev.restype = _i
     L.qsf_hip_stream_read_dev.argtypes = [C.POINTER(_vp), _i, _vp, _vp]
     L.qsf_hip_stream_read_dev.restype = _i
+    L.qsf_hip_mfma_peak_dev.argtypes = [_i, _vp, _vp]
+    L.qsf_hip_mfma_peak_dev.restype = C.c_double
     _f = C.c_float
     L.qsf_hip_rms_norm_dev.argtypes = [_vp, _vp, _vp, _i, _f, _vp]
     L.qsf_hip_layer_norm_dev.argtypes = [_vp, _vp, _vp, _vp, _i, _f, _vp]
@@ -369,6 +371,14 @@ def prefill_pack(x_bf16, m: int, cols: int, bs: int, packed, stream=None) -> Non
     aligned), shared by every 4-bit tensor of these cols and block size."""
     _check(load().qsf_hip_prefill_pack_dev(_addr(x_bf16), m, cols, bs, _addr(packed), _stream(stream)),
            "qsf_hip_prefill_pack_dev")
+
+
+def mfma_peak(iters, sink, stream=None) -> float:
+    """One launch of independent bf16 MFMA chains on every CU; returns its FLOP."""
+    flop = load().qsf_hip_mfma_peak_dev(iters, _addr(sink), _stream(stream))
+    if flop < 0:
+        _check(-1, "qsf_hip_mfma_peak_dev")
+    return float(flop)
 
 
 def stream_read(tensors, sink, stream=None) -> None:

@@ -207,3 +207,19 @@ def test_stream_read_floor_runs(hip):
     finally:
         for t in ts:
             t.free()
+
+
+def test_mfma_peak_probe(hip):
+    """The bf16 matrix-core probe the bench sets the prefill beside: one
+    launch returns its FLOP (every CU's waves, 8 chains of iters
+    v_mfma_f32_16x16x32_bf16 each), leaves the sink alone in practice, and
+    refuses a bad count."""
+    torch = torch_cuda()
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    sink = torch.zeros(4, dtype=torch.int32, device="cuda:0")
+    flop = hip.mfma_peak(16, sink, stream=torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    assert flop == cus * 4 * 4 * 16 * 8 * 2 * 16 * 16 * 32
+    assert int(sink.cpu()[0]) == 0
+    with pytest.raises(hip.QsfHipError):
+        hip.mfma_peak(0, sink)
