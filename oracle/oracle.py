@@ -349,3 +349,40 @@ class RefContainer:
 
 def ref_container() -> RefContainer | None:
     return RefContainer() if os.path.exists(REF_CONTAINER_SO) else None
+
+
+REF_GLUE_SO = os.path.join(HERE, "_ref", "libqsf_ref_glue.so")
+
+
+class RefGlue:
+    """QStream's own static engine helpers apply_rope (src/engine.c:205-234)
+    and kv_cache_store (src/engine.c:240-293), compiled from engine.c into
+    oracle/_ref behind oracle/ref_glue.c.  Loaded with lazy binding: the rest
+    of engine.c's dependencies are never called, so never bound."""
+
+    def __init__(self, path: str = REF_GLUE_SO):
+        if not os.path.exists(path):
+            raise FileNotFoundError(path)
+        L = self.lib = C.CDLL(path, mode=os.RTLD_LAZY | os.RTLD_LOCAL)
+        L.ref_glue_apply_rope.argtypes = [_vp, _vp, _i, _i, C.c_float, _i, _i]
+        L.ref_glue_apply_rope.restype = None
+        L.ref_glue_kv_store.argtypes = [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp, _vp]
+        L.ref_glue_kv_store.restype = None
+
+    def rope(self, q, k, head_dim, position, theta, n_heads, n_kv):
+        q = np.array(q, np.float32, copy=True)
+        k = np.array(k, np.float32, copy=True)
+        self.lib.ref_glue_apply_rope(_ptr(q), _ptr(k), head_dim, position, theta, n_heads, n_kv)
+        return q, k
+
+    def kv_store(self, kc, vc, ks, vs, max_seq, n_kv, head_dim, position, k, v):
+        """Writes row `position` of the layer's int8 caches in place."""
+        assert n_kv <= 64
+        k = np.ascontiguousarray(k, np.float32)
+        v = np.ascontiguousarray(v, np.float32)
+        self.lib.ref_glue_kv_store(_ptr(kc), _ptr(vc), _ptr(ks), _ptr(vs), max_seq, n_kv, head_dim, position,
+                                   _ptr(k), _ptr(v))
+
+
+def ref_glue() -> RefGlue | None:
+    return RefGlue() if os.path.exists(REF_GLUE_SO) else None

@@ -3,11 +3,14 @@
 * Functions that live in src/kernels_scalar.c (norms, softmax, activations,
   vector add/mul) are compared bit for bit with the reference's own
   translation unit compiled strictly into oracle/_ref.
-* The static helpers of src/engine.c (apply_rope, kv_cache_store, the
-  attention loop, the residual NaN check, the embedding lookup) cannot be
-  compiled alone (the reference library does not build as shipped), so
-  they are pinned by closed forms, invariants and fp64 brute force, chosen
-  so that a wrong sign, pairing, index or rounding rule fails.
+* The static helpers apply_rope and kv_cache_store of src/engine.c are
+  compared bit for bit with the reference's engine.c compiled strictly into
+  oracle/_ref (oracle/ref_glue.c includes the unit and exports them).
+* The rest of the engine's inline glue (the attention loop, the residual
+  NaN check, the embedding lookup) lives inside qsf_forward and cannot be
+  called alone, so it is pinned by closed forms, invariants and fp64 brute
+  force, chosen so that a wrong sign, pairing, index or rounding rule
+  fails; so are RoPE and the KV store as well.
 """
 from __future__ import annotations
 
@@ -61,6 +64,57 @@ def test_softmax_activations_vecops_bit_exact_vs_reference(oracle, ref):
 
 
 # ---- RoPE: closed form --------------------------------------------------------
+@pytest.fixture(scope="module")
+def ref_glue():
+    from oracle.oracle import ref_glue as rg
+    r = rg()
+    if r is None:
+        pytest.skip("oracle/_ref not built (reference sources absent)")
+    return r
+
+
+@pytest.mark.parametrize("hd,nh,nkv,position,theta", [(128, 32, 8, 0, 10000.0), (128, 4, 4, 1023, 10000.0),
+                                                      (64, 8, 2, 77777, 500000.0), (256, 2, 1, 5, 1e6),
+                                                      (80, 6, 2, 131071, 10000.0), (2, 3, 1, 9, 10000.0)])
+def test_rope_bit_exact_vs_reference(oracle, ref_glue, hd, nh, nkv, position, theta):
+    """apply_rope of the reference's engine.c against the oracle's restatement:
+    every bit of q and k, large positions included (the angle reduction)."""
+    rng = np.random.default_rng(hd + position)
+    q = (rng.standard_normal(nh * hd) * 3).astype(np.float32)
+    k = (rng.standard_normal(nkv * hd) * 3).astype(np.float32)
+    q1, k1 = oracle.rope(q, k, hd, position, theta, nh, nkv)
+    q2, k2 = ref_glue.rope(q, k, hd, position, theta, nh, nkv)
+    assert np.array_equal(q1.view(np.uint32), q2.view(np.uint32))
+    assert np.array_equal(k1.view(np.uint32), k2.view(np.uint32))
+
+
+@pytest.mark.parametrize("nkv,hd,max_seq,position,scale", [(8, 128, 16, 5, 1.0), (2, 64, 4, 3, 1e-3),
+                                                           (3, 256, 2, 0, 50.0), (1, 80, 9, 8, 1.0)])
+def test_kv_store_bit_exact_vs_reference(oracle, ref_glue, nkv, hd, max_seq, position, scale):
+    """kv_cache_store of the reference's engine.c against the oracle's: codes
+    and scales bit for bit, with a zero head, a tiny head (absmax below
+    1e-30), exact .5 ties and values that round up to a tie, and the rows
+    around the stored one left alone."""
+    rng = np.random.default_rng(nkv * hd + position)
+    k = (rng.standard_normal(nkv * hd) * scale).astype(np.float32)
+    v = (rng.standard_normal(nkv * hd) * scale).astype(np.float32)
+    k[:hd] = 0.0                                  # a zero head
+    if nkv > 1:
+        v[hd:2 * hd] = 1e-31                      # absmax below 1e-30: codes 0
+    n = min(hd, len(KV_TIE_ROW))
+    v[-hd:-hd + n] = KV_TIE_ROW[:n]               # ties and near-ties (absmax 127: inv 1)
+    outs = []
+    for impl in (oracle, ref_glue):
+        kc = np.full((nkv, max_seq, hd), 7, np.int8)
+        vc = kc.copy()
+        ks = np.full((nkv, max_seq), 0.25, np.float32)
+        vs = ks.copy()
+        impl.kv_store(kc, vc, ks, vs, max_seq, nkv, hd, position, k, v)
+        outs.append((kc, vc, ks.view(np.uint32), vs.view(np.uint32)))
+    for a, b in zip(*outs):
+        assert np.array_equal(a, b)
+
+
 def rope_freqs(head_dim, theta):
     """The reference's fp32 frequencies 1.0f / powf(theta, (float)i / head_dim)
     with the C library's powf (src/engine.c:210)."""
