@@ -632,14 +632,15 @@ __global__ __launch_bounds__(ATT_THREADS) void rope_attention_part_kernel(
 // scale * q), each product and sum rounded as in src/quant.c:95-177.
 __global__ __launch_bounds__(256) void embed_row_kernel(const uint8_t* __restrict__ blocks, int fmt,
                                                         int bs, int bb, int hd, float* out,
-                                                        int frag_row, int nq) {
+                                                        int frag_row, int nq, int plane, int nb) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= hd) return;
-    // byte j of the value's block: on-disk order (`blocks` is the row), or
-    // fragment order (`blocks` is the tensor, frag_row the row)
+    // byte j of the value's block: on-disk or row-plane order (`blocks` is
+    // the row), or fragment order (`blocks` is the tensor, frag_row the row)
     const int b = i / bs;
     auto byte_at = [&](int j) -> unsigned {
         return frag_row >= 0 ? blocks[qsf::frag_off((size_t)frag_row, b, j, nq, bb)]
+               : plane       ? blocks[qsf::plane_off(b, j, nb, bb)]
                              : blocks[(size_t)b * bb + j];
     };
     const uint32_t meta = byte_at(0) | (byte_at(1) << 8) | (byte_at(2) << 16) | (byte_at(3) << 24);
@@ -806,7 +807,7 @@ extern "C" int qk_embed_row(const qsf_hip_tensor* t, int token, float* out, hipS
     if (t->cols <= 0) return 0;
     const uint8_t* row = t->frag ? t->d_blocks : t->d_blocks + (size_t)token * t->nb * t->block_bytes;
     hipLaunchKernelGGL(embed_row_kernel, dim3((t->cols + 255) / 256), dim3(256), 0, s, row, t->fmt, t->bs,
-                       t->block_bytes, t->cols, out, t->frag ? token : -1, t->frag_nq);
+                       t->block_bytes, t->cols, out, t->frag ? token : -1, t->frag_nq, t->plane, t->nb);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

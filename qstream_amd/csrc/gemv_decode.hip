@@ -481,7 +481,7 @@ __device__ __forceinline__ void entry_at(const GemvArgs& a, int m, uint32_t e, u
 template <int FMT, int BS, int R, bool SPLIT = false>
 __device__ __forceinline__ void load_block(const uint8_t* __restrict__ w, const uint32_t (&roff)[R],
                                            int b, uint32_t (&wv)[R][1 + Fmt<FMT, BS>::CW],
-                                           uint32_t pbb = 0, int lsplit = 0) {
+                                           uint32_t pbb, int lsplit, int nb) {
     using F = Fmt<FMT, BS>;
     constexpr int NW = 1 + F::CW;
     if constexpr (SPLIT) {
@@ -507,10 +507,40 @@ __device__ __forceinline__ void load_block(const uint8_t* __restrict__ w, const 
         }
         return;
     }
-    // dwordx4 pieces, then single dwords: the address unit takes 4 lanes a
-    // clock whatever the width, so a 20-byte 2-bit block costs 2 load
-    // instructions instead of 5 (the compiler does not merge dword loads of
-    // 4-byte aligned blocks by itself)
+    if constexpr (BS <= 64) {
+        // row-plane order (tensors of blocks of at most 64 codes): dwords
+        // 4i..4i+3 of block b at 16 b in plane i (nb x 16 bytes), the last
+        // NW % 4 dwords at 4 (NW % 4) b in the tail plane after the planes.
+        // The lanes of a row group read consecutive blocks, so each 16-byte
+        // load instruction covers aligned, contiguous memory.
+        constexpr int NQ = NW / 4, NT = NW % 4;
+        const uint32_t ps = (uint32_t)nb * 16u;
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const uint32_t o = roff[r] + (uint32_t)b * 16u;
+#pragma unroll
+            for (int q = 0; q < NQ; q++) {
+                const u32x4 v = __builtin_nontemporal_load(
+                    reinterpret_cast<const u32x4_a4*>(w + (o + (uint32_t)q * ps)));
+                wv[r][4 * q] = v.x;
+                wv[r][4 * q + 1] = v.y;
+                wv[r][4 * q + 2] = v.z;
+                wv[r][4 * q + 3] = v.w;
+            }
+            if constexpr (NT > 0) {
+                const uint32_t* p = reinterpret_cast<const uint32_t*>(
+                    w + (roff[r] + (uint32_t)NQ * ps + (uint32_t)b * (4u * NT)));
+#pragma unroll
+                for (int i = 0; i < NT; i++) wv[r][4 * NQ + i] = __builtin_nontemporal_load(p + i);
+            }
+        }
+        return;
+    }
+    // on-disk order (blocks of 128 or 256 codes read whole: the table slots
+    // and prepared x): dwordx4 pieces, then single dwords: the address unit
+    // takes 4 lanes a clock whatever the width, so a 68-byte block costs 5
+    // load instructions instead of 17 (the compiler does not merge dword
+    // loads of 4-byte aligned blocks by itself)
 #pragma unroll
     for (int r = 0; r < R; r++) {
         const uint32_t* p = reinterpret_cast<const uint32_t*>(w + (roff[r] + (uint32_t)b * F::BB));
@@ -745,7 +775,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
     // next item's weights; past the last item, the last tile's row starts
     auto issue = [&](WV& wv) __attribute__((always_inline)) {
         const int b = ij < nt ? min(lig + (iq << lgl), a.nb - 1) : 0;
-        load_block<FMT, BS, R, SPLIT>(W, ioff, b, wv, a.pbb, a.lsplit);
+        load_block<FMT, BS, R, SPLIT>(W, ioff, b, wv, a.pbb, a.lsplit, a.nb);
         if (++iq == ipt) {
             iq = 0;
             ++ij;
@@ -1062,7 +1092,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
         const bool live = lig < a.nb;
         const int bl = min(lig, a.nb - 1);
         auto issue_d = [&](WV& wv) __attribute__((always_inline)) {
-            load_block<FMT, BS, R, SPLIT>(W, ioff, bl, wv, a.pbb, a.lsplit);
+            load_block<FMT, BS, R, SPLIT>(W, ioff, bl, wv, a.pbb, a.lsplit, a.nb);
             ++ij;
             at_tile(min(ij, ntl - 1));
         };
@@ -1238,7 +1268,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_chunked_kernel(GemvArgs a) {
             for (int r = 0; r < R; r++) roff[r] = (uint32_t)min(row0 + r, a.rows[m] - 1) * row_bytes;
             for (int b = c0 + lig; b < c1; b += lpg) {
                 uint32_t wv[R][1 + F::CW];
-                load_block<FMT, BS, R, SPLIT>(a.w[m], roff, b, wv, a.pbb, a.lsplit);
+                load_block<FMT, BS, R, SPLIT>(a.w[m], roff, b, wv, a.pbb, a.lsplit, a.nb);
                 compute_block<FMT, BS, R>(wv, dig + (b - c0) * F::DWS, meta[b - c0], rs[j]);
             }
         }

@@ -237,7 +237,7 @@ __device__ __forceinline__ void tile_of(int id, int nwg, int tiles_n, int& tm, i
 
 // RAGGED: k is not a multiple of 2 SK, so code stages reach past the last
 // column; their B items are zeroed (and x is zero there).
-template <int BS, bool RAGGED, bool FRAG = false>
+template <int BS, bool RAGGED, bool FRAG = false, bool PLANE = false>
 __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
     constexpr int BB = 4 + BS / 2;             // block bytes
     // two B buffers and their scales during the main loop; the output
@@ -312,6 +312,29 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
                                             ? __builtin_amdgcn_raw_buffer_load_b32(wr, o + (pa + 2) * 1024u, 0, 0)
                                             : __builtin_amdgcn_raw_buffer_load_b32(wr, ftail(b), 0, 0);
                     meta = pa == 0 ? pA.x : __builtin_amdgcn_raw_buffer_load_b32(wr, o, 0, 0);
+                    c[0] = u32x4{pA.y, pA.z, pA.w, pB.x};
+                    c[1] = u32x4{pB.y, pB.z, pB.w, pC};
+                }
+                return;
+            }
+            if constexpr (PLANE) {
+                // row-plane order, blocks of 64: block b's meta and first 12
+                // code bytes at 16 b in plane 0, the next 16 at 16 b in plane
+                // 1 (nb * 16 bytes on), the last 4 at 4 b in the tail plane
+                static_assert(BS == 64, "row-plane order: blocks of 64");
+                const uint32_t ps = (uint32_t)a.nb * 16u;
+                if (s >= ncode) {
+                    const uint32_t b0 = (uint32_t)(16 * (s - ncode) + 8 * h);
+#pragma unroll
+                    for (int j = 0; j < 8; j++)
+                        c[j >> 2][j & 3] = __builtin_amdgcn_raw_buffer_load_b32(wr, wv + (b0 + j) * 16u, 0, 0);
+                    meta = 0;
+                } else {
+                    const uint32_t b = (uint32_t)(2 * s + h);
+                    const u32x4 pA = __builtin_amdgcn_raw_buffer_load_b128(wr, wv + b * 16u, 0, 0);
+                    const u32x4 pB = __builtin_amdgcn_raw_buffer_load_b128(wr, wv + ps + b * 16u, 0, 0);
+                    const uint32_t pC = __builtin_amdgcn_raw_buffer_load_b32(wr, wv + 2u * ps + b * 4u, 0, 0);
+                    meta = pA.x;
                     c[0] = u32x4{pA.y, pA.z, pA.w, pB.x};
                     c[1] = u32x4{pB.y, pB.z, pB.w, pC};
                 }
@@ -635,18 +658,20 @@ extern "C" int qk_prefill_gemm(const qsf_hip_tensor* t, const void* d_ws, int m,
                      tiles_n, st.sz, st.sz + st.sc, 16 * st.sz <= ZP_MAX ? 16 * st.sz : 0,
                      (uint32_t)w_bytes, (uint32_t)xp_bytes, t->frag_nq};
     const dim3 grid(tiles_n * tiles_m), block(512);
-#define QK_PREFILL_CASE(B, F)                                                   \
-    if (ragged) launch<prefill_kernel<B, true, F>>(grid, block, s, a);          \
-    else launch<prefill_kernel<B, false, F>>(grid, block, s, a);
+#define QK_PREFILL_CASE(B, F, P)                                                \
+    if (ragged) launch<prefill_kernel<B, true, F, P>>(grid, block, s, a);       \
+    else launch<prefill_kernel<B, false, F, P>>(grid, block, s, a);
     switch (t->bs) {
     case 64:
-        if (t->frag) { QK_PREFILL_CASE(64, true) } else { QK_PREFILL_CASE(64, false) }
+        if (t->frag) { QK_PREFILL_CASE(64, true, false) }
+        else if (t->plane) { QK_PREFILL_CASE(64, false, true) }
+        else { QK_PREFILL_CASE(64, false, false) }
         break;
     case 128:
-        if (t->frag) { QK_PREFILL_CASE(128, true) } else { QK_PREFILL_CASE(128, false) }
+        if (t->frag) { QK_PREFILL_CASE(128, true, false) } else { QK_PREFILL_CASE(128, false, false) }
         break;
     case 256:
-        QK_PREFILL_CASE(256, false)
+        QK_PREFILL_CASE(256, false, false)
         break;
     default: return -2;
     }

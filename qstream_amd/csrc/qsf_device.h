@@ -32,6 +32,16 @@ __device__ __forceinline__ size_t frag_off(size_t row, int b, int j, int nq, int
                       : base + (size_t)k * 1024 + (size_t)lane * (size_t)(bb & 15) + (size_t)(j - 16 * k);
 }
 
+// Byte j of block b of a row of nb blocks in row-plane order (the layout of
+// qk_plane_offset in qsf_hip_internal.h), from the row's first byte: 16-byte
+// planes of nb blocks, then a tail plane of bb % 16 bytes a block.
+__device__ __forceinline__ uint32_t plane_off(int b, int j, int nb, int bb) {
+    const int k = bb >> 4;
+    return j < 16 * k ? (uint32_t)(j >> 4) * (uint32_t)nb * 16u + (uint32_t)b * 16u + (uint32_t)(j & 15)
+                      : (uint32_t)k * (uint32_t)nb * 16u + (uint32_t)b * (uint32_t)(bb & 15) +
+                            (uint32_t)(j - 16 * k);
+}
+
 // Signed 4-bit x signed 4-bit dot of 8 nibble pairs, accumulated in int32
 // (v_dot8_i32_i4).
 __device__ __forceinline__ int sdot8(uint32_t a, uint32_t b, int c) {

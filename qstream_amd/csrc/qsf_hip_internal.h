@@ -43,8 +43,10 @@ typedef struct qsf_hip_tensor {
     uint16_t* d_oval;           /* ... and n_csr fp16 values */
     void*    d_alloc;           /* base of the single device allocation */
     size_t   alloc_bytes;       /* its parts (blocks, scales, CSR) up to the tail pad */
-    int      frag;              /* 1: d_blocks in fragment order (below), 0: on-disk order */
+    int      frag;              /* 1: d_blocks in fragment order (below) */
     int      frag_nq;           /* fragment order: 4-block quads a row, ceil(nb / 4) */
+    int      plane;             /* 1: d_blocks in row-plane order (below); with frag
+                                 * 0 as well: on-disk order */
     int      registry_owned;    /* uploaded implicitly by a table-slot call */
     const void* succ;           /* table slots: the key called next with the same x ... */
     int      succ_hits;         /* ... this many times since it last differed */
@@ -66,6 +68,20 @@ typedef struct qsf_hip_tensor {
 size_t qk_frag_bytes(int rows, int nb, int block_bytes);
 /* byte j of block b of row `row` in fragment order */
 size_t qk_frag_offset(size_t row, int b, int j, int nq, int block_bytes);
+/* Row-plane order: the device layout of every other dense tensor with
+ * blocks of at most 64 codes (the blocks the dot-product GEMV reads whole).
+ * Rows stay where they are on disk (nb * bb bytes each); inside a row, bytes
+ * [16 i, 16 i + 16) of block b sit at i * nb * 16 + 16 b (plane i, for
+ * i < bb / 16), and the last bb % 16 bytes of block b at (bb / 16) * nb * 16
+ * + (bb % 16) b (the tail plane).  So a wave's 16-byte loads of consecutive
+ * blocks each read one aligned, contiguous run of 1 KB where the on-disk
+ * order gives dword-aligned loads that straddle lines, and a block's meta
+ * dword and codes arrive in one 16-byte load. */
+int qk_plane_layout(int fmt, int bs);
+/* byte j of block b of a row of nb blocks in row-plane order, from the row's
+ * first byte */
+size_t qk_plane_offset(int b, int j, int nb, int block_bytes);
+
 /* 1 when the matrix-core GEMV covers tensors of this format (QK_FMT_*),
  * block size and column count (with an outlier table when `outliers`), so
  * that they are uploaded in fragment order */

@@ -346,6 +346,34 @@ static void frag_permute(uint8_t* dst, const uint8_t* src, int rows, int nb, int
         }
 }
 
+/* Row-plane order (qsf_hip_internal.h): the blocks of at most 64 codes that
+ * the dot-product GEMV reads whole, one per lane. */
+int qk_plane_layout(int fmt, int bs) {
+    return fmt >= 0 && bs <= 64;
+}
+
+size_t qk_plane_offset(int b, int j, int nb, int block_bytes) {
+    const int k = block_bytes >> 4;
+    return j < 16 * k ? (size_t)(j >> 4) * (size_t)nb * 16 + (size_t)b * 16 + (size_t)(j & 15)
+                      : (size_t)k * (size_t)nb * 16 + (size_t)b * (size_t)(block_bytes & 15) +
+                            (size_t)(j - 16 * k);
+}
+
+/* The on-disk blocks [rows][nb][bb] into row-plane order. */
+static void plane_permute(uint8_t* dst, const uint8_t* src, int rows, int nb, int bb) {
+    const int k = bb / 16, tb = bb % 16;
+    const size_t rb = (size_t)nb * bb;
+    for (int r = 0; r < rows; r++) {
+        const uint8_t* s = src + (size_t)r * rb;
+        uint8_t* d = dst + (size_t)r * rb;
+        for (int b = 0; b < nb; b++) {
+            for (int i = 0; i < k; i++)
+                memcpy(d + (size_t)i * nb * 16 + (size_t)b * 16, s + (size_t)b * bb + 16 * i, 16);
+            if (tb) memcpy(d + (size_t)k * nb * 16 + (size_t)b * tb, s + (size_t)b * bb + 16 * k, (size_t)tb);
+        }
+    }
+}
+
 static qsf_hip_tensor* upload_locked(const void* host, int qt, int rows, int cols, int bs) {
     if (init_locked(g_dev.ready ? g_dev.device : 0) != E_OK) return NULL;
     if (!host || rows < 0 || cols < 0) {
@@ -382,13 +410,15 @@ static qsf_hip_tensor* upload_locked(const void* host, int qt, int rows, int col
     }
     t->n_outliers = n_out;
     /* device order of the blocks: fragment order where the matrix-core GEMV
-     * is the engine for the format and covers the shape, else the on-disk
-     * order.  Engine 1 takes it for the 3-bit formats, whose unpack is the
-     * costliest on the vector units; 2 for every format. */
+     * is the engine for the format and covers the shape (engine 1 takes it
+     * for the 3-bit formats, whose unpack is the costliest on the vector
+     * units; 2 for every format), else row-plane order for blocks of at most
+     * 64 codes, else the on-disk order. */
     const int engine = qk_gemv_mfma_enable(-1);
     t->frag = fmt >= 0 && rows > 0 && (engine == 2 || (engine == 1 && fmt == QK_FMT_3)) &&
               qk_mfma_layout(fmt, bs, cols, is_outlier(qt));
     t->frag_nq = (t->nb + 3) / 4;
+    t->plane = !t->frag && rows > 0 && qk_plane_layout(fmt, t->bs);
     const size_t dev_blocks_bytes = t->frag ? qk_frag_bytes(rows, t->nb, t->block_bytes) : blocks_bytes;
 
     /* CSR of the outlier table: stable counting sort by row keeps file order
@@ -462,15 +492,17 @@ static qsf_hip_tensor* upload_locked(const void* host, int qt, int rows, int col
     uint8_t* base = (uint8_t*)t->d_alloc;
     t->d_blocks = base + off_blocks;
     const uint8_t* host_blocks = is_outlier(qt) ? p + 4 + 6 * (size_t)n_out : p;
-    if (t->frag) {
+    if (t->frag || t->plane) {
         uint8_t* fb = calloc(dev_blocks_bytes ? dev_blocks_bytes : 1, 1);
         if (!fb) {
             hipFree(t->d_alloc);
             free(row_ptr); free(ocol); free(oval); free(t);
-            fail(E_OOM, "qsf_hip: fragment-order staging (%zu bytes)", dev_blocks_bytes);
+            fail(E_OOM, "qsf_hip: %s staging (%zu bytes)", t->frag ? "fragment-order" : "row-plane",
+                 dev_blocks_bytes);
             return NULL;
         }
-        frag_permute(fb, host_blocks, rows, t->nb, t->block_bytes);
+        if (t->frag) frag_permute(fb, host_blocks, rows, t->nb, t->block_bytes);
+        else plane_permute(fb, host_blocks, rows, t->nb, t->block_bytes);
         he = hipMemcpy(t->d_blocks, fb, dev_blocks_bytes, hipMemcpyHostToDevice);
         free(fb);
     } else {
