@@ -640,7 +640,7 @@ __global__ __launch_bounds__(256) void embed_row_kernel(const uint8_t* __restric
     const int b = i / bs;
     auto byte_at = [&](int j) -> unsigned {
         return frag_row >= 0 ? blocks[qsf::frag_off((size_t)frag_row, b, j, nq, bb)]
-               : plane       ? blocks[qsf::plane_off(b, j, nb, bb)]
+               : plane       ? blocks[qsf::plane_off(b, j, nb, bb, bs)]
                              : blocks[(size_t)b * bb + j];
     };
     const uint32_t meta = byte_at(0) | (byte_at(1) << 8) | (byte_at(2) << 16) | (byte_at(3) << 24);

@@ -485,25 +485,37 @@ __device__ __forceinline__ void load_block(const uint8_t* __restrict__ w, const 
     using F = Fmt<FMT, BS>;
     constexpr int NW = 1 + F::CW;
     if constexpr (SPLIT) {
-        // block b is part b % 2^lsplit of stored block b >> lsplit (pbb bytes):
-        // that block's meta dword, then the part's BS codes, which start on a
-        // byte (BS codes of any width are whole bytes) and on a dword
-        const uint32_t moff = (uint32_t)(b >> lsplit) * pbb;
-        const uint32_t coff = moff + 4u + (uint32_t)(b & ((1 << lsplit) - 1)) * (4u * F::CW);
+        // b is 64-code part b of the row (nb parts with data), part
+        // b % 2^lsplit of stored block b >> lsplit; row-plane order (blocks
+        // of 128 or 256 codes): the stored block's meta dword in the meta
+        // plane, then the part's CW code dwords, its quads at 16 b in the
+        // 16-byte planes over the row's parts (every part of every stored
+        // block, so a partial last block counts whole) and the rest at
+        // 4 (CW % 4) b in the tail plane
+        constexpr int NQ = F::CW / 4, NT = F::CW % 4;
+        (void)pbb;
+        const uint32_t nst = ((uint32_t)nb + (1u << lsplit) - 1u) >> lsplit;   // stored blocks a row
+        const uint32_t ps = (nst << lsplit) * 16u;
 #pragma unroll
         for (int r = 0; r < R; r++) {
-            wv[r][0] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(w + roff[r] + moff));
-            const uint32_t* c = reinterpret_cast<const uint32_t*>(w + roff[r] + coff);
+            wv[r][0] = __builtin_nontemporal_load(
+                reinterpret_cast<const uint32_t*>(w + (roff[r] + 4u * (uint32_t)(b >> lsplit))));
+            const uint32_t o = roff[r] + 4u * nst + (uint32_t)b * 16u;
 #pragma unroll
-            for (int i = 0; i + 4 <= F::CW; i += 4) {
-                const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_a4*>(c + i));
-                wv[r][1 + i] = v.x;
-                wv[r][2 + i] = v.y;
-                wv[r][3 + i] = v.z;
-                wv[r][4 + i] = v.w;
+            for (int q = 0; q < NQ; q++) {
+                const u32x4 v = __builtin_nontemporal_load(
+                    reinterpret_cast<const u32x4_a4*>(w + (o + (uint32_t)q * ps)));
+                wv[r][1 + 4 * q] = v.x;
+                wv[r][2 + 4 * q] = v.y;
+                wv[r][3 + 4 * q] = v.z;
+                wv[r][4 + 4 * q] = v.w;
             }
+            if constexpr (NT > 0) {
+                const uint32_t* p = reinterpret_cast<const uint32_t*>(
+                    w + (roff[r] + 4u * nst + (uint32_t)NQ * ps + (uint32_t)b * (4u * NT)));
 #pragma unroll
-            for (int i = F::CW & ~3; i < F::CW; i++) wv[r][1 + i] = __builtin_nontemporal_load(c + i);
+                for (int i = 0; i < NT; i++) wv[r][1 + 4 * NQ + i] = __builtin_nontemporal_load(p + i);
+            }
         }
         return;
     }
@@ -534,26 +546,37 @@ __device__ __forceinline__ void load_block(const uint8_t* __restrict__ w, const 
                 for (int i = 0; i < NT; i++) wv[r][4 * NQ + i] = __builtin_nontemporal_load(p + i);
             }
         }
-        return;
-    }
-    // on-disk order (blocks of 128 or 256 codes read whole: the table slots
-    // and prepared x): dwordx4 pieces, then single dwords: the address unit
-    // takes 4 lanes a clock whatever the width, so a 68-byte block costs 5
-    // load instructions instead of 17 (the compiler does not merge dword
-    // loads of 4-byte aligned blocks by itself)
+    } else {
+        // blocks of 128 or 256 codes read whole (the table slots and prepared
+        // x), from row-plane order: block b's meta dword at 4 b, then each of its
+        // P 64-code parts u = b P + p as in the split read above
+        constexpr int P = BS / 64, CWP = F::CW / P, NQ = CWP / 4, NT = CWP % 4;
+        (void)NW;
+        const uint32_t np = (uint32_t)nb * P, ps = np * 16u;
 #pragma unroll
-    for (int r = 0; r < R; r++) {
-        const uint32_t* p = reinterpret_cast<const uint32_t*>(w + (roff[r] + (uint32_t)b * F::BB));
+        for (int r = 0; r < R; r++) {
+            wv[r][0] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(w + (roff[r] + 4u * (uint32_t)b)));
 #pragma unroll
-        for (int i = 0; i + 4 <= NW; i += 4) {
-            const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_a4*>(p + i));
-            wv[r][i] = v.x;
-            wv[r][i + 1] = v.y;
-            wv[r][i + 2] = v.z;
-            wv[r][i + 3] = v.w;
+            for (int p = 0; p < P; p++) {
+                const uint32_t u = (uint32_t)b * P + (uint32_t)p;
+                const uint32_t o = roff[r] + 4u * (uint32_t)nb + u * 16u;
+#pragma unroll
+                for (int q = 0; q < NQ; q++) {
+                    const u32x4 v = __builtin_nontemporal_load(
+                        reinterpret_cast<const u32x4_a4*>(w + (o + (uint32_t)q * ps)));
+                    wv[r][1 + p * CWP + 4 * q] = v.x;
+                    wv[r][2 + p * CWP + 4 * q] = v.y;
+                    wv[r][3 + p * CWP + 4 * q] = v.z;
+                    wv[r][4 + p * CWP + 4 * q] = v.w;
+                }
+                if constexpr (NT > 0) {
+                    const uint32_t* t = reinterpret_cast<const uint32_t*>(
+                        w + (roff[r] + 4u * (uint32_t)nb + (uint32_t)NQ * ps + u * (4u * NT)));
+#pragma unroll
+                    for (int i = 0; i < NT; i++) wv[r][1 + p * CWP + 4 * NQ + i] = __builtin_nontemporal_load(t + i);
+                }
+            }
         }
-#pragma unroll
-        for (int i = NW & ~3; i < NW; i++) wv[r][i] = __builtin_nontemporal_load(p + i);
     }
 }
 

@@ -317,11 +317,31 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
                 }
                 return;
             }
-            if constexpr (PLANE) {
+            if constexpr (PLANE && BS > 64) {
+                // row-plane order, blocks of 128 or 256: block b's meta dword
+                // at 4 b, then 64-code part u's 32 code bytes at 16 u in the
+                // two 16-byte planes over the row's np parts
+                constexpr uint32_t P = BS / 64;
+                const uint32_t np = (uint32_t)a.nb * P, cb = 4u * (uint32_t)a.nb;
+                if (s >= ncode) {
+                    const uint32_t b0 = (uint32_t)(16 * (s - ncode) + 8 * h);
+#pragma unroll
+                    for (int j = 0; j < 8; j++)
+                        c[j >> 2][j & 3] = __builtin_amdgcn_raw_buffer_load_b32(wr, wv + (b0 + j) * 4u, 0, 0);
+                    meta = 0;
+                } else {
+                    const uint32_t b = BS == 128 ? (uint32_t)s : (uint32_t)s / 2;
+                    const uint32_t u = b * P + (BS == 128 ? (uint32_t)h : 2u * ((uint32_t)s % 2) + (uint32_t)h);
+                    meta = __builtin_amdgcn_raw_buffer_load_b32(wr, wv + 4u * b, 0, 0);
+                    c[0] = __builtin_amdgcn_raw_buffer_load_b128(wr, wv + cb + u * 16u, 0, 0);
+                    c[1] = __builtin_amdgcn_raw_buffer_load_b128(wr, wv + cb + np * 16u + u * 16u, 0, 0);
+                }
+                return;
+            }
+            if constexpr (PLANE && BS == 64) {
                 // row-plane order, blocks of 64: block b's meta and first 12
                 // code bytes at 16 b in plane 0, the next 16 at 16 b in plane
                 // 1 (nb * 16 bytes on), the last 4 at 4 b in the tail plane
-                static_assert(BS == 64, "row-plane order: blocks of 64");
                 const uint32_t ps = (uint32_t)a.nb * 16u;
                 if (s >= ncode) {
                     const uint32_t b0 = (uint32_t)(16 * (s - ncode) + 8 * h);
@@ -663,15 +683,13 @@ extern "C" int qk_prefill_gemm(const qsf_hip_tensor* t, const void* d_ws, int m,
     else launch<prefill_kernel<B, false, F, P>>(grid, block, s, a);
     switch (t->bs) {
     case 64:
-        if (t->frag) { QK_PREFILL_CASE(64, true, false) }
-        else if (t->plane) { QK_PREFILL_CASE(64, false, true) }
-        else { QK_PREFILL_CASE(64, false, false) }
+        if (t->frag) { QK_PREFILL_CASE(64, true, false) } else { QK_PREFILL_CASE(64, false, true) }
         break;
     case 128:
-        if (t->frag) { QK_PREFILL_CASE(128, true, false) } else { QK_PREFILL_CASE(128, false, false) }
+        if (t->frag) { QK_PREFILL_CASE(128, true, false) } else { QK_PREFILL_CASE(128, false, true) }
         break;
     case 256:
-        QK_PREFILL_CASE(256, false, false)
+        QK_PREFILL_CASE(256, false, true)
         break;
     default: return -2;
     }

@@ -32,14 +32,24 @@ __device__ __forceinline__ size_t frag_off(size_t row, int b, int j, int nq, int
                       : base + (size_t)k * 1024 + (size_t)lane * (size_t)(bb & 15) + (size_t)(j - 16 * k);
 }
 
-// Byte j of block b of a row of nb blocks in row-plane order (the layout of
-// qk_plane_offset in qsf_hip_internal.h), from the row's first byte: 16-byte
-// planes of nb blocks, then a tail plane of bb % 16 bytes a block.
-__device__ __forceinline__ uint32_t plane_off(int b, int j, int nb, int bb) {
-    const int k = bb >> 4;
-    return j < 16 * k ? (uint32_t)(j >> 4) * (uint32_t)nb * 16u + (uint32_t)b * 16u + (uint32_t)(j & 15)
-                      : (uint32_t)k * (uint32_t)nb * 16u + (uint32_t)b * (uint32_t)(bb & 15) +
-                            (uint32_t)(j - 16 * k);
+// Byte j of block b of a row of nb blocks of bs codes in row-plane order
+// (the layout of qk_plane_offset in qsf_hip_internal.h), from the row's
+// first byte.  Blocks of up to 64 codes: 16-byte planes of nb blocks, then a
+// tail plane of bb % 16 bytes a block.  Larger blocks: the meta dwords, then
+// the same planes over 64-code parts.
+__device__ __forceinline__ uint32_t plane_off(int b, int j, int nb, int bb, int bs) {
+    if (bs <= 64) {
+        const int k = bb >> 4;
+        return j < 16 * k ? (uint32_t)(j >> 4) * (uint32_t)nb * 16u + (uint32_t)b * 16u + (uint32_t)(j & 15)
+                          : (uint32_t)k * (uint32_t)nb * 16u + (uint32_t)b * (uint32_t)(bb & 15) +
+                                (uint32_t)(j - 16 * k);
+    }
+    if (j < 4) return (uint32_t)b * 4u + (uint32_t)j;
+    const int P = bs >> 6, cwb = (bb - 4) / P, k = cwb >> 4;
+    const uint32_t np = (uint32_t)nb * (uint32_t)P, u = (uint32_t)b * (uint32_t)P + (uint32_t)((j - 4) / cwb);
+    const int c = (j - 4) % cwb;
+    return c < 16 * k ? (uint32_t)nb * 4u + (uint32_t)(c >> 4) * np * 16u + u * 16u + (uint32_t)(c & 15)
+                      : (uint32_t)nb * 4u + (uint32_t)k * np * 16u + u * (uint32_t)(cwb & 15) + (uint32_t)(c - 16 * k);
 }
 
 // Signed 4-bit x signed 4-bit dot of 8 nibble pairs, accumulated in int32

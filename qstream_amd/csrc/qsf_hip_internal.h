@@ -68,19 +68,26 @@ typedef struct qsf_hip_tensor {
 size_t qk_frag_bytes(int rows, int nb, int block_bytes);
 /* byte j of block b of row `row` in fragment order */
 size_t qk_frag_offset(size_t row, int b, int j, int nq, int block_bytes);
-/* Row-plane order: the device layout of every other dense tensor with
- * blocks of at most 64 codes (the blocks the dot-product GEMV reads whole).
- * Rows stay where they are on disk (nb * bb bytes each); inside a row, bytes
- * [16 i, 16 i + 16) of block b sit at i * nb * 16 + 16 b (plane i, for
- * i < bb / 16), and the last bb % 16 bytes of block b at (bb / 16) * nb * 16
- * + (bb % 16) b (the tail plane).  So a wave's 16-byte loads of consecutive
- * blocks each read one aligned, contiguous run of 1 KB where the on-disk
- * order gives dword-aligned loads that straddle lines, and a block's meta
- * dword and codes arrive in one 16-byte load. */
+/* Row-plane order: the device layout of every other dense tensor.  Rows
+ * stay where they are on disk (nb * bb bytes each); inside a row:
+ *  - blocks of at most 64 codes (read whole, one a lane): bytes
+ *    [16 i, 16 i + 16) of block b sit at i * nb * 16 + 16 b (plane i, for
+ *    i < bb / 16), and the last bb % 16 bytes of block b at
+ *    (bb / 16) * nb * 16 + (bb % 16) b (the tail plane);
+ *  - blocks of 128 or 256 codes (read as 64-code parts, one a lane): the
+ *    meta dwords first (block b at 4 b), then the parts' code bytes, part
+ *    u = b * (bs / 64) + p holding codes [64 p, 64 p + 64) of block b, in
+ *    the same planes over parts (16-byte planes of np = nb * bs / 64 parts,
+ *    then a tail plane of cwb % 16 bytes a part, cwb = the part's code
+ *    bytes: 16, 24 or 32).
+ * So a wave's 16-byte loads of consecutive blocks or parts each read one
+ * aligned, contiguous run of 1 KB where the on-disk order gives
+ * dword-aligned loads that straddle lines and reads each line twice (codes,
+ * then meta). */
 int qk_plane_layout(int fmt, int bs);
-/* byte j of block b of a row of nb blocks in row-plane order, from the row's
- * first byte */
-size_t qk_plane_offset(int b, int j, int nb, int block_bytes);
+/* byte j of block b of a row of nb blocks of bs codes in row-plane order,
+ * from the row's first byte */
+size_t qk_plane_offset(int b, int j, int nb, int block_bytes, int bs);
 
 /* 1 when the matrix-core GEMV covers tensors of this format (QK_FMT_*),
  * block size and column count (with an outlier table when `outliers`), so

@@ -346,30 +346,59 @@ static void frag_permute(uint8_t* dst, const uint8_t* src, int rows, int nb, int
         }
 }
 
-/* Row-plane order (qsf_hip_internal.h): the blocks of at most 64 codes that
- * the dot-product GEMV reads whole, one per lane. */
+/* Row-plane order (qsf_hip_internal.h): every dense format the dot-product
+ * GEMV reads (blocks of up to 64 codes whole, larger ones as 64-code parts). */
 int qk_plane_layout(int fmt, int bs) {
-    return fmt >= 0 && bs <= 64;
+    return fmt >= 0 && (bs == 32 || bs == 64 || bs == 128 || bs == 256);
 }
 
-size_t qk_plane_offset(int b, int j, int nb, int block_bytes) {
-    const int k = block_bytes >> 4;
-    return j < 16 * k ? (size_t)(j >> 4) * (size_t)nb * 16 + (size_t)b * 16 + (size_t)(j & 15)
-                      : (size_t)k * (size_t)nb * 16 + (size_t)b * (size_t)(block_bytes & 15) +
-                            (size_t)(j - 16 * k);
+size_t qk_plane_offset(int b, int j, int nb, int block_bytes, int bs) {
+    if (bs <= 64) {
+        const int k = block_bytes >> 4;
+        return j < 16 * k ? (size_t)(j >> 4) * (size_t)nb * 16 + (size_t)b * 16 + (size_t)(j & 15)
+                          : (size_t)k * (size_t)nb * 16 + (size_t)b * (size_t)(block_bytes & 15) +
+                                (size_t)(j - 16 * k);
+    }
+    if (j < 4) return (size_t)b * 4 + (size_t)j;
+    const int P = bs / 64, cwb = (block_bytes - 4) / P, k = cwb >> 4;
+    const size_t np = (size_t)nb * P, u = (size_t)b * P + (size_t)((j - 4) / cwb);
+    const int c = (j - 4) % cwb;
+    return c < 16 * k ? (size_t)nb * 4 + (size_t)(c >> 4) * np * 16 + u * 16 + (size_t)(c & 15)
+                      : (size_t)nb * 4 + (size_t)k * np * 16 + u * (size_t)(cwb & 15) + (size_t)(c - 16 * k);
 }
 
-/* The on-disk blocks [rows][nb][bb] into row-plane order. */
-static void plane_permute(uint8_t* dst, const uint8_t* src, int rows, int nb, int bb) {
-    const int k = bb / 16, tb = bb % 16;
+/* The on-disk blocks [rows][nb][bb] into row-plane order (the layout
+ * qk_plane_offset addresses). */
+static void plane_permute(uint8_t* dst, const uint8_t* src, int rows, int nb, int bb, int bs) {
     const size_t rb = (size_t)nb * bb;
+    if (bs <= 64) {
+        const int k = bb / 16, tb = bb % 16;
+        for (int r = 0; r < rows; r++) {
+            const uint8_t* s = src + (size_t)r * rb;
+            uint8_t* d = dst + (size_t)r * rb;
+            for (int b = 0; b < nb; b++) {
+                for (int i = 0; i < k; i++)
+                    memcpy(d + (size_t)i * nb * 16 + (size_t)b * 16, s + (size_t)b * bb + 16 * i, 16);
+                if (tb) memcpy(d + (size_t)k * nb * 16 + (size_t)b * tb, s + (size_t)b * bb + 16 * k, (size_t)tb);
+            }
+        }
+        return;
+    }
+    /* part planes: the meta plane, then each 64-code part's code bytes in
+     * 16-byte planes and a tail plane (whole runs per part) */
+    const int P = bs / 64, cwb = (bb - 4) / P, k = cwb / 16, tb = cwb % 16;
+    const size_t np = (size_t)nb * P;
     for (int r = 0; r < rows; r++) {
         const uint8_t* s = src + (size_t)r * rb;
         uint8_t* d = dst + (size_t)r * rb;
         for (int b = 0; b < nb; b++) {
-            for (int i = 0; i < k; i++)
-                memcpy(d + (size_t)i * nb * 16 + (size_t)b * 16, s + (size_t)b * bb + 16 * i, 16);
-            if (tb) memcpy(d + (size_t)k * nb * 16 + (size_t)b * tb, s + (size_t)b * bb + 16 * k, (size_t)tb);
+            memcpy(d + (size_t)b * 4, s + (size_t)b * bb, 4);
+            for (int p = 0; p < P; p++) {
+                const uint8_t* cs = s + (size_t)b * bb + 4 + (size_t)p * cwb;
+                const size_t u = (size_t)b * P + (size_t)p;
+                for (int i = 0; i < k; i++) memcpy(d + (size_t)nb * 4 + (size_t)i * np * 16 + u * 16, cs + 16 * i, 16);
+                if (tb) memcpy(d + (size_t)nb * 4 + (size_t)k * np * 16 + u * (size_t)tb, cs + 16 * k, (size_t)tb);
+            }
         }
     }
 }
@@ -412,8 +441,7 @@ static qsf_hip_tensor* upload_locked(const void* host, int qt, int rows, int col
     /* device order of the blocks: fragment order where the matrix-core GEMV
      * is the engine for the format and covers the shape (engine 1 takes it
      * for the 3-bit formats, whose unpack is the costliest on the vector
-     * units; 2 for every format), else row-plane order for blocks of at most
-     * 64 codes, else the on-disk order. */
+     * units; 2 for every format), else row-plane order. */
     const int engine = qk_gemv_mfma_enable(-1);
     t->frag = fmt >= 0 && rows > 0 && (engine == 2 || (engine == 1 && fmt == QK_FMT_3)) &&
               qk_mfma_layout(fmt, bs, cols, is_outlier(qt));
@@ -502,7 +530,7 @@ static qsf_hip_tensor* upload_locked(const void* host, int qt, int rows, int col
             return NULL;
         }
         if (t->frag) frag_permute(fb, host_blocks, rows, t->nb, t->block_bytes);
-        else plane_permute(fb, host_blocks, rows, t->nb, t->block_bytes);
+        else plane_permute(fb, host_blocks, rows, t->nb, t->block_bytes, t->bs);
         he = hipMemcpy(t->d_blocks, fb, dev_blocks_bytes, hipMemcpyHostToDevice);
         free(fb);
     } else {
