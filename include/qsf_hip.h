@@ -167,9 +167,11 @@ int qsf_hip_kernel_timing_read(float* us, int max);
  * matrix-core kernel covers (cols 16..16384) are stored in its fragment
  * order and every decode GEMV over them (one-launch, gate/up, fused
  * residual + norm, table slots, prepared-x) takes that kernel; all other
- * tensors keep the on-disk order and the dot-product kernels.  2: the same
- * for the 2- and 4-bit formats too.  0: on-disk order and dot-product
- * kernels for every tensor.  A tensor keeps the engine it was uploaded
+ * tensors are stored in row-plane order (each row's block bytes regrouped
+ * into aligned 16-byte planes) and take the dot-product kernels.  2: the same
+ * for the 2- and 4-bit formats too.  0: row-plane order and dot-product
+ * kernels for every tensor.  Either way the device copy is not in on-disk
+ * order; the library reads it, callers do not.  A tensor keeps the engine it was uploaded
  * with.  For A/B comparisons and tests; both engines meet the same 1e-5
  * bound, their results differ in fp32 rounding.  engine < 0 only queries.
  * Returns the previous setting. */
