@@ -1552,6 +1552,7 @@ int plan_rt(const qsf_hip_tensor* const* t, int n, int cols, int mode, float* co
     if (any_out && !kHasOut) return -2;
     int kid;
     if (!whole) kid = 0;
+    else if (SPLIT && prepared) kid = any_out ? 11 : 12;
     else if (SPLIT) kid = any_out ? 1 : most <= 1 ? 2 : (D > 2 && most <= 2) ? 3 : 4;
     else if (prepared && any_out) kid = 5;
     else if (prepared) kid = 6;
@@ -1572,8 +1573,9 @@ thread_local const qk_norm_args* tl_norm = nullptr;
 template <int FMT, int BS, int R, bool DREG = false, bool SPLIT = false>
 int launch_rt(const qsf_hip_tensor* const* t, int n, int cols, const float* d_x,
               float* const* d_y, void* d_ws, int mode, hipStream_t s) {
-    // SPLIT: the stored blocks are t[0]->bs codes, read as parts of BS
-    if (SPLIT && (mode != QK_RUN_BOTH || t[0]->bs <= BS)) return -2;
+    // SPLIT: the stored blocks are t[0]->bs codes, read as parts of BS, x
+    // prepared here or (QK_RUN_GEMV) by qk_xprep, per part either way
+    if (SPLIT && ((mode != QK_RUN_BOTH && mode != QK_RUN_GEMV) || t[0]->bs <= BS)) return -2;
     using F = Fmt<FMT, BS>;
     const int nb = (cols + BS - 1) / BS;
     // prepared digits and block meta (QK_RUN_XPREP / a prepared run only)
@@ -1637,9 +1639,12 @@ int launch_rt(const qsf_hip_tensor* const* t, int n, int cols, const float* d_x,
         return hipGetLastError() == hipSuccess ? 0 : -1;
     }
     if constexpr (SPLIT) {
-        // one-launch decode only (the split view prepares x in its own parts)
+        // x prepared in the workgroups (1-4) or read as qk_xprep's digits of
+        // the parts (11, 12); the chunked kernel prepares its own
         switch (p.kid) {
         case 0: hipLaunchKernelGGL((gemv_chunked_kernel<FMT, BS, R, true>), g, b, p.lds, s, a); break;
+        case 11: launch_main<gemv_kernel<FMT, BS, R, DO, kHasOut, true, DREG, true>>(g, b, p.lds, s, a); break;
+        case 12: launch_main<gemv_kernel<FMT, BS, R, D, false, true, DREG, true>>(g, b, p.lds, s, a); break;
         case 1: launch_main<gemv_kernel<FMT, BS, R, DO, kHasOut, false, DREG, true>>(g, b, p.lds, s, a); break;
         case 2: launch_main<gemv_kernel<FMT, BS, R, 1, false, false, DREG, true>>(g, b, p.lds, s, a); break;
         case 3: launch_main<gemv_kernel<FMT, BS, R, (D > 2 ? 2 : D), false, false, DREG, true>>(g, b, p.lds, s, a); break;
@@ -1663,7 +1668,7 @@ template <int FMT, int BS, int R, bool DREG, bool SPLIT>
 uint64_t sig_rt(const qsf_hip_tensor* const* t, int n, int cols, int mode) {
     GemvArgs a;
     Plan p;
-    if (SPLIT && (mode != QK_RUN_BOTH || t[0]->bs <= BS)) return 0;
+    if (SPLIT && ((mode != QK_RUN_BOTH && mode != QK_RUN_GEMV) || t[0]->bs <= BS)) return 0;
     if (plan_rt<FMT, BS, R, DREG, SPLIT>(t, n, cols, mode, nullptr, a, p) < 0) return 0;
     return 1ull | (uint64_t)R << 1 | (uint64_t)DREG << 3 | (uint64_t)SPLIT << 4 |
            (uint64_t)(mode & 7) << 5 | (uint64_t)a.lpg << 8 | (uint64_t)p.kid << 16 |
@@ -1838,7 +1843,11 @@ uint64_t sig_bs(int bs, const qsf_hip_tensor* const* t, int n, int cols, int mod
 
 }  // namespace
 
+// Prepared x of blocks of 128 or 256 codes comes per 64-code part, the
+// granularity the split GEMV reads them at (as the one-launch GEMV prepares
+// them in its workgroups).
 extern "C" size_t qk_xprep_bytes(int fmt, int bs, int cols) {
+    if (bs == 128 || bs == 256) bs = 64;
     switch (fmt) {
     case QK_FMT_2: return bytes_bs<QK_FMT_2>(bs, cols);
     case QK_FMT_3: return bytes_bs<QK_FMT_3>(bs, cols);
@@ -1850,6 +1859,7 @@ extern "C" size_t qk_xprep_bytes(int fmt, int bs, int cols) {
 
 extern "C" int qk_xprep(int fmt, int bs, int cols, const float* d_x, void* d_ws, hipStream_t s) {
     if (cols <= 0) return 0;
+    if (bs == 128 || bs == 256) bs = 64;
     return launch_fmt(fmt, bs, nullptr, 0, cols, d_x, nullptr, d_ws, QK_RUN_XPREP, s);
 }
 
@@ -1860,8 +1870,8 @@ extern "C" int qk_xprep(int fmt, int bs, int cols, const float* d_x, void* d_ws,
 // 3-bit block-128 layer every launch got faster (q/k/v 9.91 -> 9.53 us, o
 // 6.48 -> 5.32, gate/up 14.26 -> 13.69, down 12.69 -> 11.92), so the view
 // is taken whatever the row count, which also keeps a grouped launch's
-// results equal to its single launches'.  One-launch mode only: prepared x
-// is laid out for the stored block size.
+// results equal to its single launches'.  Prepared x (qk_xprep) comes per
+// part too, so the prepared GEMV takes the same view.
 template <int FMT>
 int launch_split(const qsf_hip_tensor* const* t, int n, int cols, const float* x, float* const* y,
                  void* ws, int mode, hipStream_t s) {
@@ -1887,7 +1897,7 @@ extern "C" int qk_gemv_group(const qsf_hip_tensor* const* t, int n, const float*
     bool frag = false, disk = false;
     for (int i = 0; i < n; i++) (t[i]->frag ? frag : disk) = true;
     if (frag) return disk ? -2 : qk_gemv_mfma(t, n, d_x, d_y, tl_pair_act1, tl_norm, s);
-    if (mode == QK_RUN_BOTH && (bs == 128 || bs == 256)) {
+    if ((mode == QK_RUN_BOTH || mode == QK_RUN_GEMV) && (bs == 128 || bs == 256)) {
         switch (fmt) {
         case QK_FMT_2: return launch_split<QK_FMT_2>(t, n, cols, d_x, d_y, d_ws, mode, s);
         case QK_FMT_3: return launch_split<QK_FMT_3>(t, n, cols, d_x, d_y, d_ws, mode, s);
@@ -1956,7 +1966,7 @@ extern "C" uint64_t qk_gemv_signature(const qsf_hip_tensor* const* t, int n, int
             if ((t[i]->d_row_ptr != nullptr) != o) return 0;
         return 1ull | (1ull << 62) | (uint64_t)o << 1 | (uint64_t)fmt << 8 | (uint64_t)bs << 16;
     }
-    if (mode == QK_RUN_BOTH && (bs == 128 || bs == 256)) {
+    if ((mode == QK_RUN_BOTH || mode == QK_RUN_GEMV) && (bs == 128 || bs == 256)) {
         switch (fmt) {
         case QK_FMT_2: return sig_t<QK_FMT_2, 64, true>(t, n, cols, mode);
         case QK_FMT_3: return sig_t<QK_FMT_3, 64, true>(t, n, cols, mode);
@@ -1998,6 +2008,7 @@ int xstage_bs(int bs, int cols, const float* x, float* d_xcopy, void* d_ws, hipS
 extern "C" int qk_xprep_stage(int fmt, int bs, int cols, const float* x, float* d_xcopy,
                               void* d_ws, hipStream_t s) {
     if (cols <= 0) return 0;
+    if (bs == 128 || bs == 256) bs = 64;       // per 64-code part, as qk_xprep
     switch (fmt) {
     case QK_FMT_2: return xstage_bs<QK_FMT_2>(bs, cols, x, d_xcopy, d_ws, s);
     case QK_FMT_3: return xstage_bs<QK_FMT_3>(bs, cols, x, d_xcopy, d_ws, s);

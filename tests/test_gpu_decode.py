@@ -89,24 +89,29 @@ def _slots(qt, bs):
 def test_xprep_digits_exact(hip, qt, bs):
     """x -> block-fixed-point X = rint(x * 2^sh) with amax * 2^sh < 2^XB, and
     the six balanced base-16 digit words of every multiplier X * 2^shift,
-    reconstructed exactly; block meta f = 2^-sh and sum(X) * f in fp32."""
+    reconstructed exactly; block meta f = 2^-sh and sum(X) * f in fp32.
+    Blocks of 128 or 256 codes are prepared per 64-code part (the unit the
+    split GEMV reads them in), so their digits are those of 64-code blocks."""
     torch = torch_cuda()
     rng = np.random.default_rng(bs + qt)
-    cols = 5 * bs + bs // 2 + 3                  # partial last block
+    stored = bs
+    cols = 5 * stored + stored // 2 + 3          # partial last block
     x = F.gaussian(rng, cols)
-    x[bs:2 * bs] = 0.0                           # an all-zero block
-    x[2 * bs:3 * bs] *= np.float32(1e-30)        # tiny scale
-    x[3 * bs:4 * bs] *= np.float32(2.0 ** 120)   # huge scale (negative shift)
+    x[stored:2 * stored] = 0.0                   # an all-zero block
+    x[2 * stored:3 * stored] *= np.float32(1e-30)    # tiny scale
+    x[3 * stored:4 * stored] *= np.float32(2.0 ** 120)   # huge scale (negative shift)
+    bs = min(bs, 64)                             # the prepared unit
     nb = (cols + bs - 1) // bs
     cw, nc, slots = _slots(qt, bs)
     nd = 6
     dw = cw * nc * nd                            # digit words a block, a multiple of 4
     dws = dw if (dw // 4) % 2 else dw + 4        # stride: an odd number of 16-byte quads
     xb = 20 if qt == F.Q3 else 22
-    nbytes = hip.xprep_bytes(qt, bs, cols)
+    nbytes = hip.xprep_bytes(qt, stored, cols)
+    assert nbytes == hip.xprep_bytes(qt, bs, cols)
     buf = torch.zeros(nbytes + 256, dtype=torch.uint8, device="cuda:0")
     addr = (buf.data_ptr() + 255) & ~255
-    hip.xprep(qt, bs, cols, dev(x), addr, stream=_stream())
+    hip.xprep(qt, stored, cols, dev(x), addr, stream=_stream())
     raw = host(buf)[addr - buf.data_ptr():][:nbytes]
     dig = raw[:nb * dws * 4].view(np.uint32).reshape(nb, dws)
     moff = (nb * dws * 4 + 255) & ~255
