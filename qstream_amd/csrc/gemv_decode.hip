@@ -411,6 +411,11 @@ __device__ __forceinline__ float group_reduce(float v, int lpg) {
     if (lpg == 64) return qsf::group_sum_last(v, 64);
     return qsf::group_sum_last(v, lpg);
 }
+
+template <int CTRL, int BANK>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, BANK, false));
+}
 #undef QSF_DPP
 
 struct GemvArgs {
@@ -435,6 +440,8 @@ struct GemvArgs {
     int n, cols, nb, lpg, lpg_log2, chunk, tpw;
     int xs_off;                    // LDS dword offset of fp32 x (main kernel)
     int st_off, st_wave;           // LDS dword offset / floats per wave of the result stash
+    int pr_off;                    // one block a lane, one-row tiles, 64-lane groups: LDS dword
+                                   // offset of each wave's [MT][64] lane partials, or 0
     uint32_t row_bytes;            // SPLIT kernels: bytes a stored row
     uint32_t pbb;                  // SPLIT: bytes of a stored block
     int lsplit;                    // SPLIT: log2(stored block size / BS)
@@ -1119,6 +1126,16 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
             ++ij;
             at_tile(min(ij, ntl - 1));
         };
+        // Two or more tiles, one row each, in 64-lane groups: an item leaves
+        // its lane partial in LDS (slot cj of the wave's [MT][64]), and the
+        // rows are reduced together after the loop, with the pairings of
+        // group_reduce (same bits), instead of a DPP reduction an item.
+        // Outlier kernels only: config 1 (5-6 tiles a wave) 8.96-9.56 ->
+        // 8.84-8.94 us; in the plain kernels the added code alone took
+        // config 0 (one tile a wave, never this path) from 3.91-4.00 to
+        // 4.01-4.09 us.
+        float* const prs = reinterpret_cast<float*>(lds + a.pr_off) + wave * (MT * 64);
+        const bool multi = OUT && R == 1 && a.pr_off > 0 && ni >= 2;
         auto item = [&](const WV& w, int k) __attribute__((always_inline)) {
             if (live) compute_block<FMT, BS, R>(w, dreg, mreg, rs);
             if constexpr (OUT) {
@@ -1127,11 +1144,16 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
 #pragma unroll
                 for (int r = 0; r < R; r++) rs[r] += (mb >> r) & 1u ? p : 0.0f;
             }
+            if (OUT && multi) {
+                prs[cj * 64 + lane] = rs[0];
+                rs[0] = 0.0f;
+            } else {
 #pragma unroll
-            for (int r = 0; r < R; r++) {
-                const float v = group_reduce(rs[r], lpg);
-                rs[r] = 0.0f;
-                if (lig == lpg - 1) stash[cj * rpt + grp * R + r] = v;
+                for (int r = 0; r < R; r++) {
+                    const float v = group_reduce(rs[r], lpg);
+                    rs[r] = 0.0f;
+                    if (lig == lpg - 1) stash[cj * rpt + grp * R + r] = v;
+                }
             }
             ++cj;
         };
@@ -1151,6 +1173,21 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
 #pragma unroll
             for (int k = 0; k < D; k++)
                 if ((nblk - 1) * D + k < ni) item(wv[k], k);
+        }
+        if (OUT && multi) {
+            // lane 8 s + p: slot s's lanes 8 p .. 8 p + 7, paired as
+            // group_sum_last pairs lanes (l^1, l^2, the two quads), then
+            // the eight partial sums across p (its 8-lane groups, 16-lane
+            // rows 0+1 and 2+3, and the two pairs); slots past the wave's
+            // tiles hold stale values and are not stored
+            const int sl = lane >> 3, pp = lane & 7;
+            const f32x4 v0 = *reinterpret_cast<const f32x4*>(prs + sl * 64 + 8 * pp);
+            const f32x4 v1 = *reinterpret_cast<const f32x4*>(prs + sl * 64 + 8 * pp + 4);
+            float tsum = ((v0.x + v0.y) + (v0.z + v0.w)) + ((v1.x + v1.y) + (v1.z + v1.w));
+            tsum += dpp_f<0xB1, 0xF>(tsum);                 // quad_perm [1,0,3,2]
+            tsum += dpp_f<0x4E, 0xF>(tsum);                 // quad_perm [2,3,0,1]
+            tsum += dpp_f<0x141, 0xF>(tsum);                // row_half_mirror
+            if (pp == 0 && sl < nt) stash[sl] = tsum;
         }
     } else {
         for (int q = 0; q + 1 < nblk; q++) {
@@ -1543,6 +1580,18 @@ int plan_rt(const qsf_hip_tensor* const* t, int n, int cols, int mode, float* co
         a.st_off = a.xs_off + nb * BS;
         a.st_wave = ntc * rows_per_tile;
         lds = main_fixed + (size_t)ntc * per_tile;
+        // one block a lane in 64-lane groups, two or more tiles a wave, the
+        // outlier kernels: room for every wave's lane partials, one row a
+        // slot, reduced once at the wave's end
+        a.pr_off = 0;
+        if (DREG && R == 1 && lpg == 64 && ntc >= 2 && any_out) {
+            const size_t at = (lds + 15) & ~(size_t)15;
+            const size_t pr = (size_t)WAVES * MT * 64 * sizeof(float);
+            if (at + pr <= lds_limit()) {
+                a.pr_off = (int)(at / 4);
+                lds = at + pr;
+            }
+        }
     } else {
         grid = (tiles + a.tpw - 1) / a.tpw;
     }
