@@ -443,7 +443,6 @@ struct GemvArgs {
     int pr_off;                    // one block a lane, one-row tiles, 64-lane groups: LDS dword
                                    // offset of each wave's [MT][64] lane partials, or 0
     uint32_t row_bytes;            // SPLIT kernels: bytes a stored row
-    uint32_t pbb;                  // SPLIT: bytes of a stored block
     int lsplit;                    // SPLIT: log2(stored block size / BS)
     const uint32_t* xq;            // prepared digits (stride DWS), or null: prepare here
     const float2* xmeta;
@@ -488,9 +487,8 @@ __device__ __forceinline__ void entry_at(const GemvArgs& a, int m, uint32_t e, u
 template <int FMT, int BS, int R, bool SPLIT = false>
 __device__ __forceinline__ void load_block(const uint8_t* __restrict__ w, const uint32_t (&roff)[R],
                                            int b, uint32_t (&wv)[R][1 + Fmt<FMT, BS>::CW],
-                                           uint32_t pbb, int lsplit, int nb) {
+                                           int lsplit, int nb) {
     using F = Fmt<FMT, BS>;
-    constexpr int NW = 1 + F::CW;
     if constexpr (SPLIT) {
         // b is 64-code part b of the row (nb parts with data), part
         // b % 2^lsplit of stored block b >> lsplit; row-plane order (blocks
@@ -500,7 +498,6 @@ __device__ __forceinline__ void load_block(const uint8_t* __restrict__ w, const 
         // block, so a partial last block counts whole) and the rest at
         // 4 (CW % 4) b in the tail plane
         constexpr int NQ = F::CW / 4, NT = F::CW % 4;
-        (void)pbb;
         const uint32_t nst = ((uint32_t)nb + (1u << lsplit) - 1u) >> lsplit;   // stored blocks a row
         const uint32_t ps = (nst << lsplit) * 16u;
 #pragma unroll
@@ -532,7 +529,7 @@ __device__ __forceinline__ void load_block(const uint8_t* __restrict__ w, const 
         // NW % 4 dwords at 4 (NW % 4) b in the tail plane after the planes.
         // The lanes of a row group read consecutive blocks, so each 16-byte
         // load instruction covers aligned, contiguous memory.
-        constexpr int NQ = NW / 4, NT = NW % 4;
+        constexpr int NW = 1 + F::CW, NQ = NW / 4, NT = NW % 4;
         const uint32_t ps = (uint32_t)nb * 16u;
 #pragma unroll
         for (int r = 0; r < R; r++) {
@@ -558,7 +555,6 @@ __device__ __forceinline__ void load_block(const uint8_t* __restrict__ w, const 
         // x), from row-plane order: block b's meta dword at 4 b, then each of its
         // P 64-code parts u = b P + p as in the split read above
         constexpr int P = BS / 64, CWP = F::CW / P, NQ = CWP / 4, NT = CWP % 4;
-        (void)NW;
         const uint32_t np = (uint32_t)nb * P, ps = np * 16u;
 #pragma unroll
         for (int r = 0; r < R; r++) {
@@ -805,7 +801,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
     // next item's weights; past the last item, the last tile's row starts
     auto issue = [&](WV& wv) __attribute__((always_inline)) {
         const int b = ij < nt ? min(lig + (iq << lgl), a.nb - 1) : 0;
-        load_block<FMT, BS, R, SPLIT>(W, ioff, b, wv, a.pbb, a.lsplit, a.nb);
+        load_block<FMT, BS, R, SPLIT>(W, ioff, b, wv, a.lsplit, a.nb);
         if (++iq == ipt) {
             iq = 0;
             ++ij;
@@ -1122,7 +1118,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvArgs a) {
         const bool live = lig < a.nb;
         const int bl = min(lig, a.nb - 1);
         auto issue_d = [&](WV& wv) __attribute__((always_inline)) {
-            load_block<FMT, BS, R, SPLIT>(W, ioff, bl, wv, a.pbb, a.lsplit, a.nb);
+            load_block<FMT, BS, R, SPLIT>(W, ioff, bl, wv, a.lsplit, a.nb);
             ++ij;
             at_tile(min(ij, ntl - 1));
         };
@@ -1328,7 +1324,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_chunked_kernel(GemvArgs a) {
             for (int r = 0; r < R; r++) roff[r] = (uint32_t)min(row0 + r, a.rows[m] - 1) * row_bytes;
             for (int b = c0 + lig; b < c1; b += lpg) {
                 uint32_t wv[R][1 + F::CW];
-                load_block<FMT, BS, R, SPLIT>(a.w[m], roff, b, wv, a.pbb, a.lsplit, a.nb);
+                load_block<FMT, BS, R, SPLIT>(a.w[m], roff, b, wv, a.lsplit, a.nb);
                 compute_block<FMT, BS, R>(wv, dig + (b - c0) * F::DWS, meta[b - c0], rs[j]);
             }
         }
@@ -1478,7 +1474,6 @@ int plan_rt(const qsf_hip_tensor* const* t, int n, int cols, int mode, float* co
     a = GemvArgs{};
     a.n = n;
     a.row_bytes = (uint32_t)((size_t)t[0]->nb * t[0]->block_bytes);
-    a.pbb = (uint32_t)t[0]->block_bytes;
     a.lsplit = 0;
     while ((BS << a.lsplit) < t[0]->bs) a.lsplit++;
     a.cols = cols;
