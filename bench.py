@@ -986,8 +986,8 @@ def main():
                     help="eager launches only, no timing (for rocprofv3 counter passes)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path "
-              "(single-GPU hot path; see DESIGN.md for how it would shard)", file=sys.stderr)
+        print("bench.py measures one GPU: this build has no multi-GPU path (the hot path runs "
+              "on one GPU; across GPUs it would shard weight rows with no exchange)", file=sys.stderr)
         sys.exit(2)
     import torch
     from qstream_amd import qsf_hip
